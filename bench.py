@@ -1,0 +1,345 @@
+#!/usr/bin/env python
+"""Benchmark of the hip provider on one MI355X.
+
+Headline (the JSON line's `value`): BASELINE config 2, fused row softmax forward +
+backward in f16 storage with f32 math, 16384 x 4096 — one step = stable_softmax_f16
+then softmax_backward_f16 through prepared intent.jit calls; throughput = algorithmic
+bytes (fwd 4*M*N + bwd 6*M*N = 671,088,640 B) / measured step time, inputs resident in
+HBM. `roofline` is the dominant kernel (the backward) timed alone with HIP events on the
+launch stream. `operators` carries every other configuration (median of 33 graph replays,
+first dropped, 512 MiB flush of the 256 MB MALL before each), and
+`cpu_baseline` the oracle on a bounded sample on this host.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-operators] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "HBM GB/s (softmax, SpMV) and TFLOP/s (GEMM, attention) vs 1-GPU roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0          # dense bf16 / fp16
+FWD_BYTES_PER_ELEMENT, BWD_BYTES_PER_ELEMENT = 4, 6
+
+
+def log(*parts):
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+def parse():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-operators", action="store_true")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--operators", default="softmax_f32,gemm,attention,spmv")
+    return parser.parse_args()
+
+
+# ------------------------------------------------------------------------------ GPU timing
+class Flush:
+    """Zeroes 512 MiB (twice the 256 MB MALL) outside each timed interval."""
+
+    def __init__(self, device):
+        import torch
+
+        self.buffer = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+
+    def __call__(self):
+        self.buffer.zero_()
+
+
+def graph_median_ms(launch, flush, replays=33):
+    """Reference protocol (runtime/triton/cuda.py:18-44): warm up, capture, replay with a flush
+    before each timed replay, drop the first sample, report the median."""
+    import torch
+
+    launch()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            launch()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(replays):
+        flush()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        end.synchronize()
+        samples.append(start.elapsed_time(end))
+    return statistics.median(samples[1:])
+
+
+def events_ms(launch, count):
+    """Average duration of `count` back-to-back launches, HIP events on the launch stream."""
+    import torch
+
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(count):
+        launch()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / count
+
+
+# ------------------------------------------------------------------------------ CPU baseline
+def cpu_median_seconds(run):
+    """Reference CPU protocol (runtime/mojo/compilation.py:34,56-91; mojo/program.py:28-34):
+    64 MiB eviction write outside the interval, repetitions = clamp(10 ms / first, 1, 50),
+    median of 7 samples."""
+    import numpy as np
+
+    evict = np.empty(64 << 20, np.uint8)
+    begin = time.perf_counter()
+    run()
+    first = time.perf_counter() - begin
+    reps = int(min(50, max(1, 0.010 / max(first, 1e-9))))
+    samples = []
+    for _ in range(7):
+        evict.fill(1)
+        begin = time.perf_counter()
+        for _ in range(reps):
+            run()
+        samples.append((time.perf_counter() - begin) / reps)
+    return statistics.median(samples)
+
+
+def headline_cpu_baseline(x, dy):
+    import oracle
+
+    rows = 2048
+    xs, gs = x[:rows], dy[:rows]
+    workers = oracle.default_workers()
+
+    def run():
+        y = oracle.softmax_fwd(xs, workers=workers)
+        oracle.softmax_bwd(y, gs, workers=workers)
+
+    seconds = cpu_median_seconds(run)
+    nbytes = (FWD_BYTES_PER_ELEMENT + BWD_BYTES_PER_ELEMENT) * rows * x.shape[1]
+    return {"value": round(nbytes / seconds / 1e9, 3), "unit": "GB/s", "cores": workers, "kind": "port",
+            "sample": f"oracle softmax fwd+bwd f16 on rows 0..{rows - 1} of the 16384x4096 input "
+                      f"(1/{x.shape[0] // rows} of the workload), median of 7 samples, "
+                      f"{workers} OpenMP workers (min(8, allowed CPUs)); host has {os.cpu_count()} CPUs"}
+
+
+# ------------------------------------------------------------------------------ operators
+def op_softmax_f32(device, flush, cpu):
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.normalization.softmax import stable_softmax
+
+    x = inputs.softmax_f32()
+    call = intent.jit(stable_softmax, backend="hip").prepare(torch.from_numpy(x).to(device))
+    ms = graph_median_ms(call.launch, flush)
+    nbytes = 2 * 4 * x.size
+    out = {"config": "softmax fwd f32 4096x1024 (config 1)", "median_ms": round(ms, 5),
+           "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+           "note": "33.5 MB working set; timed after a 512 MiB flush"}
+    if cpu:
+        import oracle
+
+        seconds = cpu_median_seconds(lambda: oracle.softmax_fwd(x))
+        out["cpu"] = {"ms": round(seconds * 1e3, 3), "cores": oracle.default_workers(), "kind": "port"}
+    return out
+
+
+def op_gemm(device, flush, cpu):
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.contraction.gemm import bf16_gemm
+    from tests.gpu_util import to_bf16_tensor
+
+    m = n = k = 8192
+    a, b = inputs.gemm_bf16()
+    call = intent.jit(bf16_gemm, backend="hip").prepare(to_bf16_tensor(a, device), to_bf16_tensor(b, device))
+    ms = graph_median_ms(call.launch, flush)
+    flops = 2 * m * n * k
+    out = {"config": "GEMM bf16 8192^3, fp32 accumulate (config 3)", "median_ms": round(ms, 4),
+           "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        rows = 16
+        seconds = cpu_median_seconds(lambda: oracle.gemm_bf16(a[:rows], b))
+        out["cpu"] = {"tflops": round(2 * rows * n * k / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": f"{rows} rows of A"}
+    return out
+
+
+def op_attention(device, flush, cpu):
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.streaming.attention import flash_attention_fwd
+
+    q, k, v, scale = inputs.attention_f16()
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    call = intent.jit(flash_attention_fwd, backend="hip", constexprs={"CAUSAL": True}).prepare(
+        t(q), t(k), t(v), scale)
+    ms = graph_median_ms(call.launch, flush)
+    b, h, s, d = q.shape
+    flops = 4 * b * h * s * s * d // 2
+    out = {"config": "causal attention fwd f16 B4 H32 S4096 D128 (config 4)", "median_ms": round(ms, 4),
+           "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        seconds = cpu_median_seconds(lambda: oracle.attention_fwd_f16(q[:1, :1, :1024], k[:1, :1], v[:1, :1],
+                                                                      scale, True))
+        sample_flops = 4 * 1024 * 1024 * d // 2
+        out["cpu"] = {"tflops": round(sample_flops / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": "1 (batch, head) pair, first 1024 queries"}
+    return out
+
+
+def op_spmv(device, flush, cpu):
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.sparse.csr_spmv import csr_spmv
+
+    offsets, columns, values, x = inputs.spmv_f32()
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    call = intent.jit(csr_spmv, backend="hip").prepare(t(offsets), t(columns), t(values), t(x))
+    ms = graph_median_ms(call.launch, flush)
+    rows, nnz = offsets.shape[0] - 1, int(offsets[-1])
+    nbytes = 4 * (rows + 1) + 8 * nnz + 4 * x.shape[0] + 4 * rows
+    out = {"config": f"CSR SpMV f32 {rows}^2, {nnz} nnz, rank-law Zipf(1.5) rows (config 5)",
+           "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    if cpu:
+        import oracle
+
+        seconds = cpu_median_seconds(lambda: oracle.csr_spmv(offsets, columns, values, x))
+        out["cpu"] = {"gbs": round(nbytes / seconds / 1e9, 3), "cores": oracle.default_workers(), "kind": "port"}
+    return out
+
+
+OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_attention, "spmv": op_spmv}
+
+
+def read_traffic(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by a
+    copy-kernel calibration), recorded in profiles/<name>.traffic.txt as `traffic_bytes: N`."""
+    path = ROOT / "profiles" / f"{name}.traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every operator shards by rows / (batch, head) with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.backward.softmax import softmax_backward_f16
+    from intent_amd.examples.kernels.normalization.softmax import stable_softmax_f16
+
+    device = torch.device("cuda", 0)
+    rows, cols = 16384, 4096
+    log("generating config 2 inputs")
+    x_host, dy_host = inputs.softmax_f16_fwd_bwd(seed=0, rows=rows, cols=cols)
+    x, dy = torch.from_numpy(x_host).to(device), torch.from_numpy(dy_host).to(device)
+    fwd = intent.jit(stable_softmax_f16, backend="hip").prepare(x)
+    bwd = intent.jit(softmax_backward_f16, backend="hip").prepare(fwd.result(), dy)
+
+    def step():
+        fwd.launch()
+        bwd.launch()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+    fwd_bytes = FWD_BYTES_PER_ELEMENT * rows * cols
+    bwd_bytes = BWD_BYTES_PER_ELEMENT * rows * cols
+    value = (fwd_bytes + bwd_bytes) / ms_per_step / 1e6
+    log(f"fwd+bwd step {ms_per_step:.4f} ms -> {value:.1f} GB/s")
+
+    bwd_ms = events_ms(bwd.launch, max(args.steps, 20))
+    fwd_ms = events_ms(fwd.launch, max(args.steps, 20))
+    achieved = bwd_bytes / bwd_ms / 1e6
+    roofline = {"bound": "hbm", "kernel": "softmax_bwd_wave<f16,8,8> (softmax_backward_f16)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("softmax_bwd_f16_16384x4096"),
+                "avg_launch_ms": round(bwd_ms, 5), "algorithmic_bytes": bwd_bytes,
+                "fwd_kernel": {"avg_launch_ms": round(fwd_ms, 5), "achieved": round(fwd_bytes / fwd_ms / 1e6, 1),
+                               "frac": round(fwd_bytes / fwd_ms / 1e6 / HBM_PEAK_GBS, 4),
+                               "traffic": read_traffic("softmax_fwd_f16_16384x4096")}}
+    log(f"bwd kernel {bwd_ms:.4f} ms ({achieved:.1f} GB/s), fwd kernel {fwd_ms:.4f} ms")
+
+    operators = []
+    if not args.no_operators:
+        flush = Flush(device)
+        for name in [n for n in args.operators.split(",") if n]:
+            log(f"operator {name}")
+            try:
+                operators.append(OPERATORS[name](device, flush, not args.no_cpu_baseline))
+            except intent.CompilationStageError as error:
+                operators.append({"config": name, "status": "unsupported", "error": str(error)})
+            log(json.dumps(operators[-1]))
+            torch.cuda.empty_cache()
+
+    cpu_baseline = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu_baseline = headline_cpu_baseline(x_host, dy_host)
+
+    record = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "softmax fwd+bwd f16 storage / f32 math, 16384x4096, x ~ N(0,1)*3, dy ~ N(0,1), "
+                               "seed 0 (BASELINE config 2)", "rows": rows, "cols": cols,
+                   "bytes_per_step": fwd_bytes + bwd_bytes, "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": cpu_baseline, "operators": operators,
+    }
+    print(json.dumps(record), flush=True)
+    del np
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+/*
+ * intent_hip.h — C ABI of libintent_hip.so, the native side of the `hip` provider.
+ *
+ * The reference has no native ABI for these operators: each one is a Triton
+ * kernel generated at run time and launched from Python
+ * (python/intent/runtime/triton/program.py:291-389, launched by
+ * python/intent/runtime/block/program.py:66-82). Every entry point below replaces
+ * that launch for one `intent.examples` definition; the definition it serves is
+ * cited on each declaration.
+ *
+ * Conventions (all entry points):
+ *   - return an int status: INTENT_HIP_OK (0) or one of the codes below;
+ *     intent_hip_status_string() names a code, intent_hip_last_error() gives the
+ *     calling thread's detail message of the last failure;
+ *   - every pointer is a device pointer owned by the caller; extents and strides are
+ *     in elements; the innermost stride of every tensor is 1;
+ *   - the launch is asynchronous on `stream` (a hipStream_t; NULL = default stream);
+ *     nothing is allocated, nothing is synchronised;
+ *   - calls are stateless and thread-safe.
+ */
+#ifndef INTENT_HIP_H
+#define INTENT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INTENT_HIP_ABI_VERSION 1
+
+enum IntentHipStatus {
+  INTENT_HIP_OK = 0,
+  INTENT_HIP_ERR_INVALID_ARGUMENT = 1, /* bad extent, stride, alignment or dtype code */
+  INTENT_HIP_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
+  INTENT_HIP_ERR_LAUNCH = 3,           /* the HIP runtime rejected the launch */
+  INTENT_HIP_ERR_DEVICE = 4,           /* device query failed */
+  INTENT_HIP_ERR_WORKSPACE = 5         /* workspace missing or too small */
+};
+
+enum IntentHipDtype { INTENT_HIP_F32 = 0, INTENT_HIP_F16 = 1, INTENT_HIP_BF16 = 2 };
+
+/* Operator codes for intent_hip_kernel_resources(). */
+enum IntentHipOperator {
+  INTENT_HIP_OP_SOFTMAX_FWD = 0,
+  INTENT_HIP_OP_SOFTMAX_BWD = 1,
+  INTENT_HIP_OP_GEMM_BF16 = 2,
+  INTENT_HIP_OP_ATTENTION_FWD_F16 = 3,
+  INTENT_HIP_OP_CSR_SPMV_F32 = 4
+};
+
+struct IntentHipDeviceInfo {
+  char arch[64];               /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;
+  int32_t wavefront_size;
+  int64_t lds_per_workgroup;   /* bytes */
+  int64_t global_memory_bytes;
+  int32_t clock_khz;
+  int32_t memory_clock_khz;
+  int32_t memory_bus_width;    /* bits */
+  int32_t l2_bytes;
+};
+
+struct IntentHipKernelResources {
+  char kernel[128];            /* name of the kernel the selected variant launches */
+  int32_t vgprs;               /* architectural + accumulation VGPRs per lane, when reported */
+  int32_t lds_bytes;           /* static LDS per workgroup */
+  int32_t scratch_bytes;       /* private (spill) bytes per lane */
+  int32_t max_threads_per_block;
+  int32_t block_threads;       /* threads per workgroup of the launch */
+};
+
+int intent_hip_abi_version(void);
+const char *intent_hip_status_string(int status);
+const char *intent_hip_last_error(void);
+
+int intent_hip_device_count(int *count);
+/* Replaces the CUDA driver queries of python/intent/targets/nvidia/device.py:6 (target facts). */
+int intent_hip_device_info(int device, struct IntentHipDeviceInfo *out);
+
+/* Facts of the kernel a call with these extents would launch (observation,
+ * python/intent/runtime/diagnostics.py:23-145; python/intent/runtime/triton/cuda.py:46-57). */
+int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int64_t cols,
+                                struct IntentHipKernelResources *out);
+
+/* Row softmax forward, y[r,:] = softmax(x[r,:]).
+ * dtype F32: stable_softmax            (python/intent/examples/kernels/normalization/softmax.py:23-36)
+ *            y = exp(x - max) * (1 / sum)
+ * dtype F16: stable_softmax_f16        (softmax.py:39-51)   y = f16(exp(x - max) / sum), f32 math
+ * dtype BF16: chunked_softmax_bf16     (softmax.py:54-66)   y = bf16(exp(x - max) / sum), f32 math
+ * max is maximum_num (a one-sided NaN is ignored; softmax.py:12-20). */
+int intent_hip_softmax_fwd(int dtype, const void *x, void *y, int64_t rows, int64_t cols,
+                           int64_t x_row_stride, int64_t y_row_stride, void *stream);
+
+/* Row softmax backward, dx = p * (dy - sum(p * dy)), f32 accumulation.
+ * dtype F32: softmax_backward (python/intent/examples/kernels/backward/softmax.py:9-25);
+ * dtype F16: softmax_backward_f16, the f16-storage variant of the same body. */
+int intent_hip_softmax_bwd(int dtype, const void *p, const void *dy, void *dx, int64_t rows,
+                           int64_t cols, int64_t p_row_stride, int64_t dy_row_stride,
+                           int64_t dx_row_stride, void *stream);
+
+/* C = bf16(A @ B), fp32 accumulation; A [m,k], B [k,n], C [m,n], row strides lda/ldb/ldc.
+ * bf16_gemm (python/intent/examples/kernels/contraction/gemm.py:76-92). */
+int intent_hip_gemm_bf16(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
+                         int64_t lda, int64_t ldb, int64_t ldc, void *stream);
+
+/* Fused attention forward, f16 in/out, f32 online softmax in the exp2 domain.
+ * flash_attention_fwd (python/intent/examples/kernels/streaming/attention.py:428-466) with
+ * summarize_attention_chunk_f16 (:152-191), merge_attention_summaries (:82-114) and
+ * normalize_attention_summary (:417-425).
+ * q [b,h,sq,d], k [b,h,sk,d], v [b,h,sk,dv], o [b,h,sq,dv]; strides[16] holds the four
+ * element strides of q, k, v, o in that order (the last of each must be 1).
+ * causal: key j is valid for query i iff i >= j (absolute indices). Supports d = dv = 128. */
+int intent_hip_attention_fwd_f16(const void *q, const void *k, const void *v, void *o,
+                                 int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d,
+                                 int64_t dv, const int64_t strides[16], float scale, int causal,
+                                 void *stream);
+
+/* CSR SpMV y = A x, f32 values, i32 indices.
+ * csr_spmv (python/intent/examples/kernels/sparse/csr_spmv.py:11-29), with dynamic extents.
+ * The workspace (device memory, caller-owned) must hold intent_hip_csr_spmv_workspace_bytes(). */
+int intent_hip_csr_spmv_workspace_bytes(int64_t rows, int64_t nnz, size_t *bytes);
+int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t *column_indices,
+                            const float *values, const float *x, float *y, int64_t rows,
+                            int64_t cols, int64_t nnz, void *workspace, size_t workspace_bytes,
+                            void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INTENT_HIP_H */

@@ -1,0 +1,65 @@
+"""Build libintent_hip.so for gfx950 in-tree (`python -m intent_amd.build`).
+
+Each .hip file is compiled separately (in parallel) with hipcc, then linked into
+intent_amd/libintent_hip.so. Packed-FP32 instructions are disabled on purpose
+(`-Xclang -target-feature -Xclang -packed-fp32-ops`)."""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+SOURCES = PACKAGE / "csrc"
+OUTPUT = PACKAGE / "libintent_hip.so"
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    candidate = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(candidate).exists():
+        raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+    return candidate
+
+
+def compile_flags() -> list[str]:
+    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            f"-I{ROOT / 'include'}", f"-I{SOURCES}"]
+
+
+def build(verbose: bool = False) -> Path:
+    compiler = hipcc()
+    objects_dir = PACKAGE / "_build"
+    objects_dir.mkdir(exist_ok=True)
+    sources = sorted(SOURCES.glob("*.hip"))
+
+    def compile_one(source: Path) -> Path:
+        target = objects_dir / (source.stem + ".o")
+        command = [compiler, *compile_flags(), "-c", str(source), "-o", str(target)]
+        result = subprocess.run(command, capture_output=True, text=True)
+        noise = "'-packed-fp32-ops' is not a recognized feature"
+        diagnostics = "\n".join(line for line in (result.stdout + result.stderr).splitlines() if noise not in line)
+        if result.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {source.name}:\n{diagnostics}")
+        if verbose and diagnostics.strip():
+            print(diagnostics, file=sys.stderr)
+        return target
+
+    with ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
+        objects = list(pool.map(compile_one, sources))
+    temporary = OUTPUT.with_suffix(".so.tmp")
+    command = [compiler, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(temporary), *map(str, objects)]
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"link failed:\n{result.stdout}{result.stderr}")
+    os.replace(temporary, OUTPUT)
+    return OUTPUT
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

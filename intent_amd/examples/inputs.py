@@ -1,0 +1,127 @@
+"""Seeded synthetic inputs of the benchmark configurations.
+
+Conventions follow the reference's `python/intent/examples/programs/inputs.py:16-105`:
+one `np.random.default_rng(seed)` stream per configuration, drawn in the listed order;
+`normal(shape, dtype, scale)` draws `standard_normal(float32)`, casts to the storage
+dtype, multiplies by float32(scale) in f32 and casts again; `uniform(lo, hi)` draws
+float64 uniforms, rounds to float32, then to the storage dtype (round to nearest even).
+bf16 has no numpy dtype: bf16 arrays are returned as torch tensors or uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+SPMV_ROWS = 4_194_304
+SPMV_CAP = 65_536
+SPMV_C = 3.920855e8
+
+
+def _bf16_bits(values_f32: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bf16 bit patterns (NaN kept quiet)."""
+    u = np.ascontiguousarray(values_f32, np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
+
+
+def normal(rng, shape, dtype: str = "f32", scale=None) -> np.ndarray:
+    """float32/float16 array, or uint16 bf16 bits for dtype="bf16"."""
+    sample = rng.standard_normal(shape, dtype=np.float32)
+    if dtype == "f32":
+        out = sample
+        if scale is not None:
+            out = (out * np.float32(scale)).astype(np.float32)
+        return out
+    if dtype == "f16":
+        out = sample.astype(np.float16)
+        if scale is not None:
+            out = (out.astype(np.float32) * np.float32(scale)).astype(np.float16)
+        return out
+    if dtype == "bf16":
+        bits = _bf16_bits(sample)
+        if scale is not None:
+            scaled = (bits.astype(np.uint32) << 16).view(np.float32) * np.float32(scale)
+            bits = _bf16_bits(scaled)
+        return bits
+    raise ValueError(dtype)
+
+
+def uniform(rng, shape, low: float, high: float, dtype: str = "f32") -> np.ndarray:
+    sample = rng.uniform(low, high, shape).astype(np.float32)
+    if dtype == "f32":
+        return sample
+    if dtype == "f16":
+        return sample.astype(np.float16)
+    if dtype == "bf16":
+        return _bf16_bits(sample)
+    raise ValueError(dtype)
+
+
+# ------------------------------------------------------------------------------ configurations
+def softmax_f32(seed: int = 0, rows: int = 4096, cols: int = 1024) -> np.ndarray:
+    """Config 1: x = normal((4096, 1024), f32, scale=4)."""
+    return normal(np.random.default_rng(seed), (rows, cols), "f32", 4)
+
+
+def softmax_f16_fwd_bwd(seed: int = 0, rows: int = 16384, cols: int = 4096):
+    """Config 2: x = normal(f16, scale=3) then dy = normal(f16)."""
+    rng = np.random.default_rng(seed)
+    x = normal(rng, (rows, cols), "f16", 3)
+    dy = normal(rng, (rows, cols), "f16")
+    return x, dy
+
+
+def gemm_bf16(seed: int = 0, m: int = 8192, n: int = 8192, k: int = 8192):
+    """Config 3: A = U(-1,1) [m,k] -> bf16, then B = U(-1,1) [k,n] -> bf16 (uint16 bits)."""
+    rng = np.random.default_rng(seed)
+    a = uniform(rng, (m, k), -1.0, 1.0, "bf16")
+    b = uniform(rng, (k, n), -1.0, 1.0, "bf16")
+    return a, b
+
+
+def attention_f16(seed: int = 0, batch: int = 4, heads: int = 32, seq: int = 4096, dim: int = 128):
+    """Config 4: q, k, v = normal((B,H,S,D), f16) in that order; scale = float32(1/sqrt(D))."""
+    rng = np.random.default_rng(seed)
+    q = normal(rng, (batch, heads, seq, dim), "f16")
+    k = normal(rng, (batch, heads, seq, dim), "f16")
+    v = normal(rng, (batch, heads, seq, dim), "f16")
+    return q, k, v, float(np.float32(1.0 / np.sqrt(dim)))
+
+
+def zipf_row_lengths(rows: int = SPMV_ROWS, cap: int = SPMV_CAP, c: float = SPMV_C) -> np.ndarray:
+    """Rank-law Zipf(1.5) lengths L_r = min(cap, max(1, floor(c r^-1.5))), r = 1..rows."""
+    ranks = np.arange(1, rows + 1, dtype=np.float64)
+    return np.minimum(cap, np.maximum(1, np.floor(c * ranks ** -1.5))).astype(np.int64)
+
+
+def csr_matrix(rng, lengths: np.ndarray, cols: int):
+    """CSR arrays with `lengths[r]` distinct, sorted, uniform column indices per row."""
+    rows = lengths.shape[0]
+    offsets = np.zeros(rows + 1, np.int64)
+    np.cumsum(lengths, out=offsets[1:])
+    nnz = int(offsets[-1])
+    row_of = np.repeat(np.arange(rows, dtype=np.int64), lengths)
+    columns = rng.integers(0, cols, nnz, dtype=np.int64)
+    while True:
+        keys = row_of * cols + columns
+        order = np.argsort(keys, kind="stable")
+        keys = keys[order]
+        columns = columns[order]
+        duplicate = np.zeros(nnz, bool)
+        duplicate[1:] = keys[1:] == keys[:-1]
+        count = int(duplicate.sum())
+        if count == 0:
+            break
+        columns[duplicate] = rng.integers(0, cols, count, dtype=np.int64)
+    return offsets.astype(np.int32), columns.astype(np.int32)
+
+
+def spmv_f32(seed: int = 0, rows: int = SPMV_ROWS, cap: int = SPMV_CAP, c: float = SPMV_C):
+    """Config 5 (recipe A): rank-law row lengths scattered by rng.permutation(rows); per row
+    distinct sorted uniform columns (duplicates redrawn); then values = U(-1,1), x = U(-1,1)."""
+    rng = np.random.default_rng(seed)
+    lengths = zipf_row_lengths(rows, cap, c)[rng.permutation(rows)]
+    offsets, columns = csr_matrix(rng, lengths, rows)
+    values = uniform(rng, offsets[-1], -1.0, 1.0)
+    x = uniform(rng, rows, -1.0, 1.0)
+    return offsets, columns, values, x

@@ -1,0 +1,225 @@
+"""Definitions the hip provider recognises, and how each is launched.
+
+A definition is recognised by its name plus its runtime signature (access kind,
+dtype and rank of every parameter, constexpr names). The signature check stops a
+same-named definition with a different contract from being routed to a kernel.
+Recognised definitions (reference file:line of the semantics each kernel follows):
+
+  stable_softmax          normalization/softmax.py:23-36   intent_hip_softmax_fwd (f32)
+  stable_softmax_f16      normalization/softmax.py:39-51   intent_hip_softmax_fwd (f16)
+  chunked_softmax_bf16    normalization/softmax.py:54-66   intent_hip_softmax_fwd (bf16)
+  softmax_backward        backward/softmax.py:9-25         intent_hip_softmax_bwd (f32)
+  softmax_backward_f16    f16-storage variant of the same  intent_hip_softmax_bwd (f16)
+  bf16_gemm               contraction/gemm.py:76-92        intent_hip_gemm_bf16
+  flash_attention_fwd     streaming/attention.py:428-466   intent_hip_attention_fwd_f16
+  csr_spmv                sparse/csr_spmv.py:11-29         intent_hip_csr_spmv_f32
+
+(paths relative to python/intent/examples/kernels/ in the reference).
+
+Layout handling: kernels read rows with unit inner stride. An input whose inner
+stride is not 1 is copied into a contiguous device buffer at every launch (on
+the launch stream, so the copy sees the values current at launch time); an Out
+buffer with a non-unit inner stride receives the result through a contiguous
+buffer copied back after the kernel.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Callable
+
+from ...diagnostics import CompilationStageError
+from .library import (BF16, F16, F32, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM_BF16,
+                      OP_SOFTMAX_BWD, OP_SOFTMAX_FWD)
+
+
+@dataclass
+class Launch:
+    """A bound native call: `run(stream)` returns the ABI status."""
+
+    entry: str
+    run: Callable[[int], int]
+    keep: tuple = ()
+    before: tuple = ()            # callables run on the launch stream before the kernel
+    after: tuple = ()             # callables run on the launch stream after the kernel
+    configuration: tuple = ()
+    resources: Callable[[], dict | None] = field(default=lambda: None)
+
+
+@dataclass(frozen=True)
+class OperatorSpec:
+    name: str
+    signature: tuple              # per runtime parameter: ("view", access, dtype, rank) | ("scalar", dtype)
+    constexprs: tuple[str, ...]
+    plan: Callable
+    inplace_safe: bool = False    # an Out may be exactly one of the inputs (same address and strides)
+    derived: tuple = ()           # (symbol, source symbol, offset): extent(symbol) = extent(source) + offset
+
+
+IN, OUT = 0, 1
+
+
+def _view(access, dtype, rank):
+    return ("view", access, dtype, rank)
+
+
+# ------------------------------------------------------------------------------ layout helpers
+def _readable(tensor, keep, before):
+    """A unit-inner-stride tensor with the contents of `tensor` at launch time."""
+    if tensor.dim() == 0 or tensor.stride(-1) == 1 or tensor.shape[-1] <= 1 or tensor.numel() == 0:
+        return tensor
+    staged = tensor.new_empty(tensor.shape)
+    keep.append(staged)
+    before.append(lambda: staged.copy_(tensor))
+    return staged
+
+
+def _writable(tensor, keep, after):
+    if tensor.dim() == 0 or tensor.stride(-1) == 1 or tensor.shape[-1] <= 1 or tensor.numel() == 0:
+        return tensor
+    staged = tensor.new_empty(tensor.shape)
+    keep.append(staged)
+    after.append(lambda: tensor.copy_(staged))
+    return staged
+
+
+def _row_stride(tensor):
+    rows, cols = tensor.shape
+    return tensor.stride(0) if rows > 1 else cols
+
+
+# ------------------------------------------------------------------------------ softmax
+def _softmax_fwd(dtype_code):
+    def plan(lib, bound, constexprs, device):
+        x, y = bound.arguments
+        keep, before, after = [x, y], [], []
+        xk, yk = _readable(x, keep, before), _writable(y, keep, after)
+        rows, cols = x.shape
+        fn = lib.fn["softmax_fwd"]
+        args = (dtype_code, xk.data_ptr(), yk.data_ptr(), rows, cols, _row_stride(xk), _row_stride(yk))
+        return Launch("intent_hip_softmax_fwd", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                      tuple(after), (("rows", rows), ("cols", cols)),
+                      lambda: lib.kernel_resources(OP_SOFTMAX_FWD, dtype_code, rows, cols))
+    return plan
+
+
+def _softmax_bwd(dtype_code):
+    def plan(lib, bound, constexprs, device):
+        p, dy, dx = bound.arguments
+        keep, before, after = [p, dy, dx], [], []
+        pk, gk, dk = _readable(p, keep, before), _readable(dy, keep, before), _writable(dx, keep, after)
+        rows, cols = p.shape
+        fn = lib.fn["softmax_bwd"]
+        args = (dtype_code, pk.data_ptr(), gk.data_ptr(), dk.data_ptr(), rows, cols, _row_stride(pk),
+                _row_stride(gk), _row_stride(dk))
+        return Launch("intent_hip_softmax_bwd", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                      tuple(after), (("rows", rows), ("cols", cols)),
+                      lambda: lib.kernel_resources(OP_SOFTMAX_BWD, dtype_code, rows, cols))
+    return plan
+
+
+# ------------------------------------------------------------------------------ GEMM
+def _gemm_bf16(lib, bound, constexprs, device):
+    a, b, c = bound.arguments
+    keep, before, after = [a, b, c], [], []
+    ak, bk, ck = _readable(a, keep, before), _readable(b, keep, before), _writable(c, keep, after)
+    m, k = a.shape
+    n = b.shape[1]
+    fn = lib.fn["gemm_bf16"]
+    args = (ak.data_ptr(), bk.data_ptr(), ck.data_ptr(), m, n, k, _row_stride(ak), _row_stride(bk),
+            _row_stride(ck))
+    return Launch("intent_hip_gemm_bf16", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("m", m), ("n", n), ("k", k)),
+                  lambda: lib.kernel_resources(OP_GEMM_BF16, BF16, m, n))
+
+
+# ------------------------------------------------------------------------------ attention
+def _attention_f16(lib, bound, constexprs, device):
+    import ctypes
+
+    q, k, v, o, scale = bound.arguments
+    causal = bool(constexprs["CAUSAL"])
+    keep, before, after = [q, k, v, o], [], []
+    qk, kk, vk, ok = (_readable(q, keep, before), _readable(k, keep, before), _readable(v, keep, before),
+                      _writable(o, keep, after))
+    batch, heads, sq, d = q.shape
+    sk, dv = k.shape[2], v.shape[3]
+    strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
+    keep.append(strides)
+    fn = lib.fn["attention_fwd_f16"]
+    args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, heads, sq, sk, d, dv, strides,
+            float(scale), int(causal))
+    return Launch("intent_hip_attention_fwd_f16", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("sk", sk), ("d", d),
+                                 ("causal", causal)),
+                  lambda: lib.kernel_resources(OP_ATTENTION_FWD_F16, F16, sq, d))
+
+
+# ------------------------------------------------------------------------------ SpMV
+def _csr_spmv(lib, bound, constexprs, device):
+    import ctypes
+
+    import torch
+
+    offsets, columns, values, vector, output = bound.arguments
+    rows = offsets.shape[0] - 1
+    if rows < 0 or output.shape[0] != rows:
+        raise ValueError("csr_spmv requires row_offsets.shape[0] == output.shape[0] + 1")
+    if columns.shape[0] != values.shape[0]:
+        raise ValueError("csr_spmv requires column_indices and values of equal length")
+    keep, before, after = [offsets, columns, values, vector, output], [], []
+    ok, ck, vk, xk, yk = (_readable(offsets, keep, before), _readable(columns, keep, before),
+                          _readable(values, keep, before), _readable(vector, keep, before),
+                          _writable(output, keep, after))
+    nnz, cols = values.shape[0], vector.shape[0]
+    size = ctypes.c_size_t(0)
+    lib.check(lib.fn["csr_spmv_workspace_bytes"](rows, nnz, ctypes.byref(size)), "provider_preparation")
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+    keep.append(workspace)
+    fn = lib.fn["csr_spmv_f32"]
+    args = (ok.data_ptr(), ck.data_ptr(), vk.data_ptr(), xk.data_ptr(), yk.data_ptr(), rows, cols, nnz,
+            workspace.data_ptr(), size.value)
+    return Launch("intent_hip_csr_spmv_f32", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("rows", rows), ("cols", cols), ("nnz", nnz), ("workspace_bytes", size.value)),
+                  lambda: lib.kernel_resources(OP_CSR_SPMV_F32, F32, rows, nnz))
+
+
+_SPECS = (
+    OperatorSpec("stable_softmax", (_view(IN, "f32", 2), _view(OUT, "f32", 2)), (), _softmax_fwd(F32), True),
+    OperatorSpec("stable_softmax_f16", (_view(IN, "f16", 2), _view(OUT, "f16", 2)), (), _softmax_fwd(F16), True),
+    OperatorSpec("chunked_softmax_bf16", (_view(IN, "bf16", 2), _view(OUT, "bf16", 2)), (), _softmax_fwd(BF16),
+                 True),
+    OperatorSpec("softmax_backward", (_view(IN, "f32", 2), _view(IN, "f32", 2), _view(OUT, "f32", 2)), (),
+                 _softmax_bwd(F32), True),
+    OperatorSpec("softmax_backward_f16", (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(OUT, "f16", 2)), (),
+                 _softmax_bwd(F16), True),
+    OperatorSpec("bf16_gemm", (_view(IN, "bf16", 2), _view(IN, "bf16", 2), _view(OUT, "bf16", 2)), (),
+                 _gemm_bf16),
+    OperatorSpec("flash_attention_fwd", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
+                                         _view(OUT, "f16", 4), ("scalar", "f32")), ("CAUSAL",), _attention_f16),
+    OperatorSpec("csr_spmv", (_view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "f32", 1), _view(IN, "f32", 1),
+                              _view(OUT, "f32", 1)), (), _csr_spmv, derived=(("R", "R1", -1),)),
+)
+
+SPECS = {spec.name: spec for spec in _SPECS}
+
+
+def signature_of(interface) -> tuple:
+    from ..interface import ViewParameter
+
+    return tuple(("view", int(p.access), p.dtype.name, p.rank) if isinstance(p, ViewParameter)
+                 else ("scalar", p.dtype.name) for p in interface.parameters)
+
+
+def recognize(definition, interface, constexpr_names: tuple[str, ...]) -> OperatorSpec:
+    name = getattr(definition, "__name__", None)
+    spec = SPECS.get(name)
+    if spec is None:
+        raise CompilationStageError(
+            "provider_recognition", f"the hip provider has no kernel for definition {name!r}; "
+            f"supported: {', '.join(sorted(SPECS))}")
+    if signature_of(interface) != spec.signature or tuple(constexpr_names) != spec.constexprs:
+        raise CompilationStageError(
+            "provider_recognition", f"definition {name!r} does not have the signature the hip kernel implements: "
+            f"expected {spec.signature} with constexprs {spec.constexprs}, got {signature_of(interface)} "
+            f"with constexprs {tuple(constexpr_names)}")
+    return spec

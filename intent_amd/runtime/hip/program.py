@@ -1,0 +1,207 @@
+"""The hip runtime object behind `CompiledArtifact.runtime`.
+
+Implements the runtime contract the reference's `CompiledArtifact` expects
+(`python/intent/runtime/artifact.py:16-58`, `integrations/torch.py:11-14`):
+`prepare_call`, `run`, `launch`, `interface`, `infer_outputs`, `observation`,
+`close`. Its prepared call follows `python/intent/runtime/block/program.py:33-82`:
+binding happens once, `launch()` replays the bound native call on the caller's
+current stream, asynchronously; `result()` does not synchronize.
+"""
+from __future__ import annotations
+
+import threading
+
+from ...diagnostics import CompilationStageError
+from ..artifact import CompiledArtifact
+from ..diagnostics import ConfigurationAssessment, NativeObservation, NativeResource
+from ..interface import PublicInterface, ViewParameter
+from ..invocation import bind_arguments
+from ..torch_views import allocate_output, observe_view
+from .library import library
+from .operators import OperatorSpec, recognize
+
+
+def _symbols(definition, constexprs) -> dict[str, int]:
+    """Symbol name -> dimension identity, numbered as `PublicInterface.from_definition` does."""
+    symbols: dict[str, int] = {}
+    for parameter in definition.signature.parameters.values():
+        annotation = parameter.annotation
+        if all(hasattr(annotation, f) for f in ("kind", "dtype", "shape", "constraints")):
+            for extent in annotation.shape:
+                if isinstance(extent, str) and extent not in constexprs:
+                    symbols.setdefault(extent, len(symbols) + 1)
+    return symbols
+
+
+def _constexpr_parameters(definition) -> tuple[tuple[str, object], ...]:
+    out = []
+    for name, parameter in definition.signature.parameters.items():
+        annotation = parameter.annotation
+        if hasattr(annotation, "value_type") and not hasattr(annotation, "kind"):
+            out.append((name, parameter.default))
+    return tuple(out)
+
+
+class HipPreparedCall:
+    """Bound arguments, allocated outputs/workspace and the native call that uses them."""
+
+    def __init__(self, program: "HipProgram", bound, launch):
+        self._program, self._bound, self._launch = program, bound, launch
+        self._observation = None
+
+    def compile(self) -> None:
+        """Kernels are compiled ahead of time into libintent_hip.so; nothing to do."""
+
+    def launch(self) -> None:
+        import torch
+
+        program = self._program
+        index = program.device.index
+        switch = torch.cuda.current_device() != index
+        previous = torch.cuda.current_device() if switch else None
+        if switch:
+            torch.cuda.set_device(index)
+        try:
+            stream = torch.cuda.current_stream(index).cuda_stream
+            for step in self._launch.before:
+                step()
+            status = self._launch.run(stream)
+            if status != 0:
+                raise CompilationStageError("provider_invocation",
+                                            f"{self._launch.entry}: {program.library.error(status)}")
+            for step in self._launch.after:
+                step()
+        finally:
+            if switch:
+                torch.cuda.set_device(previous)
+        self._observation = program.observe(self._launch)
+
+    def result(self):
+        return self._bound.result()
+
+    @property
+    def observation(self):
+        return self._observation
+
+    def inspect_configurations(self) -> tuple:
+        return (ConfigurationAssessment(self._launch.configuration, True, ()),)
+
+
+class HipProgram:
+    def __init__(self, spec: OperatorSpec, interface: PublicInterface, symbols: dict, constexprs: dict, target):
+        import torch
+
+        self.spec, self.interface, self.constexprs, self.target = spec, interface, dict(constexprs), target
+        self.device = torch.device("cuda", target.device)
+        self.library = library()
+        self._derived = {symbols[name]: (symbols[source], offset) for name, source, offset in spec.derived
+                         if name in symbols and source in symbols}
+        self._observation = None
+        self._lock = threading.Lock()
+        self._closed = False
+
+    # -- binding ------------------------------------------------------------------------------
+    def _bind(self, arguments, outputs, *, abstract=False):
+        device = self.device
+        return bind_arguments(
+            self.interface, tuple(arguments), outputs,
+            observe_view=lambda p, v: observe_view(p, v, device=device, abstract=abstract),
+            allocate_output=lambda p, shape: allocate_output(p, shape, device=device, abstract=abstract),
+            abstract=abstract, derived=self._derived)
+
+    def _check_writable_overlap(self, bound) -> None:
+        """Writable views may not overlap another view, except an exact in-place alias that the
+        kernel supports (same address and strides; each element is read before it is written)."""
+        views = [(p, f) for p, f in zip(self.interface.parameters, bound.views) if isinstance(p, ViewParameter)]
+        for i, (left, lf) in enumerate(views):
+            for right, rf in views[i + 1:]:
+                if not (left.writable or right.writable):
+                    continue
+                if not (lf.begin < lf.end and rf.begin < rf.end and lf.begin < rf.end and rf.begin < lf.end):
+                    continue
+                exact = (lf.pointer == rf.pointer and lf.shape == rf.shape and lf.strides == rf.strides)
+                if exact and self.spec.inplace_safe and not (left.writable and right.writable):
+                    continue
+                raise ValueError(f"{left.name} and {right.name} overlap; the hip kernel for "
+                                 f"{self.spec.name} requires writable views that do not alias other views")
+
+    def prepare_call(self, arguments: tuple, *, outputs: tuple | None = None) -> HipPreparedCall:
+        if self._closed:
+            raise RuntimeError("hip program is closed")
+        if outputs is not None and not isinstance(outputs, tuple):
+            raise TypeError("outputs must be a tuple in declared Out order")
+        bound = self._bind(arguments, outputs)
+        self._check_writable_overlap(bound)
+        launch = self.spec.plan(self.library, bound, self.constexprs, self.device)
+        return HipPreparedCall(self, bound, launch)
+
+    def run(self, *arguments):
+        call = self.prepare_call(arguments)
+        call.launch()
+        return call.result()
+
+    def launch(self, *arguments) -> None:
+        inputs, outputs = self.interface.split_arguments(tuple(arguments))
+        self.prepare_call(inputs, outputs=outputs).launch()
+
+    def infer_outputs(self, arguments: tuple):
+        """Out buffers for `arguments` without touching device pointers (fake/meta tensors)."""
+        import torch
+
+        device = arguments[0].device if arguments and hasattr(arguments[0], "device") else self.device
+        bound = bind_arguments(
+            self.interface, tuple(arguments), None,
+            observe_view=lambda p, v: observe_view(p, v, device=device, abstract=True),
+            allocate_output=lambda p, shape: allocate_output(p, shape, device=device, abstract=True),
+            abstract=True, derived=self._derived)
+        del torch
+        return bound.result()
+
+    # -- observation ----------------------------------------------------------------------------
+    def observe(self, launch) -> NativeObservation:
+        facts = launch.resources() or {}
+        resources = tuple(NativeResource(name, facts.get(name), unit, "hipFuncGetAttributes", "launch",
+                                         None if name in facts else "not reported")
+                          for name, unit in (("vgprs", "registers"), ("lds_bytes", "bytes"),
+                                             ("scratch_bytes", "bytes"), ("block_threads", "threads")))
+        observation = NativeObservation("hip", launch.entry, facts.get("kernel", ""), launch.configuration,
+                                        resources)
+        self._observation = observation
+        return observation
+
+    @property
+    def observation(self):
+        return self._observation
+
+    def close(self) -> None:
+        self._closed = True
+
+
+def materialize_hip_artifact(target, definition, *, constexprs: dict, tuning_config=None,
+                             options=None) -> CompiledArtifact:
+    """Map `definition` to its hand-written kernel and wrap it as a `CompiledArtifact`."""
+    if tuning_config is not None:
+        raise CompilationStageError("provider_configuration",
+                                    "the hip provider has fixed kernel configurations; tuning_config is not accepted")
+    numerics = getattr(options, "numerics", "source") if options is not None else "source"
+    if numerics != "source":
+        raise CompilationStageError("provider_configuration", f"the hip provider supports numerics='source' only")
+    declared = _constexpr_parameters(definition)
+    names = tuple(name for name, _ in declared)
+    unknown = set(constexprs) - set(names)
+    if unknown:
+        raise CompilationStageError("frontend", f"unknown constexpr argument {sorted(unknown)[0]!r}")
+    values = {}
+    import inspect
+
+    for name, default in declared:
+        if name in constexprs:
+            values[name] = constexprs[name]
+        elif default is not inspect.Parameter.empty:
+            values[name] = default
+        else:
+            raise CompilationStageError("frontend", f"constexpr parameter {name!r} requires a value")
+    interface = PublicInterface.from_definition(definition, values)
+    spec = recognize(definition, interface, names)
+    program = HipProgram(spec, interface, _symbols(definition, values), values, target)
+    return CompiledArtifact(f"hip:{spec.name}", "", target.device, program, None, device_type="cuda")

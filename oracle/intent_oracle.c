@@ -1,0 +1,349 @@
+/*
+ * intent_oracle.c — CPU restatement of the reference semantics of the five operators.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the parity checker of the hip provider and
+ * the CPU baseline that bench.py reports; the product (intent_amd) never loads it.
+ *
+ * Each function restates one reference definition (paths relative to
+ * /root/reference/python/intent/examples/kernels/) under the numerics contract of
+ * /root/reference/doc/dsl/types-numerics-and-effects.en.md:
+ *   - reductions ("reduce") accumulate in f32, here in index order;
+ *   - ordered loops (`for nz in range(...)`) are strict left folds, here without
+ *     fused multiply-add (the file is built with -ffp-contract=off);
+ *   - casts to f16/bf16 round to nearest even (section 5.2, :105-112);
+ *   - approximate exp2/fdiv with flush_to_zero (section 5.1, :93-103) are computed
+ *     accurately and then flushed at their boundaries, which is inside the contract.
+ * CPU worker teams use the reference's static contiguous row-range split
+ * (python/intent/runtime/mojo/task_dispatch.c:28-75) and run in IEEE mode with
+ * FTZ/DAZ cleared (python/intent/runtime/mojo/fp_environment.c:3-8).
+ */
+#include <math.h>
+#include <omp.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <xmmintrin.h>
+
+#define ORACLE_F32 0
+#define ORACLE_F16 1
+#define ORACLE_BF16 2
+
+/* ------------------------------------------------------------------ IEEE environment */
+static uint32_t enter_ieee(void) {
+  uint32_t previous = _mm_getcsr();
+  _mm_setcsr(previous & ~(UINT32_C(0x8040) | UINT32_C(0x6000)));
+  return previous;
+}
+static void leave_ieee(uint32_t previous) { _mm_setcsr(previous); }
+
+/* Rank `rank` of `size` gets rows [begin, end): the first count % size ranks get one extra. */
+static void row_range(int64_t count, int rank, int size, int64_t *begin, int64_t *end) {
+  int64_t chunk = count / size, extra = count % size;
+  *begin = rank * chunk + (rank < extra ? rank : extra);
+  *end = *begin + chunk + (rank < extra);
+}
+
+static int team_size(int workers, int64_t count) {
+  if (workers < 1) workers = 1;
+  if (count < workers) workers = count > 0 ? (int)count : 1;
+  return workers;
+}
+
+/* ------------------------------------------------------------------ 16-bit formats */
+static inline uint32_t f32_bits(float v) {
+  uint32_t u;
+  memcpy(&u, &v, 4);
+  return u;
+}
+static inline float bits_f32(uint32_t u) {
+  float v;
+  memcpy(&v, &u, 4);
+  return v;
+}
+
+float oracle_half_to_float(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exponent = (h >> 10) & 0x1fu;
+  uint32_t mantissa = h & 0x3ffu;
+  if (exponent == 0x1fu) return bits_f32(sign | 0x7f800000u | (mantissa << 13));
+  if (exponent == 0) {
+    /* zero or subnormal: mantissa * 2^-24, exact in f32 */
+    float magnitude = (float)mantissa * 5.9604644775390625e-8f;
+    return sign ? -magnitude : magnitude;
+  }
+  return bits_f32(sign | ((exponent + 112u) << 23) | (mantissa << 13));
+}
+
+/* Round-to-nearest-even f32 -> f16; finite overflow gives infinity, NaN stays NaN. */
+uint16_t oracle_float_to_half(float v) {
+  uint32_t u = f32_bits(v);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t magnitude = u & 0x7fffffffu;
+  if (magnitude > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((magnitude >> 13) & 0x1ffu));
+  if (magnitude >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520: rounds to inf */
+  if (magnitude < 0x38800000u) {
+    /* result is subnormal or zero in f16: value / 2^-24 rounded to an integer, RNE */
+    float scaled = bits_f32(magnitude) * 16777216.0f; /* exact: power-of-two scale */
+    float rounded = nearbyintf(scaled);               /* default rounding mode: nearest even */
+    return (uint16_t)(sign | (uint16_t)rounded);
+  }
+  uint32_t exponent = (magnitude >> 23) - 112u;
+  uint32_t mantissa = magnitude & 0x7fffffu;
+  uint32_t result = (exponent << 10) | (mantissa >> 13);
+  uint32_t rest = mantissa & 0x1fffu;
+  if (rest > 0x1000u || (rest == 0x1000u && (result & 1u))) result += 1u; /* carry may reach inf: correct */
+  return (uint16_t)(sign | result);
+}
+
+float oracle_bf16_to_float(uint16_t h) { return bits_f32((uint32_t)h << 16); }
+
+uint16_t oracle_float_to_bf16(float v) {
+  uint32_t u = f32_bits(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+void oracle_halves_to_floats(const uint16_t *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_half_to_float(in[i]);
+}
+void oracle_floats_to_halves(const float *in, uint16_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_float_to_half(in[i]);
+}
+void oracle_floats_to_bf16(const float *in, uint16_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_float_to_bf16(in[i]);
+}
+
+static inline float load_elem(const void *base, int dtype, int64_t index) {
+  switch (dtype) {
+    case ORACLE_F16: return oracle_half_to_float(((const uint16_t *)base)[index]);
+    case ORACLE_BF16: return oracle_bf16_to_float(((const uint16_t *)base)[index]);
+    default: return ((const float *)base)[index];
+  }
+}
+static inline void store_elem(void *base, int dtype, int64_t index, float v) {
+  switch (dtype) {
+    case ORACLE_F16: ((uint16_t *)base)[index] = oracle_float_to_half(v); break;
+    case ORACLE_BF16: ((uint16_t *)base)[index] = oracle_float_to_bf16(v); break;
+    default: ((float *)base)[index] = v;
+  }
+}
+
+/* ------------------------------------------------------------------ softmax forward
+ * normalization/softmax.py:12-66. max = maximum_num fold with identity -inf (fmaxf returns
+ * the non-NaN operand); e = exp(x - max); s = sum(e).
+ * f32 (stable_softmax, :23-36):        y = e * (1.0f / s)
+ * f16/bf16 (stable_softmax_f16 :39-51, chunked_softmax_bf16 :54-66): y = cast(e / s). */
+static void softmax_fwd_rows(int dtype, const void *x, void *y, int64_t cols, int64_t xs, int64_t ys,
+                             int64_t begin, int64_t end, float *scratch) {
+  for (int64_t r = begin; r < end; ++r) {
+    float m = -INFINITY;
+    for (int64_t c = 0; c < cols; ++c) m = fmaxf(m, load_elem(x, dtype, r * xs + c));
+    float s = 0.0f;
+    for (int64_t c = 0; c < cols; ++c) {
+      scratch[c] = expf(load_elem(x, dtype, r * xs + c) - m);
+      s += scratch[c];
+    }
+    if (dtype == ORACLE_F32) {
+      const float inv = 1.0f / s;
+      for (int64_t c = 0; c < cols; ++c) store_elem(y, dtype, r * ys + c, scratch[c] * inv);
+    } else {
+      for (int64_t c = 0; c < cols; ++c) store_elem(y, dtype, r * ys + c, scratch[c] / s);
+    }
+  }
+}
+
+int oracle_softmax_fwd(int dtype, const void *x, void *y, int64_t rows, int64_t cols, int64_t xs, int64_t ys,
+                       int workers) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int size = team_size(workers, rows);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(rows, omp_get_thread_num(), size, &begin, &end);
+    float *scratch = (float *)malloc(sizeof(float) * (size_t)cols);
+    softmax_fwd_rows(dtype, x, y, cols, xs, ys, begin, end, scratch);
+    free(scratch);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ softmax backward
+ * backward/softmax.py:9-25: proj = sum(p * dy); dx = p * (dy - proj). The f16 variant casts
+ * p and dy to f32, reduces in f32 and casts dx to f16. */
+int oracle_softmax_bwd(int dtype, const void *p, const void *dy, void *dx, int64_t rows, int64_t cols, int64_t ps,
+                       int64_t dys, int64_t dxs, int workers) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int size = team_size(workers, rows);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(rows, omp_get_thread_num(), size, &begin, &end);
+    for (int64_t r = begin; r < end; ++r) {
+      float proj = 0.0f;
+      for (int64_t c = 0; c < cols; ++c) proj += load_elem(p, dtype, r * ps + c) * load_elem(dy, dtype, r * dys + c);
+      for (int64_t c = 0; c < cols; ++c) {
+        const float pc = load_elem(p, dtype, r * ps + c);
+        store_elem(dx, dtype, r * dxs + c, pc * (load_elem(dy, dtype, r * dys + c) - proj));
+      }
+    }
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ bf16 GEMM
+ * contraction/gemm.py:76-92: c = cast(matmul(a, b, acc_dtype=f32), bf16). Each c[i][j] is
+ * accumulated in f32 over k in increasing order (a row of accumulators per i, so the inner
+ * loop over j vectorises without changing any element's order). */
+int oracle_gemm_bf16(const uint16_t *a, const uint16_t *b, uint16_t *c, int64_t m, int64_t n, int64_t k,
+                     int64_t lda, int64_t ldb, int64_t ldc, int workers) {
+  if (m <= 0 || n <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int size = team_size(workers, m);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(m, omp_get_thread_num(), size, &begin, &end);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)n);
+    float *brow = (float *)malloc(sizeof(float) * (size_t)n);
+    for (int64_t i = begin; i < end; ++i) {
+      for (int64_t j = 0; j < n; ++j) acc[j] = 0.0f;
+      for (int64_t kk = 0; kk < k; ++kk) {
+        const float av = oracle_bf16_to_float(a[i * lda + kk]);
+        const uint16_t *src = b + kk * ldb;
+        for (int64_t j = 0; j < n; ++j) brow[j] = bits_f32((uint32_t)src[j] << 16);
+        for (int64_t j = 0; j < n; ++j) acc[j] = acc[j] + av * brow[j];
+      }
+      for (int64_t j = 0; j < n; ++j) c[i * ldc + j] = oracle_float_to_bf16(acc[j]);
+    }
+    free(acc);
+    free(brow);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ attention forward
+ * streaming/attention.py:428-466 (flash_attention_fwd) as a region fold over key chunks of
+ * `chunk` keys: summarize_attention_chunk_f16 (:152-191), merge_attention_summaries (:82-114),
+ * normalize_attention_summary (:417-425); scores in the exp2 domain; exp2/fdiv are the
+ * approximate flush-to-zero operations (accurate values, subnormals flushed). */
+static inline float ftz(float v) { return fabsf(v) < 1.17549435e-38f ? copysignf(0.0f, v) : v; }
+static inline float exp2_approx_ftz(float v) { return ftz(exp2f(ftz(v))); }
+static inline float rcp_approx_ftz(float v) { return ftz(1.0f / ftz(v)); }
+
+int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o, int64_t batch,
+                             int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
+                             float scale, int causal, int64_t chunk, int workers) {
+  if (batch <= 0 || heads <= 0 || sq <= 0) return 0;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const float factor = scale * log2e;
+  const int64_t count = batch * heads * sq;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *scores = (float *)malloc(sizeof(float) * (size_t)chunk);
+    float *qrow = (float *)malloc(sizeof(float) * (size_t)d);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)dv);
+    float *cacc = (float *)malloc(sizeof(float) * (size_t)dv);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t bi = item / (heads * sq), hi = (item / sq) % heads, qi = item % sq;
+      const uint16_t *qp = q + bi * strides[0] + hi * strides[1] + qi * strides[2];
+      for (int64_t t = 0; t < d; ++t) qrow[t] = oracle_half_to_float(qp[t * strides[3]]);
+      int valid = 0;
+      float maximum = 0.0f, denominator = 0.0f;
+      for (int64_t t = 0; t < dv; ++t) acc[t] = 0.0f;
+      for (int64_t k0 = 0; k0 < sk; k0 += chunk) {
+        const int64_t k1 = k0 + chunk < sk ? k0 + chunk : sk;
+        /* summarize this chunk */
+        int cvalid = 0;
+        float cmax = -INFINITY;
+        for (int64_t j = k0; j < k1; ++j) {
+          const uint16_t *kp = k + bi * strides[4] + hi * strides[5] + j * strides[6];
+          float dot = 0.0f;
+          for (int64_t t = 0; t < d; ++t) dot = dot + qrow[t] * oracle_half_to_float(kp[t * strides[7]]);
+          const int ok = !causal || qi >= j;
+          scores[j - k0] = ok ? dot * factor : -INFINITY;
+          if (ok) {
+            cvalid = 1;
+            cmax = fmaxf(cmax, scores[j - k0]);
+          }
+        }
+        if (!cvalid) cmax = 0.0f;
+        float cden = 0.0f;
+        for (int64_t t = 0; t < dv; ++t) cacc[t] = 0.0f;
+        for (int64_t j = k0; j < k1; ++j) {
+          const int ok = !causal || qi >= j;
+          const float weight = ok ? exp2_approx_ftz(scores[j - k0] - cmax) : 0.0f;
+          cden += weight;
+          const float w16 = oracle_half_to_float(oracle_float_to_half(weight));
+          const uint16_t *vp = v + bi * strides[8] + hi * strides[9] + j * strides[10];
+          for (int64_t t = 0; t < dv; ++t) cacc[t] = cacc[t] + w16 * oracle_half_to_float(vp[t * strides[11]]);
+        }
+        if (!cvalid)
+          for (int64_t t = 0; t < dv; ++t) cacc[t] = 0.0f;
+        /* merge (running, chunk) */
+        float merged = valid ? maximum : cmax;
+        if (cvalid) merged = fmaxf(merged, cmax);
+        const float left = valid ? exp2_approx_ftz((valid ? maximum : merged) - merged) : 0.0f;
+        const float right = cvalid ? exp2_approx_ftz((cvalid ? cmax : merged) - merged) : 0.0f;
+        denominator = left * denominator + right * cden;
+        for (int64_t t = 0; t < dv; ++t) acc[t] = left * acc[t] + right * cacc[t];
+        maximum = merged;
+        valid = valid || cvalid;
+      }
+      uint16_t *op = o + bi * strides[12] + hi * strides[13] + qi * strides[14];
+      const float reciprocal = rcp_approx_ftz(valid ? denominator : 1.0f);
+      for (int64_t t = 0; t < dv; ++t) op[t * strides[15]] = oracle_float_to_half(valid ? acc[t] * reciprocal : 0.0f);
+    }
+    free(scores);
+    free(qrow);
+    free(acc);
+    free(cacc);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+/* ------------------------------------------------------------------ CSR SpMV
+ * sparse/csr_spmv.py:11-29: acc = 0.0f; for nz in [off[r], off[r+1]) in order:
+ * acc = acc + values[nz] * vector[col[nz]] (product rounded, then added); y[r] = acc. */
+int oracle_csr_spmv_f32(const int32_t *off, const int32_t *col, const float *val, const float *x, float *y,
+                        int64_t rows, int workers) {
+  if (rows <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int size = team_size(workers, rows);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(rows, omp_get_thread_num(), size, &begin, &end);
+    for (int64_t r = begin; r < end; ++r) {
+      float acc = 0.0f;
+      for (int64_t nz = off[r]; nz < off[r + 1]; ++nz) {
+        const float product = val[nz] * x[col[nz]];
+        acc = acc + product;
+      }
+      y[r] = acc;
+    }
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}

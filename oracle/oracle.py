@@ -1,0 +1,154 @@
+"""ctypes wrapper of liboracle.so (built from intent_oracle.c by the Makefile here).
+
+TEST INFRASTRUCTURE ONLY (see the package docstring)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / "liboracle.so"
+F32, F16, BF16 = 0, 1, 2
+_DTYPE_CODES = {np.dtype(np.float32): F32}
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIBRARY
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            build()
+        handle = ctypes.CDLL(str(LIBRARY))
+        p, i64, i, f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+        handle.oracle_softmax_fwd.argtypes = [i, p, p, i64, i64, i64, i64, i]
+        handle.oracle_softmax_bwd.argtypes = [i, p, p, p, i64, i64, i64, i64, i64, i]
+        handle.oracle_gemm_bf16.argtypes = [p, p, p, i64, i64, i64, i64, i64, i64, i]
+        handle.oracle_attention_fwd_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
+                                                    ctypes.POINTER(i64), f, i, i64, i]
+        handle.oracle_csr_spmv_f32.argtypes = [p, p, p, p, p, i64, i]
+        for name in ("oracle_halves_to_floats", "oracle_floats_to_halves", "oracle_floats_to_bf16"):
+            getattr(handle, name).argtypes = [p, p, i64]
+        _lib = handle
+    return _lib
+
+
+def default_workers() -> int:
+    """The reference CPU default: min(8, CPUs allowed by affinity) (targets/execution.py:20-26)."""
+    return min(8, len(os.sched_getaffinity(0)))
+
+
+def _ptr(array: np.ndarray) -> int:
+    return array.ctypes.data
+
+
+def _code(array: np.ndarray, storage: str | None) -> int:
+    if storage == "bf16":
+        return BF16
+    if array.dtype == np.float16:
+        return F16
+    if array.dtype == np.float32:
+        return F32
+    raise TypeError(f"unsupported oracle dtype {array.dtype} / {storage}")
+
+
+def _rows(array: np.ndarray) -> int:
+    return array.strides[0] // array.itemsize if array.shape[0] > 1 else array.shape[1]
+
+
+def _check_2d(*arrays):
+    for a in arrays:
+        if a.ndim != 2 or a.strides[1] != a.itemsize:
+            raise ValueError("oracle expects 2-D arrays with unit inner stride")
+
+
+# -------------------------------------------------------------------------- conversions
+def half_to_float(values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, dtype=np.uint16)
+    out = np.empty(values.shape, np.float32)
+    lib().oracle_halves_to_floats(_ptr(values), _ptr(out), values.size)
+    return out
+
+
+def float_to_half_bits(values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(values.shape, np.uint16)
+    lib().oracle_floats_to_halves(_ptr(values), _ptr(out), values.size)
+    return out
+
+
+def float_to_bf16_bits(values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty(values.shape, np.uint16)
+    lib().oracle_floats_to_bf16(_ptr(values), _ptr(out), values.size)
+    return out
+
+
+def bf16_bits_to_float(bits: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# -------------------------------------------------------------------------- operators
+def softmax_fwd(x: np.ndarray, *, storage: str | None = None, workers: int | None = None) -> np.ndarray:
+    """x: float32 / float16 array, or uint16 bf16 bits with storage="bf16"."""
+    _check_2d(x)
+    y = np.empty(x.shape, x.dtype)
+    lib().oracle_softmax_fwd(_code(x, storage), _ptr(x), _ptr(y), x.shape[0], x.shape[1], _rows(x), _rows(y),
+                             workers or default_workers())
+    return y
+
+
+def softmax_bwd(p: np.ndarray, dy: np.ndarray, *, storage: str | None = None,
+                workers: int | None = None) -> np.ndarray:
+    _check_2d(p, dy)
+    if p.shape != dy.shape or p.dtype != dy.dtype:
+        raise ValueError("p and dy must match")
+    dx = np.empty(p.shape, p.dtype)
+    lib().oracle_softmax_bwd(_code(p, storage), _ptr(p), _ptr(dy), _ptr(dx), p.shape[0], p.shape[1], _rows(p),
+                             _rows(dy), _rows(dx), workers or default_workers())
+    return dx
+
+
+def gemm_bf16(a_bits: np.ndarray, b_bits: np.ndarray, *, workers: int | None = None) -> np.ndarray:
+    """a_bits [m,k], b_bits [k,n]: uint16 bf16 bit patterns; returns c bits [m,n]."""
+    _check_2d(a_bits, b_bits)
+    m, k = a_bits.shape
+    n = b_bits.shape[1]
+    c = np.empty((m, n), np.uint16)
+    lib().oracle_gemm_bf16(_ptr(a_bits), _ptr(b_bits), _ptr(c), m, n, k, _rows(a_bits), _rows(b_bits), n,
+                           workers or default_workers())
+    return c
+
+
+def attention_fwd_f16(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool, *,
+                      chunk: int = 64, workers: int | None = None) -> np.ndarray:
+    """q [B,H,Q,D], k [B,H,K,D], v [B,H,K,DV] float16; returns o [B,H,Q,DV] float16."""
+    batch, heads, sq, d = q.shape
+    sk, dv = k.shape[2], v.shape[3]
+    o = np.empty((batch, heads, sq, dv), np.float16)
+    strides = (ctypes.c_int64 * 16)(*(s // 2 for t in (q, k, v, o) for s in t.strides))
+    lib().oracle_attention_fwd_f16(_ptr(q), _ptr(k), _ptr(v), _ptr(o), batch, heads, sq, sk, d, dv, strides,
+                                   float(np.float32(scale)), int(causal), chunk, workers or default_workers())
+    return o
+
+
+def csr_spmv(offsets: np.ndarray, columns: np.ndarray, values: np.ndarray, x: np.ndarray, *,
+             workers: int | None = None) -> np.ndarray:
+    offsets = np.ascontiguousarray(offsets, np.int32)
+    columns = np.ascontiguousarray(columns, np.int32)
+    values = np.ascontiguousarray(values, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    rows = offsets.shape[0] - 1
+    y = np.empty(rows, np.float32)
+    lib().oracle_csr_spmv_f32(_ptr(offsets), _ptr(columns), _ptr(values), _ptr(x), _ptr(y), rows,
+                              workers or default_workers())
+    return y

@@ -1,0 +1,145 @@
+"""GPU parity of the softmax kernels against the CPU oracle and the golden fixtures.
+
+Tolerances: f32 outputs rel 1e-5; f16/bf16 outputs rel 2e-2 / abs 1e-2 (and, tighter,
+within one f16 ulp of the oracle)."""
+import numpy as np
+import pytest
+import torch
+
+import intent_amd as intent
+import oracle
+from intent_amd.examples import inputs
+from intent_amd.examples.kernels.backward.softmax import softmax_backward, softmax_backward_f16
+from intent_amd.examples.kernels.normalization.softmax import (chunked_softmax_bf16, stable_softmax,
+                                                               stable_softmax_f16)
+from tests.gpu_util import (announce, assert_16bit, assert_f32_rel, bf16_tensor_bits, bf16_to_f32,
+                            f16_ulp_distance, to_bf16_tensor)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape", [(4096, 1024), (7, 1000), (5, 5000), (3, 4097), (2, 64), (1, 3), (64, 4096)])
+def test_softmax_f32_matches_oracle(device, shape):
+    announce("softmax_f32", shape)
+    x = inputs.normal(np.random.default_rng(shape[1]), shape, "f32", 4)
+    y = intent.jit(stable_softmax, backend="hip").run(torch.from_numpy(x).to(device))
+    assert_f32_rel(y.cpu().numpy(), oracle.softmax_fwd(x))
+
+
+def test_softmax_f32_config1_seed0(device):
+    announce("softmax_f32 config 1")
+    x = inputs.softmax_f32()
+    y = intent.jit(stable_softmax, backend="hip").run(torch.from_numpy(x).to(device)).cpu().numpy()
+    assert_f32_rel(y, oracle.softmax_fwd(x))
+    assert np.allclose(y.astype(np.float64).sum(axis=1), 1.0, atol=1024 * 2 ** -24)
+
+
+def test_softmax_golden(device, golden):
+    announce("softmax golden")
+    g = golden("softmax")
+    run32 = intent.jit(stable_softmax, backend="hip")
+    y = run32.run(torch.from_numpy(g["softmax_f32_x"]).to(device)).cpu().numpy()
+    assert_f32_rel(y, g["softmax_f32_y"])
+    assert (y[2, ::3] == 0).all() and y[3, 17] == 1.0
+    y2 = run32.run(torch.from_numpy(g["softmax_pow2_x"]).to(device)).cpu().numpy()
+    assert (y2 == np.float32(1 / 1024)).all()
+    y16 = intent.jit(stable_softmax_f16, backend="hip").run(torch.from_numpy(g["softmax_f16_x"]).to(device))
+    assert_16bit(y16.cpu().numpy(), g["softmax_f16_y"])
+    yb = intent.jit(chunked_softmax_bf16, backend="hip").run(to_bf16_tensor(g["softmax_bf16_x"], device))
+    assert_16bit(bf16_to_f32(bf16_tensor_bits(yb)), g["softmax_bf16_y"])
+
+
+@pytest.mark.parametrize("shape", [(16384, 4096), (9, 8200), (4, 12), (33, 2048), (3, 1001)])
+def test_softmax_f16_matches_oracle(device, shape):
+    announce("softmax_f16", shape)
+    x = inputs.normal(np.random.default_rng(shape[0]), shape, "f16", 3)
+    y = intent.jit(stable_softmax_f16, backend="hip").run(torch.from_numpy(x).to(device)).cpu().numpy()
+    want = oracle.softmax_fwd(x)
+    assert_16bit(y, want)
+    ulps = f16_ulp_distance(y, want)
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.98
+
+
+def test_softmax_bf16_matches_oracle(device):
+    announce("softmax_bf16")
+    x = inputs.normal(np.random.default_rng(3), (129, 3000), "bf16", 3)
+    y = intent.jit(chunked_softmax_bf16, backend="hip").run(to_bf16_tensor(x, device))
+    want = oracle.softmax_fwd(x, storage="bf16")
+    assert_16bit(bf16_to_f32(bf16_tensor_bits(y)), bf16_to_f32(want))
+    assert np.abs(bf16_tensor_bits(y).astype(np.int32) - want.astype(np.int32)).max() <= 1
+
+
+def test_softmax_special_values(device):
+    announce("softmax special values")
+    x = np.random.default_rng(4).standard_normal((6, 4096)).astype(np.float32)
+    x[0, 5] = np.nan
+    x[1, :] = -np.inf
+    x[2, 9] = np.inf
+    x[3, ::2] = -np.inf
+    y = intent.jit(stable_softmax, backend="hip").run(torch.from_numpy(x).to(device)).cpu().numpy()
+    want = oracle.softmax_fwd(x)
+    assert np.isnan(y[:3]).all()
+    assert_f32_rel(y, want)
+    y16 = intent.jit(stable_softmax_f16, backend="hip").run(torch.from_numpy(x.astype(np.float16)).to(device))
+    assert (np.isnan(y16.cpu().numpy()) == np.isnan(oracle.softmax_fwd(x.astype(np.float16)))).all()
+
+
+def test_softmax_layouts_and_explicit_outputs(device):
+    announce("softmax layouts")
+    rng = np.random.default_rng(5)
+    base = torch.from_numpy(inputs.normal(rng, (300, 512), "f16", 3)).to(device)
+    kernel = intent.jit(stable_softmax_f16, backend="hip")
+    transposed = base.t()                                  # inner stride 512: staged through a copy
+    y = kernel.run(transposed)
+    assert_16bit(y.cpu().numpy(), oracle.softmax_fwd(np.ascontiguousarray(transposed.cpu().numpy())))
+    sliced = base[:, 100:400]                              # row stride 512, misaligned start
+    out = torch.empty(300, 300, dtype=torch.float16, device=device)
+    kernel(sliced, out)
+    assert_16bit(out.cpu().numpy(), oracle.softmax_fwd(np.ascontiguousarray(sliced.cpu().numpy())))
+    strided_out = torch.empty(512, 300, dtype=torch.float16, device=device).t()
+    kernel.prepare(sliced, outputs=(strided_out,)).launch()
+    assert_16bit(strided_out.cpu().numpy(), oracle.softmax_fwd(np.ascontiguousarray(sliced.cpu().numpy())))
+    inplace = base.clone()
+    kernel(inplace, inplace)                               # exact alias: each row is read before written
+    assert_16bit(inplace.cpu().numpy(), oracle.softmax_fwd(base.cpu().numpy()))
+    with pytest.raises(ValueError):
+        kernel(base[:, 1:], base[:, :-1])                 # partial overlap is rejected
+
+
+def test_softmax_bwd_f32_static(device):
+    announce("softmax_bwd_f32 4096x4097")
+    rng = np.random.default_rng(6)
+    p = oracle.softmax_fwd(inputs.normal(rng, (4096, 4097), "f32", 2))
+    dy = inputs.normal(rng, (4096, 4097), "f32")
+    dx = intent.jit(softmax_backward, backend="hip").run(torch.from_numpy(p).to(device),
+                                                        torch.from_numpy(dy).to(device)).cpu().numpy()
+    want = oracle.softmax_bwd(p, dy)
+    # cancelling sum: |err| <= 1e-5 * p * (|dy| + sum|p dy|)
+    scale = np.abs(p.astype(np.float64)) * (np.abs(dy) + np.sum(np.abs(p * dy), axis=1, keepdims=True))
+    assert np.all(np.abs(dx.astype(np.float64) - want) <= 1e-5 * scale + 1e-37)
+
+
+@pytest.mark.parametrize("shape", [(16384, 4096), (5, 9000), (17, 1000), (3, 8)])
+def test_softmax_bwd_f16(device, shape):
+    announce("softmax_bwd_f16", shape)
+    x, dy = inputs.softmax_f16_fwd_bwd(seed=shape[1], rows=shape[0], cols=shape[1])
+    fwd = intent.jit(stable_softmax_f16, backend="hip")
+    bwd = intent.jit(softmax_backward_f16, backend="hip")
+    y = fwd.run(torch.from_numpy(x).to(device))
+    dx = bwd.run(y, torch.from_numpy(dy).to(device)).cpu().numpy()
+    p = y.cpu().numpy()
+    want = oracle.softmax_bwd(p, dy)
+    assert_16bit(dx, want)
+    # within two f16 roundings, plus the projection's reassociation error 1e-5 * p * sum|p dy|
+    p64 = p.astype(np.float64)
+    spread = 1e-5 * np.abs(p64) * np.sum(np.abs(p64 * dy.astype(np.float64)), axis=1, keepdims=True)
+    assert np.all(np.abs(dx.astype(np.float64) - want) <= 2 ** -9 * np.abs(want.astype(np.float64)) + spread + 6e-8)
+
+
+def test_softmax_bwd_golden(device, golden):
+    announce("softmax_bwd golden")
+    g = golden("softmax_bwd")
+    dx = intent.jit(softmax_backward_f16, backend="hip").run(
+        torch.from_numpy(g["softmax_bwd_f16_p"]).to(device), torch.from_numpy(g["softmax_bwd_f16_dy"]).to(device))
+    w = g["softmax_bwd_f16_dx"]
+    assert np.all(np.abs(dx.cpu().numpy() - w) <= 2e-2 * np.abs(w) + 1e-2 * np.abs(w).max())

@@ -1,0 +1,119 @@
+"""GPU parity of the CSR SpMV kernel.
+
+Bars: index traversal bit-exact (probes with ones, one-hot x and small integers give
+exact results in any summation order); rows folded by one thread equal the oracle's
+strict left fold bit for bit (every length-1 row, always); all rows within the
+backward-error bound |y - y64| <= 1e-5 * sum|a_i x_i| against float64, and within
+(1e-5 + 2 (L-1) 2^-24) * sum|a_i x_i| against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+import intent_amd as intent
+import oracle
+from intent_amd.examples import inputs
+from intent_amd.examples.kernels.sparse.csr_spmv import csr_spmv
+from tests.gpu_util import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def run(device, offsets, columns, values, x):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    return intent.jit(csr_spmv, backend="hip").run(t(offsets), t(columns), t(values), t(x)).cpu().numpy()
+
+
+def reference64(offsets, columns, values, x):
+    rows = offsets.shape[0] - 1
+    lengths = np.diff(offsets.astype(np.int64))
+    products = values.astype(np.float64) * x[columns].astype(np.float64)
+    y64, mag = np.zeros(rows), np.zeros(rows)
+    nonempty = lengths > 0
+    starts = offsets[:-1].astype(np.int64)[nonempty]
+    if products.size:
+        y64[nonempty] = np.add.reduceat(products, starts)
+        mag[nonempty] = np.add.reduceat(np.abs(products), starts)
+    return y64, mag, lengths
+
+
+def check(device, offsets, columns, values, x):
+    y = run(device, offsets, columns, values, x)
+    want = oracle.csr_spmv(offsets, columns, values, x)
+    y64, mag, lengths = reference64(offsets, columns, values, x)
+    assert np.all(np.abs(y - y64) <= 1e-5 * mag + 1e-38), "backward error vs float64"
+    bound = (1e-5 + 2 * np.maximum(lengths - 1, 0) * 2.0 ** -24) * mag + 1e-38
+    assert np.all(np.abs(y.astype(np.float64) - want) <= bound), "vs oracle"
+    single = lengths == 1
+    assert (y[single] == want[single]).all(), "length-1 rows must be bit-exact"
+    assert (y[lengths == 0] == 0).all()
+    return y, want
+
+
+def test_spmv_golden_and_probes(device, golden):
+    announce("spmv golden")
+    g = golden("spmv")
+    off, col, val, x = g["spmv_offsets"], g["spmv_columns"], g["spmv_values"], g["spmv_x"]
+    y, _ = check(device, off, col, val, x)
+    assert np.all(np.abs(y - g["spmv_y64"]) <= 1e-5 * g["spmv_abs"] + 1e-38)
+    ones = run(device, off, col, np.ones_like(val), np.ones(off.shape[0] - 1, np.float32))
+    assert (ones == g["spmv_lengths"]).all()
+    assert (run(device, off, col, val, g["spmv_onehot_x"]) == g["spmv_onehot_y"]).all()
+
+
+@pytest.mark.parametrize("seed,rows,max_len", [(1, 5000, 40), (2, 3000, 5000), (3, 20000, 3), (4, 257, 70000)])
+def test_spmv_random_lengths(device, seed, rows, max_len):
+    announce("spmv random", seed, rows, max_len)
+    rng = np.random.default_rng(seed)
+    lengths = rng.integers(0, max_len + 1, rows)
+    lengths[rng.integers(0, rows, rows // 10)] = 0
+    offsets, columns = inputs.csr_matrix(rng, lengths, max(rows, max_len + 1))
+    values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
+    x = inputs.uniform(rng, max(rows, max_len + 1), -1, 1)
+    check(device, offsets, columns, values, x)
+    ival = rng.integers(-3, 4, values.shape).astype(np.float32)
+    ix = rng.integers(-3, 4, x.shape).astype(np.float32)
+    assert (run(device, offsets, columns, ival, ix) == oracle.csr_spmv(offsets, columns, ival, ix)).all()
+
+
+def test_spmv_block_boundaries(device):
+    """Rows whose ends fall exactly on, just before and just after workgroup boundaries."""
+    announce("spmv block boundaries")
+    lengths = np.array([2047, 0, 1, 2046, 1, 2048, 0, 0, 4095, 1, 1, 2047, 4096, 3, 0], np.int64)
+    rng = np.random.default_rng(7)
+    offsets, columns = inputs.csr_matrix(rng, lengths, 5000)
+    values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
+    x = inputs.uniform(rng, 5000, -1, 1)
+    check(device, offsets, columns, values, x)
+
+
+def test_spmv_degenerate(device):
+    announce("spmv degenerate")
+    empty = run(device, np.zeros(6, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32),
+                np.zeros(4, np.float32))
+    assert (empty == 0).all() and empty.shape == (5,)
+    one = run(device, np.array([0, 3], np.int32), np.array([0, 1, 2], np.int32),
+              np.array([1.0, 1e-8, 1e-8], np.float32), np.ones(3, np.float32))
+    assert one[0] == np.float32(1.0)                       # the ordered fold, bit for bit
+    zero_rows = run(device, np.zeros(1, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32),
+                    np.zeros(3, np.float32))
+    assert zero_rows.shape == (0,)
+
+
+def test_spmv_config5_full(device):
+    announce("spmv config 5 (4194304 rows, recipe A)")
+    offsets, columns, values, x = inputs.spmv_f32()
+    y, want = check(device, offsets, columns, values, x)
+    assert int(offsets[-1]) == 67_108_855
+
+
+def test_spmv_shape_errors(device):
+    announce("spmv shape errors")
+    t = lambda a: torch.from_numpy(np.asarray(a)).to(device)  # noqa: E731
+    kernel = intent.jit(csr_spmv, backend="hip")
+    with pytest.raises(ValueError):
+        kernel.run(t(np.array([0, 1], np.int32)), t(np.array([0, 0], np.int32)), t(np.zeros(1, np.float32)),
+                   t(np.zeros(2, np.float32)))
+    with pytest.raises(ValueError):
+        out = torch.empty(3, device=device)
+        kernel(t(np.array([0, 1], np.int32)), t(np.array([0], np.int32)), t(np.zeros(1, np.float32)),
+               t(np.zeros(2, np.float32)), out)

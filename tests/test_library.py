@@ -1,0 +1,50 @@
+"""The C-ABI library loads without a GPU and exports exactly what include/intent_hip.h declares."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from intent_amd.runtime.hip import library as hiplib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "intent_hip.h"
+
+
+def declared_entry_points():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(intent_hip_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_entry_points() == sorted(hiplib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    if not hiplib.LIBRARY_PATH.exists():
+        pytest.fail(f"{hiplib.LIBRARY_PATH} is not built")
+    handle = ctypes.CDLL(str(hiplib.LIBRARY_PATH))
+    for name in declared_entry_points():
+        assert hasattr(handle, name), name
+
+
+def test_library_loads_and_reports_abi():
+    lib = hiplib.library()
+    assert lib.abi_version == hiplib.ABI_VERSION
+    assert lib.fn["status_string"](0) == b"ok"
+    assert lib.fn["status_string"](5).startswith(b"workspace")
+
+
+def test_argument_validation_without_gpu():
+    """Extent checks run on the host before any HIP call."""
+    lib = hiplib.library()
+    status = lib.fn["softmax_fwd"](0, None, None, -1, 4, 4, 4, None)
+    assert status == 1 and b"negative" in lib.fn["last_error"]()
+    status = lib.fn["softmax_fwd"](9, 1, 1, 4, 4, 4, 4, None)
+    assert status == 1 and b"dtype" in lib.fn["last_error"]()
+    # zero-size work is a successful no-op
+    assert lib.fn["softmax_fwd"](0, None, None, 0, 4, 4, 4, None) == 0
+    size = ctypes.c_size_t(0)
+    assert lib.fn["csr_spmv_workspace_bytes"](4_194_304, 67_108_855, ctypes.byref(size)) == 0
+    assert 0 < size.value < 1 << 20
+    assert lib.fn["csr_spmv_f32"](1, 1, 1, 1, 1, 10, 10, 10, None, 0, None) == 5
+    assert lib.fn["csr_spmv_f32"](1, 1, 1, 1, 1, 2**31 - 5, 10, 10, 1, 1 << 30, None) == 2

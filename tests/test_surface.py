@@ -1,0 +1,150 @@
+"""Host-side behaviour of the intent.jit surface, checked on the CPU (no GPU needed).
+
+Binding rules follow python/intent/runtime/invocation.py:56-159 and
+python/intent/runtime/torch_views.py:23-88 of the reference; errors follow its
+classes (TypeError for count/type/dtype, ValueError for device/rank/shape/stride/
+alias, NotImplementedError for impossible output allocation)."""
+import inspect
+
+import pytest
+import torch
+
+import intent_amd as intent
+import intent_amd.language as I
+from intent_amd.examples.kernels.backward.softmax import softmax_backward, softmax_backward_f16
+from intent_amd.examples.kernels.contraction.gemm import bf16_gemm
+from intent_amd.examples.kernels.normalization.softmax import stable_softmax, stable_softmax_f16
+from intent_amd.examples.kernels.sparse.csr_spmv import csr_spmv
+from intent_amd.examples.kernels.streaming.attention import flash_attention_fwd
+from intent_amd.runtime.hip.operators import recognize
+from intent_amd.runtime.interface import PublicInterface, StrideSymbol
+from intent_amd.runtime.invocation import bind_arguments
+from intent_amd.runtime.torch_views import allocate_output, observe_view
+
+CPU = torch.device("cpu")
+
+
+def bind(defn, args, outputs=None, derived=None, constexprs=None):
+    interface = PublicInterface.from_definition(defn, constexprs)
+    return bind_arguments(interface, args, outputs,
+                          observe_view=lambda p, v: observe_view(p, v, device=CPU),
+                          allocate_output=lambda p, s: allocate_output(p, s, device=CPU), derived=derived)
+
+
+def test_interface_from_definition_matches_reference_schema():
+    iface = PublicInterface.from_definition(stable_softmax)
+    x, y = iface.parameters
+    assert (x.shape, x.dimensions, x.strides, x.noalias, int(x.access)) == ((-1, -1), (1, 2), (None, 1), True, 0)
+    assert (y.shape, y.dimensions, int(y.access)) == ((-1, -1), (1, 2), 1)
+    static = PublicInterface.from_definition(softmax_backward)
+    assert static.parameters[0].shape == (4096, 4097) and static.parameters[0].dimensions == (0, 0)
+    attn = PublicInterface.from_definition(flash_attention_fwd, {"CAUSAL": True})
+    assert [p.name for p in attn.parameters] == ["q", "k", "v", "output", "scale"]
+    assert attn.parameters[1].dimensions[2] != attn.parameters[0].dimensions[2]   # K vs Q
+    assert attn.parameters[2].dimensions[:3] == attn.parameters[1].dimensions[:3]
+    round_trip = PublicInterface.read(attn.to_json())
+    assert round_trip == attn
+
+
+def test_binding_allocates_and_checks():
+    x = torch.zeros(3, 5)
+    bound = bind(stable_softmax, (x,))
+    (y,) = bound.outputs
+    assert y.shape == (3, 5) and y.dtype == torch.float32 and y.is_contiguous()
+    with pytest.raises(TypeError):
+        bind(stable_softmax, (x.double(),))
+    with pytest.raises(ValueError):
+        bind(stable_softmax, (torch.zeros(3),))
+    with pytest.raises(TypeError):
+        bind(stable_softmax, (x, x))
+    with pytest.raises(ValueError):                       # strides (None, 1) constraint
+        bind(stable_softmax, (torch.zeros(5, 3).t(),))
+    with pytest.raises(ValueError):                       # explicit output of the wrong shape
+        bind(stable_softmax, (x,), outputs=(torch.zeros(3, 4),))
+    with pytest.raises(ValueError):                       # noalias: output aliases the input
+        bind(stable_softmax, (x,), outputs=(x,))
+    with pytest.raises(ValueError):                       # static extents
+        bind(softmax_backward, (torch.zeros(4096, 4096), torch.zeros(4096, 4096)))
+
+
+def test_shared_dimensions_and_derived_extents():
+    a = torch.zeros(4, 6, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        bind(bf16_gemm, (a, torch.zeros(5, 7, dtype=torch.bfloat16)))
+    assert bind(bf16_gemm, (a, torch.zeros(6, 7, dtype=torch.bfloat16))).outputs[0].shape == (4, 7)
+    iface = PublicInterface.from_definition(csr_spmv)
+    with pytest.raises(NotImplementedError):              # R is not derivable from symbols alone
+        iface.require_output_allocation()
+    ids = {"R1": 1, "NNZ": 2, "C": 3, "R": 4}
+    bound = bind(csr_spmv, (torch.zeros(11, dtype=torch.int32), torch.zeros(7, dtype=torch.int32),
+                            torch.zeros(7), torch.zeros(9)), derived={ids["R"]: (ids["R1"], -1)})
+    assert bound.outputs[0].shape == (10,)
+    with pytest.raises(ValueError):
+        bind(csr_spmv, (torch.zeros(11, dtype=torch.int32), torch.zeros(7, dtype=torch.int32),
+                        torch.zeros(8), torch.zeros(9)), derived={4: (1, -1)})
+
+
+def test_stride_symbols_bind_consistently():
+    @intent.kernel
+    def shared(a: I.In[I.f32, ("M", "N"), I.constraints(strides=("S", 1))],
+               b: I.Out[I.f32, ("M", "N"), I.constraints(strides=("S", 1))]):
+        pass
+
+    iface = PublicInterface.from_definition(shared)
+    assert iface.parameters[0].strides == (StrideSymbol("S"), 1)
+    big = torch.zeros(4, 10)
+    with pytest.raises(ValueError):
+        bind(shared, (big[:, :6],), outputs=(torch.zeros(4, 6),))
+    bind(shared, (big[:, :6],), outputs=(torch.zeros(4, 10)[:, :6],))
+
+
+def test_recognition_by_name_and_signature():
+    for defn, constexprs in ((stable_softmax, {}), (stable_softmax_f16, {}), (softmax_backward, {}),
+                             (softmax_backward_f16, {}), (bf16_gemm, {}), (csr_spmv, {}),
+                             (flash_attention_fwd, {"CAUSAL": True})):
+        iface = PublicInterface.from_definition(defn, constexprs)
+        assert recognize(defn, iface, tuple(constexprs)).name == defn.__name__
+
+    def f64_softmax(x: I.In[I.f64, ("M", "N")], y: I.Out[I.f64, ("M", "N")]):
+        pass
+
+    f64_softmax.__name__ = "stable_softmax"
+    impostor = intent.kernel(f64_softmax)
+    with pytest.raises(intent.CompilationStageError) as error:
+        recognize(impostor, PublicInterface.from_definition(impostor), ())
+    assert error.value.stage == "provider_recognition"
+
+    @intent.kernel
+    def layer_norm(x: I.In[I.f32, ("M", "N")], y: I.Out[I.f32, ("M", "N")]):
+        pass
+
+    with pytest.raises(intent.CompilationStageError):
+        recognize(layer_norm, PublicInterface.from_definition(layer_norm), ())
+
+
+def test_jit_surface_errors_without_gpu():
+    with pytest.raises(TypeError):
+        intent.jit(lambda x: x, backend="hip")
+    with pytest.raises(ValueError):
+        intent.jit(stable_softmax, backend="triton")
+    kernel = intent.jit(stable_softmax, backend="hip")
+    with pytest.raises(ValueError):                       # CPU tensors cannot select a hip device
+        kernel.run(torch.zeros(2, 2))
+    with pytest.raises(TypeError):
+        kernel.prepare(torch.zeros(2, 2), outputs=[torch.zeros(2, 2)])
+    with pytest.raises(ValueError):
+        kernel.interface                                  # nothing prepared yet
+    kernel.close()
+    with pytest.raises(intent.LanguageUseError):
+        stable_softmax(torch.zeros(1, 1), torch.zeros(1, 1))
+    with pytest.raises(intent.LanguageUseError):
+        I.exp(1.0)
+
+
+def test_definitions_keep_reference_signatures():
+    """Parameter names, order and annotations of the reference definitions."""
+    assert list(inspect.signature(stable_softmax.python_function).parameters) == ["x", "y"]
+    assert list(softmax_backward.signature.parameters) == ["probabilities", "upstream", "gradient"]
+    assert list(bf16_gemm.signature.parameters) == ["a", "b", "c"]
+    assert list(flash_attention_fwd.signature.parameters) == ["q", "k", "v", "output", "scale", "CAUSAL"]
+    assert list(csr_spmv.signature.parameters) == ["row_offsets", "column_indices", "values", "vector", "output"]
