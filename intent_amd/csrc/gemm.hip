@@ -1,13 +1,317 @@
-// bf16 GEMM (placeholder until the MFMA kernel lands).
+// bf16 GEMM, C = bf16(A @ B) with f32 accumulation, for gfx950 (CDNA4).
+//
+// Semantics: bf16_gemm (python/intent/examples/kernels/contraction/gemm.py:76-92):
+// accumulator = matmul(a, b, acc_dtype=f32); c = cast(accumulator, bf16) (round to
+// nearest even). A [M,K], B [K,N], C [M,N], row-major with row strides lda/ldb/ldc.
+//
+// Design (fast path):
+//   * workgroup tile 256 x 256, K step 64, 8 waves in 2 x 4, each wave 128 x 64 =
+//     4 x 2 tiles of v_mfma_f32_32x32x16_bf16 (128 accumulator registers per lane, so two
+//     waves share each SIMD);
+//   * A and B tiles pass through LDS with two stages (2 x 64 KB): the next K step's
+//     global loads are in flight while the current one is consumed;
+//   * MFMA operands need 8 consecutive k per lane. A rows are k-contiguous already;
+//     B is [K,N], so each thread of waves 4-7 loads an 8 (k) x 8 (n) block, transposes it
+//     in registers and stores n-rows of 8 k into LDS ("Bt", k-contiguous); waves 0-3 copy A;
+//   * both LDS tiles are rows of 8 16-byte chunks; chunk c of row r is stored at
+//     c ^ ((r & 7) ^ ((r >> 3) & 1)), so the 16-byte fragment reads of 16 consecutive
+//     rows (one LDS cycle) hit distinct banks;
+//   * the MFMA is issued as D = Bt_frag x A_frag, i.e. the transposed product, so each
+//     lane ends with 4 consecutive output columns of one output row per register
+//     quad and writes them as one 8-byte store;
+//   * workgroups are dispatched round-robin over the 8 XCDs; the tile order gives each
+//     XCD a contiguous run of tiles, walked 8 tile-rows at a time, so the workgroups
+//     that share an XCD's L2 share A row panels and B column panels.
+// Shapes the fast path cannot take (K or N not a multiple of 8, unaligned rows) use a
+// simple LDS-tiled f32 FMA kernel.
 #include "common.hpp"
 
 namespace intent_hip {
-int gemm_resources(int64_t, int64_t, IntentHipKernelResources *) {
-  return fail(INTENT_HIP_ERR_UNSUPPORTED, "bf16 GEMM is not built yet");
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kThreads = 512;
+constexpr int kChunksA = kBM * kBK / 8;          // 16-byte chunks of one A stage
+constexpr int kStageChunks = (kBM + kBN) * kBK / 8;
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ int swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+__device__ __forceinline__ uint16_t to_bf16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
+
+__device__ __forceinline__ uint32_t word(const uint4 &v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
+
+// Component-wise select (a whole-struct select is lowered through scratch memory).
+__device__ __forceinline__ uint4 select(bool keep, uint4 v) {
+  return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
+}
+
+// Tile order: XCD-contiguous runs (when the tile count divides by 8), then 8-row groups.
+__device__ __forceinline__ void tile_of_block(int block, int tiles_m, int tiles_n, int &tm, int &tn) {
+  const int tiles = tiles_m * tiles_n;
+  int t = block;
+  if ((tiles & 7) == 0) t = (block & 7) * (tiles >> 3) + (block >> 3);
+  const int per_group = kGroupM * tiles_n;
+  const int group = t / per_group;
+  const int first_m = group * kGroupM;
+  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int in_group = t - group * per_group;
+  tm = first_m + in_group % rows_in_group;
+  tn = in_group / rows_in_group;
+}
+
+template <bool kEdge>
+__device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                                          uint16_t *__restrict__ C, int M, int N, int K, int64_t lda,
+                                          int64_t ldb, int64_t ldc, int m0, int n0, uint4 *lds) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;   // wave tile: rows wm*128..+128, cols wn*64..+64
+
+  // Loader roles (wave-uniform). Waves 0-3 copy the A tile: rows a_row + 32 i, 16-byte
+  // chunk a_chunk (8 k). Waves 4-7 copy the B tile: k rows b_kg * 8 + j, n chunk b_nc
+  // (8 n), transposed in registers into Bt rows b_nc * 8 + m (8 k each).
+  const bool loads_a = wave < 4;
+  const int lt = tid & 255;
+  const int a_chunk = lt & 7, a_row = lt >> 3;
+  const int b_kg = lt & 7, b_nc = lt >> 3;
+  uint4 r[8];
+
+  auto load = [&](int k0) {
+    if (loads_a) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = m0 + a_row + 32 * i;
+        const int col = k0 + a_chunk * 8;
+        if (!kEdge) {
+          r[i] = *reinterpret_cast<const uint4 *>(A + static_cast<int64_t>(row) * lda + col);
+        } else {
+          const bool ok = row < M && col < K;
+          const uint16_t *p = A + static_cast<int64_t>(ok ? row : 0) * lda + (ok ? col : 0);
+          r[i] = select(ok, *reinterpret_cast<const uint4 *>(p));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int krow = k0 + b_kg * 8 + j;
+        const int col = n0 + b_nc * 8;
+        if (!kEdge) {
+          r[j] = *reinterpret_cast<const uint4 *>(B + static_cast<int64_t>(krow) * ldb + col);
+        } else {
+          const bool ok = krow < K && col < N;
+          const uint16_t *p = B + static_cast<int64_t>(ok ? krow : 0) * ldb + (ok ? col : 0);
+          r[j] = select(ok, *reinterpret_cast<const uint4 *>(p));
+        }
+      }
+    }
+  };
+
+  auto store = [&](int stage) {
+    uint4 *sa = lds + stage * kStageChunks;
+    uint4 *sb = sa + kChunksA;
+    if (loads_a) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = a_row + 32 * i;
+        sa[row * 8 + (a_chunk ^ swizzle(row))] = r[i];
+      }
+    } else {
+      // r[j] word p holds (n = 2p, n = 2p + 1) at k = j: gather the 8 k of each n.
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        uint32_t even[4], odd[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t k_lo = word(r[2 * q], p), k_hi = word(r[2 * q + 1], p);
+          even[q] = (k_lo & 0xffffu) | (k_hi << 16);
+          odd[q] = (k_lo >> 16) | (k_hi & 0xffff0000u);
+        }
+        const int n_even = b_nc * 8 + 2 * p, n_odd = n_even + 1;
+        sb[n_even * 8 + (b_kg ^ swizzle(n_even))] = make_uint4(even[0], even[1], even[2], even[3]);
+        sb[n_odd * 8 + (b_kg ^ swizzle(n_odd))] = make_uint4(odd[0], odd[1], odd[2], odd[3]);
+      }
+    }
+  };
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // Fragment rows of this lane: the swizzle depends only on the lane (rows differ by 32s).
+  const int frag_row = lane & 31;
+  const int frag_swz = swizzle(frag_row);
+  const int frag_half = lane >> 5;
+
+  auto compute = [&](int stage) {
+    const uint4 *sa = lds + stage * kStageChunks;
+    const uint4 *sb = sa + kChunksA;
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int chunk = (kk * 2 + frag_half) ^ frag_swz;
+      bf16x8_t af[4], bf[2];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        af[t] = __builtin_bit_cast(bf16x8_t, sa[(wm * 128 + t * 32 + frag_row) * 8 + chunk]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        bf[t] = __builtin_bit_cast(bf16x8_t, sb[(wn * 64 + t * 32 + frag_row) * 8 + chunk]);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
+    }
+  };
+
+  const int k_tiles = (K + kBK - 1) / kBK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    const bool more = kt + 1 < k_tiles;
+    if (more) load((kt + 1) * kBK);
+    compute(kt & 1);
+    if (more) store((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  // Epilogue: acc[mt][nt][4g + e] is C[i][n] with i = the A fragment's row (lane & 31) and
+  // n = 8g + 4 * (lane >> 5) + e within the 32-column tile; 4 consecutive n -> one 8-byte store.
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int i = m0 + wm * 128 + mt * 32 + frag_row;
+    if (kEdge && i >= M) continue;
+    uint16_t *crow = C + static_cast<int64_t>(i) * ldc;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn * 64 + nt * 32 + 8 * g + 4 * frag_half;
+        if (kEdge && n >= N) continue;
+        const f32x16_t &v = acc[mt][nt];
+        bf16x4_t packed;
+        packed[0] = static_cast<__bf16>(v[4 * g]);
+        packed[1] = static_cast<__bf16>(v[4 * g + 1]);
+        packed[2] = static_cast<__bf16>(v[4 * g + 2]);
+        packed[3] = static_cast<__bf16>(v[4 * g + 3]);
+        *reinterpret_cast<bf16x4_t *>(crow + n) = packed;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_mfma(const uint16_t *__restrict__ A,
+                                                              const uint16_t *__restrict__ B,
+                                                              uint16_t *__restrict__ C, int M, int N, int K,
+                                                              int64_t lda, int64_t ldb, int64_t ldc,
+                                                              int tiles_m, int tiles_n) {
+  __shared__ uint4 lds[2 * kStageChunks];
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const bool interior = m0 + kBM <= M && n0 + kBN <= N && (K % kBK) == 0;
+  if (interior)
+    gemm_tile<false>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
+  else
+    gemm_tile<true>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
+}
+
+// ---------------------------------------------------------------- general-shape fallback
+// 64 x 64 output tile per 256 threads (4 x 4 per thread), K in steps of 16 through LDS,
+// f32 fused multiply-add in increasing k.
+constexpr int kFT = 64, kFK = 16;
+
+__global__ __launch_bounds__(256) void gemm_bf16_simple(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                                                        uint16_t *__restrict__ C, int M, int N, int K, int64_t lda,
+                                                        int64_t ldb, int64_t ldc) {
+  __shared__ float sa[kFK][kFT + 1];
+  __shared__ float sb[kFK][kFT + 1];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int m0 = blockIdx.y * kFT, n0 = blockIdx.x * kFT;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += kFK) {
+    for (int e = threadIdx.x; e < kFT * kFK; e += 256) {
+      const int r = e / kFK, kc = e % kFK;
+      const int gm = m0 + r, gk = k0 + kc;
+      sa[kc][r] = (gm < M && gk < K) ? to_f32(bf16_t{A[static_cast<int64_t>(gm) * lda + gk]}) : 0.0f;
+      const int kr = e / kFT, nc = e % kFT;
+      const int gk2 = k0 + kr, gn = n0 + nc;
+      sb[kr][nc] = (gk2 < K && gn < N) ? to_f32(bf16_t{B[static_cast<int64_t>(gk2) * ldb + gn]}) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kc = 0; kc < kFK; ++kc)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(sa[kc][ty * 4 + i], sb[kc][tx * 4 + j], acc[i][j]);
+    __syncthreads();
+  }
+  for (int i = 0; i < 4; ++i) {
+    const int gm = m0 + ty * 4 + i;
+    if (gm >= M) continue;
+    for (int j = 0; j < 4; ++j) {
+      const int gn = n0 + tx * 4 + j;
+      if (gn < N) C[static_cast<int64_t>(gm) * ldc + gn] = to_bf16_bits(acc[i][j]);
+    }
+  }
+}
+
+bool fast_path(const void *a, const void *b, const void *c, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+               int64_t ldc) {
+  return k % 8 == 0 && n % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned(a, 16) &&
+         aligned(b, 16) && aligned(c, 8);
+}
+
+}  // namespace
+
+int gemm_resources(int64_t m, int64_t n, IntentHipKernelResources *out) {
+  (void)m;
+  (void)n;
+  return describe_kernel(reinterpret_cast<const void *>(&gemm_bf16_mfma), "gemm_bf16_mfma", kThreads, out);
+}
+
 }  // namespace intent_hip
 
-extern "C" int intent_hip_gemm_bf16(const void *, const void *, void *, int64_t, int64_t, int64_t, int64_t,
-                                    int64_t, int64_t, void *) {
-  return intent_hip::fail(INTENT_HIP_ERR_UNSUPPORTED, "bf16 GEMM is not built yet");
+using namespace intent_hip;
+
+extern "C" int intent_hip_gemm_bf16(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
+                                    int64_t lda, int64_t ldb, int64_t ldc, void *stream) {
+  if (m < 0 || n < 0 || k < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "GEMM extents must stay below 2^30");
+  if (m == 0 || n == 0) return INTENT_HIP_OK;
+  if (a == nullptr || b == nullptr || c == nullptr) {
+    if (k > 0 || c == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  }
+  if (lda < (m > 1 ? k : 0) || ldb < (k > 1 ? n : 0) || ldc < (m > 1 ? n : 0))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "row stride smaller than the row length");
+  const hipStream_t s = as_stream(stream);
+  const auto *A = static_cast<const uint16_t *>(a);
+  const auto *B = static_cast<const uint16_t *>(b);
+  auto *C = static_cast<uint16_t *>(c);
+  if (k > 0 && fast_path(a, b, c, n, k, lda, ldb, ldc)) {
+    const int tiles_m = static_cast<int>((m + kBM - 1) / kBM), tiles_n = static_cast<int>((n + kBN - 1) / kBN);
+    gemm_bf16_mfma<<<dim3(tiles_m * tiles_n), dim3(kThreads), 0, s>>>(
+        A, B, C, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), lda, ldb, ldc, tiles_m, tiles_n);
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_bf16_mfma");
+    return INTENT_HIP_OK;
+  }
+  const dim3 grid(static_cast<unsigned>((n + kFT - 1) / kFT), static_cast<unsigned>((m + kFT - 1) / kFT));
+  gemm_bf16_simple<<<grid, dim3(256), 0, s>>>(A, B, C, static_cast<int>(m), static_cast<int>(n),
+                                              static_cast<int>(k), lda, ldb, ldc);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_bf16_simple");
+  return INTENT_HIP_OK;
 }

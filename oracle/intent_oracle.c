@@ -7,7 +7,7 @@
  * Each function restates one reference definition (paths relative to
  * /root/reference/python/intent/examples/kernels/) under the numerics contract of
  * /root/reference/doc/dsl/types-numerics-and-effects.en.md:
- *   - reductions ("reduce") accumulate in f32, here in index order;
+ *   - reductions ("reduce") accumulate in f32 in the order of a vectorised reduction;
  *   - ordered loops (`for nz in range(...)`) are strict left folds, here without
  *     fused multiply-add (the file is built with -ffp-contract=off);
  *   - casts to f16/bf16 round to nearest even (section 5.2, :105-112);
@@ -129,6 +129,22 @@ static inline void store_elem(void *base, int dtype, int64_t index, float v) {
   }
 }
 
+/* Sum in the order of a vectorised CPU reduction, which is how the reference CPU backend
+ * evaluates `I.reduce.sum` (vector accumulators, then a horizontal reduce_add:
+ * lib/Target/Mojo/Serialization/Serializer.cpp:558-592): four 16-lane f32 accumulators
+ * (64 partial sums; accumulator j takes elements j, j+64, j+128, ... in order), added
+ * pairwise at the end. A reduce may be re-associated
+ * (doc/dsl/types-numerics-and-effects.en.md:154-160); a strictly sequential f32 sum would
+ * drop every term below half an ulp of the running total. */
+static float lane_sum(const float *v, int64_t n) {
+  float lanes[64];
+  for (int j = 0; j < 64; ++j) lanes[j] = 0.0f;
+  for (int64_t i = 0; i < n; ++i) lanes[i & 63] += v[i];
+  for (int width = 32; width >= 1; width >>= 1)
+    for (int j = 0; j < width; ++j) lanes[j] += lanes[j + width];
+  return lanes[0];
+}
+
 /* ------------------------------------------------------------------ softmax forward
  * normalization/softmax.py:12-66. max = maximum_num fold with identity -inf (fmaxf returns
  * the non-NaN operand); e = exp(x - max); s = sum(e).
@@ -139,11 +155,8 @@ static void softmax_fwd_rows(int dtype, const void *x, void *y, int64_t cols, in
   for (int64_t r = begin; r < end; ++r) {
     float m = -INFINITY;
     for (int64_t c = 0; c < cols; ++c) m = fmaxf(m, load_elem(x, dtype, r * xs + c));
-    float s = 0.0f;
-    for (int64_t c = 0; c < cols; ++c) {
-      scratch[c] = expf(load_elem(x, dtype, r * xs + c) - m);
-      s += scratch[c];
-    }
+    for (int64_t c = 0; c < cols; ++c) scratch[c] = expf(load_elem(x, dtype, r * xs + c) - m);
+    const float s = lane_sum(scratch, cols);
     if (dtype == ORACLE_F32) {
       const float inv = 1.0f / s;
       for (int64_t c = 0; c < cols; ++c) store_elem(y, dtype, r * ys + c, scratch[c] * inv);
@@ -185,14 +198,16 @@ int oracle_softmax_bwd(int dtype, const void *p, const void *dy, void *dx, int64
     const uint32_t inner = enter_ieee();
     int64_t begin, end;
     row_range(rows, omp_get_thread_num(), size, &begin, &end);
+    float *scratch = (float *)malloc(sizeof(float) * (size_t)cols);
     for (int64_t r = begin; r < end; ++r) {
-      float proj = 0.0f;
-      for (int64_t c = 0; c < cols; ++c) proj += load_elem(p, dtype, r * ps + c) * load_elem(dy, dtype, r * dys + c);
+      for (int64_t c = 0; c < cols; ++c) scratch[c] = load_elem(p, dtype, r * ps + c) * load_elem(dy, dtype, r * dys + c);
+      const float proj = lane_sum(scratch, cols);
       for (int64_t c = 0; c < cols; ++c) {
         const float pc = load_elem(p, dtype, r * ps + c);
         store_elem(dx, dtype, r * dxs + c, pc * (load_elem(dy, dtype, r * dys + c) - proj));
       }
     }
+    free(scratch);
     leave_ieee(inner);
   }
   leave_ieee(csr);

@@ -221,3 +221,14 @@ def test_spmv_strict_left_fold():
     assert oracle.csr_spmv(off, col, val, x)[0] == np.float32(1.0)
     val2 = np.array([1e-8, 1e-8, 1.0], np.float32)
     assert oracle.csr_spmv(off, col, val2, x)[0] == np.float32(np.float32(2e-8) + np.float32(1.0))
+
+
+def test_softmax_reduction_keeps_small_terms():
+    """A dominant entry plus many terms below half an ulp of the running sum: a strictly
+    sequential f32 sum drops all 4095 of them (relative error 1.7e-4 here); the oracle's
+    64-accumulator reduction drops only the 63 that share the dominant entry's accumulator."""
+    x = np.full((1, 4096), -17.0, np.float32)
+    x[0, 0] = 0.0
+    y = oracle.softmax_fwd(x)
+    want = torch.softmax(torch.from_numpy(x).double(), dim=1).numpy()
+    assert rel_err(y, want) < 5e-6
