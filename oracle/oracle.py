@@ -67,7 +67,7 @@ def _rows(array: np.ndarray) -> int:
 
 def _check_2d(*arrays):
     for a in arrays:
-        if a.ndim != 2 or a.strides[1] != a.itemsize:
+        if a.ndim != 2 or (a.size and a.strides[1] != a.itemsize):
             raise ValueError("oracle expects 2-D arrays with unit inner stride")
 
 
