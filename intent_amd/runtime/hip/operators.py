@@ -63,9 +63,24 @@ def _view(access, dtype, rank):
 
 
 # ------------------------------------------------------------------------------ layout helpers
-def _readable(tensor, keep, before):
-    """A unit-inner-stride tensor with the contents of `tensor` at launch time."""
-    if tensor.dim() == 0 or tensor.stride(-1) == 1 or tensor.shape[-1] <= 1 or tensor.numel() == 0:
+def _aligned(tensor, vector: int) -> bool:
+    """Unit inner stride, outer strides multiples of `vector` elements, 16-byte aligned start."""
+    if tensor.numel() == 0 or tensor.dim() == 0:
+        return True
+    if tensor.stride(-1) != 1 and tensor.shape[-1] > 1:
+        return False
+    if vector > 1:
+        if tensor.data_ptr() % 16:
+            return False
+        if any(s % vector for s, e in zip(tensor.stride()[:-1], tensor.shape[:-1]) if e > 1):
+            return False
+    return True
+
+
+def _readable(tensor, keep, before, vector: int = 1):
+    """A tensor with the contents of `tensor` at launch time whose layout the kernel takes
+    (unit inner stride; with `vector`, also aligned for 16-byte loads)."""
+    if _aligned(tensor, vector):
         return tensor
     staged = tensor.new_empty(tensor.shape)
     keep.append(staged)
@@ -73,8 +88,8 @@ def _readable(tensor, keep, before):
     return staged
 
 
-def _writable(tensor, keep, after):
-    if tensor.dim() == 0 or tensor.stride(-1) == 1 or tensor.shape[-1] <= 1 or tensor.numel() == 0:
+def _writable(tensor, keep, after, vector: int = 1):
+    if _aligned(tensor, vector):
         return tensor
     staged = tensor.new_empty(tensor.shape)
     keep.append(staged)
@@ -139,8 +154,8 @@ def _attention_f16(lib, bound, constexprs, device):
     q, k, v, o, scale = bound.arguments
     causal = bool(constexprs["CAUSAL"])
     keep, before, after = [q, k, v, o], [], []
-    qk, kk, vk, ok = (_readable(q, keep, before), _readable(k, keep, before), _readable(v, keep, before),
-                      _writable(o, keep, after))
+    qk, kk, vk, ok = (_readable(q, keep, before, 8), _readable(k, keep, before, 8),
+                      _readable(v, keep, before, 8), _writable(o, keep, after, 8))
     batch, heads, sq, d = q.shape
     sk, dv = k.shape[2], v.shape[3]
     strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
