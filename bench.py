@@ -43,6 +43,11 @@ def parse():
     parser.add_argument("--no-operators", action="store_true")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators", default="softmax_f32,gemm,attention,spmv")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
+    parser.add_argument("--only", default=None,
+                        help="run only this operator's timing (softmax_fwd, softmax_bwd or a name in --operators), "
+                             "for per-kernel profiling")
     return parser.parse_args()
 
 
@@ -178,7 +183,8 @@ def op_gemm(device, flush, cpu):
     flops = 2 * m * n * k
     out = {"config": "GEMM bf16 8192^3, fp32 accumulate (config 3)", "median_ms": round(ms, 4),
            "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
-           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops,
+           "traffic": read_traffic("gemm_bf16_8192")}
     if cpu:
         import oracle
 
@@ -205,7 +211,8 @@ def op_attention(device, flush, cpu):
     flops = 4 * b * h * s * s * d // 2
     out = {"config": "causal attention fwd f16 B4 H32 S4096 D128 (config 4)", "median_ms": round(ms, 4),
            "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
-           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops,
+           "traffic": read_traffic("attention_fwd_config4")}
     if cpu:
         import oracle
 
@@ -232,7 +239,8 @@ def op_spmv(device, flush, cpu):
     nbytes = 4 * (rows + 1) + 8 * nnz + 4 * x.shape[0] + 4 * rows
     out = {"config": f"CSR SpMV f32 {rows}^2, {nnz} nnz, rank-law Zipf(1.5) rows (config 5)",
            "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
-           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+           "traffic": read_traffic("spmv_merge_config5")}
     if cpu:
         import oracle
 
@@ -266,6 +274,22 @@ def main():
     import numpy as np
     import torch
 
+    if args.copy_calibration:
+        src = torch.ones(512 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read": src.numel(), "bytes_written": dst.numel(),
+                                               "launches": 20}}), flush=True)
+        return
+    if args.only in OPERATORS:
+        import intent_amd  # noqa: F401
+
+        device = torch.device("cuda", 0)
+        print(json.dumps(OPERATORS[args.only](device, Flush(device), False)), flush=True)
+        return
+
     import intent_amd as intent
     from intent_amd.examples import inputs
     from intent_amd.examples.kernels.backward.softmax import softmax_backward_f16
@@ -283,6 +307,12 @@ def main():
         fwd.launch()
         bwd.launch()
 
+    if args.only in ("softmax_fwd", "softmax_bwd"):
+        launch = fwd.launch if args.only == "softmax_fwd" else bwd.launch
+        fwd.launch()
+        ms = events_ms(launch, max(args.steps, 20))
+        print(json.dumps({"kernel": args.only, "avg_launch_ms": ms}), flush=True)
+        return
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
