@@ -212,6 +212,138 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
   }
 }
 
+// ---------------------------------------------------------------- interior tiles: LDS-DMA pipeline
+// K step 32, four LDS stages of 32 KB: tiles kt+1..kt+3 are in flight (global_load_lds_dwordx4 writes
+// them straight into LDS, no registers) while tile kt is multiplied. A stage holds A [256 m][32 k]
+// (rows of 4 16-byte chunks, chunk c of row r at c ^ ((r >> 1) & 3)) and B in its natural
+// [32 k][256 n] layout (rows of 32 chunks, chunk c of row k at c ^ 2 (k & 3)). B fragments are read
+// with ds_read_b64_tr_b16: in each 16-lane group, lane i, slot j receives element i % 4 of the
+// 8-byte segment addressed by lane 4 j + i / 4, so lane i addressing B[k0 + i/4][n0 + 4 (i % 4)]
+// yields B[k0 .. k0+3][n0 + i], the 4 consecutive k of one n the MFMA operand needs.
+constexpr int kDmaBK = 32;
+constexpr int kDmaStages = 4;
+constexpr int kDmaChunksA = kBM * kDmaBK / 8;            // 1024
+constexpr int kDmaStageChunks = (kBM + kBN) * kDmaBK / 8; // 2048 (32 KB)
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt with only the vector-memory counter constrained (vmcnt <= n).
+#define INTENT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8)))
+
+__device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                                              uint16_t *__restrict__ C, int K, int64_t lda, int64_t ldb,
+                                              int64_t ldc, int m0, int n0, uint4 *lds) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+
+  // Each wave issues 2 A and 2 B DMA instructions (1 KB each) per K tile. The global chunk a lane
+  // fetches is the one its LDS slot (base + 16 * lane) must hold under the swizzle.
+  const uint16_t *a_src[2];
+  const uint16_t *b_src[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int pa = (wave * 2 + i) * 64 + lane;      // A chunk slot: row pa / 4, physical chunk pa % 4
+    const int ra = pa >> 2, ca = (pa & 3) ^ ((ra >> 1) & 3);
+    a_src[i] = A + static_cast<int64_t>(m0 + ra) * lda + ca * 8;
+    const int pb = (wave * 2 + i) * 64 + lane;      // B chunk slot: row pb / 32, physical chunk pb % 32
+    const int kb = pb >> 5, cb = (pb & 31) ^ (2 * (kb & 3));
+    b_src[i] = B + static_cast<int64_t>(kb) * ldb + n0 + cb * 8;
+  }
+  auto issue = [&](int kt) {
+    uint4 *stage = lds + (kt % kDmaStages) * kDmaStageChunks;
+    const int k0 = kt * kDmaBK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_global_load_lds(a_src[i] + k0, (lds_void_t *)(stage + (wave * 2 + i) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(b_src[i] + static_cast<int64_t>(k0) * ldb,
+                                       (lds_void_t *)(stage + kDmaChunksA + (wave * 2 + i) * 64), 16, 0, 0);
+    }
+  };
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int frag_row = lane & 31;
+  const int half = lane >> 5;
+  const int a_swz = (frag_row >> 1) & 3;
+  // B transposed-read address of this lane within a 32 x 32 (k x n) block: group g = lane / 16,
+  // source role i = lane % 16 -> k = 8 (g / 2) + i / 4 (+4 for the second read), n = 16 (g % 2) + 4 (i % 4).
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int b_k = 8 * (g16 >> 1) + (i16 >> 2);
+  const int b_n = 16 * (g16 & 1) + 4 * (i16 & 3);
+
+  const int k_tiles = K / kDmaBK;
+#pragma unroll
+  for (int kt = 0; kt < kDmaStages - 1; ++kt)
+    if (kt < k_tiles) issue(kt);
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    // Wait for this wave's DMA of tile kt (later tiles may stay in flight), then for every wave's.
+    const int ahead = min(k_tiles - 1 - kt, kDmaStages - 2);
+    if (ahead >= 2) INTENT_WAIT_VMCNT(8);
+    else if (ahead == 1) INTENT_WAIT_VMCNT(4);
+    else INTENT_WAIT_VMCNT(0);
+    __syncthreads();
+    if (kt + kDmaStages - 1 < k_tiles) issue(kt + kDmaStages - 1);
+    const uint4 *sa = lds + (kt % kDmaStages) * kDmaStageChunks;
+    const uint16_t *sb = reinterpret_cast<const uint16_t *>(sa + kDmaChunksA);
+#pragma unroll
+    for (int kk = 0; kk < kDmaBK / 16; ++kk) {
+      bf16x8_t af[4], bf[2];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        af[t] = __builtin_bit_cast(bf16x8_t, sa[(wm * 128 + t * 32 + frag_row) * 4 + ((kk * 2 + half) ^ a_swz)]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        i16x4_t lo, hi;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int k = kk * 16 + b_k + 4 * r;
+          const int n = wn * 64 + t * 32 + b_n;
+          const int chunk = (n >> 3) ^ (2 * (k & 3));
+          const uint16_t *addr = sb + k * kBN + chunk * 8 + (n & 7);
+          const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)addr);
+          if (r == 0) lo = v; else hi = v;
+        }
+        const i16x4_t parts[2] = {lo, hi};
+        bf[t] = __builtin_bit_cast(bf16x8_t, parts);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
+    }
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int i = m0 + wm * 128 + mt * 32 + frag_row;
+    uint16_t *crow = C + static_cast<int64_t>(i) * ldc;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn * 64 + nt * 32 + 8 * g + 4 * half;
+        const f32x16_t &v = acc[mt][nt];
+        bf16x4_t packed;
+        packed[0] = static_cast<__bf16>(v[4 * g]);
+        packed[1] = static_cast<__bf16>(v[4 * g + 1]);
+        packed[2] = static_cast<__bf16>(v[4 * g + 2]);
+        packed[3] = static_cast<__bf16>(v[4 * g + 3]);
+        *reinterpret_cast<bf16x4_t *>(crow + n) = packed;
+      }
+  }
+}
+
 __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_mfma(const uint16_t *__restrict__ A,
                                                               const uint16_t *__restrict__ B,
                                                               uint16_t *__restrict__ C, int M, int N, int K,
@@ -221,8 +353,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_mfma(const uint16_t *__
   int tm, tn;
   tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
-  const bool interior = m0 + kBM <= M && n0 + kBN <= N && (K % kBK) == 0;
-  if (interior)
+  const bool interior = m0 + kBM <= M && n0 + kBN <= N;
+  if (interior && (K % kDmaBK) == 0)
+    gemm_tile_dma(A, B, C, K, lda, ldb, ldc, m0, n0, lds);
+  else if (interior && (K % kBK) == 0)
     gemm_tile<false>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
   else
     gemm_tile<true>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
