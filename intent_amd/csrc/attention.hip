@@ -11,16 +11,20 @@
 //
 // Design (d = dv = 128):
 //   * a workgroup owns 128 query rows of one (batch, head): 4 waves x 32 rows; key tiles of
-//     64 keys stream through LDS in two stages (K: 16 KB, V^T: 16 KB per stage), so two
-//     workgroups share a CU;
+//     64 keys stream through LDS in two stages (K: 16 KB, V: 16 KB per stage), written by
+//     global_load_lds_dwordx4 while the previous tile is consumed; two workgroups share a CU;
 //   * scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16, the wave's Q
 //     fragments stay in registers): lane l then holds 16 scores of query l % 32 per 32-key
 //     tile, so the running max/denominator of a query live in one lane pair (l, l ^ 32);
 //   * the output is accumulated transposed as well, O^T = V^T P^T: lane l holds dv values of
 //     query l % 32, so the online-softmax rescale of O is lane-local and P goes from the
 //     score registers to the MFMA B operand without leaving registers;
-//   * V^T lives in LDS with the keys of every 16-key slice permuted (bits 2 and 3 of the key
-//     swapped), so the 8 keys a lane needs for one MFMA k-slice are one 16-byte read;
+//   * V stays in its natural [key][dv] layout; the V^T operand is read with ds_read_b64_tr_b16
+//     (in each 16-lane group, lane i receives element i % 4 of the 8-byte segments addressed by
+//     lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4), so no transpose passes through registers;
+//   * the softmax scale is folded into one FMA per score, and the running maximum is only
+//     raised when a tile exceeds it by more than 8 (exp2 domain), which skips most rescales
+//     of O while keeping every weight <= 2^8;
 //   * causal: a workgroup visits key tiles up to its last query only, a wave skips tiles
 //     beyond its own last query, and only tiles crossing the diagonal are masked; the
 //     heaviest query blocks are dispatched first. All query blocks of one head share an
@@ -38,23 +42,28 @@ constexpr int kBQ = 128;     // query rows per workgroup
 constexpr int kBK = 64;      // keys per tile
 constexpr int kThreads = 256;
 constexpr int kKChunks = kBK * kD / 8;      // 16-byte chunks of a K tile (row = key, 16 chunks)
-constexpr int kVChunks = kD * kBK / 8;      // 16-byte chunks of a V^T tile (row = dv, 8 chunks)
+constexpr int kVChunks = kBK * kD / 8;      // 16-byte chunks of a V tile (row = key, 16 chunks)
 constexpr int kStageChunks = kKChunks + kVChunks;
 constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ int swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 __device__ __forceinline__ uint4 select(bool keep, uint4 v) {
   return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
 }
 
-__device__ __forceinline__ uint32_t word(const uint4 &v, int i) {
-  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
-
 struct Geometry {
   int64_t qs[4], ks[4], vs[4], os[4];  // element strides (batch, head, row, col)
 };
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt with only the vector-memory counter constrained (vmcnt <= n).
+#define INTENT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8)))
+
+// Rescale threshold of the online softmax, in the exp2 domain: the running maximum is only
+// raised when a tile's maximum exceeds it by more than this, so weights stay <= 2^8.
+constexpr float kRescaleSlack = 8.0f;
 
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t *__restrict__ Q,
                                                                   const uint16_t *__restrict__ K,
@@ -88,76 +97,27 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
       qf[ks] = __builtin_bit_cast(f16x8_t, select(ok, *reinterpret_cast<const uint4 *>(row + ks * 16 + half * 8)));
   }
 
-  // Key range of this workgroup and of this wave.
   const int q_last_block = min(q0 + kBQ, sq) - 1;
   const int k_end = causal ? min(sk, q_last_block + 1) : sk;
   const int tiles = (k_end + kBK - 1) / kBK;
   const int wave_q_last = min(wq0 + 31, sq - 1);
 
-  // Loader roles: waves 0-1 copy K (row = key, chunk kc), waves 2-3 copy V (8 keys x 8 dv
-  // blocks) and transpose them into V^T rows.
-  const bool loads_k = wave < 2;
-  const int lt = tid & 127;
-  const int k_chunk = lt & 15, k_row = lt >> 4;   // K: rows k_row + 8 i, chunk k_chunk
-  const int v_kg = lt & 7, v_dc = lt >> 3;        // V: keys v_kg*8 + j, dv chunk v_dc (0..15)
-  uint4 r[8];
-
-  auto load = [&](int kt) {
+  // DMA roles: each wave moves 4 x 64 chunks of K and of V per tile. LDS chunk slot p of a
+  // tile is row p / 16 (a key), physical chunk p % 16; K rows store logical chunk
+  // pc ^ (key & 15), V rows pc ^ 4 (key & 3). Keys beyond sk read row sk - 1 (finite data
+  // that the mask zeroes out; V tail rows are cleared in LDS below).
+  auto issue = [&](int kt) {
+    uint4 *stage = lds + (kt & 1) * kStageChunks;
     const int key0 = kt * kBK;
-    if (loads_k) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int key = key0 + k_row + 8 * i;
-        const bool ok = key < sk;
-        r[i] = select(ok, *reinterpret_cast<const uint4 *>(kbase + static_cast<int64_t>(ok ? key : 0) * g.ks[2] +
-                                                           k_chunk * 8));
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int key = key0 + v_kg * 8 + j;
-        const bool ok = key < sk;
-        r[j] = select(ok, *reinterpret_cast<const uint4 *>(vbase + static_cast<int64_t>(ok ? key : 0) * g.vs[2] +
-                                                           v_dc * 8));
-      }
-    }
-  };
-
-  auto store = [&](int stage) {
-    uint4 *sk_tile = lds + stage * kStageChunks;
-    uint4 *sv_tile = sk_tile + kKChunks;
-    if (loads_k) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = k_row + 8 * i;
-        sk_tile[row * 16 + (k_chunk ^ swizzle(row))] = r[i];
-      }
-    } else {
-      // r[j] word p = (dv = 2p, 2p + 1) at key v_kg*8 + j. V^T row dv gets the 8 keys, split
-      // into two 4-key halves by the slice permutation (bits 2 and 3 of the key swapped).
-      uint2 *sv2 = reinterpret_cast<uint2 *>(sv_tile);
-      const int slice = v_kg >> 1;                         // 16-key slice of these keys
-      const int pos_lo = slice * 16 + ((v_kg & 1) ? 4 : 0);   // keys +0..3 of this group
-      const int pos_hi = pos_lo + 8;                          // keys +4..7
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        uint32_t even[4], odd[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t a = word(r[2 * q], p), c = word(r[2 * q + 1], p);
-          even[q] = (a & 0xffffu) | (c << 16);
-          odd[q] = (a >> 16) | (c & 0xffff0000u);
-        }
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int dv = v_dc * 8 + 2 * p + e;
-          const uint32_t *w = e ? odd : even;
-          const int sw = swizzle(dv);
-          // 16-byte chunk (pos / 8) of row dv, swizzled; 8-byte half (pos % 8) / 4.
-          sv2[(dv * 8 + ((pos_lo >> 3) ^ sw)) * 2 + ((pos_lo & 7) >> 2)] = make_uint2(w[0], w[1]);
-          sv2[(dv * 8 + ((pos_hi >> 3) ^ sw)) * 2 + ((pos_hi & 7) >> 2)] = make_uint2(w[2], w[3]);
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int p = (wave * 4 + i) * 64 + lane;
+      const int row = p >> 4, pc = p & 15;
+      const int key = min(key0 + row, sk - 1);
+      __builtin_amdgcn_global_load_lds(kbase + static_cast<int64_t>(key) * g.ks[2] + (pc ^ (row & 15)) * 8,
+                                       (lds_void_t *)(stage + (wave * 4 + i) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + static_cast<int64_t>(key) * g.vs[2] + (pc ^ (4 * (row & 3))) * 8,
+                                       (lds_void_t *)(stage + kKChunks + (wave * 4 + i) * 64), 16, 0, 0);
     }
   };
 
@@ -170,85 +130,96 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
   float row_den = 0.0f;        // this lane's share of the denominator
   const float factor = scale * kLog2e;
   const int frag_row = lane & 31;
-  const int frag_swz = swizzle(frag_row);
+  // V^T transposed-read roles: group g16 = lane / 16, source index i16 = lane % 16.
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int v_key = 4 * (g16 >> 1) + (i16 >> 2);      // + 16 sl + 8 r
+  const int v_dv = 16 * (g16 & 1) + 4 * (i16 & 3);    // + 32 mt
 
-  if (tiles > 0) {
-    load(0);
-    store(0);
-  }
-  __syncthreads();
+  if (tiles > 0) issue(0);
   for (int kt = 0; kt < tiles; ++kt) {
-    const bool more = kt + 1 < tiles;
-    if (more) load(kt + 1);
+    INTENT_WAIT_VMCNT(0);
+    __syncthreads();          // tile kt is in LDS; every wave is done with tile kt - 1
+    if (kt + 1 < tiles) issue(kt + 1);
     const int key0 = kt * kBK;
+    const uint4 *sk_tile = lds + (kt & 1) * kStageChunks;
+    const uint16_t *sv_tile = reinterpret_cast<const uint16_t *>(sk_tile + kKChunks);
+    if (key0 + kBK > sk) {
+      // Tail tile: clear the V rows past the last key so masked weights meet zeros.
+      uint4 *vt = const_cast<uint4 *>(sk_tile + kKChunks);
+      for (int c = tid; c < kBK * 16; c += kThreads)
+        if (key0 + (c >> 4) >= sk) vt[c] = make_uint4(0, 0, 0, 0);
+      __syncthreads();
+    }
     const bool active = !causal || key0 <= wave_q_last;      // wave-uniform
-    if (active && wq0 < sq) {
-      const uint4 *sk_tile = lds + (kt & 1) * kStageChunks;
-      const uint4 *sv_tile = sk_tile + kKChunks;
-      // S^T for two 32-key tiles: s[st][e] is key 8 (e / 4) + 4 half + e % 4 of tile st.
-      f32x16_t s[2];
+    if (!active || wq0 >= sq) continue;
+    // S^T for two 32-key tiles: s[st][e] is key 8 (e / 4) + 4 half + e % 4 of tile st.
+    f32x16_t s[2];
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
+    for (int st = 0; st < 2; ++st) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
-        const int row = st * 32 + frag_row;
+      for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
+      const int row = st * 32 + frag_row;
 #pragma unroll
-        for (int ks = 0; ks < kD / 16; ++ks) {
-          const f16x8_t kf = __builtin_bit_cast(f16x8_t, sk_tile[row * 16 + ((ks * 2 + half) ^ frag_swz)]);
-          s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[st], 0, 0, 0);
-        }
+      for (int ks = 0; ks < kD / 16; ++ks) {
+        const f16x8_t kf = __builtin_bit_cast(f16x8_t, sk_tile[row * 16 + ((ks * 2 + half) ^ (row & 15))]);
+        s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[st], 0, 0, 0);
       }
-      // Scale, mask and this tile's maximum.
-      const bool edge = causal ? (key0 + kBK - 1 > wq0) : false;
-      const bool tail = key0 + kBK > sk;
-      float tile_max = -INFINITY;
+    }
+    // Mask (only tiles that cross the diagonal or the end) and the tile maximum of raw scores
+    // (scale * log2 e > 0, so the maximum commutes with the scaling).
+    const bool edge = causal ? (key0 + kBK - 1 > wq0) : false;
+    const bool tail = key0 + kBK > sk;
+    float tile_max = -INFINITY;
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float v = s[st][e] * factor;
-          if (edge || tail) {
-            const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-            const bool valid = key < sk && (!causal || key <= lane_q);
-            v = valid ? v : -INFINITY;
-          }
-          s[st][e] = v;
-          tile_max = fmaxf(tile_max, v);
+      for (int e = 0; e < 16; ++e) {
+        if (edge || tail) {
+          const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+          const bool valid = key < sk && (!causal || key <= lane_q);
+          s[st][e] = valid ? s[st][e] : -INFINITY;
         }
-      tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        tile_max = fmaxf(tile_max, s[st][e]);
+      }
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * factor;
+    // Raise the running maximum only when this tile exceeds it by more than the slack.
+    if (__any(tile_max > row_max + kRescaleSlack)) {
       const float new_max = fmaxf(row_max, tile_max);
-      // A row with no valid key so far keeps max -inf; its weights are 0 and its scale 1.
-      const bool any = new_max != -INFINITY;
-      const float alpha = any ? __builtin_amdgcn_exp2f(row_max - new_max) : 1.0f;
-      const float shift = any ? new_max : 0.0f;
+      const float alpha = row_max == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(row_max - new_max);
       row_max = new_max;
-      float tile_den = 0.0f;
-      f16x8_t pf[4];   // P^T fragments: slice (16 keys) sl = 2 st + (e / 8), slot j = e % 8
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = __builtin_amdgcn_exp2f(s[st][e] - shift);
-          tile_den += p;
-          pf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(p);
-        }
-      row_den = row_den * alpha + tile_den;
+      row_den *= alpha;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[mt][e] *= alpha;
-      // O^T += V^T P^T: A = V^T rows dv = 32 mt + (lane & 31), keys of slice sl in slot order.
-#pragma unroll
-      for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const int dv = mt * 32 + frag_row;
-          const f16x8_t vf = __builtin_bit_cast(f16x8_t, sv_tile[dv * 8 + ((sl * 2 + half) ^ frag_swz)]);
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sl], acc[mt], 0, 0, 0);
-        }
     }
-    if (more) store((kt + 1) & 1);
-    __syncthreads();
+    const float shift = row_max == -INFINITY ? 0.0f : row_max;
+    f16x8_t pf[4];   // P^T fragments: slice sl = 2 st + (e / 8), slot j = e % 8
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[st][e], factor, -shift));
+        row_den += p;
+        pf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(p);
+      }
+    // O^T += V^T P^T. The A operand (V^T rows dv, keys in slot order) comes from V's natural
+    // [key][dv] layout through ds_read_b64_tr_b16: read r of slice sl gives the lane keys
+    // 16 sl + 8 r + 4 half + 0..3 of its dv.
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        i16x4_t parts[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int key = sl * 16 + 8 * r + v_key;
+          const int dv = mt * 32 + v_dv;
+          const int chunk = (dv >> 3) ^ (4 * (key & 3));
+          parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kD + chunk * 8 + (dv & 7)));
+        }
+        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, parts), pf[sl], acc[mt], 0, 0, 0);
+      }
   }
 
   // Normalise and store: acc[mt][4 gq + e] is dv = 32 mt + 8 gq + 4 half + e of query lane_q.

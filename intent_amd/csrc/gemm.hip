@@ -215,7 +215,8 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
 // ---------------------------------------------------------------- interior tiles: LDS-DMA pipeline
 // K step 32, four LDS stages of 32 KB: tiles kt+1..kt+3 are in flight (global_load_lds_dwordx4 writes
 // them straight into LDS, no registers) while tile kt is multiplied. A stage holds A [256 m][32 k]
-// (rows of 4 16-byte chunks, chunk c of row r at c ^ ((r >> 1) & 3)) and B in its natural
+// (rows of 4 16-byte chunks, chunk c of row r at c ^ ((r >> 2) & 3), which spreads the fragment
+// reads of 16 consecutive rows over the 64 LDS banks) and B in its natural
 // [32 k][256 n] layout (rows of 32 chunks, chunk c of row k at c ^ 2 (k & 3)). B fragments are read
 // with ds_read_b64_tr_b16: in each 16-lane group, lane i, slot j receives element i % 4 of the
 // 8-byte segment addressed by lane 4 j + i / 4, so lane i addressing B[k0 + i/4][n0 + 4 (i % 4)]
@@ -247,7 +248,7 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int pa = (wave * 2 + i) * 64 + lane;      // A chunk slot: row pa / 4, physical chunk pa % 4
-    const int ra = pa >> 2, ca = (pa & 3) ^ ((ra >> 1) & 3);
+    const int ra = pa >> 2, ca = (pa & 3) ^ ((ra >> 2) & 3);
     a_src[i] = A + static_cast<int64_t>(m0 + ra) * lda + ca * 8;
     const int pb = (wave * 2 + i) * 64 + lane;      // B chunk slot: row pb / 32, physical chunk pb % 32
     const int kb = pb >> 5, cb = (pb & 31) ^ (2 * (kb & 3));
@@ -274,7 +275,7 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
 
   const int frag_row = lane & 31;
   const int half = lane >> 5;
-  const int a_swz = (frag_row >> 1) & 3;
+  const int a_swz = (frag_row >> 2) & 3;
   // B transposed-read address of this lane within a 32 x 32 (k x n) block: group g = lane / 16,
   // source role i = lane % 16 -> k = 8 (g / 2) + i / 4 (+4 for the second read), n = 16 (g % 2) + 4 (i % 4).
   const int g16 = lane >> 4, i16 = lane & 15;
