@@ -72,7 +72,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
                                                                   int sq, int sk, Geometry g, float scale,
                                                                   int causal, int q_blocks) {
   __shared__ uint4 lds[2 * kStageChunks];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in a scalar register
   const int bh_count = gridDim.x / q_blocks;
   const int qb = q_blocks - 1 - static_cast<int>(blockIdx.x) / bh_count;   // heaviest blocks first
   const int bh = static_cast<int>(blockIdx.x) % bh_count;
@@ -152,35 +153,50 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
     }
     const bool active = !causal || key0 <= wave_q_last;      // wave-uniform
     if (!active || wq0 >= sq) continue;
-    // S^T for two 32-key tiles: s[st][e] is key 8 (e / 4) + 4 half + e % 4 of tile st.
+    // S^T for two 32-key tiles: s[st][e] is key 8 (e / 4) + 4 half + e % 4 of tile st. The K
+    // fragments of step ks + 1 are read while the two MFMAs of step ks run.
     f32x16_t s[2];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
-      const int row = st * 32 + frag_row;
+    {
+      f16x8_t kf[2][2];
+      auto read_k = [&](int ks, int buf) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const int row = st * 32 + frag_row;
+          kf[buf][st] = __builtin_bit_cast(f16x8_t, sk_tile[row * 16 + ((ks * 2 + half) ^ (row & 15))]);
+        }
+      };
+      read_k(0, 0);
 #pragma unroll
       for (int ks = 0; ks < kD / 16; ++ks) {
-        const f16x8_t kf = __builtin_bit_cast(f16x8_t, sk_tile[row * 16 + ((ks * 2 + half) ^ (row & 15))]);
-        s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[st], 0, 0, 0);
+        if (ks + 1 < kD / 16) read_k(ks + 1, (ks + 1) & 1);
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+          s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks & 1][st], qf[ks], s[st], 0, 0, 0);
       }
     }
     // Mask (only tiles that cross the diagonal or the end) and the tile maximum of raw scores
     // (scale * log2 e > 0, so the maximum commutes with the scaling).
     const bool edge = causal ? (key0 + kBK - 1 > wq0) : false;
     const bool tail = key0 + kBK > sk;
+    if (edge || tail) {                                        // wave-uniform
+      const int limit = causal ? min(sk - 1, lane_q) : sk - 1;  // last valid key of this lane's query
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+          s[st][e] = key <= limit ? s[st][e] : -INFINITY;
+        }
+    }
     float tile_max = -INFINITY;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        if (edge || tail) {
-          const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-          const bool valid = key < sk && (!causal || key <= lane_q);
-          s[st][e] = valid ? s[st][e] : -INFINITY;
-        }
-        tile_max = fmaxf(tile_max, s[st][e]);
-      }
+      for (int e = 0; e < 16; ++e) tile_max = fmaxf(tile_max, s[st][e]);
     tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * factor;
     // Raise the running maximum only when this tile exceeds it by more than the slack.
     if (__any(tile_max > row_max + kRescaleSlack)) {
@@ -206,20 +222,31 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
     // O^T += V^T P^T. The A operand (V^T rows dv, keys in slot order) comes from V's natural
     // [key][dv] layout through ds_read_b64_tr_b16: read r of slice sl gives the lane keys
     // 16 sl + 8 r + 4 half + 0..3 of its dv.
+    {
+      f16x8_t vf[2][4];
+      auto read_v = [&](int sl, int buf) {
 #pragma unroll
-    for (int sl = 0; sl < 4; ++sl)
+        for (int mt = 0; mt < 4; ++mt) {
+          i16x4_t parts[2];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        i16x4_t parts[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int key = sl * 16 + 8 * r + v_key;
-          const int dv = mt * 32 + v_dv;
-          const int chunk = (dv >> 3) ^ (4 * (key & 3));
-          parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kD + chunk * 8 + (dv & 7)));
+          for (int r = 0; r < 2; ++r) {
+            const int key = sl * 16 + 8 * r + v_key;
+            const int dv = mt * 32 + v_dv;
+            const int chunk = (dv >> 3) ^ (4 * (key & 3));
+            parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kD + chunk * 8 + (dv & 7)));
+          }
+          vf[buf][mt] = __builtin_bit_cast(f16x8_t, parts);
         }
-        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, parts), pf[sl], acc[mt], 0, 0, 0);
+      };
+      read_v(0, 0);
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) {
+        if (sl + 1 < 4) read_v(sl + 1, (sl + 1) & 1);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl & 1][mt], pf[sl], acc[mt], 0, 0, 0);
       }
+    }
   }
 
   // Normalise and store: acc[mt][4 gq + e] is dv = 32 mt + 8 gq + 4 half + e of query lane_q.
