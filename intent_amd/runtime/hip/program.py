@@ -42,46 +42,64 @@ def _constexpr_parameters(definition) -> tuple[tuple[str, object], ...]:
     return tuple(out)
 
 
+def _raw_stream_getter():
+    """Fast accessor of the current HIP stream handle of a device (an int)."""
+    import torch
+
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw
+    return lambda index: torch.cuda.current_stream(index).cuda_stream
+
+
 class HipPreparedCall:
     """Bound arguments, allocated outputs/workspace and the native call that uses them."""
 
     def __init__(self, program: "HipProgram", bound, launch):
+        import torch
+
         self._program, self._bound, self._launch = program, bound, launch
-        self._observation = None
+        self._index = program.device.index
+        self._run = launch.run
+        self._before, self._after = launch.before, launch.after
+        self._current_device = torch.cuda.current_device
+        self._stream = _raw_stream_getter()
+        self._launched = False
 
     def compile(self) -> None:
         """Kernels are compiled ahead of time into libintent_hip.so; nothing to do."""
 
     def launch(self) -> None:
-        import torch
+        index = self._index
+        previous = self._current_device()
+        if previous != index:
+            import torch
 
-        program = self._program
-        index = program.device.index
-        switch = torch.cuda.current_device() != index
-        previous = torch.cuda.current_device() if switch else None
-        if switch:
             torch.cuda.set_device(index)
         try:
-            stream = torch.cuda.current_stream(index).cuda_stream
-            for step in self._launch.before:
+            for step in self._before:
                 step()
-            status = self._launch.run(stream)
+            status = self._run(self._stream(index))
             if status != 0:
                 raise CompilationStageError("provider_invocation",
-                                            f"{self._launch.entry}: {program.library.error(status)}")
-            for step in self._launch.after:
+                                            f"{self._launch.entry}: {self._program.library.error(status)}")
+            for step in self._after:
                 step()
         finally:
-            if switch:
+            if previous != index:
+                import torch
+
                 torch.cuda.set_device(previous)
-        self._observation = program.observe(self._launch)
+        self._launched = True
+        self._program._last_launch = self._launch
 
     def result(self):
         return self._bound.result()
 
     @property
     def observation(self):
-        return self._observation
+        """Facts of the kernel this call launched (read on demand; None before the first launch)."""
+        return self._program.observe(self._launch) if self._launched else None
 
     def inspect_configurations(self) -> tuple:
         return (ConfigurationAssessment(self._launch.configuration, True, ()),)
@@ -96,7 +114,7 @@ class HipProgram:
         self.library = library()
         self._derived = {symbols[name]: (symbols[source], offset) for name, source, offset in spec.derived
                          if name in symbols and source in symbols}
-        self._observation = None
+        self._last_launch = None
         self._lock = threading.Lock()
         self._closed = False
 
@@ -164,14 +182,12 @@ class HipProgram:
                                          None if name in facts else "not reported")
                           for name, unit in (("vgprs", "registers"), ("lds_bytes", "bytes"),
                                              ("scratch_bytes", "bytes"), ("block_threads", "threads")))
-        observation = NativeObservation("hip", launch.entry, facts.get("kernel", ""), launch.configuration,
-                                        resources)
-        self._observation = observation
-        return observation
+        return NativeObservation("hip", launch.entry, facts.get("kernel", ""), launch.configuration, resources)
 
     @property
     def observation(self):
-        return self._observation
+        """Facts of the most recent launch of this program, or None before one."""
+        return None if self._last_launch is None else self.observe(self._last_launch)
 
     def close(self) -> None:
         self._closed = True
