@@ -11,16 +11,20 @@
 // matrix-vector multiplication", SC'16). The work items are the R row ends merged with
 // the NNZ nonzeros; every workgroup takes exactly kBlockItems of them and every thread
 // kItems, whatever the row-length distribution (4M rows of length 1 next to rows of
-// 65536). Three launches:
+// 65536). Launches:
 //   1. partition: one thread per row writes the row that contains each workgroup's
 //      starting diagonal (no searches in global memory);
-//   2. merge: a workgroup stages its row ends and its products values*x[col] in LDS
-//      (coalesced col/value loads, gathers of x), each thread searches its diagonal in
-//      LDS and folds kItems items in order; partial rows are combined by a segmented
-//      scan across the workgroup; the partial row left open at the workgroup's end goes
-//      to the workspace;
-//   3. fixup: the first workgroup of each run of equal open rows adds the run's
+//   2. placement (clear, place, place_fill): logical workgroups inside one long row are
+//      mapped to the XCD whose L2 serves their column window; the rest fill free slots;
+//   3. merge: a workgroup stages its row ends and its products values*x[col] in LDS
+//      (coalesced non-temporal col/value loads that do not evict x from L2, gathers of
+//      x), each thread searches its diagonal in LDS and folds kItems items in order;
+//      partial rows are combined by a segmented scan across the workgroup; the partial
+//      row left open at the workgroup's end goes to the workspace;
+//   4. fixup: the first workgroup of each run of equal open rows adds the run's
 //      partials (in workgroup order) to y.
+// Placement changes only which hardware workgroup runs a logical block, never what the
+// block computes, so results do not depend on it.
 #include "common.hpp"
 
 namespace intent_hip {
@@ -36,10 +40,13 @@ struct Workspace {
   int32_t *splits;      // [blocks + 1]: row of each workgroup's starting diagonal
   int32_t *carry_rows;  // [blocks]: row left open at the workgroup's end, -1 if none
   float *carry_values;  // [blocks]: its partial sum
+  int32_t *perm;        // [blocks]: logical block run by hardware workgroup h
+  int32_t *overflow;    // [blocks]: logical blocks not placed on their XCD
+  int32_t *counters;    // [64]: per-XCD fill counts, overflow count
 };
 
 size_t workspace_bytes(int64_t blocks) {
-  return align256(4 * static_cast<size_t>(blocks + 1)) + 2 * align256(4 * static_cast<size_t>(blocks));
+  return align256(4 * static_cast<size_t>(blocks + 1)) + 4 * align256(4 * static_cast<size_t>(blocks)) + 256;
 }
 
 Workspace carve(void *base, int64_t blocks) {
@@ -50,7 +57,62 @@ Workspace carve(void *base, int64_t blocks) {
   w.carry_rows = reinterpret_cast<int32_t *>(p);
   p += align256(4 * static_cast<size_t>(blocks));
   w.carry_values = reinterpret_cast<float *>(p);
+  p += align256(4 * static_cast<size_t>(blocks));
+  w.perm = reinterpret_cast<int32_t *>(p);
+  p += align256(4 * static_cast<size_t>(blocks));
+  w.overflow = reinterpret_cast<int32_t *>(p);
+  p += align256(4 * static_cast<size_t>(blocks));
+  w.counters = reinterpret_cast<int32_t *>(p);
   return w;
+}
+
+constexpr int kXcds = 8;
+
+// Hardware workgroup h runs on XCD h % 8. A logical block whose items all lie inside one row
+// gathers x from a narrow column window (columns are sorted within a row); it is placed on the
+// XCD that owns that eighth of the columns, so its gathers come from that XCD's L2. Other blocks
+// fill the remaining slots. Each logical block computes the same result wherever it runs.
+__global__ __launch_bounds__(kThreads) void spmv_place(const int32_t *__restrict__ col, int32_t cols,
+                                                       int32_t blocks, int64_t total, int64_t nnz,
+                                                       Workspace ws) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (g >= blocks) return;
+  const int32_t x0 = ws.splits[g], x1 = ws.splits[g + 1];
+  const int64_t y0 = g * kBlockItems - x0;
+  const int64_t d1 = (g + 1) * kBlockItems < total ? (g + 1) * kBlockItems : total;
+  const int64_t y1 = d1 - x1;
+  int xcd = -1;
+  if (x1 - x0 <= 1 && y1 - y0 >= kBlockItems / 2 && y0 >= 0 && y1 <= nnz) {
+    const int64_t mid = (y0 + y1) / 2;
+    xcd = static_cast<int>((static_cast<int64_t>(col[mid]) * kXcds) / cols);
+    xcd = xcd < 0 ? 0 : (xcd >= kXcds ? kXcds - 1 : xcd);
+  }
+  if (xcd >= 0) {
+    const int32_t capacity = (blocks - xcd + kXcds - 1) / kXcds;   // slots h = xcd + 8 i < blocks
+    const int32_t slot = atomicAdd(&ws.counters[xcd], 1);
+    if (slot < capacity) {
+      ws.perm[xcd + kXcds * slot] = static_cast<int32_t>(g);
+      return;
+    }
+  }
+  ws.overflow[atomicAdd(&ws.counters[kXcds], 1)] = static_cast<int32_t>(g);
+}
+
+__global__ __launch_bounds__(kThreads) void spmv_place_fill(int32_t blocks, Workspace ws) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (j >= ws.counters[kXcds]) return;
+  // Free slots of XCD e are i in [filled_e, capacity_e); enumerate them XCD by XCD.
+  int64_t rank = j;
+  for (int e = 0; e < kXcds; ++e) {
+    const int32_t capacity = (blocks - e + kXcds - 1) / kXcds;
+    const int32_t filled = min(ws.counters[e], capacity);
+    const int32_t free_slots = capacity - filled;
+    if (rank < free_slots) {
+      ws.perm[e + kXcds * (filled + rank)] = ws.overflow[j];
+      return;
+    }
+    rank -= free_slots;
+  }
 }
 
 // Row r owns the diagonals [off[r] + r, off[r+1] + r + 1): its nonzeros, then its end.
@@ -84,7 +146,8 @@ __global__ __launch_bounds__(kThreads) void spmv_merge(const int32_t *__restrict
   __shared__ float s_val[kThreads];
 
   const int t = threadIdx.x;
-  const int64_t g = blockIdx.x;
+  const int32_t placed = ws.perm[blockIdx.x];  // a permutation of [0, gridDim.x) by construction
+  const int64_t g = placed < 0 ? 0 : (placed >= static_cast<int32_t>(gridDim.x) ? gridDim.x - 1 : placed);
   const int64_t d0 = g * kBlockItems;
   const int64_t d1 = d0 + kBlockItems < total ? d0 + kBlockItems : total;
   const int32_t x0 = ws.splits[g];
@@ -105,8 +168,8 @@ __global__ __launch_bounds__(kThreads) void spmv_merge(const int32_t *__restrict
     for (int k = 0; k < kItems; ++k) {
       const int i = t + k * kThreads;
       const bool live = i < n_nz;
-      c[k] = live ? col[y0 + i] : 0;
-      v[k] = live ? val[y0 + i] : 0.0f;
+      c[k] = live ? __builtin_nontemporal_load(col + y0 + i) : 0;
+      v[k] = live ? __builtin_nontemporal_load(val + y0 + i) : 0.0f;
     }
 #pragma unroll
     for (int k = 0; k < kItems; ++k) {
@@ -185,6 +248,8 @@ __global__ __launch_bounds__(kThreads) void spmv_fixup(float *__restrict__ y, in
   y[r] = __fadd_rn(sum, y[r]);
 }
 
+__global__ void spmv_clear(Workspace ws) { if (threadIdx.x < 64) ws.counters[threadIdx.x] = 0; }
+
 int64_t block_count(int64_t rows, int64_t nnz) { return (rows + nnz + kBlockItems - 1) / kBlockItems; }
 
 }  // namespace
@@ -229,6 +294,10 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   spmv_partition<<<dim3(static_cast<unsigned>((rows + 1 + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(
       row_offsets, r32, b32, ws.splits);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_partition");
+  spmv_clear<<<dim3(1), dim3(64), 0, s>>>(ws);
+  spmv_place<<<dim3(static_cast<unsigned>((blocks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(
+      column_indices, c32 > 0 ? c32 : 1, b32, total, nnz, ws);
+  spmv_place_fill<<<dim3(static_cast<unsigned>((blocks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(b32, ws);
   spmv_merge<<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s>>>(row_offsets, column_indices, values, x,
                                                                              y, r32, c32, total, ws);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_merge");
