@@ -5,15 +5,21 @@
 // nearest even). A [M,K], B [K,N], C [M,N], row-major with row strides lda/ldb/ldc.
 //
 // Design (fast path):
-//   * workgroup tile 256 x 256, K step 64, 8 waves in 2 x 4, each wave 128 x 64 =
-//     4 x 2 tiles of v_mfma_f32_32x32x16_bf16 (128 accumulator registers per lane, so two
-//     waves share each SIMD);
-//   * A and B tiles pass through LDS with two stages (2 x 64 KB): the next K step's
-//     global loads are in flight while the current one is consumed;
+//   * workgroup tile 256 x 256, 8 waves in 2 x 4, each wave 128 x 64 = 4 x 2 tiles of
+//     v_mfma_f32_32x32x16_bf16 (128 accumulator registers per lane, so two waves share
+//     each SIMD);
+//   * interior tiles with K % 32 == 0 (gemm_tile_dma) stream A and B into LDS with
+//     global_load_lds (five 32 KB stages) and read B fragments with transposing LDS reads;
+//     the two waves of a SIMD alternate between their MFMA cluster and their LDS reads
+//     (ping-pong), so the matrix pipe is fed while the other wave waits on LDS;
+//   * other tiles (gemm_tile) use K step 64 and two register-staged LDS stages
+//     (2 x 64 KB): the next K step's global loads are in flight while the current one is
+//     consumed;
 //   * MFMA operands need 8 consecutive k per lane. A rows are k-contiguous already;
-//     B is [K,N], so each thread of waves 4-7 loads an 8 (k) x 8 (n) block, transposes it
-//     in registers and stores n-rows of 8 k into LDS ("Bt", k-contiguous); waves 0-3 copy A;
-//   * both LDS tiles are rows of 8 16-byte chunks; chunk c of row r is stored at
+//     in gemm_tile B is [K,N], so each thread of waves 4-7 loads an 8 (k) x 8 (n) block,
+//     transposes it in registers and stores n-rows of 8 k into LDS ("Bt", k-contiguous);
+//     waves 0-3 copy A;
+//   * gemm_tile's LDS tiles are rows of 8 16-byte chunks; chunk c of row r is stored at
 //     c ^ ((r & 7) ^ ((r >> 3) & 1)), so the 16-byte fragment reads of 16 consecutive
 //     rows (one LDS cycle) hit distinct banks;
 //   * the MFMA is issued as D = Bt_frag x A_frag, i.e. the transposed product, so each
@@ -213,8 +219,8 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
 }
 
 // ---------------------------------------------------------------- interior tiles: LDS-DMA pipeline
-// K step 32, four LDS stages of 32 KB: tiles kt+1..kt+3 are in flight (global_load_lds_dwordx4 writes
-// them straight into LDS, no registers) while tile kt is multiplied. A stage holds A [256 m][32 k]
+// K step 32, five LDS stages of 32 KB (160 KB): up to three later tiles are in flight
+// (global_load_lds_dwordx4 writes them straight into LDS, no registers) while tile kt is multiplied. A stage holds A [256 m][32 k]
 // (rows of 4 16-byte chunks, chunk c of row r at c ^ ((r >> 2) & 3), which spreads the fragment
 // reads of 16 consecutive rows over the 64 LDS banks) and B in its natural
 // [32 k][256 n] layout (rows of 32 chunks, chunk c of row k at c ^ 2 (k & 3)). B fragments are read
@@ -222,7 +228,7 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
 // 8-byte segment addressed by lane 4 j + i / 4, so lane i addressing B[k0 + i/4][n0 + 4 (i % 4)]
 // yields B[k0 .. k0+3][n0 + i], the 4 consecutive k of one n the MFMA operand needs.
 constexpr int kDmaBK = 32;
-constexpr int kDmaStages = 4;
+constexpr int kDmaStages = 5;
 constexpr int kDmaChunksA = kBM * kDmaBK / 8;            // 1024
 constexpr int kDmaStageChunks = (kBM + kBN) * kDmaBK / 8; // 2048 (32 KB)
 
@@ -230,8 +236,21 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-// s_waitcnt with only the vector-memory counter constrained (vmcnt <= n).
+// s_waitcnt with only the vector-memory counter constrained (vmcnt <= n), and with only the LDS
+// counter constrained (lgkmcnt == 0).
 #define INTENT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8)))
+#define INTENT_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4))
+
+// Workgroup barrier of the DMA loop: s_barrier with an acquire fence (later LDS reads stay below
+// it) and no release fence. A release fence would wait for every DMA in flight (they are LDS
+// writes); DMA completion is awaited explicitly with vmcnt before the barrier instead. The
+// scheduling barriers keep each MFMA cluster on its side of the s_barrier.
+__device__ __forceinline__ void dma_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
                                               uint16_t *__restrict__ C, int K, int64_t lda, int64_t ldb,
@@ -282,48 +301,67 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
   const int b_k = 8 * (g16 >> 1) + (i16 >> 2);
   const int b_n = 16 * (g16 & 1) + 4 * (i16 & 3);
 
+  // Ping-pong schedule. Waves 0-3 and 4-7 share the four SIMDs (one of each per SIMD). Waves 4-7
+  // run one barrier behind, so between two barriers one wave of each SIMD issues its MFMA cluster
+  // (M) while the other reads its fragments from LDS and issues its DMA (R):
+  //   waves 0-3: b0 |   R0 b M0 b R1 b M1 b ... M(last) b | b
+  //   waves 4-7: b0 | b R0 b M0 b R1 b ... M(last) b
+  // Every wave executes 2 + 2 * k_tiles barriers. Before the barrier that opens the interval in
+  // which waves 0-3 read tile t, every wave has waited for its own DMA of tile t. The DMA of tile
+  // t + S - 1 overwrites stage (t - 1) % S, whose reads every wave completed (lgkmcnt 0) before an
+  // earlier barrier.
+  const bool lag = wave >= 4;
   const int k_tiles = K / kDmaBK;
 #pragma unroll
   for (int kt = 0; kt < kDmaStages - 1; ++kt)
     if (kt < k_tiles) issue(kt);
-  for (int kt = 0; kt < k_tiles; ++kt) {
-    // Wait for this wave's DMA of tile kt (later tiles may stay in flight), then for every wave's.
-    const int ahead = min(k_tiles - 1 - kt, kDmaStages - 2);
-    if (ahead >= 2) INTENT_WAIT_VMCNT(8);
-    else if (ahead == 1) INTENT_WAIT_VMCNT(4);
+  auto wait_tile = [&](int t) {   // this wave's DMA of tile t complete; later tiles may stay in flight
+    const int later = min(k_tiles - 1 - t, kDmaStages - 2);
+    if (later >= 3) INTENT_WAIT_VMCNT(12);
+    else if (later == 2) INTENT_WAIT_VMCNT(8);
+    else if (later == 1) INTENT_WAIT_VMCNT(4);
     else INTENT_WAIT_VMCNT(0);
-    __syncthreads();
-    if (kt + kDmaStages - 1 < k_tiles) issue(kt + kDmaStages - 1);
+  };
+  wait_tile(0);
+  dma_barrier();
+  if (lag) dma_barrier();
+  bf16x8_t af[2][4], bf[2][2];
+  for (int kt = 0; kt < k_tiles; ++kt) {
     const uint4 *sa = lds + (kt % kDmaStages) * kDmaStageChunks;
     const uint16_t *sb = reinterpret_cast<const uint16_t *>(sa + kDmaChunksA);
 #pragma unroll
     for (int kk = 0; kk < kDmaBK / 16; ++kk) {
-      bf16x8_t af[4], bf[2];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        af[t] = __builtin_bit_cast(bf16x8_t, sa[(wm * 128 + t * 32 + frag_row) * 4 + ((kk * 2 + half) ^ a_swz)]);
+        af[kk][t] = __builtin_bit_cast(bf16x8_t, sa[(wm * 128 + t * 32 + frag_row) * 4 + ((kk * 2 + half) ^ a_swz)]);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        i16x4_t lo, hi;
+        i16x4_t parts[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int k = kk * 16 + b_k + 4 * r;
           const int n = wn * 64 + t * 32 + b_n;
           const int chunk = (n >> 3) ^ (2 * (k & 3));
-          const uint16_t *addr = sb + k * kBN + chunk * 8 + (n & 7);
-          const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)addr);
-          if (r == 0) lo = v; else hi = v;
+          parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sb + k * kBN + chunk * 8 + (n & 7)));
         }
-        const i16x4_t parts[2] = {lo, hi};
-        bf[t] = __builtin_bit_cast(bf16x8_t, parts);
+        bf[kk][t] = __builtin_bit_cast(bf16x8_t, parts);
       }
+    }
+    if (kt + kDmaStages - 1 < k_tiles) issue(kt + kDmaStages - 1);
+    if (lag) wait_tile(kt + 1);
+    INTENT_WAIT_LGKMCNT0();
+    dma_barrier();
+#pragma unroll
+    for (int kk = 0; kk < kDmaBK / 16; ++kk)
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
-    }
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[kk][nt], af[kk][mt], acc[mt][nt], 0, 0, 0);
+    if (!lag) wait_tile(kt + 1);
+    dma_barrier();
   }
+  if (!lag) dma_barrier();
 
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
@@ -350,7 +388,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_mfma(const uint16_t *__
                                                               uint16_t *__restrict__ C, int M, int N, int K,
                                                               int64_t lda, int64_t ldb, int64_t ldc,
                                                               int tiles_m, int tiles_n) {
-  __shared__ uint4 lds[2 * kStageChunks];
+  __shared__ uint4 lds[2 * kStageChunks > kDmaStages * kDmaStageChunks ? 2 * kStageChunks : kDmaStages * kDmaStageChunks];
   int tm, tn;
   tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;

@@ -14,7 +14,7 @@
 // 65536). Launches:
 //   1. partition: one thread per row writes the row that contains each workgroup's
 //      starting diagonal (no searches in global memory);
-//   2. placement (clear, place, place_fill): logical workgroups inside one long row are
+//   2. placement (place, place_fill): logical workgroups inside one long row are
 //      mapped to the XCD whose L2 serves their column window; the rest fill free slots;
 //   3. merge: a workgroup stages its row ends and its products values*x[col] in LDS
 //      (coalesced non-temporal col/value loads that do not evict x from L2, gathers of
@@ -75,27 +75,44 @@ constexpr int kXcds = 8;
 __global__ __launch_bounds__(kThreads) void spmv_place(const int32_t *__restrict__ col, int32_t cols,
                                                        int32_t blocks, int64_t total, int64_t nnz,
                                                        Workspace ws) {
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (g >= blocks) return;
-  const int32_t x0 = ws.splits[g], x1 = ws.splits[g + 1];
-  const int64_t y0 = g * kBlockItems - x0;
-  const int64_t d1 = (g + 1) * kBlockItems < total ? (g + 1) * kBlockItems : total;
-  const int64_t y1 = d1 - x1;
+  // Slots are reserved per workgroup: LDS atomics rank the threads, then one global atomic
+  // per XCD (and one for the overflow list) reserves the workgroup's range.
+  __shared__ int32_t s_count[kXcds + 1];
+  __shared__ int32_t s_base[kXcds + 1];
+  const int t = threadIdx.x;
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + t;
+  if (t <= kXcds) s_count[t] = 0;
+  __syncthreads();
   int xcd = -1;
-  if (x1 - x0 <= 1 && y1 - y0 >= kBlockItems / 2 && y0 >= 0 && y1 <= nnz) {
-    const int64_t mid = (y0 + y1) / 2;
-    xcd = static_cast<int>((static_cast<int64_t>(col[mid]) * kXcds) / cols);
-    xcd = xcd < 0 ? 0 : (xcd >= kXcds ? kXcds - 1 : xcd);
-  }
-  if (xcd >= 0) {
-    const int32_t capacity = (blocks - xcd + kXcds - 1) / kXcds;   // slots h = xcd + 8 i < blocks
-    const int32_t slot = atomicAdd(&ws.counters[xcd], 1);
-    if (slot < capacity) {
-      ws.perm[xcd + kXcds * slot] = static_cast<int32_t>(g);
-      return;
+  if (g < blocks) {
+    const int32_t x0 = ws.splits[g], x1 = ws.splits[g + 1];
+    const int64_t y0 = g * kBlockItems - x0;
+    const int64_t d1 = (g + 1) * kBlockItems < total ? (g + 1) * kBlockItems : total;
+    const int64_t y1 = d1 - x1;
+    if (x1 - x0 <= 1 && y1 - y0 >= kBlockItems / 2 && y0 >= 0 && y1 <= nnz) {
+      const int64_t mid = (y0 + y1) / 2;
+      xcd = static_cast<int>((static_cast<int64_t>(col[mid]) * kXcds) / cols);
+      xcd = xcd < 0 ? 0 : (xcd >= kXcds ? kXcds - 1 : xcd);
     }
   }
-  ws.overflow[atomicAdd(&ws.counters[kXcds], 1)] = static_cast<int32_t>(g);
+  const int32_t local = xcd >= 0 ? atomicAdd(&s_count[xcd], 1) : 0;
+  __syncthreads();
+  if (t < kXcds) s_base[t] = s_count[t] > 0 ? atomicAdd(&ws.counters[t], s_count[t]) : 0;
+  __syncthreads();
+  bool spill = g < blocks;
+  if (xcd >= 0) {
+    const int32_t capacity = (blocks - xcd + kXcds - 1) / kXcds;   // slots h = xcd + 8 i < blocks
+    const int32_t slot = s_base[xcd] + local;
+    if (slot < capacity) {
+      ws.perm[xcd + kXcds * slot] = static_cast<int32_t>(g);
+      spill = false;
+    }
+  }
+  const int32_t rank = spill ? atomicAdd(&s_count[kXcds], 1) : 0;
+  __syncthreads();
+  if (t == 0) s_base[kXcds] = s_count[kXcds] > 0 ? atomicAdd(&ws.counters[kXcds], s_count[kXcds]) : 0;
+  __syncthreads();
+  if (spill) ws.overflow[s_base[kXcds] + rank] = static_cast<int32_t>(g);
 }
 
 __global__ __launch_bounds__(kThreads) void spmv_place_fill(int32_t blocks, Workspace ws) {
@@ -117,8 +134,12 @@ __global__ __launch_bounds__(kThreads) void spmv_place_fill(int32_t blocks, Work
 
 // Row r owns the diagonals [off[r] + r, off[r+1] + r + 1): its nonzeros, then its end.
 // It records itself as the split of every workgroup boundary g * kBlockItems inside that range.
+// Workgroup 0 also clears the placement counters (a store, not a memset node, so the launch
+// sequence can be captured in a graph).
 __global__ __launch_bounds__(kThreads) void spmv_partition(const int32_t *__restrict__ off, int32_t rows,
-                                                           int32_t blocks, int32_t *__restrict__ splits) {
+                                                           int32_t blocks, int32_t *__restrict__ splits,
+                                                           int32_t *__restrict__ counters) {
+  if (blockIdx.x == 0 && threadIdx.x < 64) counters[threadIdx.x] = 0;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (r > rows) return;
   if (r == rows) {
@@ -248,8 +269,6 @@ __global__ __launch_bounds__(kThreads) void spmv_fixup(float *__restrict__ y, in
   y[r] = __fadd_rn(sum, y[r]);
 }
 
-__global__ void spmv_clear(Workspace ws) { if (threadIdx.x < 64) ws.counters[threadIdx.x] = 0; }
-
 int64_t block_count(int64_t rows, int64_t nnz) { return (rows + nnz + kBlockItems - 1) / kBlockItems; }
 
 }  // namespace
@@ -292,9 +311,8 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   const int32_t c32 = cols > INT32_MAX ? INT32_MAX : static_cast<int32_t>(cols);
   const int64_t total = rows + nnz;
   spmv_partition<<<dim3(static_cast<unsigned>((rows + 1 + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(
-      row_offsets, r32, b32, ws.splits);
+      row_offsets, r32, b32, ws.splits, ws.counters);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_partition");
-  spmv_clear<<<dim3(1), dim3(64), 0, s>>>(ws);
   spmv_place<<<dim3(static_cast<unsigned>((blocks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(
       column_indices, c32 > 0 ? c32 : 1, b32, total, nnz, ws);
   spmv_place_fill<<<dim3(static_cast<unsigned>((blocks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(b32, ws);
