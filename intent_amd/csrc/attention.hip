@@ -154,18 +154,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
     const bool active = !causal || key0 <= wave_q_last;      // wave-uniform
     if (!active || wq0 >= sq) continue;
     // S^T for two 32-key tiles: s[st][e] is key 8 (e / 4) + 4 half + e % 4 of tile st. The K
-    // fragments of step ks + 1 are read while the two MFMAs of step ks run. Each tile accumulates
-    // its even and odd d steps in separate registers (four independent MFMA chains instead of
-    // two, so a dependent MFMA rarely waits for its predecessor), added at the end.
+    // fragments of step ks + 1 are read while the two MFMAs of step ks run.
     f32x16_t s[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[st][e] = 0.0f;
     {
-      f32x16_t sp[2][2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) sp[c][st][e] = 0.0f;
       f16x8_t kf[2][2];
       auto read_k = [&](int ks, int buf) {
 #pragma unroll
@@ -180,10 +175,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
         if (ks + 1 < kD / 16) read_k(ks + 1, (ks + 1) & 1);
 #pragma unroll
         for (int st = 0; st < 2; ++st)
-          sp[ks & 1][st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks & 1][st], qf[ks], sp[ks & 1][st], 0, 0, 0);
+          s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks & 1][st], qf[ks], s[st], 0, 0, 0);
       }
-#pragma unroll
-      for (int st = 0; st < 2; ++st) s[st] = sp[0][st] + sp[1][st];
     }
     // Mask (only tiles that cross the diagonal or the end) and the tile maximum of raw scores
     // (scale * log2 e > 0, so the maximum commutes with the scaling).
