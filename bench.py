@@ -22,12 +22,15 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "HBM GB/s (softmax, SpMV) and TFLOP/s (GEMM, attention) vs 1-GPU roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0          # dense bf16 / fp16
+MFMA_F32_PEAK_TFLOPS = 157.3       # dense fp32 MFMA
 FWD_BYTES_PER_ELEMENT, BWD_BYTES_PER_ELEMENT = 4, 6
 
 
@@ -42,7 +45,8 @@ def parse():
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-operators", action="store_true")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--operators", default="softmax_f32,gemm,attention,spmv")
+    parser.add_argument("--operators",
+                        default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -269,7 +273,126 @@ def op_spmv(device, flush, cpu):
     return out
 
 
-OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_attention, "spmv": op_spmv}
+def op_gemm_f16_relu(device, flush, cpu):
+    """`gemm` (contraction/gemm.py:54-73), f16 operands, ACTIVATION = RELU, at the config-3 shape."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.contraction.gemm import Activation, gemm
+
+    m = n = k = 8192
+    rng = np.random.default_rng(0)
+    a = inputs.uniform(rng, (m, k), -1.0, 1.0, "f16")
+    b = inputs.uniform(rng, (k, n), -1.0, 1.0, "f16")
+    call = intent.jit(gemm, backend="hip", constexprs={"ACTIVATION": Activation.RELU}).prepare(
+        torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
+    ms = graph_median_ms(call.launch, flush)
+    flops = 2 * m * n * k
+    out = {"config": "gemm f16 8192^3, ACTIVATION=RELU, fp32 accumulate", "median_ms": round(ms, 4),
+           "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        rows = 16
+        seconds = cpu_median_seconds(lambda: oracle.gemm16(a[:rows], b, relu=True))
+        out["cpu"] = {"tflops": round(2 * rows * n * k / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": f"{rows} rows of A"}
+    return out
+
+
+def _op_f32(device, flush, cpu, transpose_b):
+    """gemm_f32 / linear_f32 (contraction/gemm.py:15-38) at the reference module's shape
+    M = K = 4096, N = 14336 (gemm.py:5-7)."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.contraction.gemm import gemm_f32, linear_f32
+
+    m, k, n = 4096, 4096, 14336
+    rng = np.random.default_rng(1)
+    a = inputs.uniform(rng, (m, k), -1.0, 1.0)
+    b = inputs.uniform(rng, (n, k) if transpose_b else (k, n), -1.0, 1.0)
+    defn = linear_f32 if transpose_b else gemm_f32
+    call = intent.jit(defn, backend="hip").prepare(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
+    ms = graph_median_ms(call.launch, flush)
+    flops = 2 * m * n * k
+    out = {"config": f"{defn.__name__} M=4096 K=4096 N=14336, f32", "median_ms": round(ms, 4),
+           "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_F32_PEAK_TFLOPS, 4), "peak": MFMA_F32_PEAK_TFLOPS,
+           "flops": flops}
+    if cpu:
+        import oracle
+
+        rows = 8
+        seconds = cpu_median_seconds(lambda: oracle.gemm_f32(a[:rows], b, transpose_b=transpose_b))
+        out["cpu"] = {"tflops": round(2 * rows * n * k / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": f"{rows} rows of A"}
+    return out
+
+
+def op_gemm_f32(device, flush, cpu):
+    return _op_f32(device, flush, cpu, False)
+
+
+def op_linear_f32(device, flush, cpu):
+    return _op_f32(device, flush, cpu, True)
+
+
+def _op_attention_grouped(device, flush, cpu, bf16):
+    """flash_gqa_attention_fwd (f16, 32 query heads over 8 key/value heads) or
+    flash_attention_bf16_fwd (config 4 shapes in bf16), causal, S = 4096, D = 128."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.streaming.attention import flash_attention_bf16_fwd, flash_gqa_attention_fwd
+    from tests.gpu_util import to_bf16_tensor
+
+    b, hq, s, d = 4, 32, 4096, 128
+    group = 1 if bf16 else 4
+    hk = hq // group
+    rng = np.random.default_rng(2)
+    dtype = "bf16" if bf16 else "f16"
+    q = inputs.normal(rng, (b, hq, s, d), dtype)
+    k = inputs.normal(rng, (b, hk, s, d), dtype)
+    v = inputs.normal(rng, (b, hk, s, d), dtype)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    conv = (lambda a: to_bf16_tensor(a, device)) if bf16 else (lambda a: torch.from_numpy(a).to(device))
+    defn = flash_attention_bf16_fwd if bf16 else flash_gqa_attention_fwd
+    call = intent.jit(defn, backend="hip", constexprs={"HEAD_GROUP": group, "CAUSAL": True}).prepare(
+        conv(q), conv(k), conv(v), scale)
+    ms = graph_median_ms(call.launch, flush)
+    flops = 4 * b * hq * s * s * d // 2
+    name = ("causal attention fwd bf16 B4 H32 S4096 D128 (flash_attention_bf16_fwd)" if bf16 else
+            "causal GQA attention fwd f16 B4 HQ32 HK8 S4096 D128 (flash_gqa_attention_fwd)")
+    out = {"config": name, "median_ms": round(ms, 4), "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        seconds = cpu_median_seconds(lambda: oracle.attention_fwd(
+            np.ascontiguousarray(q[:1, :group, :1024]), np.ascontiguousarray(k[:1, :1]),
+            np.ascontiguousarray(v[:1, :1]), scale, True, head_group=group, storage="bf16" if bf16 else None))
+        sample_flops = group * 4 * 1024 * 1024 * d // 2
+        out["cpu"] = {"tflops": round(sample_flops / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": f"{group} query head(s) of one key head, first 1024 queries"}
+    return out
+
+
+def op_gqa(device, flush, cpu):
+    return _op_attention_grouped(device, flush, cpu, False)
+
+
+def op_attention_bf16(device, flush, cpu):
+    return _op_attention_grouped(device, flush, cpu, True)
+
+
+OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_attention, "spmv": op_spmv,
+             "gemm_f16_relu": op_gemm_f16_relu, "gemm_f32": op_gemm_f32, "linear_f32": op_linear_f32,
+             "gqa": op_gqa, "attention_bf16": op_attention_bf16}
 
 
 def read_traffic(name):

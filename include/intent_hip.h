@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 1
+#define INTENT_HIP_ABI_VERSION 2
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -47,8 +47,14 @@ enum IntentHipOperator {
   INTENT_HIP_OP_SOFTMAX_BWD = 1,
   INTENT_HIP_OP_GEMM_BF16 = 2,
   INTENT_HIP_OP_ATTENTION_FWD_F16 = 3,
-  INTENT_HIP_OP_CSR_SPMV_F32 = 4
+  INTENT_HIP_OP_CSR_SPMV_F32 = 4,
+  INTENT_HIP_OP_GEMM = 5,              /* dtype F16 or BF16 */
+  INTENT_HIP_OP_GEMM_F32 = 6,
+  INTENT_HIP_OP_ATTENTION_FWD = 7      /* dtype F16 or BF16 */
 };
+
+/* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
+enum IntentHipActivation { INTENT_HIP_ACT_NONE = 0, INTENT_HIP_ACT_RELU = 1 };
 
 struct IntentHipDeviceInfo {
   char arch[64];               /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
@@ -105,6 +111,22 @@ int intent_hip_softmax_bwd(int dtype, const void *p, const void *dy, void *dx, i
 int intent_hip_gemm_bf16(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
                          int64_t lda, int64_t ldb, int64_t ldc, void *stream);
 
+/* C = T(act(A @ B)), fp32 accumulation, T the operand type (dtype F16 or BF16).
+ * dtype F16: gemm (python/intent/examples/kernels/contraction/gemm.py:54-73) with the
+ *            ACTIVATION constexpr: NONE, or RELU = maximum(acc, 0.0) before the cast
+ *            (NaN propagates, types-numerics-and-effects.en.md:117);
+ * dtype BF16: bf16_gemm (gemm.py:76-92) with activation NONE (RELU is also accepted).
+ * Casts round to nearest even. A [m,k], B [k,n], C [m,n], row strides lda/ldb/ldc. */
+int intent_hip_gemm(int dtype, int activation, const void *a, const void *b, void *c, int64_t m,
+                    int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, void *stream);
+
+/* f32 GEMM with f32 accumulation (no TF32).
+ * transpose_b = 0: gemm_f32   (gemm.py:15-27), C = A @ B,   B [k,n];
+ * transpose_b = 1: linear_f32 (gemm.py:30-38), C = A @ B^T, B [n,k] (the weight).
+ * ldb is B's row stride in either layout. */
+int intent_hip_gemm_f32(const float *a, const float *b, float *c, int64_t m, int64_t n, int64_t k,
+                        int64_t lda, int64_t ldb, int64_t ldc, int transpose_b, void *stream);
+
 /* Fused attention forward, f16 in/out, f32 online softmax in the exp2 domain.
  * flash_attention_fwd (python/intent/examples/kernels/streaming/attention.py:428-466) with
  * summarize_attention_chunk_f16 (:152-191), merge_attention_summaries (:82-114) and
@@ -116,6 +138,19 @@ int intent_hip_attention_fwd_f16(const void *q, const void *k, const void *v, vo
                                  int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d,
                                  int64_t dv, const int64_t strides[16], float scale, int causal,
                                  void *stream);
+
+/* Fused attention forward with grouped key/value heads: q [b,hq,sq,d], k [b,hk,sk,d],
+ * v [b,hk,sk,dv], o [b,hq,sq,dv] with hq = q_heads = hk * head_group; query head h reads key/value
+ * head h / head_group. Same algebra as intent_hip_attention_fwd_f16, in the element type:
+ * dtype F16:  flash_gqa_attention_fwd   (streaming/attention.py:469-507; HEAD_GROUP and CAUSAL
+ *             constexprs), and flash_attention_fwd with head_group 1;
+ * dtype BF16: flash_attention_bf16_fwd  (attention.py:510-553) with
+ *             summarize_attention_chunk_bf16 (:193-237): P rounded to bf16 before P @ V, output
+ *             cast to bf16. */
+int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
+                             int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
+                             int64_t sk, int64_t d, int64_t dv, const int64_t strides[16],
+                             float scale, int causal, void *stream);
 
 /* CSR SpMV y = A x, f32 values, i32 indices.
  * csr_spmv (python/intent/examples/kernels/sparse/csr_spmv.py:11-29), with dynamic extents.

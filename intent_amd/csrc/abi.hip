@@ -92,8 +92,11 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
   switch (op) {
     case INTENT_HIP_OP_SOFTMAX_FWD: return softmax_fwd_resources(dtype, rows, cols, out);
     case INTENT_HIP_OP_SOFTMAX_BWD: return softmax_bwd_resources(dtype, rows, cols, out);
-    case INTENT_HIP_OP_GEMM_BF16: return gemm_resources(rows, cols, out);
-    case INTENT_HIP_OP_ATTENTION_FWD_F16: return attention_resources(rows, cols, out);
+    case INTENT_HIP_OP_GEMM_BF16: return gemm_resources(INTENT_HIP_BF16, rows, cols, out);
+    case INTENT_HIP_OP_GEMM: return gemm_resources(dtype, rows, cols, out);
+    case INTENT_HIP_OP_GEMM_F32: return gemm_f32_resources(rows, cols, out);
+    case INTENT_HIP_OP_ATTENTION_FWD_F16: return attention_resources(INTENT_HIP_F16, rows, cols, out);
+    case INTENT_HIP_OP_ATTENTION_FWD: return attention_resources(dtype, rows, cols, out);
     case INTENT_HIP_OP_CSR_SPMV_F32: return spmv_resources(rows, cols, out);
   }
   return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "unknown operator code %d", op);

@@ -34,8 +34,29 @@
 namespace intent_hip {
 namespace {
 
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Element type of q, k, v, o and of the rounded weights P: _Float16 (flash_attention_fwd,
+// flash_gqa_attention_fwd) or __bf16 (flash_attention_bf16_fwd).
+template <typename E> struct Elem;
+template <> struct Elem<_Float16> {
+  typedef _Float16 x8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16_t mma(x8 a, x8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Elem<__bf16> {
+  typedef __bf16 x8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16_t mma(x8 a, x8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename E>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<E>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<E>(hi))) << 16);
+}
 
 constexpr int kD = 128;
 constexpr int kBQ = 128;     // query rows per workgroup
@@ -65,12 +86,14 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // raised when a tile's maximum exceeds it by more than this, so weights stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
+template <typename E>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t *__restrict__ Q,
                                                                   const uint16_t *__restrict__ K,
                                                                   const uint16_t *__restrict__ V,
                                                                   uint16_t *__restrict__ O, int heads,
-                                                                  int sq, int sk, Geometry g, float scale,
-                                                                  int causal, int q_blocks) {
+                                                                  int head_group, int sq, int sk, Geometry g,
+                                                                  float scale, int causal, int q_blocks) {
+  typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
   __shared__ uint4 lds[2 * kStageChunks];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in a scalar register
@@ -79,8 +102,9 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
   const int bh = static_cast<int>(blockIdx.x) % bh_count;
   const int b = bh / heads, h = bh % heads;
   const uint16_t *qbase = Q + b * g.qs[0] + h * g.qs[1];
-  const uint16_t *kbase = K + b * g.ks[0] + h * g.ks[1];
-  const uint16_t *vbase = V + b * g.vs[0] + h * g.vs[1];
+  const int kh = h / head_group;   // query head h reads key/value head h / head_group
+  const uint16_t *kbase = K + b * g.ks[0] + kh * g.ks[1];
+  const uint16_t *vbase = V + b * g.vs[0] + kh * g.vs[1];
   uint16_t *obase = O + b * g.os[0] + h * g.os[1];
 
   const int q0 = qb * kBQ;
@@ -175,7 +199,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
         if (ks + 1 < kD / 16) read_k(ks + 1, (ks + 1) & 1);
 #pragma unroll
         for (int st = 0; st < 2; ++st)
-          s[st] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks & 1][st], qf[ks], s[st], 0, 0, 0);
+          s[st] = Elem<E>::mma(kf[ks & 1][st], qf[ks], s[st]);
       }
     }
     // Mask (only tiles that cross the diagonal or the end) and the tile maximum of raw scores
@@ -217,7 +241,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
       for (int e = 0; e < 16; ++e) {
         const float p = __builtin_amdgcn_exp2f(fmaf(s[st][e], factor, -shift));
         row_den += p;
-        pf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(p);
+        pf[st * 2 + (e >> 3)][e & 7] = static_cast<E>(p);
       }
     // O^T += V^T P^T. The A operand (V^T rows dv, keys in slot order) comes from V's natural
     // [key][dv] layout through ds_read_b64_tr_b16: read r of slice sl gives the lane keys
@@ -244,7 +268,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
         if (sl + 1 < 4) read_v(sl + 1, (sl + 1) & 1);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
-          acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl & 1][mt], pf[sl], acc[mt], 0, 0, 0);
+          acc[mt] = Elem<E>::mma(vf[sl & 1][mt], pf[sl], acc[mt]);
       }
     }
   }
@@ -259,31 +283,40 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
-      uint32_t w0 = static_cast<uint32_t>(from_f32<f16_t>(acc[mt][4 * gq] * inv).bits) |
-                    (static_cast<uint32_t>(from_f32<f16_t>(acc[mt][4 * gq + 1] * inv).bits) << 16);
-      uint32_t w1 = static_cast<uint32_t>(from_f32<f16_t>(acc[mt][4 * gq + 2] * inv).bits) |
-                    (static_cast<uint32_t>(from_f32<f16_t>(acc[mt][4 * gq + 3] * inv).bits) << 16);
+      const uint32_t w0 = pack2<E>(acc[mt][4 * gq] * inv, acc[mt][4 * gq + 1] * inv);
+      const uint32_t w1 = pack2<E>(acc[mt][4 * gq + 2] * inv, acc[mt][4 * gq + 3] * inv);
       *reinterpret_cast<uint2 *>(orow + mt * 32 + 8 * gq + 4 * half) = make_uint2(w0, w1);
     }
 }
 
 }  // namespace
 
-int attention_resources(int64_t sq, int64_t d, IntentHipKernelResources *out) {
+int attention_resources(int dtype, int64_t sq, int64_t d, IntentHipKernelResources *out) {
   (void)sq;
   (void)d;
-  return describe_kernel(reinterpret_cast<const void *>(&attention_fwd_d128), "attention_fwd_d128", kThreads, out);
+  if (dtype == INTENT_HIP_BF16)
+    return describe_kernel(reinterpret_cast<const void *>(&attention_fwd_d128<__bf16>), "attention_fwd_d128<bf16>",
+                           kThreads, out);
+  return describe_kernel(reinterpret_cast<const void *>(&attention_fwd_d128<_Float16>), "attention_fwd_d128<f16>",
+                         kThreads, out);
 }
 
 }  // namespace intent_hip
 
 using namespace intent_hip;
 
-extern "C" int intent_hip_attention_fwd_f16(const void *q, const void *k, const void *v, void *o, int64_t batch,
-                                            int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv,
-                                            const int64_t *strides, float scale, int causal, void *stream) {
+namespace {
+
+int launch_attention(int dtype, const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
+                     int64_t head_group, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
+                     float scale, int causal, void *stream) {
   if (batch < 0 || heads < 0 || sq < 0 || sk < 0 || d < 0 || dv < 0)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (head_group < 1 || (heads > 0 && heads % head_group != 0))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "head_group %lld must be positive and divide the %lld query heads",
+                static_cast<long long>(head_group), static_cast<long long>(heads));
+  if (dtype != INTENT_HIP_F16 && dtype != INTENT_HIP_BF16)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "attention dtype code %d (1 = f16, 2 = bf16)", dtype);
   if (batch == 0 || heads == 0 || sq == 0 || dv == 0) return INTENT_HIP_OK;
   if (d != kD || dv != kD)
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernel supports head dimension 128 (got d=%lld, dv=%lld)",
@@ -309,10 +342,36 @@ extern "C" int intent_hip_attention_fwd_f16(const void *q, const void *k, const 
   const int q_blocks = static_cast<int>((sq + kBQ - 1) / kBQ);
   const int64_t blocks = batch * heads * q_blocks;
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many attention workgroups");
-  attention_fwd_d128<<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, as_stream(stream)>>>(
-      static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
-      static_cast<uint16_t *>(o), static_cast<int>(heads), static_cast<int>(sq), static_cast<int>(sk), g, scale,
-      causal ? 1 : 0, q_blocks);
+  const auto *Qp = static_cast<const uint16_t *>(q);
+  const auto *Kp = static_cast<const uint16_t *>(k);
+  const auto *Vp = static_cast<const uint16_t *>(v);
+  auto *Op = static_cast<uint16_t *>(o);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+  const hipStream_t s = as_stream(stream);
+  if (dtype == INTENT_HIP_BF16)
+    attention_fwd_d128<__bf16><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, static_cast<int>(heads),
+                                                      static_cast<int>(head_group), static_cast<int>(sq),
+                                                      static_cast<int>(sk), g, scale, causal ? 1 : 0, q_blocks);
+  else
+    attention_fwd_d128<_Float16><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, static_cast<int>(heads),
+                                                        static_cast<int>(head_group), static_cast<int>(sq),
+                                                        static_cast<int>(sk), g, scale, causal ? 1 : 0, q_blocks);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd_d128");
   return INTENT_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int intent_hip_attention_fwd_f16(const void *q, const void *k, const void *v, void *o, int64_t batch,
+                                            int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv,
+                                            const int64_t *strides, float scale, int causal, void *stream) {
+  return launch_attention(INTENT_HIP_F16, q, k, v, o, batch, heads, 1, sq, sk, d, dv, strides, scale, causal, stream);
+}
+
+extern "C" int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
+                                        int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk,
+                                        int64_t d, int64_t dv, const int64_t *strides, float scale, int causal,
+                                        void *stream) {
+  return launch_attention(dtype, q, k, v, o, batch, q_heads, head_group, sq, sk, d, dv, strides, scale, causal,
+                          stream);
 }

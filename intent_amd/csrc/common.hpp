@@ -27,8 +27,9 @@ int describe_kernel(const void *kernel, const char *name, int block_threads,
 // Kernel selection facts exported by each operator file for intent_hip_kernel_resources().
 int softmax_fwd_resources(int dtype, int64_t rows, int64_t cols, IntentHipKernelResources *out);
 int softmax_bwd_resources(int dtype, int64_t rows, int64_t cols, IntentHipKernelResources *out);
-int gemm_resources(int64_t m, int64_t n, IntentHipKernelResources *out);
-int attention_resources(int64_t sq, int64_t d, IntentHipKernelResources *out);
+int gemm_resources(int dtype, int64_t m, int64_t n, IntentHipKernelResources *out);
+int gemm_f32_resources(int64_t m, int64_t n, IntentHipKernelResources *out);
+int attention_resources(int dtype, int64_t sq, int64_t d, IntentHipKernelResources *out);
 int spmv_resources(int64_t rows, int64_t nnz, IntentHipKernelResources *out);
 
 constexpr int kWave = 64;

@@ -35,9 +35,43 @@
 namespace intent_hip {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+// Operand element type: __bf16 (bf16_gemm) or _Float16 (gemm). Fragments of 8 elements feed
+// v_mfma_f32_32x32x16_{bf16,f16}; results are stored 4 at a time.
+template <typename E> struct Elem;
+template <> struct Elem<__bf16> {
+  typedef __bf16 x8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 x4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x16_t mma(x8 a, x8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Elem<_Float16> {
+  typedef _Float16 x8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 x4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x16_t mma(x8 a, x8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Epilogue activation on the f32 accumulator: 0 = none, 1 = ReLU as I.maximum(acc, 0.0)
+// (NaN propagates; -0 and +0 give +0).
+template <int kAct>
+__device__ __forceinline__ float activate(float v) {
+  if constexpr (kAct == 1) return v != v ? v : (v > 0.0f ? v : 0.0f);
+  return v;
+}
+
+template <typename E, int kAct>
+__device__ __forceinline__ typename Elem<E>::x4 pack4(float a, float b, float c, float d) {
+  typename Elem<E>::x4 r;
+  r[0] = static_cast<E>(activate<kAct>(a));
+  r[1] = static_cast<E>(activate<kAct>(b));
+  r[2] = static_cast<E>(activate<kAct>(c));
+  r[3] = static_cast<E>(activate<kAct>(d));
+  return r;
+}
 
 constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kThreads = 512;
@@ -47,7 +81,10 @@ constexpr int kGroupM = 8;
 
 __device__ __forceinline__ int swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-__device__ __forceinline__ uint16_t to_bf16_bits(float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); }
+template <typename E>
+__device__ __forceinline__ float element_to_f32(uint16_t bits) { return static_cast<float>(__builtin_bit_cast(E, bits)); }
+template <typename E>
+__device__ __forceinline__ uint16_t f32_to_element(float v) { return __builtin_bit_cast(uint16_t, static_cast<E>(v)); }
 
 __device__ __forceinline__ uint32_t word(const uint4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
@@ -72,7 +109,7 @@ __device__ __forceinline__ void tile_of_block(int block, int tiles_m, int tiles_
   tn = in_group / rows_in_group;
 }
 
-template <bool kEdge>
+template <typename E, int kAct, bool kEdge>
 __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
                                           uint16_t *__restrict__ C, int M, int N, int K, int64_t lda,
                                           int64_t ldb, int64_t ldc, int m0, int n0, uint4 *lds) {
@@ -166,18 +203,19 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
 #pragma unroll
     for (int kk = 0; kk < kBK / 16; ++kk) {
       const int chunk = (kk * 2 + frag_half) ^ frag_swz;
-      bf16x8_t af[4], bf[2];
+      typedef typename Elem<E>::x8 x8;
+      x8 af[4], bf[2];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        af[t] = __builtin_bit_cast(bf16x8_t, sa[(wm * 128 + t * 32 + frag_row) * 8 + chunk]);
+        af[t] = __builtin_bit_cast(x8, sa[(wm * 128 + t * 32 + frag_row) * 8 + chunk]);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
-        bf[t] = __builtin_bit_cast(bf16x8_t, sb[(wn * 64 + t * 32 + frag_row) * 8 + chunk]);
+        bf[t] = __builtin_bit_cast(x8, sb[(wn * 64 + t * 32 + frag_row) * 8 + chunk]);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[nt], af[mt], acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = Elem<E>::mma(bf[nt], af[mt], acc[mt][nt]);
     }
   };
 
@@ -207,12 +245,8 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
         const int n = n0 + wn * 64 + nt * 32 + 8 * g + 4 * frag_half;
         if (kEdge && n >= N) continue;
         const f32x16_t &v = acc[mt][nt];
-        bf16x4_t packed;
-        packed[0] = static_cast<__bf16>(v[4 * g]);
-        packed[1] = static_cast<__bf16>(v[4 * g + 1]);
-        packed[2] = static_cast<__bf16>(v[4 * g + 2]);
-        packed[3] = static_cast<__bf16>(v[4 * g + 3]);
-        *reinterpret_cast<bf16x4_t *>(crow + n) = packed;
+        *reinterpret_cast<typename Elem<E>::x4 *>(crow + n) =
+            pack4<E, kAct>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
       }
     }
   }
@@ -252,6 +286,7 @@ __device__ __forceinline__ void dma_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+template <typename E, int kAct>
 __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
                                               uint16_t *__restrict__ C, int K, int64_t lda, int64_t ldb,
                                               int64_t ldc, int m0, int n0, uint4 *lds) {
@@ -325,7 +360,8 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
   wait_tile(0);
   dma_barrier();
   if (lag) dma_barrier();
-  bf16x8_t af[2][4], bf[2][2];
+  typedef typename Elem<E>::x8 x8;
+  x8 af[2][4], bf[2][2];
   for (int kt = 0; kt < k_tiles; ++kt) {
     const uint4 *sa = lds + (kt % kDmaStages) * kDmaStageChunks;
     const uint16_t *sb = reinterpret_cast<const uint16_t *>(sa + kDmaChunksA);
@@ -333,7 +369,7 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
     for (int kk = 0; kk < kDmaBK / 16; ++kk) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        af[kk][t] = __builtin_bit_cast(bf16x8_t, sa[(wm * 128 + t * 32 + frag_row) * 4 + ((kk * 2 + half) ^ a_swz)]);
+        af[kk][t] = __builtin_bit_cast(x8, sa[(wm * 128 + t * 32 + frag_row) * 4 + ((kk * 2 + half) ^ a_swz)]);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         i16x4_t parts[2];
@@ -344,7 +380,7 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
           const int chunk = (n >> 3) ^ (2 * (k & 3));
           parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sb + k * kBN + chunk * 8 + (n & 7)));
         }
-        bf[kk][t] = __builtin_bit_cast(bf16x8_t, parts);
+        bf[kk][t] = __builtin_bit_cast(x8, parts);
       }
     }
     if (kt + kDmaStages - 1 < k_tiles) issue(kt + kDmaStages - 1);
@@ -357,7 +393,7 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[kk][nt], af[kk][mt], acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = Elem<E>::mma(bf[kk][nt], af[kk][mt], acc[mt][nt]);
     if (!lag) wait_tile(kt + 1);
     dma_barrier();
   }
@@ -373,17 +409,14 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
       for (int g = 0; g < 4; ++g) {
         const int n = n0 + wn * 64 + nt * 32 + 8 * g + 4 * half;
         const f32x16_t &v = acc[mt][nt];
-        bf16x4_t packed;
-        packed[0] = static_cast<__bf16>(v[4 * g]);
-        packed[1] = static_cast<__bf16>(v[4 * g + 1]);
-        packed[2] = static_cast<__bf16>(v[4 * g + 2]);
-        packed[3] = static_cast<__bf16>(v[4 * g + 3]);
-        *reinterpret_cast<bf16x4_t *>(crow + n) = packed;
+        *reinterpret_cast<typename Elem<E>::x4 *>(crow + n) =
+            pack4<E, kAct>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
       }
   }
 }
 
-__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_mfma(const uint16_t *__restrict__ A,
+template <typename E, int kAct>
+__global__ __launch_bounds__(kThreads, 1) void gemm_mfma(const uint16_t *__restrict__ A,
                                                               const uint16_t *__restrict__ B,
                                                               uint16_t *__restrict__ C, int M, int N, int K,
                                                               int64_t lda, int64_t ldb, int64_t ldc,
@@ -394,11 +427,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_mfma(const uint16_t *__
   const int m0 = tm * kBM, n0 = tn * kBN;
   const bool interior = m0 + kBM <= M && n0 + kBN <= N;
   if (interior && (K % kDmaBK) == 0)
-    gemm_tile_dma(A, B, C, K, lda, ldb, ldc, m0, n0, lds);
+    gemm_tile_dma<E, kAct>(A, B, C, K, lda, ldb, ldc, m0, n0, lds);
   else if (interior && (K % kBK) == 0)
-    gemm_tile<false>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
+    gemm_tile<E, kAct, false>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
   else
-    gemm_tile<true>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
+    gemm_tile<E, kAct, true>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
 }
 
 // ---------------------------------------------------------------- general-shape fallback
@@ -406,7 +439,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_mfma(const uint16_t *__
 // f32 fused multiply-add in increasing k.
 constexpr int kFT = 64, kFK = 16;
 
-__global__ __launch_bounds__(256) void gemm_bf16_simple(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+template <typename E, int kAct>
+__global__ __launch_bounds__(256) void gemm_simple(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
                                                         uint16_t *__restrict__ C, int M, int N, int K, int64_t lda,
                                                         int64_t ldb, int64_t ldc) {
   __shared__ float sa[kFK][kFT + 1];
@@ -418,10 +452,10 @@ __global__ __launch_bounds__(256) void gemm_bf16_simple(const uint16_t *__restri
     for (int e = threadIdx.x; e < kFT * kFK; e += 256) {
       const int r = e / kFK, kc = e % kFK;
       const int gm = m0 + r, gk = k0 + kc;
-      sa[kc][r] = (gm < M && gk < K) ? to_f32(bf16_t{A[static_cast<int64_t>(gm) * lda + gk]}) : 0.0f;
+      sa[kc][r] = (gm < M && gk < K) ? element_to_f32<E>(A[static_cast<int64_t>(gm) * lda + gk]) : 0.0f;
       const int kr = e / kFT, nc = e % kFT;
       const int gk2 = k0 + kr, gn = n0 + nc;
-      sb[kr][nc] = (gk2 < K && gn < N) ? to_f32(bf16_t{B[static_cast<int64_t>(gk2) * ldb + gn]}) : 0.0f;
+      sb[kr][nc] = (gk2 < K && gn < N) ? element_to_f32<E>(B[static_cast<int64_t>(gk2) * ldb + gn]) : 0.0f;
     }
     __syncthreads();
 #pragma unroll
@@ -437,7 +471,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_simple(const uint16_t *__restri
     if (gm >= M) continue;
     for (int j = 0; j < 4; ++j) {
       const int gn = n0 + tx * 4 + j;
-      if (gn < N) C[static_cast<int64_t>(gm) * ldc + gn] = to_bf16_bits(acc[i][j]);
+      if (gn < N) C[static_cast<int64_t>(gm) * ldc + gn] = f32_to_element<E>(activate<kAct>(acc[i][j]));
     }
   }
 }
@@ -450,18 +484,19 @@ bool fast_path(const void *a, const void *b, const void *c, int64_t n, int64_t k
 
 }  // namespace
 
-int gemm_resources(int64_t m, int64_t n, IntentHipKernelResources *out) {
+int gemm_resources(int dtype, int64_t m, int64_t n, IntentHipKernelResources *out) {
   (void)m;
   (void)n;
-  return describe_kernel(reinterpret_cast<const void *>(&gemm_bf16_mfma), "gemm_bf16_mfma", kThreads, out);
+  if (dtype == INTENT_HIP_F16)
+    return describe_kernel(reinterpret_cast<const void *>(&gemm_mfma<_Float16, 0>), "gemm_mfma<f16>", kThreads, out);
+  return describe_kernel(reinterpret_cast<const void *>(&gemm_mfma<__bf16, 0>), "gemm_mfma<bf16>", kThreads, out);
 }
 
-}  // namespace intent_hip
+namespace {
 
-using namespace intent_hip;
-
-extern "C" int intent_hip_gemm_bf16(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
-                                    int64_t lda, int64_t ldb, int64_t ldc, void *stream) {
+template <typename E, int kAct>
+int launch_gemm(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                int64_t ldc, void *stream) {
   if (m < 0 || n < 0 || k < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
   if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2)
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "GEMM extents must stay below 2^30");
@@ -477,14 +512,37 @@ extern "C" int intent_hip_gemm_bf16(const void *a, const void *b, void *c, int64
   auto *C = static_cast<uint16_t *>(c);
   if (k > 0 && fast_path(a, b, c, n, k, lda, ldb, ldc)) {
     const int tiles_m = static_cast<int>((m + kBM - 1) / kBM), tiles_n = static_cast<int>((n + kBN - 1) / kBN);
-    gemm_bf16_mfma<<<dim3(tiles_m * tiles_n), dim3(kThreads), 0, s>>>(
+    gemm_mfma<E, kAct><<<dim3(tiles_m * tiles_n), dim3(kThreads), 0, s>>>(
         A, B, C, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), lda, ldb, ldc, tiles_m, tiles_n);
-    if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_bf16_mfma");
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_mfma");
     return INTENT_HIP_OK;
   }
   const dim3 grid(static_cast<unsigned>((n + kFT - 1) / kFT), static_cast<unsigned>((m + kFT - 1) / kFT));
-  gemm_bf16_simple<<<grid, dim3(256), 0, s>>>(A, B, C, static_cast<int>(m), static_cast<int>(n),
-                                              static_cast<int>(k), lda, ldb, ldc);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_bf16_simple");
+  gemm_simple<E, kAct><<<grid, dim3(256), 0, s>>>(A, B, C, static_cast<int>(m), static_cast<int>(n),
+                                                  static_cast<int>(k), lda, ldb, ldc);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_simple");
   return INTENT_HIP_OK;
+}
+
+}  // namespace
+}  // namespace intent_hip
+
+using namespace intent_hip;
+
+extern "C" int intent_hip_gemm_bf16(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
+                                    int64_t lda, int64_t ldb, int64_t ldc, void *stream) {
+  return launch_gemm<__bf16, 0>(a, b, c, m, n, k, lda, ldb, ldc, stream);
+}
+
+extern "C" int intent_hip_gemm(int dtype, int activation, const void *a, const void *b, void *c, int64_t m, int64_t n,
+                               int64_t k, int64_t lda, int64_t ldb, int64_t ldc, void *stream) {
+  if (activation != 0 && activation != 1)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "activation code %d (0 = none, 1 = relu)", activation);
+  if (dtype == INTENT_HIP_F16)
+    return activation ? launch_gemm<_Float16, 1>(a, b, c, m, n, k, lda, ldb, ldc, stream)
+                      : launch_gemm<_Float16, 0>(a, b, c, m, n, k, lda, ldb, ldc, stream);
+  if (dtype == INTENT_HIP_BF16)
+    return activation ? launch_gemm<__bf16, 1>(a, b, c, m, n, k, lda, ldb, ldc, stream)
+                      : launch_gemm<__bf16, 0>(a, b, c, m, n, k, lda, ldb, ldc, stream);
+  return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "16-bit GEMM dtype code %d (1 = f16, 2 = bf16)", dtype);
 }

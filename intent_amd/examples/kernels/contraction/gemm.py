@@ -1,7 +1,53 @@
 """Dense GEMM definitions (interface of the reference's
-`python/intent/examples/kernels/contraction/gemm.py:76-92`)."""
+`python/intent/examples/kernels/contraction/gemm.py:10-92`): gemm_f32, linear_f32, the f16
+`gemm` with its ACTIVATION constexpr, and bf16_gemm."""
 import intent_amd as intent
 import intent_amd.language as I
+
+
+class Activation(I.Enum):
+    """Epilogue activation of `gemm` (gemm.py:10-12)."""
+
+    NONE = 0
+    RELU = 1
+
+
+@intent.kernel
+def gemm_f32(
+    a: I.In[I.f32, ("M", "K")],
+    b: I.In[I.f32, ("K", "N")],
+    c: I.Out[I.f32, ("M", "N")],
+):
+    M, K = a.shape
+    _, N = b.shape
+    m, n, k = I.domain(0, M), I.domain(0, N), I.domain(0, K)
+    c[m, n] = I.matmul(a[m, k], b[k, n], acc_dtype=I.f32)
+
+
+@intent.kernel
+def linear_f32(
+    x: I.In[I.f32, ("M", "K")],
+    weight: I.In[I.f32, ("N", "K")],
+    output: I.Out[I.f32, ("M", "N")],
+):
+    m, n, k = I.domain(0, x.shape[0]), I.domain(0, weight.shape[0]), I.domain(0, x.shape[1])
+    output[m, n] = I.matmul(x[m, k], weight[n, k], transpose_rhs=True, acc_dtype=I.f32)
+
+
+@intent.kernel
+def gemm(
+    a: I.In[I.f16, ("M", "K")],
+    b: I.In[I.f16, ("K", "N")],
+    c: I.Out[I.f16, ("M", "N")],
+    ACTIVATION: I.Constexpr[Activation],
+):
+    M, K = a.shape
+    _, N = b.shape
+    m, n, k = I.domain(0, M), I.domain(0, N), I.domain(0, K)
+    accumulator = I.matmul(a[m, k], b[k, n], acc_dtype=I.f32)
+    if ACTIVATION == Activation.RELU:
+        accumulator = I.maximum(accumulator, 0.0)
+    c[m, n] = I.cast(accumulator, I.f16)
 
 
 @intent.kernel

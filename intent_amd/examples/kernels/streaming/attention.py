@@ -1,5 +1,6 @@
-"""Fused attention forward definition (interface and semantics of the reference's
-`python/intent/examples/kernels/streaming/attention.py:47-191, 417-466`).
+"""Fused attention forward definitions (interface and semantics of the reference's
+`python/intent/examples/kernels/streaming/attention.py:47-237, 417-553`): flash_attention_fwd,
+flash_gqa_attention_fwd (grouped key/value heads) and flash_attention_bf16_fwd.
 
 A region fold over key chunks keeps, per query row, a summary record
 (valid, maximum, denominator, accumulator) in the exp2 domain:
@@ -70,6 +71,26 @@ def summarize_attention_chunk_f16(key_chunk, value_chunk, key_coordinates, queri
 
 
 @intent.fn
+def summarize_attention_chunk_bf16(key_chunk, value_chunk, key_coordinates, queries, query_coordinates,
+                                   scale, causal, active):
+    scores = I.matmul(queries, key_chunk, transpose_rhs=True, acc_dtype=I.f32) * (scale * I.LOG2E)
+    valid = I.full(scores.shape, fill=True, dtype=I.bool) & active
+    if causal:
+        valid = valid & (query_coordinates[:, None] >= key_coordinates[None, :])
+    masked = I.select(valid, scores, -I.inf)
+    any_valid = I.reduce.any(valid, axis=1)
+    chunk_max = I.select(any_valid, reduce_score_maximum(masked, axis=1), 0.0)
+    weights = I.select(valid, I.exp2(masked - chunk_max[:, None], approximate=True, flush_to_zero=True), 0.0)
+    return I.record(
+        valid=any_valid,
+        maximum=chunk_max,
+        denominator=I.reduce.sum(weights, axis=1),
+        accumulator=I.select(any_valid[:, None],
+                             I.matmul(I.cast(weights, I.bf16), value_chunk, acc_dtype=I.f32), 0.0),
+    )
+
+
+@intent.fn
 def normalize_attention_summary(summary):
     denominator = I.select(summary.valid, summary.denominator, 1.0)
     reciprocal = I.fdiv(1.0, denominator, approximate=True, flush_to_zero=True)
@@ -100,3 +121,59 @@ def flash_attention_fwd(
                 operands=(q[batch, head, q_axis, :], I.indices(q_axis), scale, CAUSAL),
             )
             output[batch, head, q_axis, :] = I.cast(normalize_attention_summary(summary), I.f16)
+
+
+@intent.kernel
+def flash_gqa_attention_fwd(
+    q: I.In[I.f16, ("B", "HQ", "Q", "D")],
+    k: I.In[I.f16, ("B", "HK", "K", "D")],
+    v: I.In[I.f16, ("B", "HK", "K", "DV")],
+    output: I.Out[I.f16, ("B", "HQ", "Q", "DV")],
+    scale: I.f32,
+    HEAD_GROUP: I.Constexpr[int],
+    CAUSAL: I.Constexpr[bool],
+):
+    B, HQ, Q, _ = q.shape
+    K = k.shape[2]
+    DV = v.shape[3]
+    q_axis, k_axis = I.domain(0, Q), I.domain(0, K)
+    for batch in I.parallel(I.domain(0, B)):
+        for query_head in I.parallel(I.domain(0, HQ)):
+            key_head = query_head // HEAD_GROUP
+            summary = I.region_fold(
+                source=(k[batch, key_head, k_axis, :], v[batch, key_head, k_axis, :], I.indices(k_axis)),
+                axis=0,
+                summarize=summarize_attention_chunk_f16,
+                combine=merge_attention_summaries,
+                identity=empty_attention_summary(Q, DV),
+                operands=(q[batch, query_head, q_axis, :], I.indices(q_axis), scale, CAUSAL),
+            )
+            output[batch, query_head, q_axis, :] = I.cast(normalize_attention_summary(summary), I.f16)
+
+
+@intent.kernel
+def flash_attention_bf16_fwd(
+    q: I.In[I.bf16, ("B", "HQ", "Q", "D")],
+    k: I.In[I.bf16, ("B", "HK", "K", "D")],
+    v: I.In[I.bf16, ("B", "HK", "K", "DV")],
+    output: I.Out[I.bf16, ("B", "HQ", "Q", "DV")],
+    scale: I.f32,
+    HEAD_GROUP: I.Constexpr[int],
+    CAUSAL: I.Constexpr[bool],
+):
+    B, HQ, Q, _ = q.shape
+    K = k.shape[2]
+    DV = v.shape[3]
+    q_axis, k_axis = I.domain(0, Q), I.domain(0, K)
+    for batch in I.parallel(I.domain(0, B)):
+        for query_head in I.parallel(I.domain(0, HQ)):
+            key_head = query_head // HEAD_GROUP
+            summary = I.region_fold(
+                source=(k[batch, key_head, k_axis, :], v[batch, key_head, k_axis, :], I.indices(k_axis)),
+                axis=0,
+                summarize=summarize_attention_chunk_bf16,
+                combine=merge_attention_summaries,
+                identity=empty_attention_summary(Q, DV),
+                operands=(q[batch, query_head, q_axis, :], I.indices(q_axis), scale, CAUSAL, True),
+            )
+            output[batch, query_head, q_axis, :] = I.cast(normalize_attention_summary(summary), I.bf16)

@@ -11,12 +11,14 @@ from pathlib import Path
 
 from ...diagnostics import CompilationStageError
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIBRARY_NAME = "libintent_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parents[2] / LIBRARY_NAME
 
 F32, F16, BF16 = 0, 1, 2
-OP_SOFTMAX_FWD, OP_SOFTMAX_BWD, OP_GEMM_BF16, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32 = range(5)
+(OP_SOFTMAX_FWD, OP_SOFTMAX_BWD, OP_GEMM_BF16, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_F32,
+ OP_ATTENTION_FWD) = range(8)
+ACT_NONE, ACT_RELU = 0, 1
 
 _i64, _int, _p, _f32, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 
@@ -46,8 +48,12 @@ SIGNATURES = {
     "intent_hip_softmax_fwd": (_int, (_int, _p, _p, _i64, _i64, _i64, _i64, _p)),
     "intent_hip_softmax_bwd": (_int, (_int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p)),
     "intent_hip_gemm_bf16": (_int, (_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p)),
+    "intent_hip_gemm": (_int, (_int, _int, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p)),
+    "intent_hip_gemm_f32": (_int, (_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _p)),
     "intent_hip_attention_fwd_f16": (_int, (_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                             ctypes.POINTER(_i64), _f32, _int, _p)),
+    "intent_hip_attention_fwd": (_int, (_int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        ctypes.POINTER(_i64), _f32, _int, _p)),
     "intent_hip_csr_spmv_workspace_bytes": (_int, (_i64, _i64, ctypes.POINTER(_sz))),
     "intent_hip_csr_spmv_f32": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p)),
 }

@@ -10,8 +10,13 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   chunked_softmax_bf16    normalization/softmax.py:54-66   intent_hip_softmax_fwd (bf16)
   softmax_backward        backward/softmax.py:9-25         intent_hip_softmax_bwd (f32)
   softmax_backward_f16    f16-storage variant of the same  intent_hip_softmax_bwd (f16)
+  gemm_f32                contraction/gemm.py:15-27        intent_hip_gemm_f32 (transpose_b 0)
+  linear_f32              contraction/gemm.py:30-38        intent_hip_gemm_f32 (transpose_b 1)
+  gemm                    contraction/gemm.py:54-73        intent_hip_gemm (f16, ACTIVATION)
   bf16_gemm               contraction/gemm.py:76-92        intent_hip_gemm_bf16
   flash_attention_fwd     streaming/attention.py:428-466   intent_hip_attention_fwd_f16
+  flash_gqa_attention_fwd streaming/attention.py:469-507   intent_hip_attention_fwd (f16, HEAD_GROUP)
+  flash_attention_bf16_fwd streaming/attention.py:510-553  intent_hip_attention_fwd (bf16, HEAD_GROUP)
   csr_spmv                sparse/csr_spmv.py:11-29         intent_hip_csr_spmv_f32
 
 (paths relative to python/intent/examples/kernels/ in the reference).
@@ -28,8 +33,8 @@ from dataclasses import dataclass, field
 from typing import Callable
 
 from ...diagnostics import CompilationStageError
-from .library import (BF16, F16, F32, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM_BF16,
-                      OP_SOFTMAX_BWD, OP_SOFTMAX_FWD)
+from .library import (BF16, F16, F32, OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM,
+                      OP_GEMM_BF16, OP_GEMM_F32, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD)
 
 
 @dataclass
@@ -147,6 +152,48 @@ def _gemm_bf16(lib, bound, constexprs, device):
                   lambda: lib.kernel_resources(OP_GEMM_BF16, BF16, m, n))
 
 
+def _activation_code(value) -> int:
+    """ACTIVATION constexpr (an Activation enum member, gemm.py:10-12) -> ABI code."""
+    code = getattr(value, "value", value)
+    if code not in (0, 1):
+        raise CompilationStageError("provider_configuration",
+                                    f"the hip gemm supports ACTIVATION NONE (0) or RELU (1), got {value!r}")
+    return int(code)
+
+
+def _gemm16(dtype_code):
+    def plan(lib, bound, constexprs, device):
+        a, b, c = bound.arguments
+        activation = _activation_code(constexprs.get("ACTIVATION", 0))
+        keep, before, after = [a, b, c], [], []
+        ak, bk, ck = _readable(a, keep, before), _readable(b, keep, before), _writable(c, keep, after)
+        m, k = a.shape
+        n = b.shape[1]
+        fn = lib.fn["gemm"]
+        args = (dtype_code, activation, ak.data_ptr(), bk.data_ptr(), ck.data_ptr(), m, n, k, _row_stride(ak),
+                _row_stride(bk), _row_stride(ck))
+        return Launch("intent_hip_gemm", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                      tuple(after), (("m", m), ("n", n), ("k", k), ("activation", activation)),
+                      lambda: lib.kernel_resources(OP_GEMM, dtype_code, m, n))
+    return plan
+
+
+def _gemm_f32(transpose_b: bool):
+    def plan(lib, bound, constexprs, device):
+        a, b, c = bound.arguments
+        keep, before, after = [a, b, c], [], []
+        ak, bk, ck = _readable(a, keep, before), _readable(b, keep, before), _writable(c, keep, after)
+        m, k = a.shape
+        n = b.shape[0] if transpose_b else b.shape[1]
+        fn = lib.fn["gemm_f32"]
+        args = (ak.data_ptr(), bk.data_ptr(), ck.data_ptr(), m, n, k, _row_stride(ak), _row_stride(bk),
+                _row_stride(ck), int(transpose_b))
+        return Launch("intent_hip_gemm_f32", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                      tuple(after), (("m", m), ("n", n), ("k", k), ("transpose_b", transpose_b)),
+                      lambda: lib.kernel_resources(OP_GEMM_F32, F32, m, n))
+    return plan
+
+
 # ------------------------------------------------------------------------------ attention
 def _attention_f16(lib, bound, constexprs, device):
     import ctypes
@@ -167,6 +214,37 @@ def _attention_f16(lib, bound, constexprs, device):
                   tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("sk", sk), ("d", d),
                                  ("causal", causal)),
                   lambda: lib.kernel_resources(OP_ATTENTION_FWD_F16, F16, sq, d))
+
+
+def _attention_grouped(dtype_code):
+    """flash_gqa_attention_fwd (f16) / flash_attention_bf16_fwd (bf16): key head = query head //
+    HEAD_GROUP (attention.py:485, 528)."""
+    def plan(lib, bound, constexprs, device):
+        import ctypes
+
+        q, k, v, o, scale = bound.arguments
+        causal = bool(constexprs["CAUSAL"])
+        group = constexprs["HEAD_GROUP"]
+        if isinstance(group, bool) or not isinstance(group, int) or group < 1:
+            raise CompilationStageError("provider_configuration", f"HEAD_GROUP must be a positive int, got {group!r}")
+        batch, q_heads, sq, d = q.shape
+        if k.shape[1] * group != q_heads:
+            raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({k.shape[1]}) * HEAD_GROUP "
+                             f"({group})")
+        keep, before, after = [q, k, v, o], [], []
+        qk, kk, vk, ok = (_readable(q, keep, before, 8), _readable(k, keep, before, 8),
+                          _readable(v, keep, before, 8), _writable(o, keep, after, 8))
+        sk, dv = k.shape[2], v.shape[3]
+        strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
+        keep.append(strides)
+        fn = lib.fn["attention_fwd"]
+        args = (dtype_code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, q_heads, group, sq,
+                sk, d, dv, strides, float(scale), int(causal))
+        return Launch("intent_hip_attention_fwd", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                      tuple(after), (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq),
+                                     ("sk", sk), ("d", d), ("causal", causal)),
+                      lambda: lib.kernel_resources(OP_ATTENTION_FWD, dtype_code, sq, d))
+    return plan
 
 
 # ------------------------------------------------------------------------------ SpMV
@@ -207,10 +285,22 @@ _SPECS = (
                  _softmax_bwd(F32), True),
     OperatorSpec("softmax_backward_f16", (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(OUT, "f16", 2)), (),
                  _softmax_bwd(F16), True),
+    OperatorSpec("gemm_f32", (_view(IN, "f32", 2), _view(IN, "f32", 2), _view(OUT, "f32", 2)), (),
+                 _gemm_f32(False)),
+    OperatorSpec("linear_f32", (_view(IN, "f32", 2), _view(IN, "f32", 2), _view(OUT, "f32", 2)), (),
+                 _gemm_f32(True)),
+    OperatorSpec("gemm", (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(OUT, "f16", 2)), ("ACTIVATION",),
+                 _gemm16(F16)),
     OperatorSpec("bf16_gemm", (_view(IN, "bf16", 2), _view(IN, "bf16", 2), _view(OUT, "bf16", 2)), (),
                  _gemm_bf16),
     OperatorSpec("flash_attention_fwd", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
                                          _view(OUT, "f16", 4), ("scalar", "f32")), ("CAUSAL",), _attention_f16),
+    OperatorSpec("flash_gqa_attention_fwd", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
+                                             _view(OUT, "f16", 4), ("scalar", "f32")), ("HEAD_GROUP", "CAUSAL"),
+                 _attention_grouped(F16)),
+    OperatorSpec("flash_attention_bf16_fwd", (_view(IN, "bf16", 4), _view(IN, "bf16", 4), _view(IN, "bf16", 4),
+                                              _view(OUT, "bf16", 4), ("scalar", "f32")), ("HEAD_GROUP", "CAUSAL"),
+                 _attention_grouped(BF16)),
     OperatorSpec("csr_spmv", (_view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "f32", 1), _view(IN, "f32", 1),
                               _view(OUT, "f32", 1)), (), _csr_spmv, derived=(("R", "R1", -1),)),
 )

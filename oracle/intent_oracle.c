@@ -1,5 +1,5 @@
 /*
- * intent_oracle.c — CPU restatement of the reference semantics of the five operators.
+ * intent_oracle.c — CPU restatement of the reference semantics of the hot-path operators.
  *
  * TEST INFRASTRUCTURE ONLY. This file is the parity checker of the hip provider and
  * the CPU baseline that bench.py reports; the product (intent_amd) never loads it.
@@ -214,13 +214,19 @@ int oracle_softmax_bwd(int dtype, const void *p, const void *dy, void *dx, int64
   return 0;
 }
 
-/* ------------------------------------------------------------------ bf16 GEMM
- * contraction/gemm.py:76-92: c = cast(matmul(a, b, acc_dtype=f32), bf16). Each c[i][j] is
- * accumulated in f32 over k in increasing order (a row of accumulators per i, so the inner
- * loop over j vectorises without changing any element's order). */
-int oracle_gemm_bf16(const uint16_t *a, const uint16_t *b, uint16_t *c, int64_t m, int64_t n, int64_t k,
-                     int64_t lda, int64_t ldb, int64_t ldc, int workers) {
+/* ------------------------------------------------------------------ 16-bit GEMM
+ * contraction/gemm.py:54-92: accumulator = matmul(a, b, acc_dtype=f32); for `gemm` (f16,
+ * :54-73) with ACTIVATION == RELU, accumulator = maximum(accumulator, 0.0) (NaN propagates,
+ * types-numerics-and-effects.en.md:117; maximum(-0, +0) = +0); c = cast(accumulator) to the
+ * operand type, nearest even. bf16_gemm (:76-92) is dtype bf16 without activation.
+ * Each c[i][j] is accumulated in f32 over k in increasing order (a row of accumulators per i,
+ * so the inner loop over j vectorises without changing any element's order). */
+static inline float relu_maximum(float v) { return v != v ? v : (v > 0.0f ? v : 0.0f); }
+
+int oracle_gemm16(int dtype, int activation, const uint16_t *a, const uint16_t *b, uint16_t *c, int64_t m,
+                  int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int workers) {
   if (m <= 0 || n <= 0) return 0;
+  if (dtype != 1 && dtype != 2) return 1;
   const uint32_t csr = enter_ieee();
   const int size = team_size(workers, m);
 #pragma omp parallel num_threads(size)
@@ -233,12 +239,63 @@ int oracle_gemm_bf16(const uint16_t *a, const uint16_t *b, uint16_t *c, int64_t 
     for (int64_t i = begin; i < end; ++i) {
       for (int64_t j = 0; j < n; ++j) acc[j] = 0.0f;
       for (int64_t kk = 0; kk < k; ++kk) {
-        const float av = oracle_bf16_to_float(a[i * lda + kk]);
+        const float av = load_elem(a, dtype, i * lda + kk);
         const uint16_t *src = b + kk * ldb;
-        for (int64_t j = 0; j < n; ++j) brow[j] = bits_f32((uint32_t)src[j] << 16);
+        if (dtype == ORACLE_BF16)
+          for (int64_t j = 0; j < n; ++j) brow[j] = bits_f32((uint32_t)src[j] << 16);
+        else
+          for (int64_t j = 0; j < n; ++j) brow[j] = oracle_half_to_float(src[j]);
         for (int64_t j = 0; j < n; ++j) acc[j] = acc[j] + av * brow[j];
       }
-      for (int64_t j = 0; j < n; ++j) c[i * ldc + j] = oracle_float_to_bf16(acc[j]);
+      for (int64_t j = 0; j < n; ++j) store_elem(c, dtype, i * ldc + j, activation ? relu_maximum(acc[j]) : acc[j]);
+    }
+    free(acc);
+    free(brow);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+int oracle_gemm_bf16(const uint16_t *a, const uint16_t *b, uint16_t *c, int64_t m, int64_t n, int64_t k,
+                     int64_t lda, int64_t ldb, int64_t ldc, int workers) {
+  return oracle_gemm16(2, 0, a, b, c, m, n, k, lda, ldb, ldc, workers);
+}
+
+/* ------------------------------------------------------------------ f32 GEMM
+ * contraction/gemm.py:15-38: gemm_f32, c = matmul(a, b, acc_dtype=f32); linear_f32,
+ * output = matmul(x, weight, transpose_rhs=True, acc_dtype=f32) with weight [N,K]
+ * (transpose_b = 1). f32 products and sums over k in increasing order, no fused multiply-add. */
+int oracle_gemm_f32(const float *a, const float *b, float *c, int64_t m, int64_t n, int64_t k, int64_t lda,
+                    int64_t ldb, int64_t ldc, int transpose_b, int workers) {
+  if (m <= 0 || n <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int size = team_size(workers, m);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(m, omp_get_thread_num(), size, &begin, &end);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)n);
+    float *brow = (float *)malloc(sizeof(float) * (size_t)n);
+    for (int64_t i = begin; i < end; ++i) {
+      if (transpose_b) {
+        /* weight rows are k-contiguous: one dot product per output, k ascending */
+        for (int64_t j = 0; j < n; ++j) {
+          const float *w = b + j * ldb;
+          float dot = 0.0f;
+          for (int64_t kk = 0; kk < k; ++kk) dot = dot + a[i * lda + kk] * w[kk];
+          c[i * ldc + j] = dot;
+        }
+        continue;
+      }
+      for (int64_t j = 0; j < n; ++j) acc[j] = 0.0f;
+      for (int64_t kk = 0; kk < k; ++kk) {
+        const float av = a[i * lda + kk];
+        const float *src = b + kk * ldb;
+        for (int64_t j = 0; j < n; ++j) acc[j] = acc[j] + av * src[j];
+      }
+      for (int64_t j = 0; j < n; ++j) c[i * ldc + j] = acc[j];
     }
     free(acc);
     free(brow);
@@ -249,18 +306,23 @@ int oracle_gemm_bf16(const uint16_t *a, const uint16_t *b, uint16_t *c, int64_t 
 }
 
 /* ------------------------------------------------------------------ attention forward
- * streaming/attention.py:428-466 (flash_attention_fwd) as a region fold over key chunks of
- * `chunk` keys: summarize_attention_chunk_f16 (:152-191), merge_attention_summaries (:82-114),
- * normalize_attention_summary (:417-425); scores in the exp2 domain; exp2/fdiv are the
- * approximate flush-to-zero operations (accurate values, subnormals flushed). */
+ * streaming/attention.py:428-553 as a region fold over key chunks of `chunk` keys:
+ * summarize_attention_chunk_f16 (:152-191) / summarize_attention_chunk_bf16 (:193-237, with
+ * active = True), merge_attention_summaries (:82-114), normalize_attention_summary (:417-425);
+ * scores in the exp2 domain; exp2/fdiv are the approximate flush-to-zero operations (accurate
+ * values, subnormals flushed). dtype 1 = f16 (flash_attention_fwd :428-466,
+ * flash_gqa_attention_fwd :469-507), 2 = bf16 (flash_attention_bf16_fwd :510-553): the element
+ * type of q, k, v, o and of the weights P before P @ V. Query head h reads key/value head
+ * h / head_group (key_head = query_head // HEAD_GROUP). */
 static inline float ftz(float v) { return fabsf(v) < 1.17549435e-38f ? copysignf(0.0f, v) : v; }
 static inline float exp2_approx_ftz(float v) { return ftz(exp2f(ftz(v))); }
 static inline float rcp_approx_ftz(float v) { return ftz(1.0f / ftz(v)); }
 
-int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o, int64_t batch,
-                             int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
-                             float scale, int causal, int64_t chunk, int workers) {
+int oracle_attention_fwd(int dtype, const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o,
+                         int64_t batch, int64_t heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                         int64_t dv, const int64_t *strides, float scale, int causal, int64_t chunk, int workers) {
   if (batch <= 0 || heads <= 0 || sq <= 0) return 0;
+  if ((dtype != 1 && dtype != 2) || head_group < 1 || heads % head_group) return 1;
   if (chunk <= 0) chunk = 64;
   const uint32_t csr = enter_ieee();
   const float log2e = 1.4426950408889634f;
@@ -279,7 +341,8 @@ int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_
     for (int64_t item = begin; item < end; ++item) {
       const int64_t bi = item / (heads * sq), hi = (item / sq) % heads, qi = item % sq;
       const uint16_t *qp = q + bi * strides[0] + hi * strides[1] + qi * strides[2];
-      for (int64_t t = 0; t < d; ++t) qrow[t] = oracle_half_to_float(qp[t * strides[3]]);
+      const int64_t kh = hi / head_group;
+      for (int64_t t = 0; t < d; ++t) qrow[t] = load_elem(qp, dtype, t * strides[3]);
       int valid = 0;
       float maximum = 0.0f, denominator = 0.0f;
       for (int64_t t = 0; t < dv; ++t) acc[t] = 0.0f;
@@ -289,9 +352,9 @@ int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_
         int cvalid = 0;
         float cmax = -INFINITY;
         for (int64_t j = k0; j < k1; ++j) {
-          const uint16_t *kp = k + bi * strides[4] + hi * strides[5] + j * strides[6];
+          const uint16_t *kp = k + bi * strides[4] + kh * strides[5] + j * strides[6];
           float dot = 0.0f;
-          for (int64_t t = 0; t < d; ++t) dot = dot + qrow[t] * oracle_half_to_float(kp[t * strides[7]]);
+          for (int64_t t = 0; t < d; ++t) dot = dot + qrow[t] * load_elem(kp, dtype, t * strides[7]);
           const int ok = !causal || qi >= j;
           scores[j - k0] = ok ? dot * factor : -INFINITY;
           if (ok) {
@@ -306,9 +369,10 @@ int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_
           const int ok = !causal || qi >= j;
           const float weight = ok ? exp2_approx_ftz(scores[j - k0] - cmax) : 0.0f;
           cden += weight;
-          const float w16 = oracle_half_to_float(oracle_float_to_half(weight));
-          const uint16_t *vp = v + bi * strides[8] + hi * strides[9] + j * strides[10];
-          for (int64_t t = 0; t < dv; ++t) cacc[t] = cacc[t] + w16 * oracle_half_to_float(vp[t * strides[11]]);
+          const float w16 = dtype == 2 ? oracle_bf16_to_float(oracle_float_to_bf16(weight))
+                                       : oracle_half_to_float(oracle_float_to_half(weight));
+          const uint16_t *vp = v + bi * strides[8] + kh * strides[9] + j * strides[10];
+          for (int64_t t = 0; t < dv; ++t) cacc[t] = cacc[t] + w16 * load_elem(vp, dtype, t * strides[11]);
         }
         if (!cvalid)
           for (int64_t t = 0; t < dv; ++t) cacc[t] = 0.0f;
@@ -324,7 +388,7 @@ int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_
       }
       uint16_t *op = o + bi * strides[12] + hi * strides[13] + qi * strides[14];
       const float reciprocal = rcp_approx_ftz(valid ? denominator : 1.0f);
-      for (int64_t t = 0; t < dv; ++t) op[t * strides[15]] = oracle_float_to_half(valid ? acc[t] * reciprocal : 0.0f);
+      for (int64_t t = 0; t < dv; ++t) store_elem(op, dtype, t * strides[15], valid ? acc[t] * reciprocal : 0.0f);
     }
     free(scores);
     free(qrow);
@@ -334,6 +398,12 @@ int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_
   }
   leave_ieee(csr);
   return 0;
+}
+
+int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o, int64_t batch,
+                             int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
+                             float scale, int causal, int64_t chunk, int workers) {
+  return oracle_attention_fwd(1, q, k, v, o, batch, heads, 1, sq, sk, d, dv, strides, scale, causal, chunk, workers);
 }
 
 /* ------------------------------------------------------------------ CSR SpMV

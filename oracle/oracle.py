@@ -33,6 +33,10 @@ def lib():
         handle.oracle_softmax_fwd.argtypes = [i, p, p, i64, i64, i64, i64, i]
         handle.oracle_softmax_bwd.argtypes = [i, p, p, p, i64, i64, i64, i64, i64, i]
         handle.oracle_gemm_bf16.argtypes = [p, p, p, i64, i64, i64, i64, i64, i64, i]
+        handle.oracle_gemm16.argtypes = [i, i, p, p, p, i64, i64, i64, i64, i64, i64, i]
+        handle.oracle_gemm_f32.argtypes = [p, p, p, i64, i64, i64, i64, i64, i64, i, i]
+        handle.oracle_attention_fwd.argtypes = [i, p, p, p, p, i64, i64, i64, i64, i64, i64, i64,
+                                                ctypes.POINTER(i64), f, i, i64, i]
         handle.oracle_attention_fwd_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                     ctypes.POINTER(i64), f, i, i64, i]
         handle.oracle_csr_spmv_f32.argtypes = [p, p, p, p, p, i64, i]
@@ -127,6 +131,58 @@ def gemm_bf16(a_bits: np.ndarray, b_bits: np.ndarray, *, workers: int | None = N
     lib().oracle_gemm_bf16(_ptr(a_bits), _ptr(b_bits), _ptr(c), m, n, k, _rows(a_bits), _rows(b_bits), n,
                            workers or default_workers())
     return c
+
+
+def gemm16(a: np.ndarray, b: np.ndarray, *, storage: str | None = None, relu: bool = False,
+           workers: int | None = None) -> np.ndarray:
+    """`gemm` (f16 operands, ACTIVATION NONE/RELU) or, with storage="bf16", the bf16 variant
+    (operands given as uint16 bit patterns). a [m,k], b [k,n]; returns c [m,n] in the operand
+    storage."""
+    _check_2d(a, b)
+    code = BF16 if storage == "bf16" else F16
+    if code == F16 and (a.dtype != np.float16 or b.dtype != np.float16):
+        raise TypeError("gemm16 f16 operands must be float16 arrays")
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), a.dtype)
+    status = lib().oracle_gemm16(code, int(relu), _ptr(a), _ptr(b), _ptr(c), m, n, k, _rows(a), _rows(b), n,
+                                 workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_gemm16 rejected the call ({status})")
+    return c
+
+
+def gemm_f32(a: np.ndarray, b: np.ndarray, *, transpose_b: bool = False, workers: int | None = None) -> np.ndarray:
+    """gemm_f32 (b [k,n]) or linear_f32 (transpose_b: b is the weight [n,k]); float32 arrays."""
+    _check_2d(a, b)
+    if a.dtype != np.float32 or b.dtype != np.float32:
+        raise TypeError("gemm_f32 operands must be float32 arrays")
+    m, k = a.shape
+    n = b.shape[0] if transpose_b else b.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib().oracle_gemm_f32(_ptr(a), _ptr(b), _ptr(c), m, n, k, _rows(a), _rows(b), n, int(transpose_b),
+                          workers or default_workers())
+    return c
+
+
+def attention_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool, *,
+                  head_group: int = 1, storage: str | None = None, chunk: int = 64,
+                  workers: int | None = None) -> np.ndarray:
+    """Grouped-head attention: q [B,HQ,Q,D], k [B,HK,K,D], v [B,HK,K,DV] with HQ = HK * head_group;
+    float16 arrays, or uint16 bf16 bit patterns with storage="bf16". Returns o [B,HQ,Q,DV]."""
+    batch, heads, sq, d = q.shape
+    sk, dv = k.shape[2], v.shape[3]
+    if k.shape[1] * head_group != heads or v.shape[1] != k.shape[1]:
+        raise ValueError("query heads must equal key heads * head_group")
+    code = BF16 if storage == "bf16" else F16
+    o = np.empty((batch, heads, sq, dv), q.dtype)
+    strides = (ctypes.c_int64 * 16)(*(s // 2 for t in (q, k, v, o) for s in t.strides))
+    status = lib().oracle_attention_fwd(code, _ptr(q), _ptr(k), _ptr(v), _ptr(o), batch, heads, head_group, sq, sk,
+                                        d, dv, strides, float(np.float32(scale)), int(causal), chunk,
+                                        workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_attention_fwd rejected the call ({status})")
+    return o
 
 
 def attention_fwd_f16(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool, *,

@@ -109,6 +109,51 @@ def attention_cases():
             "attn_rect_full_o": attention64(q2, k2, v2, scale, False).astype(np.float32)}
 
 
+def gemm_family_cases():
+    """`gemm` (f16, ACTIVATION), gemm_f32 and linear_f32 (contraction/gemm.py:15-73)."""
+    rng = np.random.default_rng(606)
+    a16 = inputs.normal(rng, (40, 72), "f16")
+    b16 = inputs.normal(rng, (72, 24), "f16")
+    c64 = a16.astype(np.float64) @ b16.astype(np.float64)
+    ai = rng.integers(-8, 9, (24, 40)).astype(np.float16)     # exact: integer sums < 2^11
+    bi = rng.integers(-8, 9, (40, 16)).astype(np.float16)
+    ci = ai.astype(np.float64) @ bi.astype(np.float64)
+    a32 = inputs.normal(rng, (33, 70), "f32")
+    b32 = inputs.normal(rng, (70, 45), "f32")
+    prod = np.abs(a32.astype(np.float64)) @ np.abs(b32.astype(np.float64))
+    return {"gemm16_a": a16, "gemm16_b": b16, "gemm16_c64": c64,
+            "gemm16_relu64": np.where(np.isnan(c64), c64, np.where(c64 > 0, c64, 0.0)),
+            "gemm16_int_a": ai, "gemm16_int_b": bi, "gemm16_int_c": ci.astype(np.float16),
+            "gemm32_a": a32, "gemm32_b": b32, "gemm32_c64": a32.astype(np.float64) @ b32.astype(np.float64),
+            "gemm32_abs64": prod}
+
+
+def attention_grouped64(q, k, v, scale, causal, group):
+    """Grouped heads: query head h attends with key/value head h // group."""
+    heads = np.arange(q.shape[1]) // group
+    return attention64(q, k[:, heads], v[:, heads], scale, causal)
+
+
+def attention_family_cases():
+    """flash_gqa_attention_fwd (f16) and flash_attention_bf16_fwd (attention.py:469-553)."""
+    rng = np.random.default_rng(707)
+    q = inputs.normal(rng, (1, 4, 70, 128), "f16")
+    k = inputs.normal(rng, (1, 2, 90, 128), "f16")
+    v = inputs.normal(rng, (1, 2, 90, 128), "f16")
+    qb = inputs.normal(rng, (2, 2, 66, 128), "bf16")
+    kb = inputs.normal(rng, (2, 1, 66, 128), "bf16")
+    vb = inputs.normal(rng, (2, 1, 66, 128), "bf16")
+    scale = float(np.float32(1 / np.sqrt(128)))
+    out = {"gqa_q": q, "gqa_k": k, "gqa_v": v, "gqa_scale": np.float32(scale), "gqa_group": np.int64(2),
+           "bf16_q": qb, "bf16_k": kb, "bf16_v": vb, "bf16_group": np.int64(2)}
+    for causal in (True, False):
+        tag = "causal" if causal else "full"
+        out[f"gqa_{tag}_o"] = attention_grouped64(q, k, v, scale, causal, 2).astype(np.float32)
+        out[f"bf16_{tag}_o"] = attention_grouped64(bf16_to_f64(qb), bf16_to_f64(kb), bf16_to_f64(vb), scale,
+                                                   causal, 2).astype(np.float32)
+    return out
+
+
 def spmv_cases():
     rng = np.random.default_rng(505)
     rows = 700
@@ -142,6 +187,8 @@ def main():
     np.savez_compressed(OUT / "gemm.npz", **gemm_cases())
     np.savez_compressed(OUT / "attention.npz", **attention_cases())
     np.savez_compressed(OUT / "spmv.npz", **spmv_cases())
+    np.savez_compressed(OUT / "gemm_family.npz", **gemm_family_cases())
+    np.savez_compressed(OUT / "attention_family.npz", **attention_family_cases())
     for path in sorted(OUT.glob("*.npz")):
         print(path.name, path.stat().st_size)
 

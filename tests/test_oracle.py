@@ -232,3 +232,95 @@ def test_softmax_reduction_keeps_small_terms():
     y = oracle.softmax_fwd(x)
     want = torch.softmax(torch.from_numpy(x).double(), dim=1).numpy()
     assert rel_err(y, want) < 5e-6
+
+
+# ------------------------------------------------------------------------------ GEMM family
+def test_gemm16_golden_relu_and_exact(golden):
+    g = golden("gemm_family")
+    a, b, want = g["gemm16_a"], g["gemm16_b"], g["gemm16_c64"]
+    c = oracle.gemm16(a, b).astype(np.float64)
+    assert np.all(np.abs(c - want) <= 2 ** -10 * np.abs(want) + 1e-3)     # f16 output rounding
+    r = oracle.gemm16(a, b, relu=True).astype(np.float64)
+    assert np.all(np.abs(r - g["gemm16_relu64"]) <= 2 ** -10 * np.abs(g["gemm16_relu64"]) + 1e-3)
+    assert (r[want < -1e-3] == 0).all() and not np.signbit(r).any()       # relu gives +0, never -0
+    np.testing.assert_array_equal(r, np.maximum(c, 0.0))                   # relu after the same sums
+    exact = oracle.gemm16(g["gemm16_int_a"], g["gemm16_int_b"])
+    assert (exact.view(np.uint16) == g["gemm16_int_c"].view(np.uint16)).all()
+
+
+def test_gemm16_nan_and_signed_zero():
+    a = np.array([[np.nan, 1.0], [-1.0, 0.0], [0.0, 0.0]], np.float16)
+    b = np.array([[1.0, 2.0], [3.0, 4.0]], np.float16)
+    plain = oracle.gemm16(a, b)
+    relu = oracle.gemm16(a, b, relu=True)
+    assert np.isnan(relu[0]).all() and np.isnan(plain[0]).all()           # maximum propagates NaN
+    assert (relu[1] == 0).all() and not np.signbit(relu[1]).any()         # negative sums -> +0
+    assert (plain[1] == np.array([-1.0, -2.0], np.float16)).all()
+    assert not np.signbit(relu[2]).any()
+
+
+def test_gemm16_bf16_matches_gemm_bf16():
+    rng = np.random.default_rng(12)
+    a = inputs.uniform(rng, (20, 36), -1, 1, "bf16")
+    b = inputs.uniform(rng, (36, 28), -1, 1, "bf16")
+    assert (oracle.gemm16(a, b, storage="bf16") == oracle.gemm_bf16(a, b)).all()
+
+
+def test_gemm_f32_golden_linear_and_exact(golden):
+    g = golden("gemm_family")
+    a, b, want, bound = g["gemm32_a"], g["gemm32_b"], g["gemm32_c64"], g["gemm32_abs64"]
+    c = oracle.gemm_f32(a, b)
+    assert np.all(np.abs(c - want) <= 1e-5 * bound)                        # backward-error bound
+    lin = oracle.gemm_f32(a, np.ascontiguousarray(b.T), transpose_b=True)
+    assert (lin == c).all()                                                # same sums, transposed layout
+    rng = np.random.default_rng(13)
+    ai = rng.integers(-8, 9, (17, 50)).astype(np.float32)
+    bi = rng.integers(-8, 9, (50, 9)).astype(np.float32)
+    assert (oracle.gemm_f32(ai, bi) == (ai.astype(np.float64) @ bi).astype(np.float32)).all()
+    eye = np.eye(50, dtype=np.float32)
+    assert (oracle.gemm_f32(ai, eye) == ai).all()
+    perm = rng.permutation(9)
+    assert (oracle.gemm_f32(ai, np.ascontiguousarray(bi[:, perm])) == oracle.gemm_f32(ai, bi)[:, perm]).all()
+
+
+# ------------------------------------------------------------------------------ attention family
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_grouped_golden(golden, causal):
+    g = golden("attention_family")
+    tag = "causal" if causal else "full"
+    scale = float(g["gqa_scale"])
+    o = oracle.attention_fwd(g["gqa_q"], g["gqa_k"], g["gqa_v"], scale, causal, head_group=int(g["gqa_group"]))
+    want = g[f"gqa_{tag}_o"].astype(np.float64)
+    assert np.all(np.abs(o.astype(np.float64) - want) <= 2e-2 * np.abs(want) + 1e-2)
+    ob = oracle.attention_fwd(g["bf16_q"], g["bf16_k"], g["bf16_v"], scale, causal,
+                              head_group=int(g["bf16_group"]), storage="bf16")
+    got = oracle.bf16_bits_to_float(ob).astype(np.float64)
+    want = g[f"bf16_{tag}_o"].astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4e-2 * np.abs(want) + 2e-2)       # bf16 P and output rounding
+
+
+def test_attention_grouped_equals_repeated_heads():
+    g = np.random.default_rng(14)
+    q = inputs.normal(g, (2, 6, 33, 128), "f16")
+    k = inputs.normal(g, (2, 2, 41, 128), "f16")
+    v = inputs.normal(g, (2, 2, 41, 128), "f16")
+    scale = float(np.float32(1 / np.sqrt(128)))
+    grouped = oracle.attention_fwd(q, k, v, scale, True, head_group=3)
+    heads = np.arange(6) // 3
+    repeated = oracle.attention_fwd(q, np.ascontiguousarray(k[:, heads]), np.ascontiguousarray(v[:, heads]), scale,
+                                    True)
+    assert (grouped.view(np.uint16) == repeated.view(np.uint16)).all()
+    assert (repeated.view(np.uint16) == oracle.attention_fwd_f16(
+        q, np.ascontiguousarray(k[:, heads]), np.ascontiguousarray(v[:, heads]), scale, True).view(np.uint16)).all()
+    wrong = oracle.attention_fwd(q, np.ascontiguousarray(k[:, ::-1]), np.ascontiguousarray(v[:, ::-1]), scale, True,
+                                 head_group=3)
+    assert (wrong.view(np.uint16) != grouped.view(np.uint16)).any()         # the head mapping matters
+
+
+def test_attention_bf16_first_causal_row():
+    g = np.random.default_rng(15)
+    q, k, v = (inputs.normal(g, (1, 2, 20, 128), "bf16") for _ in range(3))
+    o = oracle.attention_fwd(q, k, v, float(np.float32(1 / np.sqrt(128))), True, storage="bf16")
+    assert (o[:, :, 0, :] == v[:, :, 0, :]).all()                            # one valid key: p = 1, den = 1
+    with pytest.raises(ValueError):
+        oracle.attention_fwd(q, k[:, :1], v[:, :1], 1.0, True, head_group=3, storage="bf16")

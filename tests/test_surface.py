@@ -12,10 +12,11 @@ import torch
 import intent_amd as intent
 import intent_amd.language as I
 from intent_amd.examples.kernels.backward.softmax import softmax_backward, softmax_backward_f16
-from intent_amd.examples.kernels.contraction.gemm import bf16_gemm
+from intent_amd.examples.kernels.contraction.gemm import Activation, bf16_gemm, gemm, gemm_f32, linear_f32
 from intent_amd.examples.kernels.normalization.softmax import stable_softmax, stable_softmax_f16
 from intent_amd.examples.kernels.sparse.csr_spmv import csr_spmv
-from intent_amd.examples.kernels.streaming.attention import flash_attention_fwd
+from intent_amd.examples.kernels.streaming.attention import (flash_attention_bf16_fwd, flash_attention_fwd,
+                                                             flash_gqa_attention_fwd)
 from intent_amd.runtime.hip.operators import recognize
 from intent_amd.runtime.interface import PublicInterface, StrideSymbol
 from intent_amd.runtime.invocation import bind_arguments
@@ -101,7 +102,10 @@ def test_stride_symbols_bind_consistently():
 def test_recognition_by_name_and_signature():
     for defn, constexprs in ((stable_softmax, {}), (stable_softmax_f16, {}), (softmax_backward, {}),
                              (softmax_backward_f16, {}), (bf16_gemm, {}), (csr_spmv, {}),
-                             (flash_attention_fwd, {"CAUSAL": True})):
+                             (flash_attention_fwd, {"CAUSAL": True}), (gemm_f32, {}), (linear_f32, {}),
+                             (gemm, {"ACTIVATION": Activation.RELU}),
+                             (flash_gqa_attention_fwd, {"HEAD_GROUP": 4, "CAUSAL": True}),
+                             (flash_attention_bf16_fwd, {"HEAD_GROUP": 1, "CAUSAL": False})):
         iface = PublicInterface.from_definition(defn, constexprs)
         assert recognize(defn, iface, tuple(constexprs)).name == defn.__name__
 
@@ -148,3 +152,33 @@ def test_definitions_keep_reference_signatures():
     assert list(bf16_gemm.signature.parameters) == ["a", "b", "c"]
     assert list(flash_attention_fwd.signature.parameters) == ["q", "k", "v", "output", "scale", "CAUSAL"]
     assert list(csr_spmv.signature.parameters) == ["row_offsets", "column_indices", "values", "vector", "output"]
+    assert list(gemm.signature.parameters) == ["a", "b", "c", "ACTIVATION"]
+    assert list(gemm_f32.signature.parameters) == ["a", "b", "c"]
+    assert list(linear_f32.signature.parameters) == ["x", "weight", "output"]
+    for defn in (flash_gqa_attention_fwd, flash_attention_bf16_fwd):
+        assert list(defn.signature.parameters) == ["q", "k", "v", "output", "scale", "HEAD_GROUP", "CAUSAL"]
+    assert (Activation.NONE.value, Activation.RELU.value) == (0, 1)
+
+
+def test_sibling_plan_errors_before_launch():
+    """Constexpr and head-group checks of the plans fire before the library is touched."""
+    from types import SimpleNamespace
+
+    from intent_amd.runtime.hip import operators
+
+    with pytest.raises(intent.CompilationStageError) as error:
+        operators._activation_code(7)
+    assert error.value.stage == "provider_configuration"
+    assert operators._activation_code(Activation.RELU) == 1 and operators._activation_code(0) == 0
+    q, k = torch.zeros(1, 6, 4, 128), torch.zeros(1, 4, 4, 128)
+    bound = SimpleNamespace(arguments=(q, k, k, q, 1.0))
+    plan = operators._attention_grouped(operators.F16)
+    with pytest.raises(ValueError):                       # 6 query heads != 4 key heads * 2
+        plan(None, bound, {"HEAD_GROUP": 2, "CAUSAL": True}, CPU)
+    with pytest.raises(intent.CompilationStageError):
+        plan(None, bound, {"HEAD_GROUP": 0, "CAUSAL": True}, CPU)
+    with pytest.raises(intent.CompilationStageError):
+        plan(None, bound, {"HEAD_GROUP": True, "CAUSAL": True}, CPU)
+    iface = PublicInterface.from_definition(flash_gqa_attention_fwd, {"HEAD_GROUP": 2, "CAUSAL": True})
+    with pytest.raises(intent.CompilationStageError):     # constexprs in the wrong order are another contract
+        recognize(flash_gqa_attention_fwd, iface, ("CAUSAL", "HEAD_GROUP"))
