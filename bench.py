@@ -46,7 +46,8 @@ def parse():
     parser.add_argument("--no-operators", action="store_true")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators",
-                        default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16")
+                        default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
+                                "attention_bwd,attention_bwd_large")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -390,9 +391,65 @@ def op_attention_bf16(device, flush, cpu):
     return _op_attention_grouped(device, flush, cpu, True)
 
 
+def _op_attention_bwd(device, flush, cpu, large):
+    """The three-kernel attention backward (programs/attention_backward.py) as one prepared
+    sequence: the reference example's shape (backward/attention.py:7-13: B2, HQ8, HK2, S1024, D64)
+    or a large grouped shape (B4, HQ32, HK8, S4096, D128); causal."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.programs.attention_backward import AttentionBackward
+
+    b, hq, hk, s, d = (4, 32, 8, 4096, 128) if large else (2, 8, 2, 1024, 64)
+    rng = np.random.default_rng(3)
+    q = inputs.normal(rng, (b, hq, s, d), "f16")
+    k = inputs.normal(rng, (b, hk, s, d), "f16")
+    v = inputs.normal(rng, (b, hk, s, d), "f16")
+    o = inputs.normal(rng, (b, hq, s, d), "f16")
+    do = inputs.normal(rng, (b, hq, s, d), "f16")
+    lse = (rng.standard_normal((b, hq, s)) * 0.5 + np.log(s)).astype(np.float32)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    program = AttentionBackward.from_jit(lambda defn, **kw: intent.jit(defn, backend="hip", **kw),
+                                         head_group=hq // hk, causal=True)
+    call = program.prepare(t(q), t(k), t(v), t(o), t(do), t(lse), scale)
+    ms = graph_median_ms(call.launch, flush)
+    flops = 14 * b * hq * s * s * d // 2          # dQ: 3 products, dK/dV: 4 products, causal half
+    out = {"config": f"causal attention backward f16 B{b} HQ{hq} HK{hk} S{s} D{d} (delta + dK/dV + dQ)",
+           "median_ms": round(ms, 4), "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        n = 512
+        qs, ks, vs = (np.ascontiguousarray(a[:1, :1, :n]) for a in (q, k, v))
+        os_, dos = np.ascontiguousarray(o[:1, :1, :n]), np.ascontiguousarray(do[:1, :1, :n])
+        ls = np.ascontiguousarray(lse[:1, :1, :n])
+
+        def run():
+            delta = oracle.attention_bwd_delta(os_, dos)
+            oracle.attention_bwd_dq(qs, ks, vs, dos, ls, delta, scale, True)
+            oracle.attention_bwd_dkdv(qs, ks, vs, dos, ls, delta, scale, True)
+
+        seconds = cpu_median_seconds(run)
+        out["cpu"] = {"tflops": round(14 * n * n * d / 2 / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": f"one head, first {n} queries and keys"}
+    return out
+
+
+def op_attention_bwd(device, flush, cpu):
+    return _op_attention_bwd(device, flush, cpu, False)
+
+
+def op_attention_bwd_large(device, flush, cpu):
+    return _op_attention_bwd(device, flush, cpu, True)
+
+
 OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_attention, "spmv": op_spmv,
              "gemm_f16_relu": op_gemm_f16_relu, "gemm_f32": op_gemm_f32, "linear_f32": op_linear_f32,
-             "gqa": op_gqa, "attention_bf16": op_attention_bf16}
+             "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
+             "attention_bwd_large": op_attention_bwd_large}
 
 
 def read_traffic(name):

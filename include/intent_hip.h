@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 2
+#define INTENT_HIP_ABI_VERSION 3
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -50,7 +50,10 @@ enum IntentHipOperator {
   INTENT_HIP_OP_CSR_SPMV_F32 = 4,
   INTENT_HIP_OP_GEMM = 5,              /* dtype F16 or BF16 */
   INTENT_HIP_OP_GEMM_F32 = 6,
-  INTENT_HIP_OP_ATTENTION_FWD = 7      /* dtype F16 or BF16 */
+  INTENT_HIP_OP_ATTENTION_FWD = 7,     /* dtype F16 or BF16 */
+  INTENT_HIP_OP_ATTENTION_BWD_DELTA = 8, /* cols = head dimension */
+  INTENT_HIP_OP_ATTENTION_BWD_DQ = 9,
+  INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -151,6 +154,34 @@ int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void
                              int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
                              int64_t sk, int64_t d, int64_t dv, const int64_t strides[16],
                              float scale, int causal, void *stream);
+
+/* Attention backward, f16 storage with f32 arithmetic, head dimension d = 64 or 128
+ * (python/intent/examples/kernels/backward/attention.py; the three kernels of
+ * programs/attention_backward.py:1-41). Shapes: q, dout, dq [b,hq,sq,d]; k, v, dk, dv [b,hk,sk,d]
+ * with hq = q_heads = hk * head_group; lse, delta [b,hq,sq] f32; lse is the natural log of the
+ * forward's softmax denominator. Every 4-D operand has unit inner stride.
+ *
+ * delta = sum_d o * dout: attention_backward_delta (:17-34). strides[11]: o[4], dout[4], delta[3]. */
+int intent_hip_attention_bwd_delta(const void *o, const void *dout, float *delta, int64_t batch,
+                                   int64_t heads, int64_t sq, int64_t d, const int64_t strides[11],
+                                   void *stream);
+
+/* dq = f16(scale * sum_k f16(p * (dout.v - delta)) k), p = exp2(q.k * scale * log2e - lse * log2e),
+ * causal validity q >= k: attention_backward_dq (:171-211) with summarize_query_gradients
+ * (:140-163). strides[26]: q, k, v, dout (4 each), lse[3], delta[3], dq[4]. */
+int intent_hip_attention_bwd_dq(const void *q, const void *k, const void *v, const void *dout,
+                                const float *lse, const float *delta, void *dq, int64_t batch,
+                                int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                                const int64_t strides[26], float scale, int causal, void *stream);
+
+/* dk = f16(scale * sum_q f16(ds) q), dv = f16(sum_q f16(p) dout), summed over the head_group query
+ * heads of each key head: attention_backward_dkdv (:87-137) with summarize_key_value_gradients
+ * (:47-79). strides[30]: q, k, v, dout (4 each), lse[3], delta[3], dk[4], dv[4]. */
+int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
+                                  const float *lse, const float *delta, void *dk, void *dv,
+                                  int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
+                                  int64_t sk, int64_t d, const int64_t strides[30], float scale,
+                                  int causal, void *stream);
 
 /* CSR SpMV y = A x, f32 values, i32 indices.
  * csr_spmv (python/intent/examples/kernels/sparse/csr_spmv.py:11-29), with dynamic extents.

@@ -1,0 +1,563 @@
+// Attention backward (f16 storage, f32 arithmetic) for gfx950: delta, dQ and dK/dV.
+//
+// Semantics (python/intent/examples/kernels/backward/attention.py):
+//   attention_backward_delta (:17-34): delta[b,h,q] = sum_d o * do (f32);
+//   attention_backward_dq (:171-211) with summarize_query_gradients (:140-163);
+//   attention_backward_dkdv (:87-137) with summarize_key_value_gradients (:47-79):
+//     s = q . k (f32); p = exp2(s * scale * log2 e - lse * log2 e) (v_exp_f32, approximate);
+//     causal validity q >= k; excluded pairs have p = 0 and dS = 0;
+//     dp = do . v; dS = p * (dp - delta);
+//     dV = sum_q f16(p) do; dK = scale * sum_q f16(dS) q; dQ = scale * sum_k f16(dS) k.
+//   Query head h uses key/value head h / head_group; dK/dV of a key head sum over the
+//   head_group query heads that share it. The summed axes are reassociated (region folds
+//   combined by addition).
+//
+// Design (head dimension D = 64 or 128, v_mfma_f32_32x32x16_f16 throughout):
+//   * dQ: a workgroup owns 128 queries of one (batch, query head), 4 waves x 32; 64-key tiles of
+//     K and V stream through double-buffered LDS (global_load_lds_dwordx4). Per 32-key half:
+//     S^T = K Q^T and dP^T = V dO^T with the wave's Q and dO fragments in registers (lane l
+//     holds the scores of query l % 32), dS^T rounded to f16 in registers, then
+//     dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16 from K's natural [key][d] layout.
+//   * dK/dV: a workgroup owns 128 keys of one (batch, key head), 4 waves x 32; 64-query tiles of
+//     Q and dO (of every query head in the group) stream through LDS, with their lse and delta.
+//     Per 32-query half: S = Q K^T and dP = dO V^T with the wave's K and V fragments in
+//     registers (lane l holds key l % 32), P and dS rounded to f16 in registers, then
+//     dV^T += dO^T P and dK^T += Q^T dS with transposing LDS reads of Q and dO.
+//   * Rows past the end of a tensor read its last row (finite data that the mask excludes).
+//     Causal work is skipped per wave where no pair of a tile is valid.
+#include "common.hpp"
+
+namespace intent_hip {
+namespace {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kThreads = 256;
+constexpr int kRows = 128;     // queries (dQ) or keys (dK/dV) per workgroup
+constexpr int kTile = 64;      // keys (dQ) or queries (dK/dV) per streamed tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+#define INTENT_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
+
+__device__ __forceinline__ f32x16_t mma(f16x8_t a, f16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint4 select(bool keep, uint4 v) {
+  return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+}
+
+// Element strides of the backward operands (batch, head, row, col for 4-D; batch, head, row for
+// lse and delta).
+struct BwdGeometry {
+  int64_t q[4], k[4], v[4], dout[4], lse[3], delta[3], out0[4], out1[4];
+};
+
+// LDS tile of kTile rows of D f16 (rows of D / 8 16-byte chunks). Chunk c of row r is stored at
+// c ^ swz(r); both row reads and transposing reads go through this map, so any swizzle is
+// correct; this one spreads the transposing reads of 4 consecutive rows over distinct chunks.
+template <int D>
+__device__ __forceinline__ int swz(int row) {
+  return (D == 128 ? 4 : 2) * (row & 3);
+}
+
+// Row fragment of an MFMA A operand: rows `row` (lane & 31 within a 32-row block), 8
+// consecutive columns starting at 16 ks + 8 half.
+template <int D>
+__device__ __forceinline__ f16x8_t row_frag(const uint4 *tile, int row, int ks, int half) {
+  return __builtin_bit_cast(f16x8_t, tile[row * (D / 8) + ((ks * 2 + half) ^ swz<D>(row))]);
+}
+
+// Transposed fragment (A operand rows = columns of the tile): this lane receives rows
+// 16 sl + 8 r + 4 half + 0..3 of column 32 mt + (its column), for r = 0, 1.
+template <int D>
+__device__ __forceinline__ f16x8_t tr_frag(const uint16_t *tile, int sl, int mt, int t_row, int t_col) {
+  i16x4_t parts[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = sl * 16 + 8 * r + t_row;
+    const int col = mt * 32 + t_col;
+    const int chunk = (col >> 3) ^ swz<D>(row);
+    parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(tile + row * D + chunk * 8 + (col & 7)));
+  }
+  return __builtin_bit_cast(f16x8_t, parts);
+}
+
+// ---------------------------------------------------------------- delta
+// D / 8 lanes per row, 8 elements (one 16-byte load of o and of do) per lane.
+template <int D>
+__global__ __launch_bounds__(kThreads) void attention_bwd_delta(const uint16_t *__restrict__ O,
+                                                                const uint16_t *__restrict__ G,
+                                                                float *__restrict__ delta, int heads, int sq,
+                                                                int64_t rows, BwdGeometry g) {
+  constexpr int kLanes = D / 8;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t row = t / kLanes;
+  const int part = static_cast<int>(t % kLanes);
+  const bool live = row < rows;
+  const int64_t r = live ? row : 0;
+  const int64_t b = r / (static_cast<int64_t>(heads) * sq), h = (r / sq) % heads, q = r % sq;
+  const uint4 ov = *reinterpret_cast<const uint4 *>(O + b * g.q[0] + h * g.q[1] + q * g.q[2] + part * 8);
+  const uint4 gv = *reinterpret_cast<const uint4 *>(G + b * g.dout[0] + h * g.dout[1] + q * g.dout[2] + part * 8);
+  const f16x8_t of = __builtin_bit_cast(f16x8_t, ov), gf = __builtin_bit_cast(f16x8_t, gv);
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sum = fmaf(static_cast<float>(of[i]), static_cast<float>(gf[i]), sum);
+#pragma unroll
+  for (int off = kLanes / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (live && part == 0) delta[b * g.delta[0] + h * g.delta[1] + q * g.delta[2]] = sum;
+}
+
+// ---------------------------------------------------------------- dQ
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
+    const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
+    uint16_t *__restrict__ DQ, int heads, int head_group, int sq, int sk, BwdGeometry g, float scale, int causal,
+    int q_blocks) {
+  constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one K (or V) tile
+  constexpr int kDma = kChunks / kThreads;         // per thread per operand
+  __shared__ uint4 lds[2 * 2 * kChunks];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh_count = gridDim.x / q_blocks;
+  const int qb = q_blocks - 1 - static_cast<int>(blockIdx.x) / bh_count;   // heaviest blocks first
+  const int bh = static_cast<int>(blockIdx.x) % bh_count;
+  const int b = bh / heads, h = bh % heads, kh = h / head_group;
+  const uint16_t *kbase = K + b * g.k[0] + kh * g.k[1];
+  const uint16_t *vbase = V + b * g.v[0] + kh * g.v[1];
+
+  const int wq0 = qb * kRows + wave * 32;
+  const int lane_q = wq0 + (lane & 31);
+  const int half = lane >> 5;
+  const bool q_ok = lane_q < sq;
+  const int qr = q_ok ? lane_q : 0;
+
+  f16x8_t qf[D / 16], of[D / 16];
+  {
+    const uint16_t *qrow = Q + b * g.q[0] + h * g.q[1] + static_cast<int64_t>(qr) * g.q[2];
+    const uint16_t *grow = G + b * g.dout[0] + h * g.dout[1] + static_cast<int64_t>(qr) * g.dout[2];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      qf[ks] = __builtin_bit_cast(f16x8_t, select(q_ok, *reinterpret_cast<const uint4 *>(qrow + ks * 16 + half * 8)));
+      of[ks] = __builtin_bit_cast(f16x8_t, select(q_ok, *reinterpret_cast<const uint4 *>(grow + ks * 16 + half * 8)));
+    }
+  }
+  const float lse2 = q_ok ? LSE[b * g.lse[0] + h * g.lse[1] + static_cast<int64_t>(qr) * g.lse[2]] * kLog2e : 0.0f;
+  const float dlt = q_ok ? DELTA[b * g.delta[0] + h * g.delta[1] + static_cast<int64_t>(qr) * g.delta[2]] : 0.0f;
+  INTENT_WAIT_VMCNT0();
+
+  const int q_last_block = min(qb * kRows + kRows, sq) - 1;
+  const int k_end = causal ? min(sk, q_last_block + 1) : sk;
+  const int tiles = (k_end + kTile - 1) / kTile;
+  const int wave_q_last = min(wq0 + 31, sq - 1);
+
+  auto issue = [&](int kt) {
+    uint4 *stage = lds + (kt & 1) * 2 * kChunks;
+    const int key0 = kt * kTile;
+#pragma unroll
+    for (int i = 0; i < kDma; ++i) {
+      const int p = (wave * kDma + i) * 64 + lane;
+      const int row = p / (D / 8), pc = p % (D / 8);
+      const int key = min(key0 + row, sk - 1);
+      const int src = (pc ^ swz<D>(row)) * 8;
+      __builtin_amdgcn_global_load_lds(kbase + static_cast<int64_t>(key) * g.k[2] + src,
+                                       (lds_void_t *)(stage + (wave * kDma + i) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + static_cast<int64_t>(key) * g.v[2] + src,
+                                       (lds_void_t *)(stage + kChunks + (wave * kDma + i) * 64), 16, 0, 0);
+    }
+  };
+
+  f32x16_t acc[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[mt][e] = 0.0f;
+  const float c1 = scale * kLog2e;
+  const int frag_row = lane & 31;
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int t_row = 4 * (g16 >> 1) + (i16 >> 2);
+  const int t_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+
+  if (tiles > 0) issue(0);
+  for (int kt = 0; kt < tiles; ++kt) {
+    INTENT_WAIT_VMCNT0();
+    __syncthreads();          // tile kt is in LDS; every wave is done with tile kt - 1
+    if (kt + 1 < tiles) issue(kt + 1);
+    const int key0 = kt * kTile;
+    if ((causal && key0 > wave_q_last) || wq0 >= sq) continue;   // wave-uniform
+    const uint4 *ktile = lds + (kt & 1) * 2 * kChunks;
+    const uint4 *vtile = ktile + kChunks;
+    f16x8_t dsf[4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      f32x16_t s, dp;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        s = mma(row_frag<D>(ktile, st * 32 + frag_row, ks, half), qf[ks], s);
+        dp = mma(row_frag<D>(vtile, st * 32 + frag_row, ks, half), of[ks], dp);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+        const bool valid = key < sk && (!causal || key <= lane_q);
+        const float p = valid ? __builtin_amdgcn_exp2f(fmaf(s[e], c1, -lse2)) : 0.0f;
+        dsf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dlt) : 0.0f);
+      }
+    }
+    const uint16_t *kt16 = reinterpret_cast<const uint16_t *>(ktile);
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt) acc[mt] = mma(tr_frag<D>(kt16, sl, mt, t_row, t_col), dsf[sl], acc[mt]);
+  }
+
+  if (!q_ok) return;
+  uint16_t *orow = DQ + b * g.out0[0] + h * g.out0[1] + static_cast<int64_t>(lane_q) * g.out0[2];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq)
+      *reinterpret_cast<uint2 *>(orow + mt * 32 + 8 * gq + 4 * half) =
+          make_uint2(pack_f16x2(acc[mt][4 * gq] * scale, acc[mt][4 * gq + 1] * scale),
+                     pack_f16x2(acc[mt][4 * gq + 2] * scale, acc[mt][4 * gq + 3] * scale));
+}
+
+// ---------------------------------------------------------------- dK / dV
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
+    const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
+    uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, int kv_heads, int head_group, int sq, int sk,
+    BwdGeometry g, float scale, int causal, int k_blocks) {
+  constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one Q (or dO) tile
+  constexpr int kDma = kChunks / kThreads;
+  constexpr int kStage = 2 * kChunks + 2 * (kTile / 4);   // Q, dO, then lse and delta (64 floats each)
+  __shared__ uint4 lds[2 * kStage];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh_count = gridDim.x / k_blocks;
+  const int kb = static_cast<int>(blockIdx.x) / bh_count;   // causal: first key blocks see the most queries
+  const int bh = static_cast<int>(blockIdx.x) % bh_count;
+  const int b = bh / kv_heads, kh = bh % kv_heads;
+
+  const int wk0 = kb * kRows + wave * 32;
+  const int lane_k = wk0 + (lane & 31);
+  const int half = lane >> 5;
+  const bool k_ok = lane_k < sk;
+  const int kr = k_ok ? lane_k : 0;
+
+  f16x8_t kf[D / 16], vf[D / 16];
+  {
+    const uint16_t *krow = K + b * g.k[0] + kh * g.k[1] + static_cast<int64_t>(kr) * g.k[2];
+    const uint16_t *vrow = V + b * g.v[0] + kh * g.v[1] + static_cast<int64_t>(kr) * g.v[2];
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      kf[ks] = __builtin_bit_cast(f16x8_t, select(k_ok, *reinterpret_cast<const uint4 *>(krow + ks * 16 + half * 8)));
+      vf[ks] = __builtin_bit_cast(f16x8_t, select(k_ok, *reinterpret_cast<const uint4 *>(vrow + ks * 16 + half * 8)));
+    }
+    INTENT_WAIT_VMCNT0();
+  }
+
+  // Query tiles: for each of the head_group query heads, the 64-query tiles that can hold a valid
+  // pair for this workgroup's keys (causal: queries >= its first key).
+  const int q_tiles = (sq + kTile - 1) / kTile;
+  const int first = causal ? min(kb * kRows / kTile, q_tiles) : 0;
+  const int per_head = q_tiles - first;
+  const int tiles = head_group * per_head;
+
+  auto tile_head = [&](int t) { return kh * head_group + t / per_head; };
+  auto tile_q0 = [&](int t) { return (first + t % per_head) * kTile; };
+  auto issue = [&](int t) {
+    uint4 *stage = lds + (t & 1) * kStage;
+    const int hq = tile_head(t), q0 = tile_q0(t);
+    const uint16_t *qbase = Q + b * g.q[0] + hq * g.q[1];
+    const uint16_t *gbase = G + b * g.dout[0] + hq * g.dout[1];
+#pragma unroll
+    for (int i = 0; i < kDma; ++i) {
+      const int p = (wave * kDma + i) * 64 + lane;
+      const int row = p / (D / 8), pc = p % (D / 8);
+      const int q = min(q0 + row, sq - 1);
+      const int src = (pc ^ swz<D>(row)) * 8;
+      __builtin_amdgcn_global_load_lds(qbase + static_cast<int64_t>(q) * g.q[2] + src,
+                                       (lds_void_t *)(stage + (wave * kDma + i) * 64), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(gbase + static_cast<int64_t>(q) * g.dout[2] + src,
+                                       (lds_void_t *)(stage + kChunks + (wave * kDma + i) * 64), 16, 0, 0);
+    }
+    if (wave < 2) {   // lse (wave 0) and delta (wave 1): one float of row q0 + lane per lane
+      const int q = min(q0 + lane, sq - 1);
+      const float *src = wave == 0 ? LSE + b * g.lse[0] + hq * g.lse[1] + static_cast<int64_t>(q) * g.lse[2]
+                                   : DELTA + b * g.delta[0] + hq * g.delta[1] + static_cast<int64_t>(q) * g.delta[2];
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(stage + 2 * kChunks + wave * (kTile / 4)), 4, 0, 0);
+    }
+  };
+
+  f32x16_t acc_k[D / 32], acc_v[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_k[mt][e] = acc_v[mt][e] = 0.0f;
+  const float c1 = scale * kLog2e;
+  const int frag_row = lane & 31;
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int t_row = 4 * (g16 >> 1) + (i16 >> 2);
+  const int t_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+
+  if (tiles > 0) issue(0);
+  for (int t = 0; t < tiles; ++t) {
+    INTENT_WAIT_VMCNT0();
+    __syncthreads();
+    if (t + 1 < tiles) issue(t + 1);
+    const int q0 = tile_q0(t);
+    if (wk0 >= sk || (causal && q0 + kTile - 1 < wk0)) continue;   // wave-uniform: no valid pair
+    const uint4 *qtile = lds + (t & 1) * kStage;
+    const uint4 *gtile = qtile + kChunks;
+    const float *lse_s = reinterpret_cast<const float *>(qtile + 2 * kChunks);
+    const float *dlt_s = lse_s + kTile;
+    // lse_s[i] / dlt_s[i] hold row q0 + i (the last row for i past the end, excluded by the mask).
+    f16x8_t pf[4], dsf[4];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      f32x16_t s, dp;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+        s = mma(row_frag<D>(qtile, st * 32 + frag_row, ks, half), kf[ks], s);
+        dp = mma(row_frag<D>(gtile, st * 32 + frag_row, ks, half), vf[ks], dp);
+      }
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int local = st * 32 + 8 * e4 + 4 * half;        // rows local .. local + 3 of the tile
+        const float4 l4 = *reinterpret_cast<const float4 *>(lse_s + local);
+        const float4 d4 = *reinterpret_cast<const float4 *>(dlt_s + local);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e = 4 * e4 + j;
+          const int q = q0 + local + j;
+          const bool valid = q < sq && (!causal || lane_k <= q);
+          const float p = valid ? __builtin_amdgcn_exp2f(fmaf(s[e], c1, -lv[j] * kLog2e)) : 0.0f;
+          pf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(p);
+          dsf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dv[j]) : 0.0f);
+        }
+      }
+    }
+    const uint16_t *q16 = reinterpret_cast<const uint16_t *>(qtile);
+    const uint16_t *g16p = reinterpret_cast<const uint16_t *>(gtile);
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl)
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt) {
+        acc_v[mt] = mma(tr_frag<D>(g16p, sl, mt, t_row, t_col), pf[sl], acc_v[mt]);
+        acc_k[mt] = mma(tr_frag<D>(q16, sl, mt, t_row, t_col), dsf[sl], acc_k[mt]);
+      }
+  }
+
+  if (!k_ok) return;
+  uint16_t *krow = DK + b * g.out0[0] + kh * g.out0[1] + static_cast<int64_t>(lane_k) * g.out0[2];
+  uint16_t *vrow = DV + b * g.out1[0] + kh * g.out1[1] + static_cast<int64_t>(lane_k) * g.out1[2];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int col = mt * 32 + 8 * gq + 4 * half;
+      *reinterpret_cast<uint2 *>(krow + col) =
+          make_uint2(pack_f16x2(acc_k[mt][4 * gq] * scale, acc_k[mt][4 * gq + 1] * scale),
+                     pack_f16x2(acc_k[mt][4 * gq + 2] * scale, acc_k[mt][4 * gq + 3] * scale));
+      *reinterpret_cast<uint2 *>(vrow + col) = make_uint2(pack_f16x2(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1]),
+                                                          pack_f16x2(acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]));
+    }
+}
+
+}  // namespace
+}  // namespace intent_hip
+
+namespace intent_hip {
+
+int attention_bwd_resources(int64_t which, int64_t d, IntentHipKernelResources *out) {
+  const bool d64 = d == 64;
+  switch (which) {
+    case 0:
+      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_delta<64>), "attention_bwd_delta<64>",
+                                   kThreads, out)
+                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_delta<128>),
+                                   "attention_bwd_delta<128>", kThreads, out);
+    case 1:
+      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dq<64>), "attention_bwd_dq<64>",
+                                   kThreads, out)
+                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dq<128>), "attention_bwd_dq<128>",
+                                   kThreads, out);
+    default:
+      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<64>), "attention_bwd_dkdv<64>",
+                                   kThreads, out)
+                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<128>),
+                                   "attention_bwd_dkdv<128>", kThreads, out);
+  }
+}
+
+namespace {
+
+// Shared checks of the 4-D f16 operands: unit inner stride, other strides multiples of 8
+// elements, 16-byte aligned starts (8-byte for outputs written 4 elements at a time).
+int check_operand(const void *p, const int64_t *st, int out, const char *name) {
+  if (st[3] != 1) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "%s needs unit inner stride", name);
+  for (int i = 0; i < 3; ++i)
+    if (st[i] % (out ? 4 : 8))
+      return fail(INTENT_HIP_ERR_UNSUPPORTED, "%s strides must be multiples of %d elements", name, out ? 4 : 8);
+  if (!aligned(p, out ? 8 : 16)) return fail(INTENT_HIP_ERR_UNSUPPORTED, "%s must be %d-byte aligned", name, out ? 8 : 16);
+  return INTENT_HIP_OK;
+}
+
+int check_common(int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d) {
+  if (batch < 0 || q_heads < 0 || sq < 0 || sk < 0 || d < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (head_group < 1 || (q_heads > 0 && q_heads % head_group != 0))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "head_group %lld must be positive and divide the %lld query heads",
+                static_cast<long long>(head_group), static_cast<long long>(q_heads));
+  if (d != 64 && d != 128)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention backward supports head dimension 64 or 128 (got %lld)",
+                static_cast<long long>(d));
+  if (sq > INT32_MAX / 2 || sk > INT32_MAX / 2 || batch * q_heads > INT32_MAX / 64)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention extents too large for one launch");
+  return INTENT_HIP_OK;
+}
+
+void load_geometry(BwdGeometry &g, const int64_t *s, bool two_outputs) {
+  for (int i = 0; i < 4; ++i) {
+    g.q[i] = s[i];
+    g.k[i] = s[4 + i];
+    g.v[i] = s[8 + i];
+    g.dout[i] = s[12 + i];
+    g.out0[i] = s[22 + i];
+    g.out1[i] = two_outputs ? s[26 + i] : 0;
+  }
+  for (int i = 0; i < 3; ++i) {
+    g.lse[i] = s[16 + i];
+    g.delta[i] = s[19 + i];
+  }
+}
+
+}  // namespace
+}  // namespace intent_hip
+
+using namespace intent_hip;
+
+extern "C" int intent_hip_attention_bwd_delta(const void *o, const void *dout, float *delta, int64_t batch,
+                                              int64_t heads, int64_t sq, int64_t d, const int64_t *strides,
+                                              void *stream) {
+  if (const int rc = check_common(batch, heads, 1, sq, 0, d)) return rc;
+  if (batch == 0 || heads == 0 || sq == 0) return INTENT_HIP_OK;
+  if (o == nullptr || dout == nullptr || delta == nullptr || strides == nullptr)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  if (int rc = check_operand(o, strides, 0, "output")) return rc;
+  if (int rc = check_operand(dout, strides + 4, 0, "grad_output")) return rc;
+  BwdGeometry g{};
+  for (int i = 0; i < 4; ++i) {
+    g.q[i] = strides[i];
+    g.dout[i] = strides[4 + i];
+  }
+  for (int i = 0; i < 3; ++i) g.delta[i] = strides[8 + i];
+  const int64_t rows = batch * heads * sq;
+  const int64_t threads = rows * (d / 8);
+  const dim3 grid(static_cast<unsigned>((threads + kThreads - 1) / kThreads));
+  const auto *O = static_cast<const uint16_t *>(o);
+  const auto *G = static_cast<const uint16_t *>(dout);
+  if (d == 64)
+    attention_bwd_delta<64><<<grid, dim3(kThreads), 0, as_stream(stream)>>>(O, G, delta, static_cast<int>(heads),
+                                                                            static_cast<int>(sq), rows, g);
+  else
+    attention_bwd_delta<128><<<grid, dim3(kThreads), 0, as_stream(stream)>>>(O, G, delta, static_cast<int>(heads),
+                                                                             static_cast<int>(sq), rows, g);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_delta");
+  return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_attention_bwd_dq(const void *q, const void *k, const void *v, const void *dout,
+                                           const float *lse, const float *delta, void *dq, int64_t batch,
+                                           int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                                           const int64_t *strides, float scale, int causal, void *stream) {
+  if (const int rc = check_common(batch, q_heads, head_group, sq, sk, d)) return rc;
+  if (batch == 0 || q_heads == 0 || sq == 0) return INTENT_HIP_OK;
+  if (strides == nullptr || q == nullptr || dout == nullptr || lse == nullptr || delta == nullptr || dq == nullptr ||
+      (sk > 0 && (k == nullptr || v == nullptr)))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  if (int rc = check_operand(q, strides, 0, "q")) return rc;
+  if (int rc = check_operand(k, strides + 4, 0, "k")) return rc;
+  if (int rc = check_operand(v, strides + 8, 0, "v")) return rc;
+  if (int rc = check_operand(dout, strides + 12, 0, "grad_output")) return rc;
+  if (int rc = check_operand(dq, strides + 22, 1, "grad_q")) return rc;
+  BwdGeometry g{};
+  load_geometry(g, strides, false);
+  const int q_blocks = static_cast<int>((sq + kRows - 1) / kRows);
+  const int64_t blocks = batch * q_heads * q_blocks;
+  if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
+  const auto *Q = static_cast<const uint16_t *>(q);
+  const auto *K = static_cast<const uint16_t *>(k);
+  const auto *V = static_cast<const uint16_t *>(v);
+  const auto *G = static_cast<const uint16_t *>(dout);
+  auto *DQ = static_cast<uint16_t *>(dq);
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const hipStream_t s = as_stream(stream);
+  const int hq = static_cast<int>(q_heads), grp = static_cast<int>(head_group);
+  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk);
+  if (d == 64)
+    attention_bwd_dq<64><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DQ, hq, grp, iq, ik, g, scale,
+                                                         causal ? 1 : 0, q_blocks);
+  else
+    attention_bwd_dq<128><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DQ, hq, grp, iq, ik, g, scale,
+                                                          causal ? 1 : 0, q_blocks);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dq");
+  return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
+                                             const float *lse, const float *delta, void *dk, void *dv, int64_t batch,
+                                             int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                                             const int64_t *strides, float scale, int causal, void *stream) {
+  if (const int rc = check_common(batch, q_heads, head_group, sq, sk, d)) return rc;
+  if (batch == 0 || q_heads == 0 || sk == 0) return INTENT_HIP_OK;
+  if (strides == nullptr || k == nullptr || v == nullptr || dk == nullptr || dv == nullptr ||
+      (sq > 0 && (q == nullptr || dout == nullptr || lse == nullptr || delta == nullptr)))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  if (int rc = check_operand(q, strides, 0, "q")) return rc;
+  if (int rc = check_operand(k, strides + 4, 0, "k")) return rc;
+  if (int rc = check_operand(v, strides + 8, 0, "v")) return rc;
+  if (int rc = check_operand(dout, strides + 12, 0, "grad_output")) return rc;
+  if (int rc = check_operand(dk, strides + 22, 1, "grad_k")) return rc;
+  if (int rc = check_operand(dv, strides + 26, 1, "grad_v")) return rc;
+  BwdGeometry g{};
+  load_geometry(g, strides, true);
+  const int64_t kv_heads = q_heads / head_group;
+  const int k_blocks = static_cast<int>((sk + kRows - 1) / kRows);
+  const int64_t blocks = batch * kv_heads * k_blocks;
+  if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
+  const auto *Q = static_cast<const uint16_t *>(q);
+  const auto *K = static_cast<const uint16_t *>(k);
+  const auto *V = static_cast<const uint16_t *>(v);
+  const auto *G = static_cast<const uint16_t *>(dout);
+  auto *DK = static_cast<uint16_t *>(dk);
+  auto *DV = static_cast<uint16_t *>(dv);
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const hipStream_t s = as_stream(stream);
+  const int hk = static_cast<int>(kv_heads), grp = static_cast<int>(head_group);
+  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk);
+  if (d == 64)
+    attention_bwd_dkdv<64><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, hk, grp, iq, ik, g, scale,
+                                                           causal ? 1 : 0, k_blocks);
+  else
+    attention_bwd_dkdv<128><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, hk, grp, iq, ik, g, scale,
+                                                            causal ? 1 : 0, k_blocks);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv");
+  return INTENT_HIP_OK;
+}

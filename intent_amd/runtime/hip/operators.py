@@ -18,6 +18,9 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   flash_gqa_attention_fwd streaming/attention.py:469-507   intent_hip_attention_fwd (f16, HEAD_GROUP)
   flash_attention_bf16_fwd streaming/attention.py:510-553  intent_hip_attention_fwd (bf16, HEAD_GROUP)
   csr_spmv                sparse/csr_spmv.py:11-29         intent_hip_csr_spmv_f32
+  attention_backward_delta backward/attention.py:17-34     intent_hip_attention_bwd_delta
+  attention_backward_dkdv backward/attention.py:87-137     intent_hip_attention_bwd_dkdv
+  attention_backward_dq   backward/attention.py:171-211    intent_hip_attention_bwd_dq
 
 (paths relative to python/intent/examples/kernels/ in the reference).
 
@@ -33,8 +36,9 @@ from dataclasses import dataclass, field
 from typing import Callable
 
 from ...diagnostics import CompilationStageError
-from .library import (BF16, F16, F32, OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM,
-                      OP_GEMM_BF16, OP_GEMM_F32, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD)
+from .library import (BF16, F16, F32, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
+                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32,
+                      OP_SOFTMAX_BWD, OP_SOFTMAX_FWD)
 
 
 @dataclass
@@ -247,6 +251,70 @@ def _attention_grouped(dtype_code):
     return plan
 
 
+# ------------------------------------------------------------------------------ attention backward
+def _strides(*tensors):
+    import ctypes
+
+    values = [st for t in tensors for st in t.stride()]
+    return (ctypes.c_int64 * len(values))(*values)
+
+
+def _attention_bwd_delta(lib, bound, constexprs, device):
+    o, dout, delta = bound.arguments
+    keep, before, after = [o, dout, delta], [], []
+    ok, gk = _readable(o, keep, before, 8), _readable(dout, keep, before, 8)
+    batch, heads, sq, d = o.shape
+    strides = _strides(ok, gk, delta)
+    keep.append(strides)
+    fn = lib.fn["attention_bwd_delta"]
+    args = (ok.data_ptr(), gk.data_ptr(), delta.data_ptr(), batch, heads, sq, d, strides)
+    return Launch("intent_hip_attention_bwd_delta", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("d", d)),
+                  lambda: lib.kernel_resources(OP_ATTENTION_BWD_DELTA, F16, sq, d))
+
+
+def _backward_group(q, k, constexprs):
+    group = constexprs["HEAD_GROUP"]
+    if isinstance(group, bool) or not isinstance(group, int) or group < 1:
+        raise CompilationStageError("provider_configuration", f"HEAD_GROUP must be a positive int, got {group!r}")
+    if k.shape[1] * group != q.shape[1]:
+        raise ValueError(f"query heads ({q.shape[1]}) must equal key/value heads ({k.shape[1]}) * HEAD_GROUP "
+                         f"({group})")
+    return group
+
+
+def _attention_bwd(kind):
+    """attention_backward_dq (kind "dq") / attention_backward_dkdv (kind "dkdv"); lse and delta are
+    read through their own strides, 4-D operands with unit inner stride (staged otherwise)."""
+    def plan(lib, bound, constexprs, device):
+        if kind == "dq":
+            q, k, v, dout, lse, delta, out, scale = bound.arguments
+            outs = (out,)
+        else:
+            q, k, v, dout, lse, delta, grad_k, grad_v, scale = bound.arguments
+            outs = (grad_k, grad_v)
+        group = _backward_group(q, k, constexprs)
+        causal = bool(constexprs["CAUSAL"])
+        keep, before, after = [q, k, v, dout, lse, delta, *outs], [], []
+        ins = [_readable(t, keep, before, 8) for t in (q, k, v, dout)]
+        staged_outs = [_writable(t, keep, after, 8) for t in outs]
+        batch, q_heads, sq, d = q.shape
+        sk = k.shape[2]
+        strides = _strides(*ins, lse, delta, *staged_outs)
+        keep.append(strides)
+        fn = lib.fn[f"attention_bwd_{kind}"]
+        args = (*(t.data_ptr() for t in ins), lse.data_ptr(), delta.data_ptr(),
+                *(t.data_ptr() for t in staged_outs), batch, q_heads, group, sq, sk, d, strides, float(scale),
+                int(causal))
+        op = OP_ATTENTION_BWD_DQ if kind == "dq" else OP_ATTENTION_BWD_DKDV
+        return Launch(f"intent_hip_attention_bwd_{kind}", lambda stream: fn(*args, stream), tuple(keep),
+                      tuple(before), tuple(after),
+                      (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq), ("sk", sk),
+                       ("d", d), ("causal", causal)),
+                      lambda: lib.kernel_resources(op, F16, sq, d))
+    return plan
+
+
 # ------------------------------------------------------------------------------ SpMV
 def _csr_spmv(lib, bound, constexprs, device):
     import ctypes
@@ -301,6 +369,16 @@ _SPECS = (
     OperatorSpec("flash_attention_bf16_fwd", (_view(IN, "bf16", 4), _view(IN, "bf16", 4), _view(IN, "bf16", 4),
                                               _view(OUT, "bf16", 4), ("scalar", "f32")), ("HEAD_GROUP", "CAUSAL"),
                  _attention_grouped(BF16)),
+    OperatorSpec("attention_backward_delta", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(OUT, "f32", 3)), (),
+                 _attention_bwd_delta),
+    OperatorSpec("attention_backward_dkdv",
+                 (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
+                  _view(IN, "f32", 3), _view(IN, "f32", 3), _view(OUT, "f16", 4), _view(OUT, "f16", 4),
+                  ("scalar", "f32")), ("HEAD_GROUP", "CAUSAL"), _attention_bwd("dkdv")),
+    OperatorSpec("attention_backward_dq",
+                 (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
+                  _view(IN, "f32", 3), _view(IN, "f32", 3), _view(OUT, "f16", 4), ("scalar", "f32")),
+                 ("HEAD_GROUP", "CAUSAL"), _attention_bwd("dq")),
     OperatorSpec("csr_spmv", (_view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "f32", 1), _view(IN, "f32", 1),
                               _view(OUT, "f32", 1)), (), _csr_spmv, derived=(("R", "R1", -1),)),
 )

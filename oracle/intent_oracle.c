@@ -406,6 +406,173 @@ int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_
   return oracle_attention_fwd(1, q, k, v, o, batch, heads, 1, sq, sk, d, dv, strides, scale, causal, chunk, workers);
 }
 
+/* ------------------------------------------------------------------ attention backward
+ * backward/attention.py (f16 storage, f32 arithmetic):
+ *   attention_backward_delta (:17-34): delta[b,h,q] = sum_d f32(o) * f32(do) (a reduce);
+ *   attention_backward_dq (:171-211) with summarize_query_gradients (:140-163): per query,
+ *     p = exp2_approx_ftz(s * (scale * log2e) - lse * log2e), s = q . k (f32); causal validity
+ *     q >= k; dp = do . v; ds = p * (dp - delta); dq = sum over valid keys of f16(ds) * k;
+ *     grad_q = f16(dq * scale);
+ *   attention_backward_dkdv (:87-137) with summarize_key_value_gradients (:47-79): per key of
+ *     key head hk, over the HEAD_GROUP query heads hk * G + g and their queries in order:
+ *     dv = sum f16(p) * do, dk = sum f16(ds) * q over valid pairs; grad_k = f16(dk * scale),
+ *     grad_v = f16(dv).
+ * Excluded (causally invalid) pairs contribute nothing (masked_gradient_product, :37-44). The
+ * key axis of dq and the query axis of dk/dv are region folds whose chunks are combined by
+ * addition (:82-84, :166-168); each chunk of `chunk` positions is summed, then added. lse is
+ * the natural logarithm of the forward's softmax denominator (programs/attention_backward.py:25).
+ * Strides are in elements: delta: o[4], do[4], delta[3]; dq: q, k, v, do (4 each), lse[3],
+ * delta[3], dq[4]; dkdv: the same inputs, then dk[4], dv[4]. */
+int oracle_attention_bwd_delta(const uint16_t *o, const uint16_t *dout, float *delta, int64_t batch, int64_t heads,
+                               int64_t sq, int64_t d, const int64_t *st, int workers) {
+  if (batch <= 0 || heads <= 0 || sq <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int64_t count = batch * heads * sq;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *prod = (float *)malloc(sizeof(float) * (size_t)(d > 0 ? d : 1));
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t bi = item / (heads * sq), hi = (item / sq) % heads, qi = item % sq;
+      const uint16_t *op = o + bi * st[0] + hi * st[1] + qi * st[2];
+      const uint16_t *gp = dout + bi * st[4] + hi * st[5] + qi * st[6];
+      for (int64_t t = 0; t < d; ++t) prod[t] = oracle_half_to_float(op[t * st[3]]) * oracle_half_to_float(gp[t * st[7]]);
+      delta[bi * st[8] + hi * st[9] + qi * st[10]] = lane_sum(prod, d);
+    }
+    free(prod);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+static float dot_f16(const uint16_t *a, int64_t as, const uint16_t *b, int64_t bs, int64_t d) {
+  float acc = 0.0f;
+  for (int64_t t = 0; t < d; ++t) acc = acc + oracle_half_to_float(a[t * as]) * oracle_half_to_float(b[t * bs]);
+  return acc;
+}
+
+int oracle_attention_bwd_dq(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *dout,
+                            const float *lse, const float *delta, uint16_t *dq, int64_t batch, int64_t heads,
+                            int64_t head_group, int64_t sq, int64_t sk, int64_t d, const int64_t *st, float scale,
+                            int causal, int64_t chunk, int workers) {
+  if (batch <= 0 || heads <= 0 || sq <= 0) return 0;
+  if (head_group < 1 || heads % head_group) return 1;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const float factor = scale * log2e;
+  const int64_t count = batch * heads * sq;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)d);
+    float *part = (float *)malloc(sizeof(float) * (size_t)d);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t bi = item / (heads * sq), hi = (item / sq) % heads, qi = item % sq, kh = hi / head_group;
+      const uint16_t *qp = q + bi * st[0] + hi * st[1] + qi * st[2];
+      const uint16_t *gp = dout + bi * st[12] + hi * st[13] + qi * st[14];
+      const float l = lse[bi * st[16] + hi * st[17] + qi * st[18]];
+      const float dl = delta[bi * st[19] + hi * st[20] + qi * st[21]];
+      for (int64_t t = 0; t < d; ++t) acc[t] = 0.0f;
+      for (int64_t k0 = 0; k0 < sk; k0 += chunk) {
+        const int64_t k1 = k0 + chunk < sk ? k0 + chunk : sk;
+        for (int64_t t = 0; t < d; ++t) part[t] = 0.0f;
+        for (int64_t j = k0; j < k1; ++j) {
+          if (causal && qi < j) continue;                        /* excluded pair */
+          const uint16_t *kp = k + bi * st[4] + kh * st[5] + j * st[6];
+          const uint16_t *vp = v + bi * st[8] + kh * st[9] + j * st[10];
+          const float s = dot_f16(qp, st[3], kp, st[7], d);
+          const float p = exp2_approx_ftz(s * factor - l * log2e);
+          const float dp = dot_f16(gp, st[15], vp, st[11], d);
+          const float ds16 = oracle_half_to_float(oracle_float_to_half(p * (dp - dl)));
+          for (int64_t t = 0; t < d; ++t) part[t] = part[t] + ds16 * oracle_half_to_float(kp[t * st[7]]);
+        }
+        for (int64_t t = 0; t < d; ++t) acc[t] = acc[t] + part[t];
+      }
+      uint16_t *out = dq + bi * st[22] + hi * st[23] + qi * st[24];
+      for (int64_t t = 0; t < d; ++t) out[t * st[25]] = oracle_float_to_half(acc[t] * scale);
+    }
+    free(acc);
+    free(part);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+int oracle_attention_bwd_dkdv(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *dout,
+                              const float *lse, const float *delta, uint16_t *dk, uint16_t *dv, int64_t batch,
+                              int64_t heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d, const int64_t *st,
+                              float scale, int causal, int64_t chunk, int workers) {
+  if (batch <= 0 || heads <= 0 || sk <= 0) return 0;
+  if (head_group < 1 || heads % head_group) return 1;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const float factor = scale * log2e;
+  const int64_t kv_heads = heads / head_group;
+  const int64_t count = batch * kv_heads * sk;
+  const int64_t members = head_group * sq;                      /* the region-fold axis */
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *ak = (float *)malloc(sizeof(float) * (size_t)d), *av = (float *)malloc(sizeof(float) * (size_t)d);
+    float *pk = (float *)malloc(sizeof(float) * (size_t)d), *pv = (float *)malloc(sizeof(float) * (size_t)d);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t bi = item / (kv_heads * sk), kh = (item / sk) % kv_heads, kj = item % sk;
+      const uint16_t *kp = k + bi * st[4] + kh * st[5] + kj * st[6];
+      const uint16_t *vp = v + bi * st[8] + kh * st[9] + kj * st[10];
+      for (int64_t t = 0; t < d; ++t) ak[t] = av[t] = 0.0f;
+      for (int64_t m0 = 0; m0 < members; m0 += chunk) {
+        const int64_t m1 = m0 + chunk < members ? m0 + chunk : members;
+        for (int64_t t = 0; t < d; ++t) pk[t] = pv[t] = 0.0f;
+        for (int64_t member = m0; member < m1; ++member) {
+          const int64_t hi = kh * head_group + member / sq, qi = member % sq;
+          if (causal && kj > qi) continue;                       /* excluded pair */
+          const uint16_t *qp = q + bi * st[0] + hi * st[1] + qi * st[2];
+          const uint16_t *gp = dout + bi * st[12] + hi * st[13] + qi * st[14];
+          const float l = lse[bi * st[16] + hi * st[17] + qi * st[18]];
+          const float dl = delta[bi * st[19] + hi * st[20] + qi * st[21]];
+          const float s = dot_f16(kp, st[7], qp, st[3], d);
+          const float p = exp2_approx_ftz(s * factor - l * log2e);
+          const float p16 = oracle_half_to_float(oracle_float_to_half(p));
+          for (int64_t t = 0; t < d; ++t) pv[t] = pv[t] + p16 * oracle_half_to_float(gp[t * st[15]]);
+          const float dp = dot_f16(vp, st[11], gp, st[15], d);
+          const float ds16 = oracle_half_to_float(oracle_float_to_half(p * (dp - dl)));
+          for (int64_t t = 0; t < d; ++t) pk[t] = pk[t] + ds16 * oracle_half_to_float(qp[t * st[3]]);
+        }
+        for (int64_t t = 0; t < d; ++t) {
+          ak[t] = ak[t] + pk[t];
+          av[t] = av[t] + pv[t];
+        }
+      }
+      uint16_t *ko = dk + bi * st[22] + kh * st[23] + kj * st[24];
+      uint16_t *vo = dv + bi * st[26] + kh * st[27] + kj * st[28];
+      for (int64_t t = 0; t < d; ++t) {
+        ko[t * st[25]] = oracle_float_to_half(ak[t] * scale);
+        vo[t * st[29]] = oracle_float_to_half(av[t]);
+      }
+    }
+    free(ak);
+    free(av);
+    free(pk);
+    free(pv);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
 /* ------------------------------------------------------------------ CSR SpMV
  * sparse/csr_spmv.py:11-29: acc = 0.0f; for nz in [off[r], off[r+1]) in order:
  * acc = acc + values[nz] * vector[col[nz]] (product rounded, then added); y[r] = acc. */

@@ -40,6 +40,11 @@ def lib():
         handle.oracle_attention_fwd_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                     ctypes.POINTER(i64), f, i, i64, i]
         handle.oracle_csr_spmv_f32.argtypes = [p, p, p, p, p, i64, i]
+        handle.oracle_attention_bwd_delta.argtypes = [p, p, p, i64, i64, i64, i64, ctypes.POINTER(i64), i]
+        handle.oracle_attention_bwd_dq.argtypes = [p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
+                                                   ctypes.POINTER(i64), f, i, i64, i]
+        handle.oracle_attention_bwd_dkdv.argtypes = [p, p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
+                                                     ctypes.POINTER(i64), f, i, i64, i]
         for name in ("oracle_halves_to_floats", "oracle_floats_to_halves", "oracle_floats_to_bf16"):
             getattr(handle, name).argtypes = [p, p, i64]
         _lib = handle
@@ -195,6 +200,52 @@ def attention_fwd_f16(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
     lib().oracle_attention_fwd_f16(_ptr(q), _ptr(k), _ptr(v), _ptr(o), batch, heads, sq, sk, d, dv, strides,
                                    float(np.float32(scale)), int(causal), chunk, workers or default_workers())
     return o
+
+
+def _elem_strides(*arrays):
+    return [st // a.itemsize for a in arrays for st in a.strides]
+
+
+def attention_bwd_delta(o: np.ndarray, dout: np.ndarray, *, workers: int | None = None) -> np.ndarray:
+    """attention_backward_delta: o, dout float16 [B,H,Q,D]; returns delta float32 [B,H,Q]."""
+    batch, heads, sq, d = o.shape
+    delta = np.empty((batch, heads, sq), np.float32)
+    strides = (ctypes.c_int64 * 11)(*_elem_strides(o, dout, delta))
+    lib().oracle_attention_bwd_delta(_ptr(o), _ptr(dout), _ptr(delta), batch, heads, sq, d, strides,
+                                     workers or default_workers())
+    return delta
+
+
+def attention_bwd_dq(q, k, v, dout, lse, delta, scale: float, causal: bool, *, head_group: int = 1,
+                     chunk: int = 64, workers: int | None = None) -> np.ndarray:
+    """attention_backward_dq: q/dout [B,HQ,Q,D], k/v [B,HK,K,D] float16; lse/delta [B,HQ,Q] float32."""
+    batch, heads, sq, d = q.shape
+    sk = k.shape[2]
+    dq = np.empty(q.shape, np.float16)
+    strides = (ctypes.c_int64 * 26)(*_elem_strides(q, k, v, dout, lse, delta, dq))
+    status = lib().oracle_attention_bwd_dq(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse), _ptr(delta), _ptr(dq),
+                                           batch, heads, head_group, sq, sk, d, strides, float(np.float32(scale)),
+                                           int(causal), chunk, workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_attention_bwd_dq rejected the call ({status})")
+    return dq
+
+
+def attention_bwd_dkdv(q, k, v, dout, lse, delta, scale: float, causal: bool, *, head_group: int = 1,
+                       chunk: int = 64, workers: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """attention_backward_dkdv: returns (grad_k, grad_v) float16 [B,HK,K,D]."""
+    batch, heads, sq, d = q.shape
+    sk = k.shape[2]
+    dk = np.empty(k.shape, np.float16)
+    dv = np.empty(v.shape, np.float16)
+    strides = (ctypes.c_int64 * 30)(*_elem_strides(q, k, v, dout, lse, delta, dk, dv))
+    status = lib().oracle_attention_bwd_dkdv(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse), _ptr(delta),
+                                             _ptr(dk), _ptr(dv), batch, heads, head_group, sq, sk, d, strides,
+                                             float(np.float32(scale)), int(causal), chunk,
+                                             workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_attention_bwd_dkdv rejected the call ({status})")
+    return dk, dv
 
 
 def csr_spmv(offsets: np.ndarray, columns: np.ndarray, values: np.ndarray, x: np.ndarray, *,

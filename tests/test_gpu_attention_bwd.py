@@ -1,0 +1,111 @@
+"""GPU parity of the attention backward (delta, dK/dV, dQ) through the AttentionBackward program
+(the reference's programs/attention_backward.py) and intent.jit, and of the authored-backward
+autograd registration flow (the reference's examples/softmax_forward_backward.py:11-28).
+
+Bar: f16 gradients within rel 2e-2 of the oracle plus an absolute 1e-2 of the tensor's largest
+magnitude (the f16 roundings of P and dS and the reassociated sums); delta (f32) within rel 1e-5
+of the oracle. Inputs are finite; causally excluded pairs then contribute exactly zero in both."""
+import numpy as np
+import pytest
+import torch
+
+import intent_amd as intent
+import oracle
+from intent_amd.examples import inputs
+from intent_amd.examples.programs.attention_backward import AttentionBackward
+from tests.gpu_util import announce, assert_f32_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, want, rel=2e-2, frac=1e-2):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert not np.isnan(got).any()
+    bound = rel * np.abs(want) + frac * max(np.abs(want).max(), 1e-3)
+    worst = np.unravel_index(np.argmax(np.abs(got - want) - bound), got.shape)
+    assert np.all(np.abs(got - want) <= bound), f"at {worst}: got {got[worst]} want {want[worst]}"
+
+
+def case(seed, batch, hq, hk, sq, sk, d):
+    rng = np.random.default_rng(seed)
+    q = inputs.normal(rng, (batch, hq, sq, d), "f16")
+    k = inputs.normal(rng, (batch, hk, sk, d), "f16")
+    v = inputs.normal(rng, (batch, hk, sk, d), "f16")
+    o = inputs.normal(rng, (batch, hq, sq, d), "f16")
+    do = inputs.normal(rng, (batch, hq, sq, d), "f16")
+    lse = (rng.standard_normal((batch, hq, sq)) * 0.5 + np.log(max(sk, 1))).astype(np.float32)
+    return q, k, v, o, do, lse
+
+
+@pytest.mark.parametrize("shape,causal", [((2, 8, 2, 1024, 1024, 64), True), ((1, 4, 4, 300, 300, 64), True),
+                                          ((1, 2, 1, 200, 333, 64), False), ((1, 4, 2, 257, 257, 128), True),
+                                          ((2, 2, 2, 130, 70, 128), False), ((1, 1, 1, 1, 1, 64), True)])
+def test_attention_backward_matches_oracle(device, shape, causal):
+    batch, hq, hk, sq, sk, d = shape
+    announce("attention backward", shape, causal)
+    q, k, v, o, do, lse = case(sq + sk + d, batch, hq, hk, sq, sk, d)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    program = AttentionBackward.from_jit(lambda defn, **kw: intent.jit(defn, backend="hip", **kw),
+                                         head_group=hq // hk, causal=causal)
+    grad_q, grad_k, grad_v = program.run(t(q), t(k), t(v), t(o), t(do), t(lse), scale)
+    delta = oracle.attention_bwd_delta(o, do)
+    want_dq = oracle.attention_bwd_dq(q, k, v, do, lse, delta, scale, causal, head_group=hq // hk)
+    want_dk, want_dv = oracle.attention_bwd_dkdv(q, k, v, do, lse, delta, scale, causal, head_group=hq // hk)
+    close(grad_q.cpu().numpy(), want_dq)
+    close(grad_k.cpu().numpy(), want_dk)
+    close(grad_v.cpu().numpy(), want_dv)
+
+
+def test_attention_backward_delta_and_explicit_outputs(device):
+    announce("attention backward delta / outputs")
+    from intent_amd.examples.kernels.backward.attention import attention_backward_delta
+
+    q, k, v, o, do, lse = case(3, 2, 4, 2, 96, 96, 64)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    delta = intent.jit(attention_backward_delta, backend="hip").run(t(o), t(do)).cpu().numpy()
+    assert_f32_rel(delta, oracle.attention_bwd_delta(o, do), rel=1e-5, floor=1e-4)
+    program = AttentionBackward.from_jit(lambda defn, **kw: intent.jit(defn, backend="hip", **kw), head_group=2,
+                                         causal=True)
+    outputs = (torch.empty(2, 4, 96, 64, dtype=torch.float16, device=device),
+               torch.empty(2, 2, 96, 64, dtype=torch.float16, device=device),
+               torch.empty(2, 2, 96, 64, dtype=torch.float16, device=device))
+    call = program.prepare(t(q), t(k), t(v), t(o), t(do), t(lse), 0.125, outputs=outputs)
+    assert call.kernel_count == 3
+    call.launch()
+    assert call.result()[0] is outputs[0]
+    reference = program.run(t(q), t(k), t(v), t(o), t(do), t(lse), 0.125)
+    for got, want in zip(outputs, reference):
+        assert torch.equal(got, want)
+
+
+def test_authored_softmax_backward_autograd(device):
+    """examples/softmax_forward_backward.py: forward and authored backward as torch ops, the
+    backward registered with register_autograd."""
+    announce("softmax autograd registration")
+    from intent_amd.examples.kernels.backward.softmax import softmax_backward
+    from intent_amd.examples.kernels.normalization.softmax import stable_softmax
+
+    x = torch.randn((4096, 4097), dtype=torch.float32, device=device, requires_grad=True)
+    upstream = torch.randn_like(x)
+    forward = intent.jit(stable_softmax, backend="hip")
+    backward = intent.jit(softmax_backward, backend="hip")
+    probabilities = forward.prepare(x.detach()).result()
+    backward.prepare(probabilities, upstream)
+    operation = forward.as_torch_op("intent_amd_tests::softmax_forward")
+    backward_operation = backward.as_torch_op("intent_amd_tests::softmax_backward")
+
+    def setup_context(ctx, inputs, output):  # noqa: F811 (torch passes these by keyword)
+        ctx.save_for_backward(output)
+
+    def backward_formula(ctx, grad):
+        p, = ctx.saved_tensors
+        return backward_operation(p, grad)
+
+    operation.register_autograd(backward_formula, setup_context=setup_context)
+    y = operation(x)
+    y.backward(upstream)
+    reference = x.detach().clone().requires_grad_(True)
+    torch.softmax(reference, dim=1).backward(upstream)
+    assert torch.allclose(y, torch.softmax(x.detach(), dim=1), rtol=1e-5, atol=1e-7)
+    assert torch.allclose(x.grad, reference.grad, rtol=1e-4, atol=1e-6)

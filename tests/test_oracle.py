@@ -324,3 +324,61 @@ def test_attention_bf16_first_causal_row():
     assert (o[:, :, 0, :] == v[:, :, 0, :]).all()                            # one valid key: p = 1, den = 1
     with pytest.raises(ValueError):
         oracle.attention_fwd(q, k[:, :1], v[:, :1], 1.0, True, head_group=3, storage="bf16")
+
+
+# ------------------------------------------------------------------------------ attention backward
+def _attention_autograd64(q, k, v, do, scale, causal, group):
+    """float64 reference: forward with grouped heads, lse, and autograd gradients."""
+    tq, tk, tv = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (q, k, v))
+    kk, vv = tk.repeat_interleave(group, dim=1), tv.repeat_interleave(group, dim=1)
+    s = torch.einsum("bhqd,bhkd->bhqk", tq, kk) * scale
+    if causal:
+        s = s.masked_fill(torch.ones(q.shape[2], k.shape[2], dtype=torch.bool).triu(1), float("-inf"))
+    lse = torch.logsumexp(s, -1)
+    o = torch.einsum("bhqk,bhkd->bhqd", torch.softmax(s, -1), vv)
+    o.backward(torch.tensor(do, dtype=torch.float64))
+    return o.detach().numpy(), lse.detach().numpy(), tq.grad.numpy(), tk.grad.numpy(), tv.grad.numpy()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("d,group", [(64, 4), (128, 1)])
+def test_attention_backward_matches_autograd(causal, d, group):
+    rng = np.random.default_rng(16 + d + group)
+    hk, sq = 2, 45
+    q = inputs.normal(rng, (1, hk * group, sq, d), "f16")
+    k = inputs.normal(rng, (1, hk, sq, d), "f16")
+    v = inputs.normal(rng, (1, hk, sq, d), "f16")
+    do = inputs.normal(rng, (1, hk * group, sq, d), "f16")
+    scale = float(np.float32(1 / np.sqrt(d)))
+    o, lse, gq, gk, gv = _attention_autograd64(q, k, v, do, scale, causal, group)
+    o16 = o.astype(np.float16)
+    delta = oracle.attention_bwd_delta(o16, do)
+    np.testing.assert_allclose(delta, np.sum(o16.astype(np.float64) * do.astype(np.float64), -1), rtol=1e-5,
+                               atol=1e-5)
+    lse32 = lse.astype(np.float32)
+    dq = oracle.attention_bwd_dq(q, k, v, do, lse32, delta, scale, causal, head_group=group)
+    dk, dv = oracle.attention_bwd_dkdv(q, k, v, do, lse32, delta, scale, causal, head_group=group)
+    for got, want in ((dq, gq), (dk, gk), (dv, gv)):
+        err = np.abs(got.astype(np.float64) - want)
+        assert np.all(err <= 2e-2 * np.abs(want) + 5e-3 * max(1.0, np.abs(want).max()))
+
+
+def test_attention_backward_grouped_sums_heads():
+    """dK/dV of a key head equal the sum of the ungrouped results of its query heads."""
+    rng = np.random.default_rng(17)
+    q = inputs.normal(rng, (1, 4, 30, 64), "f16")
+    k = inputs.normal(rng, (1, 2, 30, 64), "f16")
+    v = inputs.normal(rng, (1, 2, 30, 64), "f16")
+    do = inputs.normal(rng, (1, 4, 30, 64), "f16")
+    lse = rng.standard_normal((1, 4, 30)).astype(np.float32) + 6.0
+    delta = rng.standard_normal((1, 4, 30)).astype(np.float32)
+    dk, dv = oracle.attention_bwd_dkdv(q, k, v, do, lse, delta, 0.125, True, head_group=2)
+    heads = np.arange(4) // 2
+    kr, vr = np.ascontiguousarray(k[:, heads]), np.ascontiguousarray(v[:, heads])
+    dk1, dv1 = oracle.attention_bwd_dkdv(q, kr, vr, do, lse, delta, 0.125, True, head_group=1)
+    for grouped, single in ((dk, dk1), (dv, dv1)):
+        summed = single.astype(np.float64).reshape(1, 2, 2, 30, 64).sum(axis=2)
+        assert np.all(np.abs(grouped.astype(np.float64) - summed) <= 2e-3 * np.abs(summed) + 2e-3)
+    dq = oracle.attention_bwd_dq(q, k, v, do, lse, delta, 0.125, True, head_group=2)
+    dq1 = oracle.attention_bwd_dq(q, kr, vr, do, lse, delta, 0.125, True, head_group=1)
+    assert (dq.view(np.uint16) == dq1.view(np.uint16)).all()                # dq only reads K/V

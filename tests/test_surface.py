@@ -182,3 +182,41 @@ def test_sibling_plan_errors_before_launch():
     iface = PublicInterface.from_definition(flash_gqa_attention_fwd, {"HEAD_GROUP": 2, "CAUSAL": True})
     with pytest.raises(intent.CompilationStageError):     # constexprs in the wrong order are another contract
         recognize(flash_gqa_attention_fwd, iface, ("CAUSAL", "HEAD_GROUP"))
+
+
+def test_attention_backward_definitions_and_sequence():
+    from intent_amd.examples.kernels.backward.attention import (attention_backward_delta, attention_backward_dkdv,
+                                                                attention_backward_dq)
+    from intent_amd.runtime import PreparedSequence
+
+    options = {"HEAD_GROUP": 4, "CAUSAL": True}
+    for defn, constexprs in ((attention_backward_delta, {}), (attention_backward_dkdv, options),
+                             (attention_backward_dq, options)):
+        iface = PublicInterface.from_definition(defn, constexprs)
+        assert recognize(defn, iface, tuple(constexprs)).name == defn.__name__
+    assert list(attention_backward_dq.signature.parameters) == [
+        "q", "k", "v", "grad_output", "lse", "delta", "grad_q", "scale", "HEAD_GROUP", "CAUSAL"]
+    assert list(attention_backward_dkdv.signature.parameters) == [
+        "q", "k", "v", "grad_output", "lse", "delta", "grad_k", "grad_v", "scale", "HEAD_GROUP", "CAUSAL"]
+    assert PublicInterface.from_definition(attention_backward_dq, options).parameters[6].noalias
+
+    order = []
+
+    class Call:
+        def __init__(self, name):
+            self.name, self.observation = name, None
+
+        def compile(self):
+            order.append(("compile", self.name))
+
+        def launch(self):
+            order.append(("launch", self.name))
+
+    sequence = PreparedSequence((Call("a"), PreparedSequence((Call("b"), Call("c")), outputs=None)), outputs=(1, 2))
+    sequence.compile()
+    sequence.launch()
+    assert order == [("compile", "a"), ("compile", "b"), ("compile", "c"), ("launch", "a"), ("launch", "b"),
+                     ("launch", "c")]
+    assert sequence.result() == (1, 2) and sequence.kernel_count == 3
+    with pytest.raises(ValueError):
+        PreparedSequence((), outputs=None)
