@@ -7,6 +7,7 @@ Use it as `import intent_amd as intent`.
 """
 from . import language
 from .api import Definition, DefinitionKind, HelperDefinition, KernelDefinition, fn, kernel
+from .compiler import GeneratedProgram, generate
 from .diagnostics import CompilationStageError, DefinitionError, IntentError, LanguageUseError
 from .jit import JITKernel, jit
 from .runtime import (CompiledArtifact, ConfigurationAssessment, NativeObservation, NativeResource,
@@ -27,4 +28,5 @@ class CompileOptions:
 __all__ = ["language", "Definition", "DefinitionKind", "HelperDefinition", "KernelDefinition", "fn", "kernel",
            "CompilationStageError", "DefinitionError", "IntentError", "LanguageUseError", "JITKernel", "jit",
            "CompiledArtifact", "ConfigurationAssessment", "NativeObservation", "NativeResource",
-           "PreparedCall", "PublicInterface", "ScalarParameter", "ViewParameter", "CompileOptions"]
+           "PreparedCall", "PublicInterface", "ScalarParameter", "ViewParameter", "CompileOptions",
+           "GeneratedProgram", "generate"]

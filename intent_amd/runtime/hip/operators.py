@@ -406,3 +406,12 @@ def recognize(definition, interface, constexpr_names: tuple[str, ...]) -> Operat
             f"expected {spec.signature} with constexprs {spec.constexprs}, got {signature_of(interface)} "
             f"with constexprs {tuple(constexpr_names)}")
     return spec
+
+
+def recognize_saved(name: str, signature: tuple, constexpr_names: tuple[str, ...]) -> OperatorSpec:
+    """Recognition of a saved program (no definition object): by name, signature and constexprs."""
+    spec = SPECS.get(name)
+    if spec is None or tuple(signature) != spec.signature or tuple(constexpr_names) != spec.constexprs:
+        raise CompilationStageError("provider_recognition",
+                                    f"saved program {name!r} does not match a kernel of this hip provider")
+    return spec

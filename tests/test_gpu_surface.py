@@ -121,3 +121,24 @@ def test_errors_on_gpu(device):
         kernel.run(torch.zeros(2, 2))                     # CPU tensor
     with pytest.raises(intent.CompilationStageError):
         intent.jit(stable_softmax, backend="hip", constexprs={"BOGUS": 1}).run(torch.zeros(2, 2, device=device))
+
+
+def test_saved_program_runs_like_jit(device, tmp_path):
+    """examples/softmax.py --program: a generated program saved, loaded and bound to a local target
+    runs the same kernel as intent.jit."""
+    announce("saved program")
+    from intent_amd.examples.kernels.normalization.softmax import stable_softmax_f16
+    from intent_amd.targets.hip import HipTarget
+    from intent_amd.targets.local import resolve_local, select_device
+
+    x = torch.randn((512, 1000), device=device, dtype=torch.float16)
+    path = intent.generate(stable_softmax_f16, target=HipTarget(device.index or 0)).save(tmp_path / "softmax")
+    target = resolve_local("hip", select_device("hip", (x,), str(device)))
+    softmax = intent.GeneratedProgram.load(path).materialize(target=target)
+    y = softmax.run(x)
+    want = intent.jit(stable_softmax_f16, backend="hip").run(x)
+    assert torch.equal(y, want)
+    out = torch.empty_like(x)
+    call = softmax.prepare(x, outputs=(out,))
+    call.launch()
+    assert call.result() is out and torch.equal(out, want)

@@ -220,3 +220,38 @@ def test_attention_backward_definitions_and_sequence():
     assert sequence.result() == (1, 2) and sequence.kernel_count == 3
     with pytest.raises(ValueError):
         PreparedSequence((), outputs=None)
+
+
+def test_generated_program_save_load_roundtrip(tmp_path):
+    """generate -> save (kernel.source, kernel.mlir, artifact.json) -> load -> materialize, without a GPU."""
+    import json
+    from types import SimpleNamespace
+
+    target = SimpleNamespace(device=0, architecture="gfx950")
+    program = intent.generate(gemm, target=target, constexprs={"ACTIVATION": Activation.RELU})
+    path = program.save(tmp_path / "gemm_relu")
+    assert sorted(p.name for p in path.iterdir()) == ["artifact.json", "kernel.mlir", "kernel.source"]
+    loaded = intent.GeneratedProgram.load(path)
+    assert loaded.entry_name == "gemm" and loaded.metadata == program.metadata
+    assert loaded.metadata["constexprs"]["ACTIVATION"] == {"enum": "Activation", "name": "RELU", "value": 1}
+    assert loaded.interface.to_json() == PublicInterface.from_definition(
+        gemm, {"ACTIVATION": Activation.RELU}).to_json()
+    with pytest.raises(intent.CompilationStageError):
+        loaded.materialize()                                   # a loaded program has no device
+    artifact = loaded.materialize(target=target)
+    assert artifact.interface.to_json() == loaded.interface.to_json()
+    assert artifact.runtime.constexprs == {"ACTIVATION": 1}
+    with pytest.raises(intent.CompilationStageError):
+        program.save(path)                                     # never overwrites
+    with pytest.raises(intent.CompilationStageError):
+        loaded.materialize(target=SimpleNamespace(device=0, architecture="gfx942"))
+    metadata = json.loads((path / "artifact.json").read_text())
+    metadata["signature"][0][2] = "bf16"                       # tampered contract
+    (path / "artifact.json").write_text(json.dumps(metadata))
+    with pytest.raises(intent.CompilationStageError) as error:
+        intent.GeneratedProgram.load(path).materialize(target=target)
+    assert error.value.stage == "provider_recognition"
+    (path / "kernel.source").write_text("")
+    with pytest.raises(intent.CompilationStageError) as error:
+        intent.GeneratedProgram.load(path)
+    assert error.value.stage == "generated_program_loading"
