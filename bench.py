@@ -47,7 +47,7 @@ def parse():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
-                                "attention_bwd,attention_bwd_large")
+                                "attention_bwd,attention_bwd_large,paged_decode")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -446,10 +446,58 @@ def op_attention_bwd_large(device, flush, cpu):
     return _op_attention_bwd(device, flush, cpu, True)
 
 
+def op_paged_decode(device, flush, cpu):
+    """Split-K paged grouped-query decode (programs/composition.py PagedDecode: partials + merge)
+    at the paged_attention.py constants: B8, HQ32, HK8, D128, 64-token pages, 16 splits, sequence
+    lengths 8191..6413, each sequence owning ceil(length / 64) shuffled pages."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.programs.composition import PagedDecode
+
+    arrays = inputs.paged_decode(seed=4, layout="exact")
+    q, key_cache, value_cache, page_offsets, page_indices, lengths, split_offsets = arrays
+    batch, hq, d = q.shape
+    hk, splits, page_size = key_cache.shape[2], 16, 64
+    scale = float(np.float32(1 / np.sqrt(d)))
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    program = PagedDecode.from_jit(lambda defn, **kw: intent.jit(defn, backend="hip", **kw), page_size=page_size,
+                                   head_group=hq // hk, splits=splits)
+    call = program.prepare(*(t(a) for a in arrays), scale)
+    ms = graph_median_ms(call.launch, flush)
+    partials, merge = call.calls
+    partial_ms, merge_ms = sequence_kernel_ms(partials.launch, merge.launch, 50)
+    tokens = int(lengths.astype(np.int64).sum())
+    kv_bytes = tokens * hk * 2 * d * 2                       # K and V rows of every active token
+    partial_bytes = batch * hq * splits * (d + 1) * 4          # written by the partials, read by the merge
+    nbytes = kv_bytes + batch * hq * d * 2 + 2 * partial_bytes + batch * hq * d * 2 + 4 * (
+        page_offsets.size + page_indices.size + lengths.size + split_offsets.size)
+    out = {"config": f"paged GQA decode f16 B{batch} HQ{hq} HK{hk} D{d} page 64, {splits} splits, "
+                     f"{tokens} cached tokens (partials + split-K merge)",
+           "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+           "partials_ms": round(partial_ms, 4), "merge_ms": round(merge_ms, 4),
+           "partials_gbs": round((kv_bytes + partial_bytes) / partial_ms / 1e6, 1),
+           "traffic": read_traffic("paged_decode_partials")}
+    if cpu:
+        import oracle
+
+        def run():
+            lse, part = oracle.paged_decode_partials(*arrays, scale, page_size=page_size, head_group=hq // hk,
+                                                     splits=splits)
+            oracle.splitk_reduce_f32_to_f16(part, lse)
+
+        seconds = cpu_median_seconds(run)
+        out["cpu"] = {"gbs": round(nbytes / seconds / 1e9, 3), "cores": oracle.default_workers(), "kind": "port",
+                      "sample": "the whole workload"}
+    return out
+
+
 OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_attention, "spmv": op_spmv,
              "gemm_f16_relu": op_gemm_f16_relu, "gemm_f32": op_gemm_f32, "linear_f32": op_linear_f32,
              "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
-             "attention_bwd_large": op_attention_bwd_large}
+             "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode}
 
 
 def read_traffic(name):

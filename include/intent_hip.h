@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 3
+#define INTENT_HIP_ABI_VERSION 4
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -53,7 +53,9 @@ enum IntentHipOperator {
   INTENT_HIP_OP_ATTENTION_FWD = 7,     /* dtype F16 or BF16 */
   INTENT_HIP_OP_ATTENTION_BWD_DELTA = 8, /* cols = head dimension */
   INTENT_HIP_OP_ATTENTION_BWD_DQ = 9,
-  INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10
+  INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10,
+  INTENT_HIP_OP_PAGED_DECODE_PARTIALS = 11, /* rows = HEAD_GROUP, cols = head dimension */
+  INTENT_HIP_OP_SPLITK_REDUCE = 12
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -182,6 +184,40 @@ int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, c
                                   int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
                                   int64_t sk, int64_t d, const int64_t strides[30], float scale,
                                   int causal, void *stream);
+
+/* Paged grouped-query decode attention over one page range per (batch, split): f16 q, caches,
+ * f32 partial results. paged_gqa_decode_partials
+ * (python/intent/examples/kernels/streaming/paged_attention.py:77-165) with
+ * summarize_masked_attention_chunk (streaming/attention.py:250-285); launched first by
+ * PagedDecode (programs/composition.py:95-122).
+ * Shapes: q [batch, q_heads, d]; key_cache [pages, ps, kv_heads, d]; value_cache
+ * [pages, ps, kv_heads, dv]; page_offsets [batch + 1], lengths [batch], split_offsets
+ * [batch * splits + 1], page_indices [positions] (i32); partial_lse [batch, q_heads, splits] and
+ * partial_output [batch, q_heads, splits, dv] (f32). q_heads = kv_heads * head_group,
+ * head_group 1..16, d = dv = 64 or 128; page_size is the PAGE_SIZE constexpr (logical tokens per
+ * page). Job j = b * splits + s covers page positions split_offsets[j] .. split_offsets[j+1];
+ * a token is active while its logical index is below lengths[b]. partial_lse is base 2
+ * (max + ln(den) * log2 e, -inf for an empty job); partial_output = acc / den (0 for an empty
+ * job). Out-of-range page positions and physical pages are clamped, never dereferenced.
+ * strides[18]: q[3], key_cache[4], value_cache[4], partial_lse[3], partial_output[4]. */
+int intent_hip_paged_decode_partials(const void *q, const void *key_cache, const void *value_cache,
+                                     const int32_t *page_offsets, const int32_t *page_indices,
+                                     const int32_t *lengths, const int32_t *split_offsets,
+                                     float *partial_lse, float *partial_output, int64_t batch,
+                                     int64_t q_heads, int64_t d, int64_t pages, int64_t ps,
+                                     int64_t kv_heads, int64_t dv, int64_t positions, int64_t page_size,
+                                     int64_t head_group, int64_t splits, const int64_t strides[18],
+                                     float scale, void *stream);
+
+/* Split-K merge: out[b,h,:] = f16(sum_s w_s partial[b,h,s,:] * rcp(sum_s w_s)),
+ * w_s = exp(lse[b,h,s] - max_s lse[b,h,s]) with the natural exponential, as
+ * splitk_attention_f32_to_f16_reduce (streaming/splitk_reduce.py:129-155) writes it; launched
+ * second by PagedDecode (programs/composition.py:95-122). partial f32 [batch, heads, splits, d],
+ * lse f32 [batch, heads, splits], out f16 [batch, heads, d].
+ * strides[10]: partial[4], lse[3], out[3]. */
+int intent_hip_splitk_reduce_f32_to_f16(const float *partial, const float *lse, void *out, int64_t batch,
+                                        int64_t heads, int64_t splits, int64_t d, const int64_t strides[10],
+                                        void *stream);
 
 /* CSR SpMV y = A x, f32 values, i32 indices.
  * csr_spmv (python/intent/examples/kernels/sparse/csr_spmv.py:11-29), with dynamic extents.

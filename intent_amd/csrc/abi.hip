@@ -101,6 +101,8 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     case INTENT_HIP_OP_ATTENTION_BWD_DELTA: return attention_bwd_resources(0, cols, out);
     case INTENT_HIP_OP_ATTENTION_BWD_DQ: return attention_bwd_resources(1, cols, out);
     case INTENT_HIP_OP_ATTENTION_BWD_DKDV: return attention_bwd_resources(2, cols, out);
+    case INTENT_HIP_OP_PAGED_DECODE_PARTIALS: return decode_resources(0, cols, rows, out);
+    case INTENT_HIP_OP_SPLITK_REDUCE: return decode_resources(1, cols, rows, out);
   }
   return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "unknown operator code %d", op);
 }

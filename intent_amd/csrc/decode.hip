@@ -1,0 +1,361 @@
+// Paged grouped-query decode attention, split over page ranges, and the split-K merge, for gfx950.
+//
+// Semantics:
+//   paged_gqa_decode_partials (python/intent/examples/kernels/streaming/paged_attention.py:77-165)
+//     with summarize_masked_attention_chunk (streaming/attention.py:250-285): for job
+//     j = batch * SPLITS + split and key head kh, the HEAD_GROUP query heads kh * G + g attend over
+//     the job's tokens t: page position first + t / PS (first = split_offsets[j]), physical page
+//     page_indices[position], offset t % PS, logical token (position - page_offsets[batch]) *
+//     PAGE_SIZE + offset, active while below sequence_lengths[batch]. Scores in the exp2 domain,
+//     weights rounded to f16 before P @ V (f32 accumulation); partial_lse = max + ln(den) * log2 e
+//     (-inf for an empty job), partial_output = acc * (1 / den) (0 for an empty job).
+//   splitk_attention_f32_to_f16_reduce (streaming/splitk_reduce.py:129-155): per (batch, head)
+//     m = maximum_num over splits of lse, w = exp(lse - m) (natural exponential, as the
+//     definition writes it), out = f16(sum w * partial * rcp_approx(sum w)).
+// The running maximum replaces each chunk's maximum before P is rounded, and the summed axes are
+// reassociated; the 16-bit tolerance covers both. Page positions and physical pages are clamped
+// into their arrays (the definition assumes them in bounds), so a bad index cannot fault.
+//
+// Design (both kernels memory-bound):
+//   * partials: one workgroup per (job, key head), 4 waves taking 64-token chunks in turn. Per
+//     chunk, lane t scores token t against the group's queries (kept in LDS as f32); chunk
+//     maxima and sums are wave reductions; P goes through LDS to the P @ V phase, where lane l
+//     owns output dimensions (V rows are read coalesced, 4 bytes per lane per token). The four
+//     waves' states are merged in wave order at the end.
+//   * merge: one wave per (batch, head); lanes own output dimensions, the split loop is serial.
+#include "common.hpp"
+
+namespace intent_hip {
+namespace {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kChunk = 64;            // tokens per wave step
+constexpr int kMaxGroup = 16;          // query heads per key head
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct DecodeGeometry {
+  int64_t q[3], k[4], v[4], lse[3], out[4];
+};
+
+// kG bounds the query heads per key head (the group runs 1..kG; register arrays are sized by kG
+// and every loop over them is unrolled with a uniform guard, so nothing is indexed dynamically).
+template <int D, int kG>
+__global__ __launch_bounds__(kThreads) void paged_decode_partials(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ KC, const uint16_t *__restrict__ VC,
+    const int32_t *__restrict__ page_offsets, const int32_t *__restrict__ page_indices,
+    const int32_t *__restrict__ lengths, const int32_t *__restrict__ split_offsets, float *__restrict__ LSE,
+    float *__restrict__ OUT, int kv_heads, int group, int splits, int64_t pages, int ps, int64_t positions,
+    int page_size, DecodeGeometry g, float scale) {
+  constexpr int kDims = D / 64;        // output dimensions per lane
+  __shared__ float q_s[kG * D];
+  __shared__ float p_s[kWaves][kG][kChunk];
+  __shared__ int64_t row_s[kWaves][kChunk];   // per token: physical row offset (elements) in the caches
+  __shared__ float m_s[kWaves][kG], den_s[kWaves][kG];
+  __shared__ float acc_s[kWaves][kG][D];
+  __shared__ int valid_s[kWaves];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = static_cast<int>(blockIdx.x) % kv_heads;
+  const int job = static_cast<int>(blockIdx.x) / kv_heads;
+  const int b = job / splits, split = job % splits;
+  const int first = split_offsets[job];
+  int64_t count = static_cast<int64_t>(split_offsets[job + 1]) - first;
+  count = count < 0 ? 0 : (count > positions ? positions : count);
+  const int tokens = static_cast<int>(count * ps);     // host checks positions * ps < 2^31
+  const int64_t length = lengths[b], page_begin = page_offsets[b];
+  const float c1 = scale * kLog2e;
+
+  for (int i = tid; i < group * D; i += kThreads) {
+    const int gq = i / D, c = i % D;
+    q_s[i] = static_cast<float>(__builtin_bit_cast(_Float16, Q[b * g.q[0] + (kh * group + gq) * g.q[1] + c]));
+  }
+  __syncthreads();
+
+  float m[kG], den[kG], acc[kG][kDims];
+#pragma unroll
+  for (int gq = 0; gq < kG; ++gq) {
+    m[gq] = -INFINITY;
+    den[gq] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kDims; ++j) acc[gq][j] = 0.0f;
+  }
+  bool valid = false;
+
+  for (int c0 = wave * kChunk; c0 < tokens; c0 += kWaves * kChunk) {
+    // Scores: lane t <-> token c0 + t.
+    const int flat = c0 + lane;
+    bool active = false;
+    float s[kG];
+#pragma unroll
+    for (int gq = 0; gq < kG; ++gq) s[gq] = 0.0f;
+    int64_t key_row = 0;
+    if (flat < tokens) {
+      int64_t position = first + flat / ps;
+      position = position < 0 ? 0 : (position >= positions ? positions - 1 : position);
+      const int offset = flat % ps;
+      int64_t physical = page_indices[position];
+      physical = physical < 0 ? 0 : (physical >= pages ? pages - 1 : physical);
+      active = (position - page_begin) * page_size + offset < length;
+      key_row = physical * g.k[0] + offset * g.k[1] + kh * g.k[2];
+      row_s[wave][lane] = physical * g.v[0] + offset * g.v[1] + kh * g.v[2];
+    }
+    if (active) {                                  // inactive tokens are never read for scores
+      const uint16_t *krow = KC + key_row;
+      f16x8_t kv[D / 8];
+#pragma unroll
+      for (int c = 0; c < D / 8; ++c) kv[c] = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4 *>(krow + 8 * c));
+#pragma unroll
+      for (int c = 0; c < D / 8; ++c) {
+#pragma unroll
+        for (int gq = 0; gq < kG; ++gq) {
+          if (gq < group) {
+            const float4 qa = *reinterpret_cast<const float4 *>(q_s + gq * D + 8 * c);
+            const float4 qb = *reinterpret_cast<const float4 *>(q_s + gq * D + 8 * c + 4);
+            float t = s[gq];
+            t = fmaf(qa.x, static_cast<float>(kv[c][0]), t);
+            t = fmaf(qa.y, static_cast<float>(kv[c][1]), t);
+            t = fmaf(qa.z, static_cast<float>(kv[c][2]), t);
+            t = fmaf(qa.w, static_cast<float>(kv[c][3]), t);
+            t = fmaf(qb.x, static_cast<float>(kv[c][4]), t);
+            t = fmaf(qb.y, static_cast<float>(kv[c][5]), t);
+            t = fmaf(qb.z, static_cast<float>(kv[c][6]), t);
+            t = fmaf(qb.w, static_cast<float>(kv[c][7]), t);
+            s[gq] = t;
+          }
+        }
+      }
+    }
+    if (!__any(active)) continue;                  // wave-uniform: no active token in this chunk
+    valid = true;
+    // Chunk summary as the definition forms it: weights against the chunk's own maximum, rounded
+    // to f16 for P @ V; the chunk is then merged into the running state with exp2 factors.
+    float left[kG], right[kG];
+#pragma unroll
+    for (int gq = 0; gq < kG; ++gq) {
+      left[gq] = 0.0f;
+      right[gq] = 0.0f;
+      if (gq < group) {
+        const float score = active ? s[gq] * c1 : -INFINITY;
+        const float chunk_max = wave_max(score);
+        const float p = active ? __builtin_amdgcn_exp2f(score - chunk_max) : 0.0f;
+        const float chunk_den = wave_sum(p);
+        const float next = fmaxf(m[gq], chunk_max);
+        left[gq] = m[gq] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[gq] - next);
+        right[gq] = __builtin_amdgcn_exp2f(chunk_max - next);
+        m[gq] = next;
+        den[gq] = left[gq] * den[gq] + right[gq] * chunk_den;
+        p_s[wave][gq][lane] = static_cast<float>(static_cast<_Float16>(p));
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // P @ V: lane l owns dimensions l * kDims .. + kDims; V rows are read whole by the wave.
+    float cacc[kG][kDims];
+#pragma unroll
+    for (int gq = 0; gq < kG; ++gq)
+#pragma unroll
+      for (int j = 0; j < kDims; ++j) cacc[gq][j] = 0.0f;
+    const int chunk_tokens = tokens - c0 < kChunk ? tokens - c0 : kChunk;
+#pragma unroll 4
+    for (int t = 0; t < chunk_tokens; ++t) {
+      const uint16_t *vrow = VC + row_s[wave][t];
+      float vv[kDims];
+      if constexpr (kDims == 2) {
+        const uint32_t pair = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(vrow) + lane);
+        vv[0] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair & 0xffffu)));
+        vv[1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16)));
+      } else {
+        vv[0] = static_cast<float>(__builtin_bit_cast(_Float16, __builtin_nontemporal_load(vrow + lane)));
+      }
+#pragma unroll
+      for (int gq = 0; gq < kG; ++gq) {
+        if (gq < group) {
+          const float p = p_s[wave][gq][t];
+#pragma unroll
+          for (int j = 0; j < kDims; ++j) cacc[gq][j] = fmaf(p, vv[j], cacc[gq][j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int gq = 0; gq < kG; ++gq)
+      if (gq < group)
+#pragma unroll
+        for (int j = 0; j < kDims; ++j) acc[gq][j] = left[gq] * acc[gq][j] + right[gq] * cacc[gq][j];
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // Merge the waves' states in wave order.
+  if (lane == 0) valid_s[wave] = valid ? 1 : 0;
+#pragma unroll
+  for (int gq = 0; gq < kG; ++gq) {
+    if (gq < group) {
+      if (lane == 0) {
+        m_s[wave][gq] = m[gq];
+        den_s[wave][gq] = den[gq];
+      }
+#pragma unroll
+      for (int j = 0; j < kDims; ++j) acc_s[wave][gq][lane * kDims + j] = acc[gq][j];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < group * D; i += kThreads) {
+    const int gq = i / D, c = i % D;
+    float top = -INFINITY;
+    bool any = false;
+    for (int w = 0; w < kWaves; ++w)
+      if (valid_s[w]) {
+        any = true;
+        top = fmaxf(top, m_s[w][gq]);
+      }
+    float total = 0.0f, value = 0.0f;
+    for (int w = 0; w < kWaves; ++w)
+      if (valid_s[w]) {
+        const float f = __builtin_amdgcn_exp2f(m_s[w][gq] - top);
+        total = fmaf(f, den_s[w][gq], total);
+        value = fmaf(f, acc_s[w][gq][c], value);
+      }
+    const int h = kh * group + gq;
+    float *orow = OUT + b * g.out[0] + h * g.out[1] + split * g.out[2];
+    orow[c] = any ? value * (1.0f / total) : 0.0f;
+    if (c == 0) LSE[b * g.lse[0] + h * g.lse[1] + split * g.lse[2]] = any ? top + logf(total) * kLog2e : -INFINITY;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void splitk_reduce_f32_to_f16(const float *__restrict__ P,
+                                                                     const float *__restrict__ LSE,
+                                                                     uint16_t *__restrict__ OUT, int heads, int splits,
+                                                                     int d, int64_t rows, DecodeGeometry g) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t b = row / heads, h = row % heads;
+  const float *lse = LSE + b * g.lse[0] + h * g.lse[1];
+  float top = -INFINITY;
+  for (int s = 0; s < splits; ++s) top = fmaxf(top, lse[s * g.lse[2]]);
+  float den = 0.0f;
+  for (int s = 0; s < splits; ++s) den += expf(lse[s * g.lse[2]] - top);
+  const float inv = __builtin_amdgcn_rcpf(den);
+  for (int c = lane; c < d; c += 64) {
+    float num = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+      const float w = expf(lse[s * g.lse[2]] - top);
+      num = fmaf(w, P[b * g.q[0] + h * g.q[1] + s * g.q[2] + c], num);
+    }
+    OUT[b * g.out[0] + h * g.out[1] + c] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(num * inv));
+  }
+}
+
+}  // namespace
+
+template <int D>
+const void *partials_kernel(int64_t group, const char **name) {
+  if (group <= 4) {
+    *name = D == 64 ? "paged_decode_partials<64,4>" : "paged_decode_partials<128,4>";
+    return reinterpret_cast<const void *>(&paged_decode_partials<D, 4>);
+  }
+  if (group <= 8) {
+    *name = D == 64 ? "paged_decode_partials<64,8>" : "paged_decode_partials<128,8>";
+    return reinterpret_cast<const void *>(&paged_decode_partials<D, 8>);
+  }
+  *name = D == 64 ? "paged_decode_partials<64,16>" : "paged_decode_partials<128,16>";
+  return reinterpret_cast<const void *>(&paged_decode_partials<D, 16>);
+}
+
+int decode_resources(int64_t which, int64_t d, int64_t group, IntentHipKernelResources *out) {
+  if (which == 1)
+    return describe_kernel(reinterpret_cast<const void *>(&splitk_reduce_f32_to_f16), "splitk_reduce_f32_to_f16",
+                           kThreads, out);
+  const char *name = nullptr;
+  const void *kernel = d == 64 ? partials_kernel<64>(group, &name) : partials_kernel<128>(group, &name);
+  return describe_kernel(kernel, name, kThreads, out);
+}
+
+}  // namespace intent_hip
+
+using namespace intent_hip;
+
+extern "C" int intent_hip_paged_decode_partials(const void *q, const void *key_cache, const void *value_cache,
+                                                const int32_t *page_offsets, const int32_t *page_indices,
+                                                const int32_t *lengths, const int32_t *split_offsets,
+                                                float *partial_lse, float *partial_output, int64_t batch,
+                                                int64_t q_heads, int64_t d, int64_t pages, int64_t ps,
+                                                int64_t kv_heads, int64_t dv, int64_t positions,
+                                                int64_t page_size, int64_t head_group, int64_t splits,
+                                                const int64_t *strides, float scale, void *stream) {
+  if (batch < 0 || q_heads < 0 || d < 0 || pages < 0 || ps < 0 || kv_heads < 0 || dv < 0 || positions < 0 ||
+      splits < 0)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (head_group < 1 || head_group > kMaxGroup || q_heads != kv_heads * head_group)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT,
+                "query heads (%lld) must equal key heads (%lld) * HEAD_GROUP (%lld), HEAD_GROUP in 1..%d",
+                static_cast<long long>(q_heads), static_cast<long long>(kv_heads),
+                static_cast<long long>(head_group), kMaxGroup);
+  if (batch == 0 || q_heads == 0 || splits == 0) return INTENT_HIP_OK;
+  if ((d != 64 && d != 128) || dv != d)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "paged decode supports D = DV = 64 or 128 (got %lld, %lld)",
+                static_cast<long long>(d), static_cast<long long>(dv));
+  if (page_size < 1 || ps < 1) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "page sizes must be positive");
+  if (pages < 1 || positions < 1) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "empty page cache or page table");
+  if (strides == nullptr || q == nullptr || key_cache == nullptr || value_cache == nullptr ||
+      page_offsets == nullptr || page_indices == nullptr || lengths == nullptr || split_offsets == nullptr ||
+      partial_lse == nullptr || partial_output == nullptr)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  DecodeGeometry g{};
+  for (int i = 0; i < 3; ++i) g.q[i] = strides[i];
+  for (int i = 0; i < 4; ++i) {
+    g.k[i] = strides[3 + i];
+    g.v[i] = strides[7 + i];
+    g.out[i] = strides[14 + i];
+  }
+  for (int i = 0; i < 3; ++i) g.lse[i] = strides[11 + i];
+  if (g.q[2] != 1 || g.k[3] != 1 || g.v[3] != 1 || g.out[3] != 1)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "q, caches and partial_output need unit inner stride");
+  for (int i = 0; i < 3; ++i)
+    if (g.k[i] % 8 || g.v[i] % 2)
+      return fail(INTENT_HIP_ERR_UNSUPPORTED, "cache strides must be multiples of 8 (keys) and 2 (values)");
+  if (!aligned(key_cache, 16) || !aligned(value_cache, 4))
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "key cache must be 16-byte and value cache 4-byte aligned");
+  const int64_t blocks = batch * splits * kv_heads;
+  if (blocks > INT32_MAX || ps > INT32_MAX || page_size > INT32_MAX || positions * ps >= INT32_MAX)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "extents too large");
+  const auto *Q = static_cast<const uint16_t *>(q);
+  const auto *K = static_cast<const uint16_t *>(key_cache);
+  const auto *V = static_cast<const uint16_t *>(value_cache);
+  const char *name = nullptr;
+  const void *kernel = d == 64 ? partials_kernel<64>(head_group, &name) : partials_kernel<128>(head_group, &name);
+  int kv = static_cast<int>(kv_heads), grp = static_cast<int>(head_group), spl = static_cast<int>(splits);
+  int ps32 = static_cast<int>(ps), psize = static_cast<int>(page_size);
+  void *args[] = {&Q, &K, &V, &page_offsets, &page_indices, &lengths, &split_offsets, &partial_lse, &partial_output,
+                  &kv, &grp, &spl, &pages, &ps32, &positions, &psize, &g, &scale};
+  const hipError_t rc = hipLaunchKernel(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), args, 0,
+                                        as_stream(stream));
+  if (rc != hipSuccess) return launch_status(name);
+  return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_splitk_reduce_f32_to_f16(const float *partial, const float *lse, void *out, int64_t batch,
+                                                   int64_t heads, int64_t splits, int64_t d, const int64_t *strides,
+                                                   void *stream) {
+  if (batch < 0 || heads < 0 || splits < 0 || d < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (batch == 0 || heads == 0 || d == 0) return INTENT_HIP_OK;
+  if (partial == nullptr || lse == nullptr || out == nullptr || strides == nullptr)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  if (splits > INT32_MAX || d > INT32_MAX || heads > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "extents too large");
+  DecodeGeometry g{};
+  for (int i = 0; i < 3; ++i) g.q[i] = strides[i];
+  for (int i = 0; i < 3; ++i) g.lse[i] = strides[4 + i];
+  for (int i = 0; i < 3; ++i) g.out[i] = strides[7 + i];
+  if ((strides[3] != 1 || strides[9] != 1) && d > 1)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "partial and output need unit inner stride");
+  const int64_t rows = batch * heads;
+  const dim3 grid(static_cast<unsigned>((rows + kWaves - 1) / kWaves));
+  splitk_reduce_f32_to_f16<<<grid, dim3(kThreads), 0, as_stream(stream)>>>(
+      partial, lse, static_cast<uint16_t *>(out), static_cast<int>(heads), static_cast<int>(splits),
+      static_cast<int>(d), rows, g);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("splitk_reduce_f32_to_f16");
+  return INTENT_HIP_OK;
+}

@@ -125,3 +125,35 @@ def spmv_f32(seed: int = 0, rows: int = SPMV_ROWS, cap: int = SPMV_CAP, c: float
     values = uniform(rng, offsets[-1], -1.0, 1.0)
     x = uniform(rng, rows, -1.0, 1.0)
     return offsets, columns, values, x
+
+
+def paged_decode(seed: int = 0, batch: int = 8, query_heads: int = 32, kv_heads: int = 8, dim: int = 128,
+                 page_size: int = 64, lengths=(8191, 7937, 7683, 7429, 7175, 6921, 6667, 6413), splits: int = 16,
+                 shuffle: bool = True, layout: str = "padded"):
+    """Inputs of paged_gqa_decode_partials (streaming/paged_attention.py:13-22 constants by default),
+    with physical pages in a permuted order when `shuffle`.
+
+    layout "padded": every sequence gets ceil(max length / page_size) pages rounded up to a multiple
+    of `splits`, and split j covers an equal run of them (trailing splits of a short sequence hold
+    only inactive tokens). layout "exact": sequence b owns ceil(length_b / page_size) pages and its
+    splits cover near-equal runs floor(j n / splits) .. floor((j + 1) n / splits).
+    Returns (q, key_cache, value_cache, page_offsets, page_indices, lengths, split_offsets)."""
+    rng = np.random.default_rng(seed)
+    lengths = np.asarray(lengths, np.int32)[:batch]
+    if layout == "padded":
+        per_sequence = -(-int(lengths.max()) // page_size)
+        per_sequence = -(-per_sequence // splits) * splits
+        counts = np.full(batch, per_sequence, np.int64)
+    elif layout == "exact":
+        counts = -(-lengths.astype(np.int64) // page_size)
+    else:
+        raise ValueError(f"unknown layout {layout!r}")
+    page_offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    pages = max(int(page_offsets[-1]), 1)
+    q = normal(rng, (batch, query_heads, dim), "f16")
+    key_cache = normal(rng, (pages, page_size, kv_heads, dim), "f16")
+    value_cache = normal(rng, (pages, page_size, kv_heads, dim), "f16")
+    page_indices = (rng.permutation(pages) if shuffle else np.arange(pages)).astype(np.int32)
+    split_offsets = np.concatenate([[0]] + [page_offsets[b] + (np.arange(1, splits + 1) * counts[b]) // splits
+                                            for b in range(batch)]).astype(np.int32)
+    return q, key_cache, value_cache, page_offsets, page_indices, lengths, split_offsets

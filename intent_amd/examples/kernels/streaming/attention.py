@@ -91,6 +91,20 @@ def summarize_attention_chunk_bf16(key_chunk, value_chunk, key_coordinates, quer
 
 
 @intent.fn
+def summarize_masked_attention_chunk(key_chunk, value_chunk, key_coordinates, active, queries, query_coordinates,
+                                     scale):
+    """Decode chunk summary: every pair of an active key is valid (attention.py:250-290)."""
+    scores = I.matmul(queries, key_chunk, transpose_rhs=True, acc_dtype=I.f32) * (scale * I.LOG2E)
+    valid = I.full(scores.shape, fill=True, dtype=I.bool) & active[None, :]
+    masked = I.select(valid, scores, -I.inf)
+    any_valid = I.reduce.any(valid, axis=1)
+    chunk_max = I.select(any_valid, reduce_score_maximum(masked, axis=1), 0.0)
+    weights = I.select(valid, I.exp2(masked - chunk_max[:, None], approximate=True, flush_to_zero=True), 0.0)
+    return I.record(valid=any_valid, maximum=chunk_max, denominator=I.reduce.sum(weights, axis=1),
+                    accumulator=I.matmul(I.cast(weights, I.f16), value_chunk, acc_dtype=I.f32))
+
+
+@intent.fn
 def normalize_attention_summary(summary):
     denominator = I.select(summary.valid, summary.denominator, 1.0)
     reciprocal = I.fdiv(1.0, denominator, approximate=True, flush_to_zero=True)

@@ -21,6 +21,8 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   attention_backward_delta backward/attention.py:17-34     intent_hip_attention_bwd_delta
   attention_backward_dkdv backward/attention.py:87-137     intent_hip_attention_bwd_dkdv
   attention_backward_dq   backward/attention.py:171-211    intent_hip_attention_bwd_dq
+  paged_gqa_decode_partials streaming/paged_attention.py:77-165  intent_hip_paged_decode_partials
+  splitk_attention_f32_to_f16_reduce streaming/splitk_reduce.py:129-155  intent_hip_splitk_reduce_f32_to_f16
 
 (paths relative to python/intent/examples/kernels/ in the reference).
 
@@ -38,7 +40,7 @@ from typing import Callable
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
                       OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32,
-                      OP_SOFTMAX_BWD, OP_SOFTMAX_FWD)
+                      OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
 @dataclass
@@ -315,6 +317,66 @@ def _attention_bwd(kind):
     return plan
 
 
+# ------------------------------------------------------------------------------ paged decode
+def _positive_constexpr(constexprs, name):
+    value = constexprs[name]
+    if isinstance(value, bool) or not isinstance(value, int) or value < 1:
+        raise CompilationStageError("provider_configuration", f"{name} must be a positive int, got {value!r}")
+    return value
+
+
+def _paged_decode_partials(lib, bound, constexprs, device):
+    """paged_gqa_decode_partials: one workgroup per (job, key head). The page tables are read as
+    given; positions and physical pages outside their arrays are clamped by the kernel."""
+    (q, key_cache, value_cache, page_offsets, page_indices, lengths, split_offsets, partial_lse, partial_output,
+     scale) = bound.arguments
+    page_size = _positive_constexpr(constexprs, "PAGE_SIZE")
+    group = _positive_constexpr(constexprs, "HEAD_GROUP")
+    splits = _positive_constexpr(constexprs, "SPLITS")
+    batch, q_heads, d = q.shape
+    pages, ps, kv_heads, dv = value_cache.shape
+    if page_offsets.shape[0] != batch + 1:
+        raise ValueError(f"page_offsets must hold batch + 1 = {batch + 1} entries, got {page_offsets.shape[0]}")
+    if split_offsets.shape[0] != batch * splits + 1:
+        raise ValueError(f"split_offsets must hold batch * SPLITS + 1 = {batch * splits + 1} entries, "
+                         f"got {split_offsets.shape[0]}")
+    if kv_heads * group != q_heads:
+        raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({kv_heads}) * HEAD_GROUP ({group})")
+    keep = [q, key_cache, value_cache, page_offsets, page_indices, lengths, split_offsets, partial_lse,
+            partial_output]
+    before, after = [], []
+    qk = _readable(q, keep, before)
+    kk, vk = _readable(key_cache, keep, before, 8), _readable(value_cache, keep, before, 8)
+    tables = [_readable(t, keep, before) for t in (page_offsets, page_indices, lengths, split_offsets)]
+    ok = _writable(partial_output, keep, after)
+    strides = _strides(qk, kk, vk, partial_lse, ok)
+    keep.append(strides)
+    fn = lib.fn["paged_decode_partials"]
+    args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), *(t.data_ptr() for t in tables), partial_lse.data_ptr(),
+            ok.data_ptr(), batch, q_heads, d, pages, ps, kv_heads, dv, page_indices.shape[0], page_size, group,
+            splits, strides, float(scale))
+    return Launch("intent_hip_paged_decode_partials", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after),
+                  (("batch", batch), ("q_heads", q_heads), ("kv_heads", kv_heads), ("head_group", group),
+                   ("d", d), ("pages", pages), ("ps", ps), ("page_size", page_size), ("splits", splits)),
+                  lambda: lib.kernel_resources(OP_PAGED_DECODE_PARTIALS, F16, group, d))
+
+
+def _splitk_reduce(lib, bound, constexprs, device):
+    partial, lse, output = bound.arguments
+    keep, before, after = [partial, lse, output], [], []
+    pk, outk = _readable(partial, keep, before), _writable(output, keep, after)
+    batch, heads, splits, d = partial.shape
+    strides = _strides(pk, lse, outk)
+    keep.append(strides)
+    fn = lib.fn["splitk_reduce_f32_to_f16"]
+    args = (pk.data_ptr(), lse.data_ptr(), outk.data_ptr(), batch, heads, splits, d, strides)
+    return Launch("intent_hip_splitk_reduce_f32_to_f16", lambda stream: fn(*args, stream), tuple(keep),
+                  tuple(before), tuple(after),
+                  (("batch", batch), ("heads", heads), ("splits", splits), ("d", d)),
+                  lambda: lib.kernel_resources(OP_SPLITK_REDUCE, F32, batch * heads, d))
+
+
 # ------------------------------------------------------------------------------ SpMV
 def _csr_spmv(lib, bound, constexprs, device):
     import ctypes
@@ -379,6 +441,13 @@ _SPECS = (
                  (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
                   _view(IN, "f32", 3), _view(IN, "f32", 3), _view(OUT, "f16", 4), ("scalar", "f32")),
                  ("HEAD_GROUP", "CAUSAL"), _attention_bwd("dq")),
+    OperatorSpec("paged_gqa_decode_partials",
+                 (_view(IN, "f16", 3), _view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "i32", 1),
+                  _view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "i32", 1), _view(OUT, "f32", 3),
+                  _view(OUT, "f32", 4), ("scalar", "f32")), ("PAGE_SIZE", "HEAD_GROUP", "SPLITS"),
+                 _paged_decode_partials),
+    OperatorSpec("splitk_attention_f32_to_f16_reduce", (_view(IN, "f32", 4), _view(IN, "f32", 3),
+                                                        _view(OUT, "f16", 3)), (), _splitk_reduce),
     OperatorSpec("csr_spmv", (_view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "f32", 1), _view(IN, "f32", 1),
                               _view(OUT, "f32", 1)), (), _csr_spmv, derived=(("R", "R1", -1),)),
 )

@@ -573,6 +573,137 @@ int oracle_attention_bwd_dkdv(const uint16_t *q, const uint16_t *k, const uint16
   return 0;
 }
 
+/* ------------------------------------------------------------------ paged decode (split-K)
+ * streaming/paged_attention.py:77-165 (paged_gqa_decode_partials) with
+ * summarize_masked_attention_chunk (streaming/attention.py:250-285) and
+ * merge_attention_summaries (:82-114); contiguous layouts: q [B,HQ,D], key_cache [P,PS,HK,D],
+ * value_cache [P,PS,HK,DV], partial_lse [B,HQ,SPLITS], partial_output [B,HQ,SPLITS,DV].
+ * Job j = batch * SPLITS + split covers page positions [split_offsets[j], split_offsets[j+1]);
+ * token t of the job: position first + t / PS, offset t % PS, physical page page_indices[position],
+ * logical token (position - page_offsets[batch]) * PAGE_SIZE + offset, active below the sequence
+ * length. Chunks of `chunk` tokens are summarized (exp2 domain, P rounded to f16) and merged.
+ * partial_lse = maximum + logf(denominator) * log2e, partial_output = accumulator * (1 / den);
+ * an empty job gives -inf and zeros. */
+int oracle_paged_decode_partials(const uint16_t *q, const uint16_t *kc, const uint16_t *vc, const int32_t *page_offsets,
+                                 const int32_t *page_indices, const int32_t *lengths, const int32_t *split_offsets,
+                                 float *partial_lse, float *partial_out, int64_t batch, int64_t heads, int64_t d,
+                                 int64_t ps, int64_t kv_heads, int64_t dv, int64_t page_size, int64_t head_group,
+                                 int64_t splits, float scale, int64_t chunk, int workers) {
+  if (batch <= 0 || heads <= 0 || splits <= 0) return 0;
+  if (head_group < 1 || heads != kv_heads * head_group) return 1;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const float factor = scale * log2e;
+  const int64_t count = batch * splits * heads;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)dv), *cacc = (float *)malloc(sizeof(float) * (size_t)dv);
+    float *scores = (float *)malloc(sizeof(float) * (size_t)chunk);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t job = item / heads, h = item % heads, b = job / splits, split = job % splits;
+      const int64_t kh = h / head_group;
+      const int64_t first = split_offsets[job], pages = split_offsets[job + 1] - split_offsets[job];
+      const int64_t tokens = pages * ps, length = lengths[b], page_begin = page_offsets[b];
+      const uint16_t *qp = q + (b * heads + h) * d;
+      int valid = 0;
+      float maximum = 0.0f, denominator = 0.0f;
+      for (int64_t t = 0; t < dv; ++t) acc[t] = 0.0f;
+      for (int64_t t0 = 0; t0 < tokens; t0 += chunk) {
+        const int64_t t1 = t0 + chunk < tokens ? t0 + chunk : tokens;
+        int cvalid = 0;
+        float cmax = -INFINITY;
+        for (int64_t t = t0; t < t1; ++t) {
+          const int64_t position = first + t / ps, offset = t % ps;
+          const int64_t logical = (position - page_begin) * page_size + offset;
+          const int active = logical < length;
+          const uint16_t *kp = kc + ((page_indices[position] * ps + offset) * kv_heads + kh) * d;
+          float dot = 0.0f;
+          for (int64_t c = 0; c < d; ++c) dot = dot + oracle_half_to_float(qp[c]) * oracle_half_to_float(kp[c]);
+          scores[t - t0] = active ? dot * factor : -INFINITY;
+          if (active) {
+            cvalid = 1;
+            cmax = fmaxf(cmax, scores[t - t0]);
+          }
+        }
+        if (!cvalid) cmax = 0.0f;
+        float cden = 0.0f;
+        for (int64_t c = 0; c < dv; ++c) cacc[c] = 0.0f;
+        for (int64_t t = t0; t < t1; ++t) {
+          const int64_t position = first + t / ps, offset = t % ps;
+          const int active = (position - page_begin) * page_size + offset < length;
+          const float weight = active ? exp2_approx_ftz(scores[t - t0] - cmax) : 0.0f;
+          cden += weight;
+          const float w16 = oracle_half_to_float(oracle_float_to_half(weight));
+          const uint16_t *vp = vc + ((page_indices[position] * ps + offset) * kv_heads + kh) * dv;
+          for (int64_t c = 0; c < dv; ++c) cacc[c] = cacc[c] + w16 * oracle_half_to_float(vp[c]);
+        }
+        float merged = valid ? maximum : cmax;
+        if (cvalid) merged = fmaxf(merged, cmax);
+        const float left = valid ? exp2_approx_ftz(maximum - merged) : 0.0f;
+        const float right = cvalid ? exp2_approx_ftz(cmax - merged) : 0.0f;
+        denominator = left * denominator + right * cden;
+        for (int64_t c = 0; c < dv; ++c) acc[c] = left * acc[c] + right * cacc[c];
+        maximum = merged;
+        valid = valid || cvalid;
+      }
+      const float safe = valid ? denominator : 1.0f;
+      const float inverse = 1.0f / safe;
+      partial_lse[(b * heads + h) * splits + split] = valid ? maximum + logf(safe) * log2e : -INFINITY;
+      float *op = partial_out + ((b * heads + h) * splits + split) * dv;
+      for (int64_t c = 0; c < dv; ++c) op[c] = valid ? acc[c] * inverse : 0.0f;
+    }
+    free(acc);
+    free(cacc);
+    free(scores);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+/* streaming/splitk_reduce.py:129-155 (splitk_attention_f32_to_f16_reduce): per (b, h),
+ * m = maximum_num over splits of lse (identity -inf), w_s = expf(lse_s - m) (a natural exponential,
+ * as the definition writes it), out = f16((sum_s w_s * partial_s) * rcp_approx(sum_s w_s)). All
+ * splits empty (-inf) gives NaN, as the definition does. Contiguous [B,H,S,D], [B,H,S], [B,H,D]. */
+int oracle_splitk_reduce_f32_to_f16(const float *partial, const float *lse, uint16_t *out, int64_t batch,
+                                    int64_t heads, int64_t splits, int64_t d, int workers) {
+  if (batch <= 0 || heads <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int64_t count = batch * heads;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *num = (float *)malloc(sizeof(float) * (size_t)(d > 0 ? d : 1));
+    for (int64_t row = begin; row < end; ++row) {
+      const float *l = lse + row * splits;
+      float m = -INFINITY;
+      for (int64_t s = 0; s < splits; ++s) m = fmaxf(m, l[s]);
+      float den = 0.0f;
+      for (int64_t c = 0; c < d; ++c) num[c] = 0.0f;
+      for (int64_t s = 0; s < splits; ++s) {
+        const float w = expf(l[s] - m);
+        den = den + w;
+        const float *p = partial + (row * splits + s) * d;
+        for (int64_t c = 0; c < d; ++c) num[c] = num[c] + w * p[c];
+      }
+      const float r = rcp_approx_ftz(den);
+      for (int64_t c = 0; c < d; ++c) out[row * d + c] = oracle_float_to_half(num[c] * r);
+    }
+    free(num);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
 /* ------------------------------------------------------------------ CSR SpMV
  * sparse/csr_spmv.py:11-29: acc = 0.0f; for nz in [off[r], off[r+1]) in order:
  * acc = acc + values[nz] * vector[col[nz]] (product rounded, then added); y[r] = acc. */

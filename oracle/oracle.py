@@ -40,6 +40,9 @@ def lib():
         handle.oracle_attention_fwd_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                     ctypes.POINTER(i64), f, i, i64, i]
         handle.oracle_csr_spmv_f32.argtypes = [p, p, p, p, p, i64, i]
+        handle.oracle_paged_decode_partials.argtypes = [p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
+                                                        i64, i64, i64, f, i64, i]
+        handle.oracle_splitk_reduce_f32_to_f16.argtypes = [p, p, p, i64, i64, i64, i64, i]
         handle.oracle_attention_bwd_delta.argtypes = [p, p, p, i64, i64, i64, i64, ctypes.POINTER(i64), i]
         handle.oracle_attention_bwd_dq.argtypes = [p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                    ctypes.POINTER(i64), f, i, i64, i]
@@ -246,6 +249,37 @@ def attention_bwd_dkdv(q, k, v, dout, lse, delta, scale: float, causal: bool, *,
     if status:
         raise ValueError(f"oracle_attention_bwd_dkdv rejected the call ({status})")
     return dk, dv
+
+
+def paged_decode_partials(q, key_cache, value_cache, page_offsets, page_indices, lengths, split_offsets,
+                          scale: float, *, page_size: int, head_group: int, splits: int, chunk: int = 64,
+                          workers: int | None = None):
+    """paged_gqa_decode_partials: returns (partial_lse [B,HQ,SPLITS] f32, partial_output [B,HQ,SPLITS,DV] f32)."""
+    q, kc, vc = (np.ascontiguousarray(a, np.float16) for a in (q, key_cache, value_cache))
+    po, pi, ln, so = (np.ascontiguousarray(a, np.int32) for a in (page_offsets, page_indices, lengths,
+                                                                   split_offsets))
+    batch, heads, d = q.shape
+    ps, kv_heads, dv = kc.shape[1], kc.shape[2], vc.shape[3]
+    lse = np.empty((batch, heads, splits), np.float32)
+    out = np.empty((batch, heads, splits, dv), np.float32)
+    status = lib().oracle_paged_decode_partials(_ptr(q), _ptr(kc), _ptr(vc), _ptr(po), _ptr(pi), _ptr(ln), _ptr(so),
+                                                _ptr(lse), _ptr(out), batch, heads, d, ps, kv_heads, dv, page_size,
+                                                head_group, splits, float(np.float32(scale)), chunk,
+                                                workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_paged_decode_partials rejected the call ({status})")
+    return lse, out
+
+
+def splitk_reduce_f32_to_f16(partial, partial_lse, *, workers: int | None = None) -> np.ndarray:
+    """splitk_attention_f32_to_f16_reduce: partial [B,H,S,D] f32, lse [B,H,S] f32 -> [B,H,D] f16."""
+    partial = np.ascontiguousarray(partial, np.float32)
+    lse = np.ascontiguousarray(partial_lse, np.float32)
+    batch, heads, splits, d = partial.shape
+    out = np.empty((batch, heads, d), np.float16)
+    lib().oracle_splitk_reduce_f32_to_f16(_ptr(partial), _ptr(lse), _ptr(out), batch, heads, splits, d,
+                                          workers or default_workers())
+    return out
 
 
 def csr_spmv(offsets: np.ndarray, columns: np.ndarray, values: np.ndarray, x: np.ndarray, *,

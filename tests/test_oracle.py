@@ -382,3 +382,62 @@ def test_attention_backward_grouped_sums_heads():
     dq = oracle.attention_bwd_dq(q, k, v, do, lse, delta, 0.125, True, head_group=2)
     dq1 = oracle.attention_bwd_dq(q, kr, vr, do, lse, delta, 0.125, True, head_group=1)
     assert (dq.view(np.uint16) == dq1.view(np.uint16)).all()                # dq only reads K/V
+
+
+# ------------------------------------------------------------------------------ paged decode
+def _decode64(q, kc, vc, page_offsets, page_indices, lengths, scale, group, page_size):
+    """float64 decode attention over each sequence's logical tokens; also the base-2 lse."""
+    batch, heads, d = q.shape
+    out = np.zeros((batch, heads, vc.shape[3]))
+    lse2 = np.zeros((batch, heads))
+    for b in range(batch):
+        tokens = np.arange(lengths[b])
+        physical = page_indices[page_offsets[b] + tokens // page_size]
+        for h in range(heads):
+            k = kc[physical, tokens % page_size, h // group].astype(np.float64)
+            v = vc[physical, tokens % page_size, h // group].astype(np.float64)
+            s = k @ q[b, h].astype(np.float64) * scale
+            m = s.max()
+            w = np.exp(s - m)
+            out[b, h] = w @ v / w.sum()
+            lse2[b, h] = (m + np.log(w.sum())) / np.log(2)
+    return out, lse2
+
+
+def test_paged_decode_partials_one_split_is_attention():
+    q, kc, vc, po, pi, ln, so = inputs.paged_decode(seed=18, batch=3, query_heads=8, kv_heads=2, dim=64,
+                                                    page_size=16, lengths=(200, 37, 64), splits=1)
+    scale = float(np.float32(1 / np.sqrt(64)))
+    lse, out = oracle.paged_decode_partials(q, kc, vc, po, pi, ln, so, scale, page_size=16, head_group=4, splits=1)
+    want, want_lse = _decode64(q, kc, vc, po, pi, ln, scale, 4, 16)
+    assert np.all(np.abs(out[:, :, 0] - want) <= 2e-2 * np.abs(want) + 1e-2)
+    assert np.all(np.abs(lse[:, :, 0] - want_lse) <= 1e-4 * np.abs(want_lse) + 1e-4)
+
+
+def test_paged_decode_split_partials_merge_in_base_two():
+    q, kc, vc, po, pi, ln, so = inputs.paged_decode(seed=19, batch=2, query_heads=4, kv_heads=1, dim=64,
+                                                    page_size=16, lengths=(250, 90), splits=4)
+    scale = 0.125
+    lse, out = oracle.paged_decode_partials(q, kc, vc, po, pi, ln, so, scale, page_size=16, head_group=4, splits=4)
+    assert np.isneginf(lse[1, :, 3]).all() and (out[1, :, 3] == 0).all()   # sequence 1 ends before split 3
+    m = lse.max(axis=-1, keepdims=True)
+    w = np.exp2(lse.astype(np.float64) - m)
+    merged = np.einsum("bhs,bhsd->bhd", w, out.astype(np.float64)) / w.sum(-1)[..., None]
+    want, _ = _decode64(q, kc, vc, po, pi, ln, scale, 4, 16)
+    assert np.all(np.abs(merged - want) <= 2e-2 * np.abs(want) + 1e-2)
+
+
+def test_splitk_reduce_formula_and_empty_rows():
+    rng = np.random.default_rng(20)
+    partial = rng.standard_normal((2, 3, 5, 64)).astype(np.float32)
+    lse = (rng.standard_normal((2, 3, 5)) * 3).astype(np.float32)
+    lse[0, 1, 2] = -np.inf
+    lse[1, 2, :] = -np.inf
+    out = oracle.splitk_reduce_f32_to_f16(partial, lse).astype(np.float64)
+    l64 = lse.astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        w = np.exp(l64 - l64.max(-1, keepdims=True))                   # natural exp, as the definition writes
+        want = np.einsum("bhs,bhsd->bhd", w, partial.astype(np.float64)) / w.sum(-1)[..., None]
+    ok = ~np.isnan(want)
+    assert np.isnan(out[1, 2]).all() and np.isnan(want[1, 2]).all()    # every split empty -> NaN
+    assert np.all(np.abs(out[ok] - want[ok]) <= 2e-3 * np.abs(want[ok]) + 1e-3)
