@@ -7,7 +7,7 @@ then softmax_backward_f16 through prepared intent.jit calls; throughput = algori
 bytes (fwd 4*M*N + bwd 6*M*N = 671,088,640 B) / measured step time, inputs resident in
 HBM. `roofline` is the dominant kernel (the backward), timed with HIP events on the launch
 stream between the launches of the real fwd/bwd sequence. `operators` carries every other configuration (median of 33 graph replays,
-first dropped, 512 MiB flush of the 256 MB MALL before each), and
+first dropped, 512 MiB write-then-read flush of the 256 MB MALL before each), and
 `cpu_baseline` the oracle on a bounded sample on this host.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-operators] [--no-cpu-baseline]
@@ -58,15 +58,23 @@ def parse():
 
 # ------------------------------------------------------------------------------ GPU timing
 class Flush:
-    """Zeroes 512 MiB (twice the 256 MB MALL) outside each timed interval."""
+    """Writes zeros over 512 MiB (twice the 256 MB MALL), then reads it back, outside each timed
+    interval. The zero fill alone evicts the inputs but leaves the caches full of dirty lines
+    whose write-back the next (timed) kernel would pay for (measured: +28 us on the paged-decode
+    partials); the read-back leaves clean, unrelated lines, so the timed kernel starts cold and
+    pays only for its own traffic."""
 
     def __init__(self, device):
         import torch
 
         self.buffer = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+        self.words = self.buffer.view(torch.int32)
 
     def __call__(self):
+        import torch
+
         self.buffer.zero_()
+        torch.sum(self.words, dtype=torch.int64)
 
 
 def graph_median_ms(launch, flush, replays=33):

@@ -12,23 +12,28 @@
 //   splitk_attention_f32_to_f16_reduce (streaming/splitk_reduce.py:129-155): per (batch, head)
 //     m = maximum_num over splits of lse, w = exp(lse - m) (natural exponential, as the
 //     definition writes it), out = f16(sum w * partial * rcp_approx(sum w)).
-// The running maximum replaces each chunk's maximum before P is rounded, and the summed axes are
-// reassociated; the 16-bit tolerance covers both. Page positions and physical pages are clamped
-// into their arrays (the definition assumes them in bounds), so a bad index cannot fault.
+// P is rounded against each 64-token chunk's own maximum, as the definition's chunk summary does;
+// the chunk's merge factor exp2(chunk max - running max) is folded into the stored weights, and
+// the summed axes are reassociated. Scores use v_dot2_f32_f16 (f16 pair products summed in f32).
+// Page positions and physical pages are clamped into their arrays (the definition assumes them in
+// bounds), so a bad index cannot fault.
 //
 // Design (both kernels memory-bound):
 //   * partials: one workgroup per (job, key head), 4 waves taking 64-token chunks in turn. Per
-//     chunk, lane t scores token t against the group's queries (kept in LDS as f32); chunk
-//     maxima and sums are wave reductions; P goes through LDS to the P @ V phase, where lane l
-//     owns output dimensions (V rows are read coalesced, 4 bytes per lane per token). The four
-//     waves' states are merged in wave order at the end.
-//   * merge: one wave per (batch, head); lanes own output dimensions, the split loop is serial.
+//     chunk, lane t scores token t against the group's queries (f16 in LDS, read as broadcasts);
+//     chunk maxima and sums are wave reductions; P goes through LDS to the P @ V phase, where
+//     each lane loads 16 bytes of a V row (D / 8 lanes per token, the chunk's loads in flight
+//     together) and accumulates 8 output dimensions. Lanes sharing dimensions are folded once per
+//     job, then the four waves' states are merged in wave order.
+//   * merge: one single-wave workgroup per (batch, head) row; lanes own output dimensions, the
+//     split loop is unrolled so its loads overlap.
 #include "common.hpp"
 
 namespace intent_hip {
 namespace {
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
@@ -43,14 +48,17 @@ struct DecodeGeometry {
 // kG bounds the query heads per key head (the group runs 1..kG; register arrays are sized by kG
 // and every loop over them is unrolled with a uniform guard, so nothing is indexed dynamically).
 template <int D, int kG>
-__global__ __launch_bounds__(kThreads) void paged_decode_partials(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kG <= 4 ? 4 : 2))) void paged_decode_partials(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ KC, const uint16_t *__restrict__ VC,
     const int32_t *__restrict__ page_offsets, const int32_t *__restrict__ page_indices,
     const int32_t *__restrict__ lengths, const int32_t *__restrict__ split_offsets, float *__restrict__ LSE,
     float *__restrict__ OUT, int kv_heads, int group, int splits, int64_t pages, int ps, int64_t positions,
     int page_size, DecodeGeometry g, float scale) {
-  constexpr int kDims = D / 64;        // output dimensions per lane
-  __shared__ float q_s[kG * D];
+  constexpr int kLanesPerToken = D / 8;            // 16 bytes of a row per lane
+  constexpr int kTokensPerLoad = 64 / kLanesPerToken;
+  constexpr int kSlots = kChunk / kTokensPerLoad;   // loads per lane for a whole chunk
+  constexpr int kBatch = kG >= 16 ? kSlots / 4 : kSlots / 2;
+  __shared__ __attribute__((aligned(16))) uint16_t q_s[kG * D];
   __shared__ float p_s[kWaves][kG][kChunk];
   __shared__ int64_t row_s[kWaves][kChunk];   // per token: physical row offset (elements) in the caches
   __shared__ float m_s[kWaves][kG], den_s[kWaves][kG];
@@ -59,8 +67,13 @@ __global__ __launch_bounds__(kThreads) void paged_decode_partials(
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kh = static_cast<int>(blockIdx.x) % kv_heads;
-  const int job = static_cast<int>(blockIdx.x) / kv_heads;
+  // Workgroups go to the 8 XCDs round-robin; give each XCD a contiguous run of (job, key head)
+  // items so every key head of a job runs on one XCD together and the 2 KB token rows of the
+  // interleaved caches are read whole, close in time.
+  const int n = static_cast<int>(gridDim.x), xcd = static_cast<int>(blockIdx.x) % 8;
+  const int item = xcd * (n / 8) + (xcd < n % 8 ? xcd : n % 8) + static_cast<int>(blockIdx.x) / 8;
+  const int kh = item % kv_heads;
+  const int job = item / kv_heads;
   const int b = job / splits, split = job % splits;
   const int first = split_offsets[job];
   int64_t count = static_cast<int64_t>(split_offsets[job + 1]) - first;
@@ -71,17 +84,18 @@ __global__ __launch_bounds__(kThreads) void paged_decode_partials(
 
   for (int i = tid; i < group * D; i += kThreads) {
     const int gq = i / D, c = i % D;
-    q_s[i] = static_cast<float>(__builtin_bit_cast(_Float16, Q[b * g.q[0] + (kh * group + gq) * g.q[1] + c]));
+    q_s[i] = Q[b * g.q[0] + (kh * group + gq) * g.q[1] + c];
   }
   __syncthreads();
 
-  float m[kG], den[kG], acc[kG][kDims];
+  const int token_lane = lane / kLanesPerToken, dim0 = (lane % kLanesPerToken) * 8;
+  float m[kG], den[kG], acc[kG][8];
 #pragma unroll
   for (int gq = 0; gq < kG; ++gq) {
     m[gq] = -INFINITY;
     den[gq] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kDims; ++j) acc[gq][j] = 0.0f;
+    for (int e = 0; e < 8; ++e) acc[gq][e] = 0.0f;
   }
   bool valid = false;
 
@@ -104,27 +118,26 @@ __global__ __launch_bounds__(kThreads) void paged_decode_partials(
       row_s[wave][lane] = physical * g.v[0] + offset * g.v[1] + kh * g.v[2];
     }
     if (active) {                                  // inactive tokens are never read for scores
-      const uint16_t *krow = KC + key_row;
-      f16x8_t kv[D / 8];
+      // q.k with v_dot2_f32_f16 (products of f16 pairs summed in f32), half a row at a time.
+      const uint4 *krow = reinterpret_cast<const uint4 *>(KC + key_row);
 #pragma unroll
-      for (int c = 0; c < D / 8; ++c) kv[c] = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4 *>(krow + 8 * c));
+      for (int half = 0; half < 2; ++half) {
+        uint4 kv[D / 16];
 #pragma unroll
-      for (int c = 0; c < D / 8; ++c) {
+        for (int c = 0; c < D / 16; ++c) kv[c] = krow[half * (D / 16) + c];
 #pragma unroll
-        for (int gq = 0; gq < kG; ++gq) {
-          if (gq < group) {
-            const float4 qa = *reinterpret_cast<const float4 *>(q_s + gq * D + 8 * c);
-            const float4 qb = *reinterpret_cast<const float4 *>(q_s + gq * D + 8 * c + 4);
-            float t = s[gq];
-            t = fmaf(qa.x, static_cast<float>(kv[c][0]), t);
-            t = fmaf(qa.y, static_cast<float>(kv[c][1]), t);
-            t = fmaf(qa.z, static_cast<float>(kv[c][2]), t);
-            t = fmaf(qa.w, static_cast<float>(kv[c][3]), t);
-            t = fmaf(qb.x, static_cast<float>(kv[c][4]), t);
-            t = fmaf(qb.y, static_cast<float>(kv[c][5]), t);
-            t = fmaf(qb.z, static_cast<float>(kv[c][6]), t);
-            t = fmaf(qb.w, static_cast<float>(kv[c][7]), t);
-            s[gq] = t;
+        for (int c = 0; c < D / 16; ++c) {
+#pragma unroll
+          for (int gq = 0; gq < kG; ++gq) {
+            if (gq < group) {
+              const uint4 qv = *reinterpret_cast<const uint4 *>(q_s + gq * D + (half * (D / 16) + c) * 8);
+              float t = s[gq];
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.x), __builtin_bit_cast(f16x2_t, kv[c].x), t, false);
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.y), __builtin_bit_cast(f16x2_t, kv[c].y), t, false);
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.z), __builtin_bit_cast(f16x2_t, kv[c].z), t, false);
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.w), __builtin_bit_cast(f16x2_t, kv[c].w), t, false);
+              s[gq] = t;
+            }
           }
         }
       }
@@ -132,12 +145,12 @@ __global__ __launch_bounds__(kThreads) void paged_decode_partials(
     if (!__any(active)) continue;                  // wave-uniform: no active token in this chunk
     valid = true;
     // Chunk summary as the definition forms it: weights against the chunk's own maximum, rounded
-    // to f16 for P @ V; the chunk is then merged into the running state with exp2 factors.
-    float left[kG], right[kG];
+    // to f16 for P @ V; the chunk joins the running state with exp2 factors (left for the state,
+    // right for the chunk, folded into the stored weights).
+    float left[kG];
 #pragma unroll
     for (int gq = 0; gq < kG; ++gq) {
-      left[gq] = 0.0f;
-      right[gq] = 0.0f;
+      left[gq] = 1.0f;
       if (gq < group) {
         const float score = active ? s[gq] * c1 : -INFINITY;
         const float chunk_max = wave_max(score);
@@ -145,48 +158,55 @@ __global__ __launch_bounds__(kThreads) void paged_decode_partials(
         const float chunk_den = wave_sum(p);
         const float next = fmaxf(m[gq], chunk_max);
         left[gq] = m[gq] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[gq] - next);
-        right[gq] = __builtin_amdgcn_exp2f(chunk_max - next);
+        const float right = __builtin_amdgcn_exp2f(chunk_max - next);
         m[gq] = next;
-        den[gq] = left[gq] * den[gq] + right[gq] * chunk_den;
-        p_s[wave][gq][lane] = static_cast<float>(static_cast<_Float16>(p));
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    // P @ V: lane l owns dimensions l * kDims .. + kDims; V rows are read whole by the wave.
-    float cacc[kG][kDims];
-#pragma unroll
-    for (int gq = 0; gq < kG; ++gq)
-#pragma unroll
-      for (int j = 0; j < kDims; ++j) cacc[gq][j] = 0.0f;
-    const int chunk_tokens = tokens - c0 < kChunk ? tokens - c0 : kChunk;
-#pragma unroll 4
-    for (int t = 0; t < chunk_tokens; ++t) {
-      const uint16_t *vrow = VC + row_s[wave][t];
-      float vv[kDims];
-      if constexpr (kDims == 2) {
-        const uint32_t pair = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(vrow) + lane);
-        vv[0] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair & 0xffffu)));
-        vv[1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16)));
-      } else {
-        vv[0] = static_cast<float>(__builtin_bit_cast(_Float16, __builtin_nontemporal_load(vrow + lane)));
-      }
-#pragma unroll
-      for (int gq = 0; gq < kG; ++gq) {
-        if (gq < group) {
-          const float p = p_s[wave][gq][t];
-#pragma unroll
-          for (int j = 0; j < kDims; ++j) cacc[gq][j] = fmaf(p, vv[j], cacc[gq][j]);
-        }
+        den[gq] = left[gq] * den[gq] + right * chunk_den;
+        p_s[wave][gq][lane] = right * static_cast<float>(static_cast<_Float16>(p));
       }
     }
 #pragma unroll
     for (int gq = 0; gq < kG; ++gq)
       if (gq < group)
 #pragma unroll
-        for (int j = 0; j < kDims; ++j) acc[gq][j] = left[gq] * acc[gq][j] + right[gq] * cacc[gq][j];
+        for (int j = 0; j < 8; ++j) acc[gq][j] *= left[gq];
+    __builtin_amdgcn_wave_barrier();
+    // P @ V: lane l reads dimensions 8 (l % kLanesPerToken) .. + 8 of token
+    // slot * kTokensPerLoad + l / kLanesPerToken; one load per slot, all slots of a batch in flight.
+    const int chunk_tokens = tokens - c0 < kChunk ? tokens - c0 : kChunk;
+#pragma unroll
+    for (int base = 0; base < kSlots; base += kBatch) {
+      f16x8_t vv[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int token = (base + j) * kTokensPerLoad + token_lane;
+        vv[j] = f16x8_t{};
+        if (token < chunk_tokens)
+          vv[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8_t *>(VC + row_s[wave][token] + dim0));
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int token = (base + j) * kTokensPerLoad + token_lane;
+#pragma unroll
+        for (int gq = 0; gq < kG; ++gq) {
+          if (gq < group) {
+            const float p = p_s[wave][gq][token];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[gq][e] = fmaf(p, static_cast<float>(vv[j][e]), acc[gq][e]);
+          }
+        }
+      }
+    }
     __builtin_amdgcn_wave_barrier();
   }
+
+  // Lanes that share dimensions hold sums over different tokens: fold them once.
+#pragma unroll
+  for (int gq = 0; gq < kG; ++gq)
+    if (gq < group)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int x = kLanesPerToken; x < 64; x <<= 1) acc[gq][e] += __shfl_xor(acc[gq][e], x);
 
   // Merge the waves' states in wave order.
   if (lane == 0) valid_s[wave] = valid ? 1 : 0;
@@ -197,8 +217,9 @@ __global__ __launch_bounds__(kThreads) void paged_decode_partials(
         m_s[wave][gq] = m[gq];
         den_s[wave][gq] = den[gq];
       }
+      if (lane < kLanesPerToken)
 #pragma unroll
-      for (int j = 0; j < kDims; ++j) acc_s[wave][gq][lane * kDims + j] = acc[gq][j];
+        for (int e = 0; e < 8; ++e) acc_s[wave][gq][dim0 + e] = acc[gq][e];
     }
   }
   __syncthreads();
@@ -225,26 +246,28 @@ __global__ __launch_bounds__(kThreads) void paged_decode_partials(
   }
 }
 
-__global__ __launch_bounds__(kThreads) void splitk_reduce_f32_to_f16(const float *__restrict__ P,
-                                                                     const float *__restrict__ LSE,
-                                                                     uint16_t *__restrict__ OUT, int heads, int splits,
-                                                                     int d, int64_t rows, DecodeGeometry g) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  if (row >= rows) return;
+// One wave per (batch, head) row, one workgroup per row so the rows spread over every CU. Lanes
+// own output dimensions; the split loop is unrolled so its loads are in flight together.
+__global__ __launch_bounds__(64) void splitk_reduce_f32_to_f16(const float *__restrict__ P,
+                                                              const float *__restrict__ LSE,
+                                                              uint16_t *__restrict__ OUT, int heads, int splits,
+                                                              int d, DecodeGeometry g) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
   const int64_t b = row / heads, h = row % heads;
   const float *lse = LSE + b * g.lse[0] + h * g.lse[1];
   float top = -INFINITY;
-  for (int s = 0; s < splits; ++s) top = fmaxf(top, lse[s * g.lse[2]]);
+  for (int s = lane; s < splits; s += 64) top = fmaxf(top, lse[s * g.lse[2]]);
+  top = wave_max(top);
   float den = 0.0f;
-  for (int s = 0; s < splits; ++s) den += expf(lse[s * g.lse[2]] - top);
+  for (int s = lane; s < splits; s += 64) den += expf(lse[s * g.lse[2]] - top);
+  den = wave_sum(den);
   const float inv = __builtin_amdgcn_rcpf(den);
+  const float *prow = P + b * g.q[0] + h * g.q[1];
   for (int c = lane; c < d; c += 64) {
     float num = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-      const float w = expf(lse[s * g.lse[2]] - top);
-      num = fmaf(w, P[b * g.q[0] + h * g.q[1] + s * g.q[2] + c], num);
-    }
+#pragma unroll 8
+    for (int s = 0; s < splits; ++s) num = fmaf(expf(lse[s * g.lse[2]] - top), prow[s * g.q[2] + c], num);
     OUT[b * g.out[0] + h * g.out[1] + c] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(num * inv));
   }
 }
@@ -268,7 +291,7 @@ const void *partials_kernel(int64_t group, const char **name) {
 int decode_resources(int64_t which, int64_t d, int64_t group, IntentHipKernelResources *out) {
   if (which == 1)
     return describe_kernel(reinterpret_cast<const void *>(&splitk_reduce_f32_to_f16), "splitk_reduce_f32_to_f16",
-                           kThreads, out);
+                           64, out);
   const char *name = nullptr;
   const void *kernel = d == 64 ? partials_kernel<64>(group, &name) : partials_kernel<128>(group, &name);
   return describe_kernel(kernel, name, kThreads, out);
@@ -315,10 +338,10 @@ extern "C" int intent_hip_paged_decode_partials(const void *q, const void *key_c
   if (g.q[2] != 1 || g.k[3] != 1 || g.v[3] != 1 || g.out[3] != 1)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "q, caches and partial_output need unit inner stride");
   for (int i = 0; i < 3; ++i)
-    if (g.k[i] % 8 || g.v[i] % 2)
-      return fail(INTENT_HIP_ERR_UNSUPPORTED, "cache strides must be multiples of 8 (keys) and 2 (values)");
-  if (!aligned(key_cache, 16) || !aligned(value_cache, 4))
-    return fail(INTENT_HIP_ERR_UNSUPPORTED, "key cache must be 16-byte and value cache 4-byte aligned");
+    if (g.k[i] % 8 || g.v[i] % 8)
+      return fail(INTENT_HIP_ERR_UNSUPPORTED, "cache strides must be multiples of 8 elements");
+  if (!aligned(key_cache, 16) || !aligned(value_cache, 16))
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "key and value caches must be 16-byte aligned");
   const int64_t blocks = batch * splits * kv_heads;
   if (blocks > INT32_MAX || ps > INT32_MAX || page_size > INT32_MAX || positions * ps >= INT32_MAX)
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "extents too large");
@@ -352,10 +375,10 @@ extern "C" int intent_hip_splitk_reduce_f32_to_f16(const float *partial, const f
   if ((strides[3] != 1 || strides[9] != 1) && d > 1)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "partial and output need unit inner stride");
   const int64_t rows = batch * heads;
-  const dim3 grid(static_cast<unsigned>((rows + kWaves - 1) / kWaves));
-  splitk_reduce_f32_to_f16<<<grid, dim3(kThreads), 0, as_stream(stream)>>>(
+  if (rows > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "extents too large");
+  splitk_reduce_f32_to_f16<<<dim3(static_cast<unsigned>(rows)), dim3(64), 0, as_stream(stream)>>>(
       partial, lse, static_cast<uint16_t *>(out), static_cast<int>(heads), static_cast<int>(splits),
-      static_cast<int>(d), rows, g);
+      static_cast<int>(d), g);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("splitk_reduce_f32_to_f16");
   return INTENT_HIP_OK;
 }

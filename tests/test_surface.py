@@ -222,6 +222,27 @@ def test_attention_backward_definitions_and_sequence():
         PreparedSequence((), outputs=None)
 
 
+def test_paged_decode_definitions_recognised_with_reference_signatures():
+    from intent_amd.examples.kernels.streaming.paged_attention import paged_gqa_decode_partials
+    from intent_amd.examples.kernels.streaming.splitk_reduce import splitk_attention_f32_to_f16_reduce
+    from intent_amd.examples.programs.composition import PagedDecode
+
+    options = {"PAGE_SIZE": 16, "HEAD_GROUP": 4, "SPLITS": 8}
+    iface = PublicInterface.from_definition(paged_gqa_decode_partials, options)
+    assert recognize(paged_gqa_decode_partials, iface, tuple(options)).name == "paged_gqa_decode_partials"
+    assert list(paged_gqa_decode_partials.signature.parameters) == [
+        "q", "key_cache", "value_cache", "page_offsets", "page_indices", "sequence_lengths", "split_offsets",
+        "partial_lse", "partial_output", "scale", "PAGE_SIZE", "HEAD_GROUP", "SPLITS"]
+    # the SPLITS constexpr sizes both outputs, so they allocate from the inputs alone
+    outputs = [p for p in iface.parameters if getattr(p, "writable", False)]
+    assert [p.shape[-1] for p in outputs][:1] == [8]
+    iface.require_output_allocation()
+    merge = PublicInterface.from_definition(splitk_attention_f32_to_f16_reduce, {})
+    assert recognize(splitk_attention_f32_to_f16_reduce, merge, ()).name == "splitk_attention_f32_to_f16_reduce"
+    assert list(splitk_attention_f32_to_f16_reduce.signature.parameters) == ["partial", "partial_lse", "output"]
+    assert PagedDecode.mutable_inputs == ()
+
+
 def test_generated_program_save_load_roundtrip(tmp_path):
     """generate -> save (kernel.source, kernel.mlir, artifact.json) -> load -> materialize, without a GPU."""
     import json
