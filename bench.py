@@ -47,7 +47,7 @@ def parse():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
-                                "attention_bwd,attention_bwd_large,paged_decode")
+                                "attention_bwd,attention_bwd_large,paged_decode,spmm")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -502,10 +502,42 @@ def op_paged_decode(device, flush, cpu):
     return out
 
 
+def op_spmm(device, flush, cpu):
+    """csr_spmm at the sparse/csr_spmm.py:5-9 constants: 8192 x 8192, 32 nonzeros per row, 128 f32
+    features. The dense operand (4 MB) is re-read per nonzero from L2/MALL; algorithmic HBM bytes
+    are the CSR arrays, dense once and the output."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.sparse.csr_spmm import csr_spmm
+
+    offsets, columns, values, dense = inputs.csr_spmm()
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    call = intent.jit(csr_spmm, backend="hip").prepare(t(offsets), t(columns), t(values), t(dense))
+    ms = graph_median_ms(call.launch, flush)
+    rows, nnz = offsets.shape[0] - 1, int(offsets[-1])
+    cols, features = dense.shape
+    nbytes = 4 * (rows + 1) + 8 * nnz + 4 * cols * features + 4 * rows * features
+    gathered = 4 * nnz * features
+    out = {"config": f"CSR SpMM f32 {rows}x{cols}, {nnz} nnz (32 per row), {features} features",
+           "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+           "gathered_gbs": round(gathered / ms / 1e6, 1), "gflops": round(2 * nnz * features / ms / 1e6, 1)}
+    if cpu:
+        import oracle
+
+        seconds = cpu_median_seconds(lambda: oracle.csr_spmm(offsets, columns, values, dense))
+        out["cpu"] = {"gbs": round(nbytes / seconds / 1e9, 3), "cores": oracle.default_workers(), "kind": "port",
+                      "sample": "the whole workload"}
+    return out
+
+
 OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_attention, "spmv": op_spmv,
              "gemm_f16_relu": op_gemm_f16_relu, "gemm_f32": op_gemm_f32, "linear_f32": op_linear_f32,
              "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
-             "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode}
+             "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode,
+             "spmm": op_spmm}
 
 
 def read_traffic(name):

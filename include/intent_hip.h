@@ -55,7 +55,8 @@ enum IntentHipOperator {
   INTENT_HIP_OP_ATTENTION_BWD_DQ = 9,
   INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10,
   INTENT_HIP_OP_PAGED_DECODE_PARTIALS = 11, /* rows = HEAD_GROUP, cols = head dimension */
-  INTENT_HIP_OP_SPLITK_REDUCE = 12
+  INTENT_HIP_OP_SPLITK_REDUCE = 12,
+  INTENT_HIP_OP_CSR_SPMM_F32 = 13         /* cols = features */
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -226,6 +227,17 @@ int intent_hip_csr_spmv_workspace_bytes(int64_t rows, int64_t nnz, size_t *bytes
 int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t *column_indices,
                             const float *values, const float *x, float *y, int64_t rows,
                             int64_t cols, int64_t nnz, void *workspace, size_t workspace_bytes,
+                            void *stream);
+
+/* CSR SpMM out = A dense, f32 values and features, i32 indices.
+ * csr_spmm (python/intent/examples/kernels/sparse/csr_spmm.py:11-33), with dynamic extents:
+ * row_offsets [rows + 1], column_indices and values [nnz], dense [cols, features] with row stride
+ * ldd, out [rows, features] with row stride ldo. Each output element is the left fold over the
+ * row's nonzeros in order, acc = acc + values[nz] * dense[col, f] with the product rounded before
+ * the add. Columns outside [0, cols) read row cols - 1; offsets are clamped to [0, nnz]. */
+int intent_hip_csr_spmm_f32(const int32_t *row_offsets, const int32_t *column_indices,
+                            const float *values, const float *dense, float *out, int64_t rows,
+                            int64_t cols, int64_t nnz, int64_t features, int64_t ldd, int64_t ldo,
                             void *stream);
 
 #ifdef __cplusplus

@@ -127,6 +127,16 @@ def spmv_f32(seed: int = 0, rows: int = SPMV_ROWS, cap: int = SPMV_CAP, c: float
     return offsets, columns, values, x
 
 
+def csr_spmm(seed: int = 0, rows: int = 8192, cols: int = 8192, per_row: int = 32, features: int = 128):
+    """Inputs of csr_spmm at the sparse/csr_spmm.py:5-9 constants by default: `per_row` distinct,
+    sorted, uniform columns in every row; values = U(-1,1); dense = U(-1,1) [cols, features]."""
+    rng = np.random.default_rng(seed)
+    offsets, columns = csr_matrix(rng, np.full(rows, per_row, np.int64), cols)
+    values = uniform(rng, offsets[-1], -1.0, 1.0)
+    dense = uniform(rng, (cols, features), -1.0, 1.0)
+    return offsets, columns, values, dense
+
+
 def paged_decode(seed: int = 0, batch: int = 8, query_heads: int = 32, kv_heads: int = 8, dim: int = 128,
                  page_size: int = 64, lengths=(8191, 7937, 7683, 7429, 7175, 6921, 6667, 6413), splits: int = 16,
                  shuffle: bool = True, layout: str = "padded"):

@@ -23,6 +23,7 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   attention_backward_dq   backward/attention.py:171-211    intent_hip_attention_bwd_dq
   paged_gqa_decode_partials streaming/paged_attention.py:77-165  intent_hip_paged_decode_partials
   splitk_attention_f32_to_f16_reduce streaming/splitk_reduce.py:129-155  intent_hip_splitk_reduce_f32_to_f16
+  csr_spmm                sparse/csr_spmm.py:11-33         intent_hip_csr_spmm_f32
 
 (paths relative to python/intent/examples/kernels/ in the reference).
 
@@ -40,7 +41,7 @@ from typing import Callable
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
                       OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32,
-                      OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
+                      OP_CSR_SPMM_F32, OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
 @dataclass
@@ -406,6 +407,28 @@ def _csr_spmv(lib, bound, constexprs, device):
                   lambda: lib.kernel_resources(OP_CSR_SPMV_F32, F32, rows, nnz))
 
 
+def _csr_spmm(lib, bound, constexprs, device):
+    """csr_spmm: rows read through their own strides (unit inner stride required, staged otherwise)."""
+    offsets, columns, values, dense, output = bound.arguments
+    rows = offsets.shape[0] - 1
+    if rows < 0 or output.shape[0] != rows:
+        raise ValueError("csr_spmm requires row_offsets.shape[0] == output.shape[0] + 1")
+    if columns.shape[0] != values.shape[0]:
+        raise ValueError("csr_spmm requires column_indices and values of equal length")
+    if dense.shape[1] != output.shape[1]:
+        raise ValueError("csr_spmm requires dense and output of equal feature width")
+    keep, before, after = [offsets, columns, values, dense, output], [], []
+    ok, ck, vk = (_readable(offsets, keep, before), _readable(columns, keep, before), _readable(values, keep, before))
+    dk, outk = _readable(dense, keep, before), _writable(output, keep, after)
+    nnz, cols, features = values.shape[0], dense.shape[0], dense.shape[1]
+    fn = lib.fn["csr_spmm_f32"]
+    args = (ok.data_ptr(), ck.data_ptr(), vk.data_ptr(), dk.data_ptr(), outk.data_ptr(), rows, cols, nnz, features,
+            _row_stride(dk) if cols else features, _row_stride(outk) if rows else features)
+    return Launch("intent_hip_csr_spmm_f32", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("rows", rows), ("cols", cols), ("nnz", nnz), ("features", features)),
+                  lambda: lib.kernel_resources(OP_CSR_SPMM_F32, F32, rows, features))
+
+
 _SPECS = (
     OperatorSpec("stable_softmax", (_view(IN, "f32", 2), _view(OUT, "f32", 2)), (), _softmax_fwd(F32), True),
     OperatorSpec("stable_softmax_f16", (_view(IN, "f16", 2), _view(OUT, "f16", 2)), (), _softmax_fwd(F16), True),
@@ -448,6 +471,8 @@ _SPECS = (
                  _paged_decode_partials),
     OperatorSpec("splitk_attention_f32_to_f16_reduce", (_view(IN, "f32", 4), _view(IN, "f32", 3),
                                                         _view(OUT, "f16", 3)), (), _splitk_reduce),
+    OperatorSpec("csr_spmm", (_view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "f32", 1), _view(IN, "f32", 2),
+                              _view(OUT, "f32", 2)), (), _csr_spmm, derived=(("R", "R1", -1),)),
     OperatorSpec("csr_spmv", (_view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "f32", 1), _view(IN, "f32", 1),
                               _view(OUT, "f32", 1)), (), _csr_spmv, derived=(("R", "R1", -1),)),
 )

@@ -704,6 +704,38 @@ int oracle_splitk_reduce_f32_to_f16(const float *partial, const float *lse, uint
   return 0;
 }
 
+/* ------------------------------------------------------------------ CSR SpMM
+ * sparse/csr_spmm.py:11-33: per row r and feature f, acc = 0.0f; for nz in [off[r], off[r+1]) in
+ * order: acc = acc + values[nz] * dense[col[nz], f] (product rounded, then added); out[r, f] = acc.
+ * dense [cols, features] with row stride ldd, out [rows, features] with row stride ldo. */
+int oracle_csr_spmm_f32(const int32_t *off, const int32_t *col, const float *val, const float *dense, float *out,
+                        int64_t rows, int64_t features, int64_t ldd, int64_t ldo, int workers) {
+  if (rows <= 0 || features <= 0) return 0;
+  const uint32_t csr = enter_ieee();
+  const int size = team_size(workers, rows);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(rows, omp_get_thread_num(), size, &begin, &end);
+    for (int64_t r = begin; r < end; ++r) {
+      float *o = out + r * ldo;
+      for (int64_t f = 0; f < features; ++f) o[f] = 0.0f;
+      for (int64_t nz = off[r]; nz < off[r + 1]; ++nz) {
+        const float v = val[nz];
+        const float *d = dense + (int64_t)col[nz] * ldd;
+        for (int64_t f = 0; f < features; ++f) {
+          const float product = v * d[f];
+          o[f] = o[f] + product;
+        }
+      }
+    }
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
 /* ------------------------------------------------------------------ CSR SpMV
  * sparse/csr_spmv.py:11-29: acc = 0.0f; for nz in [off[r], off[r+1]) in order:
  * acc = acc + values[nz] * vector[col[nz]] (product rounded, then added); y[r] = acc. */

@@ -40,6 +40,7 @@ def lib():
         handle.oracle_attention_fwd_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                     ctypes.POINTER(i64), f, i, i64, i]
         handle.oracle_csr_spmv_f32.argtypes = [p, p, p, p, p, i64, i]
+        handle.oracle_csr_spmm_f32.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i]
         handle.oracle_paged_decode_partials.argtypes = [p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                         i64, i64, i64, f, i64, i]
         handle.oracle_splitk_reduce_f32_to_f16.argtypes = [p, p, p, i64, i64, i64, i64, i]
@@ -279,6 +280,20 @@ def splitk_reduce_f32_to_f16(partial, partial_lse, *, workers: int | None = None
     out = np.empty((batch, heads, d), np.float16)
     lib().oracle_splitk_reduce_f32_to_f16(_ptr(partial), _ptr(lse), _ptr(out), batch, heads, splits, d,
                                           workers or default_workers())
+    return out
+
+
+def csr_spmm(offsets: np.ndarray, columns: np.ndarray, values: np.ndarray, dense: np.ndarray, *,
+             workers: int | None = None) -> np.ndarray:
+    """csr_spmm: out [rows, features] f32, each feature folded over the row's nonzeros in order."""
+    offsets = np.ascontiguousarray(offsets, np.int32)
+    columns = np.ascontiguousarray(columns, np.int32)
+    values = np.ascontiguousarray(values, np.float32)
+    dense = np.ascontiguousarray(dense, np.float32)
+    rows, features = offsets.shape[0] - 1, dense.shape[1]
+    out = np.empty((rows, features), np.float32)
+    lib().oracle_csr_spmm_f32(_ptr(offsets), _ptr(columns), _ptr(values), _ptr(dense), _ptr(out), rows, features,
+                              features, features, workers or default_workers())
     return out
 
 

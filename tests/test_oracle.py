@@ -441,3 +441,34 @@ def test_splitk_reduce_formula_and_empty_rows():
     ok = ~np.isnan(want)
     assert np.isnan(out[1, 2]).all() and np.isnan(want[1, 2]).all()    # every split empty -> NaN
     assert np.all(np.abs(out[ok] - want[ok]) <= 2e-3 * np.abs(want[ok]) + 1e-3)
+
+
+def test_csr_spmm_columns_are_pinned_spmv_folds():
+    """Every output column is csr_spmv of that dense column, bit for bit (same left fold, product
+    rounded then added); the csr_spmv oracle is pinned by its golden vectors."""
+    offsets, columns, values, dense = inputs.csr_spmm(seed=21, rows=300, cols=257, per_row=9, features=13)
+    out = oracle.csr_spmm(offsets, columns, values, dense)
+    for f in range(dense.shape[1]):
+        assert (out[:, f] == oracle.csr_spmv(offsets, columns, values, np.ascontiguousarray(dense[:, f]))).all()
+
+
+def test_csr_spmm_against_scipy_float64_and_probes():
+    import scipy.sparse
+
+    offsets, columns, values, dense = inputs.csr_spmm(seed=22, rows=512, cols=400, per_row=17, features=64)
+    out = oracle.csr_spmm(offsets, columns, values, dense).astype(np.float64)
+    a = scipy.sparse.csr_matrix((values.astype(np.float64), columns, offsets), shape=(512, 400))
+    want = a @ dense.astype(np.float64)
+    mag = abs(a) @ np.abs(dense.astype(np.float64))
+    assert np.all(np.abs(out - want) <= 17 * 2.0 ** -24 * mag + 1e-38)
+    # identity dense: out[r, c] = value of (r, c) (exact); ragged rows with empty ones
+    lengths = np.array([0, 3, 1, 0, 5], np.int64)
+    rng = np.random.default_rng(23)
+    off, col = inputs.csr_matrix(rng, lengths, 6)
+    val = inputs.uniform(rng, off[-1], -1, 1)
+    got = oracle.csr_spmm(off, col, val, np.eye(6, dtype=np.float32))
+    expect = np.zeros((5, 6), np.float32)
+    for r in range(5):
+        for nz in range(off[r], off[r + 1]):
+            expect[r, col[nz]] = val[nz]
+    assert (got == expect).all()

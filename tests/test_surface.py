@@ -243,6 +243,14 @@ def test_paged_decode_definitions_recognised_with_reference_signatures():
     assert PagedDecode.mutable_inputs == ()
 
 
+def test_csr_spmm_definition_recognised_with_reference_signature():
+    from intent_amd.examples.kernels.sparse.csr_spmm import csr_spmm
+
+    iface = PublicInterface.from_definition(csr_spmm, {})
+    assert recognize(csr_spmm, iface, ()).name == "csr_spmm"
+    assert list(csr_spmm.signature.parameters) == ["row_offsets", "column_indices", "values", "dense", "output"]
+
+
 def test_generated_program_save_load_roundtrip(tmp_path):
     """generate -> save (kernel.source, kernel.mlir, artifact.json) -> load -> materialize, without a GPU."""
     import json
