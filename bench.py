@@ -487,7 +487,7 @@ def op_paged_decode(device, flush, cpu):
            "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
            "partials_ms": round(partial_ms, 4), "merge_ms": round(merge_ms, 4),
            "partials_gbs": round((kv_bytes + partial_bytes) / partial_ms / 1e6, 1),
-           "traffic": read_traffic("paged_decode_partials")}
+           "traffic": read_traffic("paged_decode_partials_b8_hq32_hk8_d128")}
     if cpu:
         import oracle
 
@@ -523,7 +523,8 @@ def op_spmm(device, flush, cpu):
     out = {"config": f"CSR SpMM f32 {rows}x{cols}, {nnz} nnz (32 per row), {features} features",
            "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
            "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
-           "gathered_gbs": round(gathered / ms / 1e6, 1), "gflops": round(2 * nnz * features / ms / 1e6, 1)}
+           "gathered_gbs": round(gathered / ms / 1e6, 1), "gflops": round(2 * nnz * features / ms / 1e6, 1),
+           "traffic": read_traffic("csr_spmm_8192_f128")}
     if cpu:
         import oracle
 
