@@ -7,10 +7,10 @@
 // Backward (python/intent/examples/kernels/backward/softmax.py:9-25):
 //   proj = sum(p * dy), dx = p * (dy - proj)   (f32 accumulation; f16 storage variant casts)
 //
-// Design: one wavefront owns one row. The row is loaded once with 128-bit loads
-// (lane l of chunk c reads columns [(64c + l) * V, +V)), held in registers, reduced
-// with DPP (no LDS, no barrier), and written once with non-temporal stores: one HBM read
-// and one write per element, the minimum. Rows longer than the register-resident limit, or rows whose
+// Design: one wavefront owns one row, two rows per workgroup. The row is loaded once with
+// 128-bit loads (lane l of chunk c reads columns [(64c + l) * V, +V)), held in registers,
+// reduced with DPP (no LDS, no barrier), and written once: one HBM read and one write per
+// element, the minimum. Rows longer than the register-resident limit, or rows whose
 // layout rules out 128-bit access, use a scalar variant; rows longer than 64 * 64
 // scalar elements use a streaming variant that re-reads the row (3 passes forward,
 // 2 backward).
@@ -21,11 +21,15 @@
 namespace intent_hip {
 namespace {
 
-constexpr int kRowsPerBlock = 4;
+constexpr int kRowsPerBlock = 2;
 constexpr int kBlock = kRowsPerBlock * kWave;
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------- vector load / store
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-bit rows are read with non-temporal loads (each element is read once) and 128-bit accesses.
 template <typename T, int V>
 __device__ __forceinline__ void load_row_chunk(const T *p, float (&out)[V]) {
   if constexpr (V == 1) {
@@ -36,36 +40,36 @@ __device__ __forceinline__ void load_row_chunk(const T *p, float (&out)[V]) {
     out[0] = raw.x; out[1] = raw.y; out[2] = raw.z; out[3] = raw.w;
   } else {
     static_assert(V == 8, "16-bit vectors hold 8 elements");
-    const uint4 raw = *reinterpret_cast<const uint4 *>(p);
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    const u32x4_t raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      out[2 * i] = to_f32(T{static_cast<uint16_t>(w[i] & 0xffffu)});
-      out[2 * i + 1] = to_f32(T{static_cast<uint16_t>(w[i] >> 16)});
+      out[2 * i] = to_f32(T{static_cast<uint16_t>(raw[i] & 0xffffu)});
+      out[2 * i + 1] = to_f32(T{static_cast<uint16_t>(raw[i] >> 16)});
     }
   }
 }
 
-// Output rows are written with non-temporal stores: nothing reads them back inside the kernel,
-// and keeping them out of the caches measured 6.4 TB/s forward and 6.9 TB/s backward on
-// 16384 x 4096 f16, against 6.0 and 5.1 TB/s with ordinary stores.
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-template <typename T, int V>
+// kStream selects non-temporal stores. The forward stores normally: in the forward -> backward
+// sequence its output is the backward's input and may still be in the MALL when it is read. The
+// backward's output is not read again and is streamed. Measured on the 16384 x 4096 f16 step
+// (graph replays): 118.9 us with this choice, 126.0 us with both streamed, 136.1 us with
+// neither.
+template <typename T, int V, bool kStream>
 __device__ __forceinline__ void store_row_chunk(T *p, const float (&in)[V]) {
   if constexpr (V == 1) {
     p[0] = from_f32<T>(in[0]);
   } else if constexpr (sizeof(T) == 4) {
     const f32x4_t v = {in[0], in[1], in[2], in[3]};
-    __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t *>(p));
+    if constexpr (kStream) __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t *>(p));
+    else *reinterpret_cast<f32x4_t *>(p) = v;
   } else {
     u32x4_t w;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       w[i] = static_cast<uint32_t>(from_f32<T>(in[2 * i]).bits) |
              (static_cast<uint32_t>(from_f32<T>(in[2 * i + 1]).bits) << 16);
-    __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t *>(p));
+    if constexpr (kStream) __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t *>(p));
+    else *reinterpret_cast<u32x4_t *>(p) = w;
   }
 }
 
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(kBlock) void softmax_fwd_wave(const T *x, T *y, int
       float o[V];
 #pragma unroll
       for (int i = 0; i < V; ++i) o[i] = sizeof(T) == 4 ? v[c][i] * r : quotient(v[c][i], s, r);
-      store_row_chunk<T, V>(yr + col, o);
+      store_row_chunk<T, V, false>(yr + col, o);
     }
   }
 }
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(kBlock) void softmax_bwd_wave(const T *p, const T *
       float o[V];
 #pragma unroll
       for (int i = 0; i < V; ++i) o[i] = pv[c][i] * (gv[c][i] - proj);
-      store_row_chunk<T, V>(dr + col, o);
+      store_row_chunk<T, V, true>(dr + col, o);
     }
   }
 }
