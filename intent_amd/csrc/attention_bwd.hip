@@ -42,6 +42,22 @@ constexpr int kTile = 64;      // keys (dQ) or queries (dK/dV) per streamed tile
 constexpr float kLog2e = 1.4426950408889634f;
 
 #define INTENT_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
+// s_waitcnt with only the vector-memory counter constrained (vmcnt <= n, n < 64).
+#define INTENT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8)))
+
+// Streamed tiles go through kStages LDS stages: up to kStages - 1 tiles are in flight while one
+// is consumed (the DMA latency is long next to one tile's arithmetic when few workgroups run).
+constexpr int kStages = 4;
+
+// Wait until at most `later` tiles' DMAs (kPerTile instructions each, issued after the awaited
+// tile) are still in flight for this wave.
+template <int kPerTile>
+__device__ __forceinline__ void wait_tiles_after(int later) {
+  static_assert(kPerTile * (kStages - 2) < 64, "vmcnt range");
+  if (later >= 2) INTENT_WAIT_VMCNT(2 * kPerTile);
+  else if (later == 1) INTENT_WAIT_VMCNT(kPerTile);
+  else INTENT_WAIT_VMCNT(0);
+}
 
 __device__ __forceinline__ f32x16_t mma(f16x8_t a, f16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -119,14 +135,13 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_delta(const uint16_t *
 
 // ---------------------------------------------------------------- dQ
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
+__device__ __forceinline__ void attention_bwd_dq_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DQ, int heads, int head_group, int sq, int sk, BwdGeometry g, float scale, int causal,
-    int q_blocks) {
+    int q_blocks, uint4 *lds) {
   constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one K (or V) tile
   constexpr int kDma = kChunks / kThreads;         // per thread per operand
-  __shared__ uint4 lds[2 * 2 * kChunks];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh_count = gridDim.x / q_blocks;
@@ -162,7 +177,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
   const int wave_q_last = min(wq0 + 31, sq - 1);
 
   auto issue = [&](int kt) {
-    uint4 *stage = lds + (kt & 1) * 2 * kChunks;
+    uint4 *stage = lds + (kt % kStages) * 2 * kChunks;
     const int key0 = kt * kTile;
 #pragma unroll
     for (int i = 0; i < kDma; ++i) {
@@ -188,14 +203,14 @@ __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
   const int t_row = 4 * (g16 >> 1) + (i16 >> 2);
   const int t_col = 16 * (g16 & 1) + 4 * (i16 & 3);
 
-  if (tiles > 0) issue(0);
+  for (int kt = 0; kt < kStages - 1 && kt < tiles; ++kt) issue(kt);
   for (int kt = 0; kt < tiles; ++kt) {
-    INTENT_WAIT_VMCNT0();
+    wait_tiles_after<2 * kDma>(min(tiles - 1 - kt, kStages - 2));
     __syncthreads();          // tile kt is in LDS; every wave is done with tile kt - 1
-    if (kt + 1 < tiles) issue(kt + 1);
+    if (kt + kStages - 1 < tiles) issue(kt + kStages - 1);   // into tile kt - 1's stage
     const int key0 = kt * kTile;
     if ((causal && key0 > wave_q_last) || wq0 >= sq) continue;   // wave-uniform
-    const uint4 *ktile = lds + (kt & 1) * 2 * kChunks;
+    const uint4 *ktile = lds + (kt % kStages) * 2 * kChunks;
     const uint4 *vtile = ktile + kChunks;
     f16x8_t dsf[4];
 #pragma unroll
@@ -234,17 +249,27 @@ __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
                      pack_f16x2(acc[mt][4 * gq + 2] * scale, acc[mt][4 * gq + 3] * scale));
 }
 
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
+    const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
+    uint16_t *__restrict__ DQ, int heads, int head_group, int sq, int sk, BwdGeometry g, float scale, int causal,
+    int q_blocks) {
+  constexpr int kChunks = kTile * D / 8;
+  __shared__ uint4 lds[kStages * 2 * kChunks];
+  attention_bwd_dq_body<D>(Q, K, V, G, LSE, DELTA, DQ, heads, head_group, sq, sk, g, scale, causal, q_blocks, lds);
+}
+
 // ---------------------------------------------------------------- dK / dV
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
+__device__ __forceinline__ void attention_bwd_dkdv_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, int kv_heads, int head_group, int sq, int sk,
-    BwdGeometry g, float scale, int causal, int k_blocks) {
+    BwdGeometry g, float scale, int causal, int k_blocks, uint4 *lds) {
   constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one Q (or dO) tile
   constexpr int kDma = kChunks / kThreads;
   constexpr int kStage = 2 * kChunks + 2 * (kTile / 4);   // Q, dO, then lse and delta (64 floats each)
-  __shared__ uint4 lds[2 * kStage];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh_count = gridDim.x / k_blocks;
@@ -280,7 +305,7 @@ __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
   auto tile_head = [&](int t) { return kh * head_group + t / per_head; };
   auto tile_q0 = [&](int t) { return (first + t % per_head) * kTile; };
   auto issue = [&](int t) {
-    uint4 *stage = lds + (t & 1) * kStage;
+    uint4 *stage = lds + (t % kStages) * kStage;
     const int hq = tile_head(t), q0 = tile_q0(t);
     const uint16_t *qbase = Q + b * g.q[0] + hq * g.q[1];
     const uint16_t *gbase = G + b * g.dout[0] + hq * g.dout[1];
@@ -314,14 +339,17 @@ __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
   const int t_row = 4 * (g16 >> 1) + (i16 >> 2);
   const int t_col = 16 * (g16 & 1) + 4 * (i16 & 3);
 
-  if (tiles > 0) issue(0);
+  for (int t = 0; t < kStages - 1 && t < tiles; ++t) issue(t);
   for (int t = 0; t < tiles; ++t) {
-    INTENT_WAIT_VMCNT0();
-    __syncthreads();
-    if (t + 1 < tiles) issue(t + 1);
+    // Waves 0 and 1 also move lse and delta: one more DMA instruction per tile.
+    const int later = min(tiles - 1 - t, kStages - 2);
+    if (wave < 2) wait_tiles_after<2 * kDma + 1>(later);
+    else wait_tiles_after<2 * kDma>(later);
+    __syncthreads();          // tile t is in LDS; every wave is done with tile t - 1
+    if (t + kStages - 1 < tiles) issue(t + kStages - 1);   // into tile t - 1's stage
     const int q0 = tile_q0(t);
     if (wk0 >= sk || (causal && q0 + kTile - 1 < wk0)) continue;   // wave-uniform: no valid pair
-    const uint4 *qtile = lds + (t & 1) * kStage;
+    const uint4 *qtile = lds + (t % kStages) * kStage;
     const uint4 *gtile = qtile + kChunks;
     const float *lse_s = reinterpret_cast<const float *>(qtile + 2 * kChunks);
     const float *dlt_s = lse_s + kTile;
@@ -379,6 +407,18 @@ __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
       *reinterpret_cast<uint2 *>(vrow + col) = make_uint2(pack_f16x2(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1]),
                                                           pack_f16x2(acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]));
     }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
+    const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
+    uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, int kv_heads, int head_group, int sq, int sk,
+    BwdGeometry g, float scale, int causal, int k_blocks) {
+  constexpr int kStage = 2 * (kTile * D / 8) + 2 * (kTile / 4);
+  __shared__ uint4 lds[kStages * kStage];
+  attention_bwd_dkdv_body<D>(Q, K, V, G, LSE, DELTA, DK, DV, kv_heads, head_group, sq, sk, g, scale, causal,
+                             k_blocks, lds);
 }
 
 }  // namespace
