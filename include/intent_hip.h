@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 4
+#define INTENT_HIP_ABI_VERSION 5
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -185,6 +185,23 @@ int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, c
                                   int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
                                   int64_t sk, int64_t d, const int64_t strides[30], float scale,
                                   int causal, void *stream);
+
+/* The same with a caller-owned device workspace. When head_group > 1 and the grid above would
+ * hold fewer than 256 workgroups (batch * kv_heads * ceil(sk / 128)), each query head of the
+ * group gets its own workgroups, which write unscaled f32 partial sums to the workspace
+ * ([2][head_group][batch][kv_heads][sk][d]: dK, then dV); a second kernel folds them over the
+ * group in head order, scales dK and casts. intent_hip_attention_bwd_dkdv_workspace_bytes gives
+ * the size (0 when the split is not taken; the workspace may then be NULL, and a NULL workspace
+ * always selects the unsplit kernel). The workspace must be 16-byte aligned. No counterpart in
+ * the reference: the reference's single kernel launch (backward/attention.py:87-137) has no
+ * workspace. */
+int intent_hip_attention_bwd_dkdv_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_group,
+                                                  int64_t sq, int64_t sk, int64_t d, size_t *bytes);
+int intent_hip_attention_bwd_dkdv_ws(const void *q, const void *k, const void *v, const void *dout,
+                                     const float *lse, const float *delta, void *dk, void *dv,
+                                     int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
+                                     int64_t sk, int64_t d, const int64_t strides[30], float scale,
+                                     int causal, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Paged grouped-query decode attention over one page range per (batch, split): f16 q, caches,
  * f32 partial results. paged_gqa_decode_partials

@@ -261,12 +261,15 @@ __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
 }
 
 // ---------------------------------------------------------------- dK / dV
-template <int D>
+// kSplit: the workgroup takes one query head of the group (grid x head_group) and writes its
+// unscaled f32 dK and dV sums to `partial` ([group][batch][kv_heads][sk][D], dK then dV), which
+// attention_bwd_dkdv_reduce folds over the group. Used when too few workgroups would run.
+template <int D, bool kSplit>
 __device__ __forceinline__ void attention_bwd_dkdv_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
-    uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, int kv_heads, int head_group, int sq, int sk,
-    BwdGeometry g, float scale, int causal, int k_blocks, uint4 *lds) {
+    uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, float *__restrict__ partial, int kv_heads,
+    int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks, uint4 *lds) {
   constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one Q (or dO) tile
   constexpr int kDma = kChunks / kThreads;
   constexpr int kStage = 2 * kChunks + 2 * (kTile / 4);   // Q, dO, then lse and delta (64 floats each)
@@ -274,7 +277,9 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh_count = gridDim.x / k_blocks;
   const int kb = static_cast<int>(blockIdx.x) / bh_count;   // causal: first key blocks see the most queries
-  const int bh = static_cast<int>(blockIdx.x) % bh_count;
+  const int bhs = static_cast<int>(blockIdx.x) % bh_count;
+  const int split = kSplit ? bhs % head_group : 0;          // the query head of the group (split mode)
+  const int bh = kSplit ? bhs / head_group : bhs;
   const int b = bh / kv_heads, kh = bh % kv_heads;
 
   const int wk0 = kb * kRows + wave * 32;
@@ -300,9 +305,9 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   const int q_tiles = (sq + kTile - 1) / kTile;
   const int first = causal ? min(kb * kRows / kTile, q_tiles) : 0;
   const int per_head = q_tiles - first;
-  const int tiles = head_group * per_head;
+  const int tiles = (kSplit ? 1 : head_group) * per_head;
 
-  auto tile_head = [&](int t) { return kh * head_group + t / per_head; };
+  auto tile_head = [&](int t) { return kh * head_group + (kSplit ? split : t / per_head); };
   auto tile_q0 = [&](int t) { return (first + t % per_head) * kTile; };
   auto issue = [&](int t) {
     uint4 *stage = lds + (t % kStages) * kStage;
@@ -394,6 +399,23 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   }
 
   if (!k_ok) return;
+  if constexpr (kSplit) {
+    const int64_t rows = static_cast<int64_t>(gridDim.x / (k_blocks * head_group)) * sk;   // batch * kv_heads * sk
+    const int64_t row = (static_cast<int64_t>(b) * kv_heads + kh) * sk + lane_k;
+    float *pk = partial + (static_cast<int64_t>(split) * rows + row) * D;
+    float *pv = partial + (static_cast<int64_t>(head_group + split) * rows + row) * D;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int col = mt * 32 + 8 * gq + 4 * half;
+        *reinterpret_cast<float4 *>(pk + col) =
+            make_float4(acc_k[mt][4 * gq], acc_k[mt][4 * gq + 1], acc_k[mt][4 * gq + 2], acc_k[mt][4 * gq + 3]);
+        *reinterpret_cast<float4 *>(pv + col) =
+            make_float4(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1], acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]);
+      }
+    return;
+  }
   uint16_t *krow = DK + b * g.out0[0] + kh * g.out0[1] + static_cast<int64_t>(lane_k) * g.out0[2];
   uint16_t *vrow = DV + b * g.out1[0] + kh * g.out1[1] + static_cast<int64_t>(lane_k) * g.out1[2];
 #pragma unroll
@@ -409,16 +431,44 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
     }
 }
 
-template <int D>
+template <int D, bool kSplit>
 __global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
-    uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, int kv_heads, int head_group, int sq, int sk,
-    BwdGeometry g, float scale, int causal, int k_blocks) {
+    uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, float *__restrict__ partial, int kv_heads,
+    int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks) {
   constexpr int kStage = 2 * (kTile * D / 8) + 2 * (kTile / 4);
   __shared__ uint4 lds[kStages * kStage];
-  attention_bwd_dkdv_body<D>(Q, K, V, G, LSE, DELTA, DK, DV, kv_heads, head_group, sq, sk, g, scale, causal,
-                             k_blocks, lds);
+  attention_bwd_dkdv_body<D, kSplit>(Q, K, V, G, LSE, DELTA, DK, DV, partial, kv_heads, head_group, sq, sk, g,
+                                     scale, causal, k_blocks, lds);
+}
+
+// dK = f16(scale * sum over the group of the partial dK), dV = f16(sum of the partial dV); four
+// columns per thread, in group order.
+template <int D>
+__global__ __launch_bounds__(kThreads) void attention_bwd_dkdv_reduce(const float *__restrict__ partial,
+                                                                      uint16_t *__restrict__ DK,
+                                                                      uint16_t *__restrict__ DV, int kv_heads,
+                                                                      int head_group, int sk, int64_t rows,
+                                                                      BwdGeometry g, float scale) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (t >= rows * (D / 4)) return;
+  const int64_t row = t / (D / 4);
+  const int col = static_cast<int>(t % (D / 4)) * 4;
+  const int64_t k = row % sk, bh = row / sk;
+  const int64_t b = bh / kv_heads, kh = bh % kv_heads;
+  float4 sk4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), sv4 = sk4;
+  for (int i = 0; i < head_group; ++i) {
+    const float4 a = *reinterpret_cast<const float4 *>(partial + (i * rows + row) * D + col);
+    const float4 c = *reinterpret_cast<const float4 *>(partial + ((head_group + i) * rows + row) * D + col);
+    sk4 = make_float4(sk4.x + a.x, sk4.y + a.y, sk4.z + a.z, sk4.w + a.w);
+    sv4 = make_float4(sv4.x + c.x, sv4.y + c.y, sv4.z + c.z, sv4.w + c.w);
+  }
+  uint16_t *krow = DK + b * g.out0[0] + kh * g.out0[1] + k * g.out0[2];
+  uint16_t *vrow = DV + b * g.out1[0] + kh * g.out1[1] + k * g.out1[2];
+  *reinterpret_cast<uint2 *>(krow + col) =
+      make_uint2(pack_f16x2(sk4.x * scale, sk4.y * scale), pack_f16x2(sk4.z * scale, sk4.w * scale));
+  *reinterpret_cast<uint2 *>(vrow + col) = make_uint2(pack_f16x2(sv4.x, sv4.y), pack_f16x2(sv4.z, sv4.w));
 }
 
 }  // namespace
@@ -440,9 +490,9 @@ int attention_bwd_resources(int64_t which, int64_t d, IntentHipKernelResources *
                  : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dq<128>), "attention_bwd_dq<128>",
                                    kThreads, out);
     default:
-      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<64>), "attention_bwd_dkdv<64>",
+      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<64, false>), "attention_bwd_dkdv<64>",
                                    kThreads, out)
-                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<128>),
+                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<128, false>),
                                    "attention_bwd_dkdv<128>", kThreads, out);
   }
 }
@@ -561,10 +611,40 @@ extern "C" int intent_hip_attention_bwd_dq(const void *q, const void *k, const v
   return INTENT_HIP_OK;
 }
 
-extern "C" int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
-                                             const float *lse, const float *delta, void *dk, void *dv, int64_t batch,
-                                             int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
-                                             const int64_t *strides, float scale, int causal, void *stream) {
+namespace {
+
+// dK/dV split by query head: taken when head_group > 1 and fewer than kSplitBelow workgroups of
+// the unsplit kernel would run (the first key block then walks head_group times the query tiles
+// alone). The workspace holds the unscaled f32 partial sums, dK then dV.
+constexpr int64_t kSplitBelow = 256;
+
+bool dkdv_split(int64_t batch, int64_t q_heads, int64_t head_group, int64_t sk) {
+  if (head_group < 2 || batch <= 0 || q_heads <= 0 || sk <= 0) return false;
+  const int64_t blocks = batch * (q_heads / head_group) * ((sk + kRows - 1) / kRows);
+  return blocks < kSplitBelow;
+}
+
+int64_t dkdv_workspace(int64_t batch, int64_t q_heads, int64_t head_group, int64_t sk, int64_t d) {
+  return 2 * head_group * batch * (q_heads / head_group) * sk * d * static_cast<int64_t>(sizeof(float));
+}
+
+}  // namespace
+
+extern "C" int intent_hip_attention_bwd_dkdv_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_group,
+                                                             int64_t sq, int64_t sk, int64_t d, size_t *bytes) {
+  if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
+  if (const int rc = check_common(batch, q_heads, head_group, sq, sk, d)) return rc;
+  *bytes = dkdv_split(batch, q_heads, head_group, sk)
+               ? static_cast<size_t>(dkdv_workspace(batch, q_heads, head_group, sk, d))
+               : 0;
+  return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_attention_bwd_dkdv_ws(const void *q, const void *k, const void *v, const void *dout,
+                                                const float *lse, const float *delta, void *dk, void *dv,
+                                                int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
+                                                int64_t sk, int64_t d, const int64_t *strides, float scale,
+                                                int causal, void *workspace, size_t workspace_bytes, void *stream) {
   if (const int rc = check_common(batch, q_heads, head_group, sq, sk, d)) return rc;
   if (batch == 0 || q_heads == 0 || sk == 0) return INTENT_HIP_OK;
   if (strides == nullptr || k == nullptr || v == nullptr || dk == nullptr || dv == nullptr ||
@@ -580,7 +660,13 @@ extern "C" int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const
   load_geometry(g, strides, true);
   const int64_t kv_heads = q_heads / head_group;
   const int k_blocks = static_cast<int>((sk + kRows - 1) / kRows);
-  const int64_t blocks = batch * kv_heads * k_blocks;
+  const bool split = dkdv_split(batch, q_heads, head_group, sk);
+  const int64_t need = split ? dkdv_workspace(batch, q_heads, head_group, sk, d) : 0;
+  if (split && workspace != nullptr && (workspace_bytes < static_cast<size_t>(need) || !aligned(workspace, 16)))
+    return fail(INTENT_HIP_ERR_WORKSPACE, "dK/dV needs %lld 16-byte aligned workspace bytes, got %zu",
+                static_cast<long long>(need), workspace_bytes);
+  const bool use_split = split && workspace != nullptr;
+  const int64_t blocks = batch * kv_heads * k_blocks * (use_split ? head_group : 1);
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
   const auto *Q = static_cast<const uint16_t *>(q);
   const auto *K = static_cast<const uint16_t *>(k);
@@ -588,16 +674,42 @@ extern "C" int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const
   const auto *G = static_cast<const uint16_t *>(dout);
   auto *DK = static_cast<uint16_t *>(dk);
   auto *DV = static_cast<uint16_t *>(dv);
+  auto *P = static_cast<float *>(workspace);
   const dim3 grid(static_cast<unsigned>(blocks));
   const hipStream_t s = as_stream(stream);
   const int hk = static_cast<int>(kv_heads), grp = static_cast<int>(head_group);
-  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk);
+  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk), c = causal ? 1 : 0;
+  if (use_split) {
+    if (d == 64)
+      attention_bwd_dkdv<64, true><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, P, hk, grp, iq,
+                                                                   ik, g, scale, c, k_blocks);
+    else
+      attention_bwd_dkdv<128, true><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, P, hk, grp, iq,
+                                                                    ik, g, scale, c, k_blocks);
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv");
+    const int64_t rows = batch * kv_heads * sk;
+    const dim3 rgrid(static_cast<unsigned>((rows * (d / 4) + kThreads - 1) / kThreads));
+    if (d == 64)
+      attention_bwd_dkdv_reduce<64><<<rgrid, dim3(kThreads), 0, s>>>(P, DK, DV, hk, grp, ik, rows, g, scale);
+    else
+      attention_bwd_dkdv_reduce<128><<<rgrid, dim3(kThreads), 0, s>>>(P, DK, DV, hk, grp, ik, rows, g, scale);
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv_reduce");
+    return INTENT_HIP_OK;
+  }
   if (d == 64)
-    attention_bwd_dkdv<64><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, hk, grp, iq, ik, g, scale,
-                                                           causal ? 1 : 0, k_blocks);
+    attention_bwd_dkdv<64, false><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, nullptr, hk, grp,
+                                                                  iq, ik, g, scale, c, k_blocks);
   else
-    attention_bwd_dkdv<128><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, hk, grp, iq, ik, g, scale,
-                                                            causal ? 1 : 0, k_blocks);
+    attention_bwd_dkdv<128, false><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, nullptr, hk, grp,
+                                                                   iq, ik, g, scale, c, k_blocks);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv");
   return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
+                                             const float *lse, const float *delta, void *dk, void *dv, int64_t batch,
+                                             int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                                             const int64_t *strides, float scale, int causal, void *stream) {
+  return intent_hip_attention_bwd_dkdv_ws(q, k, v, dout, lse, delta, dk, dv, batch, q_heads, head_group, sq, sk, d,
+                                          strides, scale, causal, nullptr, 0, stream);
 }

@@ -305,15 +305,32 @@ def _attention_bwd(kind):
         sk = k.shape[2]
         strides = _strides(*ins, lse, delta, *staged_outs)
         keep.append(strides)
-        fn = lib.fn[f"attention_bwd_{kind}"]
         args = (*(t.data_ptr() for t in ins), lse.data_ptr(), delta.data_ptr(),
                 *(t.data_ptr() for t in staged_outs), batch, q_heads, group, sq, sk, d, strides, float(scale),
                 int(causal))
+        configuration = (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq), ("sk", sk),
+                         ("d", d), ("causal", causal))
+        if kind == "dkdv":
+            # Small grids split the query heads of a group over workgroups; the f32 partial sums
+            # need a workspace, allocated here once per prepared call.
+            import ctypes
+
+            import torch
+
+            size = ctypes.c_size_t(0)
+            lib.check(lib.fn["attention_bwd_dkdv_workspace_bytes"](batch, q_heads, group, sq, sk, d,
+                                                                  ctypes.byref(size)), "provider_preparation")
+            workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
+            if workspace is not None:
+                keep.append(workspace)
+            fn = lib.fn["attention_bwd_dkdv_ws"]
+            args = (*args, workspace.data_ptr() if workspace is not None else None, size.value)
+            configuration += (("workspace_bytes", size.value),)
+        else:
+            fn = lib.fn["attention_bwd_dq"]
         op = OP_ATTENTION_BWD_DQ if kind == "dq" else OP_ATTENTION_BWD_DKDV
         return Launch(f"intent_hip_attention_bwd_{kind}", lambda stream: fn(*args, stream), tuple(keep),
-                      tuple(before), tuple(after),
-                      (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq), ("sk", sk),
-                       ("d", d), ("causal", causal)),
+                      tuple(before), tuple(after), configuration,
                       lambda: lib.kernel_resources(op, F16, sq, d))
     return plan
 

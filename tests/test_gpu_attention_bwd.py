@@ -109,3 +109,53 @@ def test_authored_softmax_backward_autograd(device):
     torch.softmax(reference, dim=1).backward(upstream)
     assert torch.allclose(y, torch.softmax(x.detach(), dim=1), rtol=1e-5, atol=1e-7)
     assert torch.allclose(x.grad, reference.grad, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 2, 1024, 1024, 64), (1, 6, 3, 300, 200, 128)])
+def test_dkdv_split_matches_unsplit_through_the_c_abi(device, shape):
+    """intent_hip_attention_bwd_dkdv_ws with a workspace (query heads split over workgroups, f32
+    partials folded by a second kernel) against the same entry with no workspace (one workgroup
+    walks every head of the group): the sums differ only in association, so within 2 f16 ulp plus
+    1e-3 of the largest magnitude; both against the oracle."""
+    import ctypes
+
+    from intent_amd.runtime.hip.library import library
+
+    batch, hq, hk, sq, sk, d = shape
+    announce("dK/dV split vs unsplit", shape)
+    q, k, v, o, do, lse = case(sum(shape), batch, hq, hk, sq, sk, d)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    tq, tk, tv, tdo, tlse = t(q), t(k), t(v), t(do), t(lse)
+    delta_np = oracle.attention_bwd_delta(o, do)
+    tdelta = t(delta_np)
+    lib = library()
+    size = ctypes.c_size_t(0)
+    assert lib.fn["attention_bwd_dkdv_workspace_bytes"](batch, hq, hq // hk, sq, sk, d, ctypes.byref(size)) == 0
+    assert size.value == 2 * hq * batch * sk * d * 4            # the split is taken for these grids
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=device)
+    results = []
+    for ws in (workspace, None):
+        dk = torch.empty_like(tk)
+        dv = torch.empty_like(tv)
+        st = [x for a in (tq, tk, tv, tdo) for x in a.stride()] + list(tlse.stride()) + list(tdelta.stride()) + \
+            list(dk.stride()) + list(dv.stride())
+        strides = (ctypes.c_int64 * 30)(*st)
+        rc = lib.fn["attention_bwd_dkdv_ws"](tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tdo.data_ptr(),
+                                             tlse.data_ptr(), tdelta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                             batch, hq, hq // hk, sq, sk, d, strides, float(np.float32(d ** -0.5)),
+                                             1, ws.data_ptr() if ws is not None else None,
+                                             size.value if ws is not None else 0,
+                                             torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        results.append((dk.cpu().numpy().astype(np.float64), dv.cpu().numpy().astype(np.float64)))
+    torch.cuda.synchronize()
+    want_dk, want_dv = oracle.attention_bwd_dkdv(q, k, v, do, lse, delta_np, float(np.float32(d ** -0.5)), True,
+                                                 head_group=hq // hk)
+    for i, want in enumerate((want_dk, want_dv)):
+        split, unsplit = results[0][i], results[1][i]
+        bound = 2 * 2.0 ** -10 * np.abs(unsplit) + 1e-3 * np.abs(unsplit).max()
+        assert np.all(np.abs(split - unsplit) <= bound)
+        close(split, want)
+    small = ctypes.c_size_t(0)
+    assert lib.fn["attention_bwd_dkdv_workspace_bytes"](4, 32, 4, 4096, 4096, 128, ctypes.byref(small)) == 0
+    assert small.value == 0                                     # large grids never split
