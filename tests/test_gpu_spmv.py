@@ -66,9 +66,10 @@ def test_spmv_random_lengths(device, seed, rows, max_len):
     rng = np.random.default_rng(seed)
     lengths = rng.integers(0, max_len + 1, rows)
     lengths[rng.integers(0, rows, rows // 10)] = 0
-    offsets, columns = inputs.csr_matrix(rng, lengths, max(rows, max_len + 1))
+    cols = max(rows, 4 * max_len + 1)     # room for distinct columns: redraws of duplicates stay few
+    offsets, columns = inputs.csr_matrix(rng, lengths, cols)
     values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
-    x = inputs.uniform(rng, max(rows, max_len + 1), -1, 1)
+    x = inputs.uniform(rng, cols, -1, 1)
     check(device, offsets, columns, values, x)
     ival = rng.integers(-3, 4, values.shape).astype(np.float32)
     ix = rng.integers(-3, 4, x.shape).astype(np.float32)
