@@ -80,10 +80,16 @@ struct BwdGeometry {
 
 // LDS tile of kTile rows of D f16 (rows of D / 8 16-byte chunks). Chunk c of row r is stored at
 // c ^ swz(r); both row reads and transposing reads go through this map, so any swizzle is
-// correct; this one spreads the transposing reads of 4 consecutive rows over distinct chunks.
+// correct. This one is conflict-free for both (64 banks, 256 bytes per bank row):
+//   * 16-byte row reads of 16 consecutive rows land on 16 distinct 16-byte slots of a bank row
+//     (D = 128: one row per bank row, swz a bijection of r % 16; D = 64: two rows per bank row,
+//     swz a bijection of (r / 2) % 8);
+//   * transposing reads of 4 consecutive rows (starting at a multiple of 4) over an aligned group
+//     of 4 chunks land on 4 disjoint chunk groups.
 template <int D>
 __device__ __forceinline__ int swz(int row) {
-  return (D == 128 ? 4 : 2) * (row & 3);
+  if constexpr (D == 128) return ((row & 3) << 2) | ((row >> 2) & 3);
+  return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
 }
 
 // Row fragment of an MFMA A operand: rows `row` (lane & 31 within a 32-row block), 8

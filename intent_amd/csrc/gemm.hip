@@ -257,7 +257,8 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
 // (global_load_lds_dwordx4 writes them straight into LDS, no registers) while tile kt is multiplied. A stage holds A [256 m][32 k]
 // (rows of 4 16-byte chunks, chunk c of row r at c ^ ((r >> 2) & 3), which spreads the fragment
 // reads of 16 consecutive rows over the 64 LDS banks) and B in its natural
-// [32 k][256 n] layout (rows of 32 chunks, chunk c of row k at c ^ 2 (k & 3)). B fragments are read
+// [32 k][256 n] layout (rows of 32 chunks, chunk c of row k at c ^ 4 (k & 3), so the transposing
+// reads of 4 consecutive k rows land on 4 disjoint groups of 4 chunks). B fragments are read
 // with ds_read_b64_tr_b16: in each 16-lane group, lane i, slot j receives element i % 4 of the
 // 8-byte segment addressed by lane 4 j + i / 4, so lane i addressing B[k0 + i/4][n0 + 4 (i % 4)]
 // yields B[k0 .. k0+3][n0 + i], the 4 consecutive k of one n the MFMA operand needs.
@@ -305,7 +306,7 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
     const int ra = pa >> 2, ca = (pa & 3) ^ ((ra >> 2) & 3);
     a_src[i] = A + static_cast<int64_t>(m0 + ra) * lda + ca * 8;
     const int pb = (wave * 2 + i) * 64 + lane;      // B chunk slot: row pb / 32, physical chunk pb % 32
-    const int kb = pb >> 5, cb = (pb & 31) ^ (2 * (kb & 3));
+    const int kb = pb >> 5, cb = (pb & 31) ^ (4 * (kb & 3));
     b_src[i] = B + static_cast<int64_t>(kb) * ldb + n0 + cb * 8;
   }
   auto issue = [&](int kt) {
@@ -377,7 +378,7 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
         for (int r = 0; r < 2; ++r) {
           const int k = kk * 16 + b_k + 4 * r;
           const int n = wn * 64 + t * 32 + b_n;
-          const int chunk = (n >> 3) ^ (2 * (k & 3));
+          const int chunk = (n >> 3) ^ (4 * (k & 3));
           parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sb + k * kBN + chunk * 8 + (n & 7)));
         }
         bf[kk][t] = __builtin_bit_cast(x8, parts);
