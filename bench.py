@@ -161,22 +161,48 @@ def cpu_median_seconds(run):
 
 
 def headline_cpu_baseline(x, dy):
+    """The oracle on a bounded sample, with the reference's default worker count (min(8, allowed
+    CPUs), targets/execution.py:20-26) and again with every allowed CPU."""
     import oracle
 
     rows = 2048
     xs, gs = x[:rows], dy[:rows]
-    workers = oracle.default_workers()
-
-    def run():
-        y = oracle.softmax_fwd(xs, workers=workers)
-        oracle.softmax_bwd(y, gs, workers=workers)
-
-    seconds = cpu_median_seconds(run)
     nbytes = (FWD_BYTES_PER_ELEMENT + BWD_BYTES_PER_ELEMENT) * rows * x.shape[1]
-    return {"value": round(nbytes / seconds / 1e9, 3), "unit": "GB/s", "cores": workers, "kind": "port",
+
+    def rate(workers):
+        def run():
+            y = oracle.softmax_fwd(xs, workers=workers)
+            oracle.softmax_bwd(y, gs, workers=workers)
+
+        return round(nbytes / cpu_median_seconds(run) / 1e9, 3)
+
+    workers = oracle.default_workers()
+    allowed = len(os.sched_getaffinity(0))
+    return {"value": rate(workers), "unit": "GB/s", "cores": workers, "kind": "port",
             "sample": f"oracle softmax fwd+bwd f16 on rows 0..{rows - 1} of the 16384x4096 input "
                       f"(1/{x.shape[0] // rows} of the workload), median of 7 samples, "
-                      f"{workers} OpenMP workers (min(8, allowed CPUs)); host has {os.cpu_count()} CPUs"}
+                      f"{workers} OpenMP workers (min(8, allowed CPUs)); host has {os.cpu_count()} CPUs",
+            "all_cores": {"value": rate(allowed), "cores": allowed}}
+
+
+def box_reference(device, flush):
+    """Figures of the box itself, beside the kernels' rooflines: a torch device copy of 512 MiB
+    (read + write GB/s) and torch.matmul bf16 8192^3 (hipBLASLt), both median graph replays
+    after the flush."""
+    import torch
+
+    src = torch.ones(512 << 20, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    copy_ms = graph_median_ms(lambda: dst.copy_(src), flush)
+    del src, dst
+    g = torch.Generator(device="cpu").manual_seed(0)
+    a = (torch.rand((8192, 8192), generator=g) * 2 - 1).to(torch.bfloat16).to(device)
+    b = (torch.rand((8192, 8192), generator=g) * 2 - 1).to(torch.bfloat16).to(device)
+    c = torch.empty((8192, 8192), dtype=torch.bfloat16, device=device)
+    gemm_ms = graph_median_ms(lambda: torch.matmul(a, b, out=c), flush)
+    return {"torch_copy_gbs": round(2 * (512 << 20) / copy_ms / 1e6, 1),
+            "hipblaslt_bf16_gemm_8192_tflops": round(2 * 8192 ** 3 / gemm_ms / 1e9, 1),
+            "hipblaslt_bf16_gemm_8192_ms": round(gemm_ms, 4)}
 
 
 # ------------------------------------------------------------------------------ operators
@@ -660,6 +686,12 @@ def main():
             log(json.dumps(operators[-1]))
             torch.cuda.empty_cache()
 
+    reference = None
+    if not args.no_operators:
+        log("box reference figures")
+        reference = box_reference(device, Flush(device))
+        torch.cuda.empty_cache()
+
     cpu_baseline = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -674,7 +706,7 @@ def main():
                    "bytes_per_step": fwd_bytes + bwd_bytes, "parallelism": "single GPU",
                    "timing": "K eager steps (prepared fwd + bwd launches) between HIP events after W warm-ups",
                    "graph_ms_per_step": round(graph_ms, 5)},
-        "roofline": roofline, "cpu_baseline": cpu_baseline, "operators": operators,
+        "roofline": roofline, "cpu_baseline": cpu_baseline, "operators": operators, "box_reference": reference,
     }
     print(json.dumps(record), flush=True)
     del np
