@@ -52,8 +52,8 @@ enum IntentHipOperator {
   INTENT_HIP_OP_GEMM_F32 = 6,
   INTENT_HIP_OP_ATTENTION_FWD = 7,     /* dtype F16 or BF16 */
   INTENT_HIP_OP_ATTENTION_BWD_DELTA = 8, /* cols = head dimension */
-  INTENT_HIP_OP_ATTENTION_BWD_DQ = 9,
-  INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10,
+  INTENT_HIP_OP_ATTENTION_BWD_DQ = 9,    /* rows = batch * query heads * queries, cols = head dimension */
+  INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10, /* rows = batch * key heads * keys, cols = head dimension */
   INTENT_HIP_OP_PAGED_DECODE_PARTIALS = 11, /* rows = HEAD_GROUP, cols = head dimension */
   INTENT_HIP_OP_SPLITK_REDUCE = 12,
   INTENT_HIP_OP_CSR_SPMM_F32 = 13         /* cols = features */

@@ -98,9 +98,9 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     case INTENT_HIP_OP_ATTENTION_FWD_F16: return attention_resources(INTENT_HIP_F16, rows, cols, out);
     case INTENT_HIP_OP_ATTENTION_FWD: return attention_resources(dtype, rows, cols, out);
     case INTENT_HIP_OP_CSR_SPMV_F32: return spmv_resources(rows, cols, out);
-    case INTENT_HIP_OP_ATTENTION_BWD_DELTA: return attention_bwd_resources(0, cols, out);
-    case INTENT_HIP_OP_ATTENTION_BWD_DQ: return attention_bwd_resources(1, cols, out);
-    case INTENT_HIP_OP_ATTENTION_BWD_DKDV: return attention_bwd_resources(2, cols, out);
+    case INTENT_HIP_OP_ATTENTION_BWD_DELTA: return attention_bwd_resources(0, rows, cols, out);
+    case INTENT_HIP_OP_ATTENTION_BWD_DQ: return attention_bwd_resources(1, rows, cols, out);
+    case INTENT_HIP_OP_ATTENTION_BWD_DKDV: return attention_bwd_resources(2, rows, cols, out);
     case INTENT_HIP_OP_PAGED_DECODE_PARTIALS: return decode_resources(0, cols, rows, out);
     case INTENT_HIP_OP_SPLITK_REDUCE: return decode_resources(1, cols, rows, out);
     case INTENT_HIP_OP_CSR_SPMM_F32: return spmm_resources(cols, out);

@@ -13,16 +13,23 @@
 //   combined by addition).
 //
 // Design (head dimension D = 64 or 128, v_mfma_f32_32x32x16_f16 throughout):
-//   * dQ: a workgroup owns 128 queries of one (batch, query head), 4 waves x 32; 64-key tiles of
-//     K and V stream through double-buffered LDS (global_load_lds_dwordx4). Per 32-key half:
+//   * dQ: a workgroup owns 32 queries per wave of one (batch, query head); 64-key tiles of K and
+//     V stream through LDS (global_load_lds_dwordx4, kStages stages). Per 32-key half:
 //     S^T = K Q^T and dP^T = V dO^T with the wave's Q and dO fragments in registers (lane l
 //     holds the scores of query l % 32), dS^T rounded to f16 in registers, then
-//     dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16 from K's natural [key][d] layout.
-//   * dK/dV: a workgroup owns 128 keys of one (batch, key head), 4 waves x 32; 64-query tiles of
-//     Q and dO (of every query head in the group) stream through LDS, with their lse and delta.
-//     Per 32-query half: S = Q K^T and dP = dO V^T with the wave's K and V fragments in
-//     registers (lane l holds key l % 32), P and dS rounded to f16 in registers, then
-//     dV^T += dO^T P and dK^T += Q^T dS with transposing LDS reads of Q and dO.
+//     dQ^T += K^T dS^T over that half's keys, with K^T read by ds_read_b64_tr_b16 from K's
+//     natural [key][d] layout.
+//   * dK/dV: a workgroup owns 32 keys per wave of one (batch, key head); 64-query tiles of Q and
+//     dO (of every query head in the group) stream through LDS, with their lse and delta. Per
+//     32-query half: S = Q K^T and dP = dO V^T with the wave's K and V fragments in registers
+//     (lane l holds key l % 32), P and dS rounded to f16 in registers, then dV^T += dO^T P and
+//     dK^T += Q^T dS over that half's queries, with transposing LDS reads of Q and dO.
+//   * Wide grids (at least kWideRows rows) run 8 waves per workgroup, two per SIMD: while one
+//     wave issues MFMAs (at raised priority, s_setprio 1) the other's exp and LDS work fills the
+//     gaps, and each streamed tile serves 256 rows. dK/dV then runs as two kernels, dK (S, dP,
+//     dK) and dV (S, dV), each within the 256 registers a lane has at two waves per SIMD; the
+//     combined kernel needs about 400. Narrow grids run 4 waves per workgroup (more workgroups),
+//     dK and dV together.
 //   * Rows past the end of a tensor read its last row (finite data that the mask excludes).
 //     Causal work is skipped per wave where no pair of a tile is valid.
 #include "common.hpp"
@@ -36,9 +43,15 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int kThreads = 256;
-constexpr int kRows = 128;     // queries (dQ) or keys (dK/dV) per workgroup
-constexpr int kTile = 64;      // keys (dQ) or queries (dK/dV) per streamed tile
+constexpr int kThreads = 256;   // delta, the split reduction, and the 4-wave dQ / dK-dV kernels
+constexpr int kRows = 128;      // queries (dQ) or keys (dK/dV) per 4-wave workgroup
+constexpr int kTile = 64;       // keys (dQ) or queries (dK/dV) per streamed tile
+// Calls with at least this many rows (batch x heads x sequence, query heads for dQ, key heads for
+// dK/dV) use the 8-wave, 256-row workgroups: enough rows for 256 of them.
+constexpr int64_t kWideRows = 256 * 256;
+
+// The part of dK/dV a kernel computes.
+enum DkdvPart { kBoth = 0, kOnlyDk = 1, kOnlyDv = 2 };
 constexpr float kLog2e = 1.4426950408889634f;
 
 #define INTENT_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
@@ -140,14 +153,17 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_delta(const uint16_t *
 }
 
 // ---------------------------------------------------------------- dQ
-template <int D>
+// kW waves of 32 queries per workgroup (4 or 8).
+template <int D, int kW>
 __device__ __forceinline__ void attention_bwd_dq_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DQ, int heads, int head_group, int sq, int sk, BwdGeometry g, float scale, int causal,
     int q_blocks, uint4 *lds) {
   constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one K (or V) tile
-  constexpr int kDma = kChunks / kThreads;         // per thread per operand
+  constexpr int kDma = kChunks / (kW * 64);        // per thread per operand
+  constexpr int kQRows = kW * 32;
+  static_assert(kDma * kW * 64 == kChunks, "DMA split");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh_count = gridDim.x / q_blocks;
@@ -157,7 +173,7 @@ __device__ __forceinline__ void attention_bwd_dq_body(
   const uint16_t *kbase = K + b * g.k[0] + kh * g.k[1];
   const uint16_t *vbase = V + b * g.v[0] + kh * g.v[1];
 
-  const int wq0 = qb * kRows + wave * 32;
+  const int wq0 = qb * kQRows + wave * 32;
   const int lane_q = wq0 + (lane & 31);
   const int half = lane >> 5;
   const bool q_ok = lane_q < sq;
@@ -177,7 +193,7 @@ __device__ __forceinline__ void attention_bwd_dq_body(
   const float dlt = q_ok ? DELTA[b * g.delta[0] + h * g.delta[1] + static_cast<int64_t>(qr) * g.delta[2]] : 0.0f;
   INTENT_WAIT_VMCNT0();
 
-  const int q_last_block = min(qb * kRows + kRows, sq) - 1;
+  const int q_last_block = min(qb * kQRows + kQRows, sq) - 1;
   const int k_end = causal ? min(sk, q_last_block + 1) : sk;
   const int tiles = (k_end + kTile - 1) / kTile;
   const int wave_q_last = min(wq0 + 31, sq - 1);
@@ -218,30 +234,35 @@ __device__ __forceinline__ void attention_bwd_dq_body(
     if ((causal && key0 > wave_q_last) || wq0 >= sq) continue;   // wave-uniform
     const uint4 *ktile = lds + (kt % kStages) * 2 * kChunks;
     const uint4 *vtile = ktile + kChunks;
-    f16x8_t dsf[4];
+    const uint16_t *kt16 = reinterpret_cast<const uint16_t *>(ktile);
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
+      f16x8_t dsf[2];
       f32x16_t s, dp;
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.0f;
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         s = mma(row_frag<D>(ktile, st * 32 + frag_row, ks, half), qf[ks], s);
         dp = mma(row_frag<D>(vtile, st * 32 + frag_row, ks, half), of[ks], dp);
       }
+      __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
         const bool valid = key < sk && (!causal || key <= lane_q);
         const float p = valid ? __builtin_amdgcn_exp2f(fmaf(s[e], c1, -lse2)) : 0.0f;
-        dsf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dlt) : 0.0f);
+        dsf[e >> 3][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dlt) : 0.0f);
       }
+      // This half's 32 keys are 16-key slices 2 st and 2 st + 1 of the tile.
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int mt = 0; mt < D / 32; ++mt) acc[mt] = mma(tr_frag<D>(kt16, st * 2 + h2, mt, t_row, t_col), dsf[h2], acc[mt]);
+      __builtin_amdgcn_s_setprio(0);
     }
-    const uint16_t *kt16 = reinterpret_cast<const uint16_t *>(ktile);
-#pragma unroll
-    for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt) acc[mt] = mma(tr_frag<D>(kt16, sl, mt, t_row, t_col), dsf[sl], acc[mt]);
   }
 
   if (!q_ok) return;
@@ -255,29 +276,33 @@ __device__ __forceinline__ void attention_bwd_dq_body(
                      pack_f16x2(acc[mt][4 * gq + 2] * scale, acc[mt][4 * gq + 3] * scale));
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dq(
+template <int D, int kW>
+__global__ __launch_bounds__(kW * 64, 1) void attention_bwd_dq(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DQ, int heads, int head_group, int sq, int sk, BwdGeometry g, float scale, int causal,
     int q_blocks) {
   constexpr int kChunks = kTile * D / 8;
   __shared__ uint4 lds[kStages * 2 * kChunks];
-  attention_bwd_dq_body<D>(Q, K, V, G, LSE, DELTA, DQ, heads, head_group, sq, sk, g, scale, causal, q_blocks, lds);
+  attention_bwd_dq_body<D, kW>(Q, K, V, G, LSE, DELTA, DQ, heads, head_group, sq, sk, g, scale, causal, q_blocks, lds);
 }
 
 // ---------------------------------------------------------------- dK / dV
 // kSplit: the workgroup takes one query head of the group (grid x head_group) and writes its
 // unscaled f32 dK and dV sums to `partial` ([group][batch][kv_heads][sk][D], dK then dV), which
 // attention_bwd_dkdv_reduce folds over the group. Used when too few workgroups would run.
-template <int D, bool kSplit>
+// kPart: dK and dV together, or one of them (DkdvPart); kW: waves of 32 keys per workgroup.
+template <int D, bool kSplit, int kPart, int kW>
 __device__ __forceinline__ void attention_bwd_dkdv_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, float *__restrict__ partial, int kv_heads,
     int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks, uint4 *lds) {
   constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one Q (or dO) tile
-  constexpr int kDma = kChunks / kThreads;
+  constexpr int kDma = kChunks / (kW * 64);
+  constexpr int kKRows = kW * 32;
+  constexpr bool kDoK = kPart != kOnlyDv, kDoV = kPart != kOnlyDk;
+  static_assert(kDma * kW * 64 == kChunks, "DMA split");
   constexpr int kStage = 2 * kChunks + 2 * (kTile / 4);   // Q, dO, then lse and delta (64 floats each)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -288,7 +313,7 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   const int bh = kSplit ? bhs / head_group : bhs;
   const int b = bh / kv_heads, kh = bh % kv_heads;
 
-  const int wk0 = kb * kRows + wave * 32;
+  const int wk0 = kb * kKRows + wave * 32;
   const int lane_k = wk0 + (lane & 31);
   const int half = lane >> 5;
   const bool k_ok = lane_k < sk;
@@ -301,7 +326,8 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
       kf[ks] = __builtin_bit_cast(f16x8_t, select(k_ok, *reinterpret_cast<const uint4 *>(krow + ks * 16 + half * 8)));
-      vf[ks] = __builtin_bit_cast(f16x8_t, select(k_ok, *reinterpret_cast<const uint4 *>(vrow + ks * 16 + half * 8)));
+      if constexpr (kDoK)
+        vf[ks] = __builtin_bit_cast(f16x8_t, select(k_ok, *reinterpret_cast<const uint4 *>(vrow + ks * 16 + half * 8)));
     }
     INTENT_WAIT_VMCNT0();
   }
@@ -309,7 +335,7 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   // Query tiles: for each of the head_group query heads, the 64-query tiles that can hold a valid
   // pair for this workgroup's keys (causal: queries >= its first key).
   const int q_tiles = (sq + kTile - 1) / kTile;
-  const int first = causal ? min(kb * kRows / kTile, q_tiles) : 0;
+  const int first = causal ? min(kb * kKRows / kTile, q_tiles) : 0;
   const int per_head = q_tiles - first;
   const int tiles = (kSplit ? 1 : head_group) * per_head;
 
@@ -331,7 +357,7 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
       __builtin_amdgcn_global_load_lds(gbase + static_cast<int64_t>(q) * g.dout[2] + src,
                                        (lds_void_t *)(stage + kChunks + (wave * kDma + i) * 64), 16, 0, 0);
     }
-    if (wave < 2) {   // lse (wave 0) and delta (wave 1): one float of row q0 + lane per lane
+    if (wave < (kDoK ? 2 : 1)) {   // lse (wave 0) and delta (wave 1): one float of row q0 + lane per lane
       const int q = min(q0 + lane, sq - 1);
       const float *src = wave == 0 ? LSE + b * g.lse[0] + hq * g.lse[1] + static_cast<int64_t>(q) * g.lse[2]
                                    : DELTA + b * g.delta[0] + hq * g.delta[1] + static_cast<int64_t>(q) * g.delta[2];
@@ -354,7 +380,7 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   for (int t = 0; t < tiles; ++t) {
     // Waves 0 and 1 also move lse and delta: one more DMA instruction per tile.
     const int later = min(tiles - 1 - t, kStages - 2);
-    if (wave < 2) wait_tiles_after<2 * kDma + 1>(later);
+    if (wave < (kDoK ? 2 : 1)) wait_tiles_after<2 * kDma + 1>(later);
     else wait_tiles_after<2 * kDma>(later);
     __syncthreads();          // tile t is in LDS; every wave is done with tile t - 1
     if (t + kStages - 1 < tiles) issue(t + kStages - 1);   // into tile t - 1's stage
@@ -365,22 +391,26 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
     const float *lse_s = reinterpret_cast<const float *>(qtile + 2 * kChunks);
     const float *dlt_s = lse_s + kTile;
     // lse_s[i] / dlt_s[i] hold row q0 + i (the last row for i past the end, excluded by the mask).
-    f16x8_t pf[4], dsf[4];
+    const uint16_t *q16 = reinterpret_cast<const uint16_t *>(qtile);
+    const uint16_t *g16p = reinterpret_cast<const uint16_t *>(gtile);
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
+      f16x8_t pf[2], dsf[2];
       f32x16_t s, dp;
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.0f;
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
         s = mma(row_frag<D>(qtile, st * 32 + frag_row, ks, half), kf[ks], s);
-        dp = mma(row_frag<D>(gtile, st * 32 + frag_row, ks, half), vf[ks], dp);
+        if constexpr (kDoK) dp = mma(row_frag<D>(gtile, st * 32 + frag_row, ks, half), vf[ks], dp);
       }
+      __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
         const int local = st * 32 + 8 * e4 + 4 * half;        // rows local .. local + 3 of the tile
         const float4 l4 = *reinterpret_cast<const float4 *>(lse_s + local);
-        const float4 d4 = *reinterpret_cast<const float4 *>(dlt_s + local);
+        const float4 d4 = kDoK ? *reinterpret_cast<const float4 *>(dlt_s + local) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -388,20 +418,21 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
           const int q = q0 + local + j;
           const bool valid = q < sq && (!causal || lane_k <= q);
           const float p = valid ? __builtin_amdgcn_exp2f(fmaf(s[e], c1, -lv[j] * kLog2e)) : 0.0f;
-          pf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(p);
-          dsf[st * 2 + (e >> 3)][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dv[j]) : 0.0f);
+          if constexpr (kDoV) pf[e >> 3][e & 7] = static_cast<_Float16>(p);
+          if constexpr (kDoK) dsf[e >> 3][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dv[j]) : 0.0f);
         }
       }
+      // This half's 32 queries are 16-query slices 2 st and 2 st + 1 of the tile.
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int mt = 0; mt < D / 32; ++mt) {
+          if constexpr (kDoV) acc_v[mt] = mma(tr_frag<D>(g16p, st * 2 + h2, mt, t_row, t_col), pf[h2], acc_v[mt]);
+          if constexpr (kDoK) acc_k[mt] = mma(tr_frag<D>(q16, st * 2 + h2, mt, t_row, t_col), dsf[h2], acc_k[mt]);
+        }
+      __builtin_amdgcn_s_setprio(0);
     }
-    const uint16_t *q16 = reinterpret_cast<const uint16_t *>(qtile);
-    const uint16_t *g16p = reinterpret_cast<const uint16_t *>(gtile);
-#pragma unroll
-    for (int sl = 0; sl < 4; ++sl)
-#pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt) {
-        acc_v[mt] = mma(tr_frag<D>(g16p, sl, mt, t_row, t_col), pf[sl], acc_v[mt]);
-        acc_k[mt] = mma(tr_frag<D>(q16, sl, mt, t_row, t_col), dsf[sl], acc_k[mt]);
-      }
   }
 
   if (!k_ok) return;
@@ -415,10 +446,12 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         const int col = mt * 32 + 8 * gq + 4 * half;
-        *reinterpret_cast<float4 *>(pk + col) =
-            make_float4(acc_k[mt][4 * gq], acc_k[mt][4 * gq + 1], acc_k[mt][4 * gq + 2], acc_k[mt][4 * gq + 3]);
-        *reinterpret_cast<float4 *>(pv + col) =
-            make_float4(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1], acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]);
+        if constexpr (kDoK)
+          *reinterpret_cast<float4 *>(pk + col) =
+              make_float4(acc_k[mt][4 * gq], acc_k[mt][4 * gq + 1], acc_k[mt][4 * gq + 2], acc_k[mt][4 * gq + 3]);
+        if constexpr (kDoV)
+          *reinterpret_cast<float4 *>(pv + col) =
+              make_float4(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1], acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]);
       }
     return;
   }
@@ -429,23 +462,25 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const int col = mt * 32 + 8 * gq + 4 * half;
-      *reinterpret_cast<uint2 *>(krow + col) =
-          make_uint2(pack_f16x2(acc_k[mt][4 * gq] * scale, acc_k[mt][4 * gq + 1] * scale),
-                     pack_f16x2(acc_k[mt][4 * gq + 2] * scale, acc_k[mt][4 * gq + 3] * scale));
-      *reinterpret_cast<uint2 *>(vrow + col) = make_uint2(pack_f16x2(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1]),
-                                                          pack_f16x2(acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]));
+      if constexpr (kDoK)
+        *reinterpret_cast<uint2 *>(krow + col) =
+            make_uint2(pack_f16x2(acc_k[mt][4 * gq] * scale, acc_k[mt][4 * gq + 1] * scale),
+                       pack_f16x2(acc_k[mt][4 * gq + 2] * scale, acc_k[mt][4 * gq + 3] * scale));
+      if constexpr (kDoV)
+        *reinterpret_cast<uint2 *>(vrow + col) = make_uint2(pack_f16x2(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1]),
+                                                            pack_f16x2(acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]));
     }
 }
 
-template <int D, bool kSplit>
-__global__ __launch_bounds__(kThreads, 1) void attention_bwd_dkdv(
+template <int D, bool kSplit, int kPart, int kW>
+__global__ __launch_bounds__(kW * 64, 1) void attention_bwd_dkdv(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, float *__restrict__ partial, int kv_heads,
     int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks) {
   constexpr int kStage = 2 * (kTile * D / 8) + 2 * (kTile / 4);
   __shared__ uint4 lds[kStages * kStage];
-  attention_bwd_dkdv_body<D, kSplit>(Q, K, V, G, LSE, DELTA, DK, DV, partial, kv_heads, head_group, sq, sk, g,
+  attention_bwd_dkdv_body<D, kSplit, kPart, kW>(Q, K, V, G, LSE, DELTA, DK, DV, partial, kv_heads, head_group, sq, sk, g,
                                      scale, causal, k_blocks, lds);
 }
 
@@ -482,24 +517,36 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_dkdv_reduce(const floa
 
 namespace intent_hip {
 
-int attention_bwd_resources(int64_t which, int64_t d, IntentHipKernelResources *out) {
-  const bool d64 = d == 64;
+// rows: batch x heads x sequence of the call (query heads and queries for dQ, key heads and keys
+// for dK/dV); it selects the variant as the launch does. Wide dK/dV launches two kernels; the
+// first (dK) is described.
+int attention_bwd_resources(int64_t which, int64_t rows, int64_t d, IntentHipKernelResources *out) {
+  const bool d64 = d == 64, wide = rows >= kWideRows;
+  const auto describe = [out](const void *kernel, const char *name, int threads) {
+    return describe_kernel(kernel, name, threads, out);
+  };
   switch (which) {
     case 0:
-      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_delta<64>), "attention_bwd_delta<64>",
-                                   kThreads, out)
-                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_delta<128>),
-                                   "attention_bwd_delta<128>", kThreads, out);
+      return d64 ? describe(reinterpret_cast<const void *>(&attention_bwd_delta<64>), "attention_bwd_delta<64>", kThreads)
+                 : describe(reinterpret_cast<const void *>(&attention_bwd_delta<128>), "attention_bwd_delta<128>",
+                            kThreads);
     case 1:
-      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dq<64>), "attention_bwd_dq<64>",
-                                   kThreads, out)
-                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dq<128>), "attention_bwd_dq<128>",
-                                   kThreads, out);
+      if (wide)
+        return d64 ? describe(reinterpret_cast<const void *>(&attention_bwd_dq<64, 8>), "attention_bwd_dq<64,8>", 512)
+                   : describe(reinterpret_cast<const void *>(&attention_bwd_dq<128, 8>), "attention_bwd_dq<128,8>", 512);
+      return d64 ? describe(reinterpret_cast<const void *>(&attention_bwd_dq<64, 4>), "attention_bwd_dq<64,4>", kThreads)
+                 : describe(reinterpret_cast<const void *>(&attention_bwd_dq<128, 4>), "attention_bwd_dq<128,4>",
+                            kThreads);
     default:
-      return d64 ? describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<64, false>), "attention_bwd_dkdv<64>",
-                                   kThreads, out)
-                 : describe_kernel(reinterpret_cast<const void *>(&attention_bwd_dkdv<128, false>),
-                                   "attention_bwd_dkdv<128>", kThreads, out);
+      if (wide)
+        return d64 ? describe(reinterpret_cast<const void *>(&attention_bwd_dkdv<64, false, kOnlyDk, 8>),
+                              "attention_bwd_dk<64,8>", 512)
+                   : describe(reinterpret_cast<const void *>(&attention_bwd_dkdv<128, false, kOnlyDk, 8>),
+                              "attention_bwd_dk<128,8>", 512);
+      return d64 ? describe(reinterpret_cast<const void *>(&attention_bwd_dkdv<64, false, kBoth, 4>),
+                            "attention_bwd_dkdv<64,4>", kThreads)
+                 : describe(reinterpret_cast<const void *>(&attention_bwd_dkdv<128, false, kBoth, 4>),
+                            "attention_bwd_dkdv<128,4>", kThreads);
   }
 }
 
@@ -579,6 +626,73 @@ extern "C" int intent_hip_attention_bwd_delta(const void *o, const void *dout, f
   return INTENT_HIP_OK;
 }
 
+namespace {
+
+// attention_bwd_dq<D, kW> over every (batch, query head) and block of 32 kW queries.
+template <int D, int kW>
+int launch_dq(const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *G, const float *lse,
+              const float *delta, uint16_t *DQ, int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
+              int64_t sk, const BwdGeometry &g, float scale, int causal, hipStream_t s) {
+  const int q_blocks = static_cast<int>((sq + kW * 32 - 1) / (kW * 32));
+  const int64_t blocks = batch * q_heads * q_blocks;
+  if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
+  attention_bwd_dq<D, kW><<<dim3(static_cast<unsigned>(blocks)), dim3(kW * 64), 0, s>>>(
+      Q, K, V, G, lse, delta, DQ, static_cast<int>(q_heads), static_cast<int>(head_group), static_cast<int>(sq),
+      static_cast<int>(sk), g, scale, causal, q_blocks);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dq");
+  return INTENT_HIP_OK;
+}
+
+// attention_bwd_dkdv<D, kSplit, kPart, kW> over every (batch, key head) and block of 32 kW keys
+// (times head_group when split).
+template <int D, bool kSplit, int kPart, int kW>
+int launch_dkdv(const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *G, const float *lse,
+                const float *delta, uint16_t *DK, uint16_t *DV, float *partial, int64_t batch, int64_t kv_heads,
+                int64_t head_group, int64_t sq, int64_t sk, const BwdGeometry &g, float scale, int causal,
+                hipStream_t s) {
+  const int k_blocks = static_cast<int>((sk + kW * 32 - 1) / (kW * 32));
+  const int64_t blocks = batch * kv_heads * k_blocks * (kSplit ? head_group : 1);
+  if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
+  attention_bwd_dkdv<D, kSplit, kPart, kW><<<dim3(static_cast<unsigned>(blocks)), dim3(kW * 64), 0, s>>>(
+      Q, K, V, G, lse, delta, DK, DV, partial, static_cast<int>(kv_heads), static_cast<int>(head_group),
+      static_cast<int>(sq), static_cast<int>(sk), g, scale, causal, k_blocks);
+  if (hipPeekAtLastError() != hipSuccess)
+    return launch_status(kPart == kOnlyDk ? "attention_bwd_dk" : kPart == kOnlyDv ? "attention_bwd_dv" : "attention_bwd_dkdv");
+  return INTENT_HIP_OK;
+}
+
+// dK and dV of one call: split by query head with a workspace (then folded), as two 8-wave
+// kernels on wide grids, or as one 4-wave kernel.
+template <int D>
+int run_dkdv(const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *G, const float *lse,
+             const float *delta, uint16_t *DK, uint16_t *DV, float *partial, bool use_split, int64_t batch,
+             int64_t kv_heads, int64_t head_group, int64_t sq, int64_t sk, const BwdGeometry &g, float scale,
+             int causal, hipStream_t s) {
+  if (use_split) {
+    if (int rc = launch_dkdv<D, true, kBoth, 4>(Q, K, V, G, lse, delta, DK, DV, partial, batch, kv_heads, head_group,
+                                                sq, sk, g, scale, causal, s))
+      return rc;
+    const int64_t rows = batch * kv_heads * sk;
+    const dim3 rgrid(static_cast<unsigned>((rows * (D / 4) + kThreads - 1) / kThreads));
+    attention_bwd_dkdv_reduce<D><<<rgrid, dim3(kThreads), 0, s>>>(partial, DK, DV, static_cast<int>(kv_heads),
+                                                                  static_cast<int>(head_group), static_cast<int>(sk),
+                                                                  rows, g, scale);
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv_reduce");
+    return INTENT_HIP_OK;
+  }
+  if (batch * kv_heads * sk >= kWideRows) {
+    if (int rc = launch_dkdv<D, false, kOnlyDk, 8>(Q, K, V, G, lse, delta, DK, DV, nullptr, batch, kv_heads,
+                                                   head_group, sq, sk, g, scale, causal, s))
+      return rc;
+    return launch_dkdv<D, false, kOnlyDv, 8>(Q, K, V, G, lse, delta, DK, DV, nullptr, batch, kv_heads, head_group, sq,
+                                             sk, g, scale, causal, s);
+  }
+  return launch_dkdv<D, false, kBoth, 4>(Q, K, V, G, lse, delta, DK, DV, nullptr, batch, kv_heads, head_group, sq, sk,
+                                         g, scale, causal, s);
+}
+
+}  // namespace
+
 extern "C" int intent_hip_attention_bwd_dq(const void *q, const void *k, const void *v, const void *dout,
                                            const float *lse, const float *delta, void *dq, int64_t batch,
                                            int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
@@ -595,26 +709,19 @@ extern "C" int intent_hip_attention_bwd_dq(const void *q, const void *k, const v
   if (int rc = check_operand(dq, strides + 22, 1, "grad_q")) return rc;
   BwdGeometry g{};
   load_geometry(g, strides, false);
-  const int q_blocks = static_cast<int>((sq + kRows - 1) / kRows);
-  const int64_t blocks = batch * q_heads * q_blocks;
-  if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
   const auto *Q = static_cast<const uint16_t *>(q);
   const auto *K = static_cast<const uint16_t *>(k);
   const auto *V = static_cast<const uint16_t *>(v);
   const auto *G = static_cast<const uint16_t *>(dout);
   auto *DQ = static_cast<uint16_t *>(dq);
-  const dim3 grid(static_cast<unsigned>(blocks));
+  const bool wide = batch * q_heads * sq >= kWideRows;
+  const int c = causal ? 1 : 0;
   const hipStream_t s = as_stream(stream);
-  const int hq = static_cast<int>(q_heads), grp = static_cast<int>(head_group);
-  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk);
   if (d == 64)
-    attention_bwd_dq<64><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DQ, hq, grp, iq, ik, g, scale,
-                                                         causal ? 1 : 0, q_blocks);
-  else
-    attention_bwd_dq<128><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DQ, hq, grp, iq, ik, g, scale,
-                                                          causal ? 1 : 0, q_blocks);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dq");
-  return INTENT_HIP_OK;
+    return wide ? launch_dq<64, 8>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s)
+                : launch_dq<64, 4>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s);
+  return wide ? launch_dq<128, 8>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s)
+              : launch_dq<128, 4>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s);
 }
 
 namespace {
@@ -665,15 +772,12 @@ extern "C" int intent_hip_attention_bwd_dkdv_ws(const void *q, const void *k, co
   BwdGeometry g{};
   load_geometry(g, strides, true);
   const int64_t kv_heads = q_heads / head_group;
-  const int k_blocks = static_cast<int>((sk + kRows - 1) / kRows);
   const bool split = dkdv_split(batch, q_heads, head_group, sk);
   const int64_t need = split ? dkdv_workspace(batch, q_heads, head_group, sk, d) : 0;
   if (split && workspace != nullptr && (workspace_bytes < static_cast<size_t>(need) || !aligned(workspace, 16)))
     return fail(INTENT_HIP_ERR_WORKSPACE, "dK/dV needs %lld 16-byte aligned workspace bytes, got %zu",
                 static_cast<long long>(need), workspace_bytes);
   const bool use_split = split && workspace != nullptr;
-  const int64_t blocks = batch * kv_heads * k_blocks * (use_split ? head_group : 1);
-  if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
   const auto *Q = static_cast<const uint16_t *>(q);
   const auto *K = static_cast<const uint16_t *>(k);
   const auto *V = static_cast<const uint16_t *>(v);
@@ -681,35 +785,13 @@ extern "C" int intent_hip_attention_bwd_dkdv_ws(const void *q, const void *k, co
   auto *DK = static_cast<uint16_t *>(dk);
   auto *DV = static_cast<uint16_t *>(dv);
   auto *P = static_cast<float *>(workspace);
-  const dim3 grid(static_cast<unsigned>(blocks));
   const hipStream_t s = as_stream(stream);
-  const int hk = static_cast<int>(kv_heads), grp = static_cast<int>(head_group);
-  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk), c = causal ? 1 : 0;
-  if (use_split) {
-    if (d == 64)
-      attention_bwd_dkdv<64, true><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, P, hk, grp, iq,
-                                                                   ik, g, scale, c, k_blocks);
-    else
-      attention_bwd_dkdv<128, true><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, P, hk, grp, iq,
-                                                                    ik, g, scale, c, k_blocks);
-    if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv");
-    const int64_t rows = batch * kv_heads * sk;
-    const dim3 rgrid(static_cast<unsigned>((rows * (d / 4) + kThreads - 1) / kThreads));
-    if (d == 64)
-      attention_bwd_dkdv_reduce<64><<<rgrid, dim3(kThreads), 0, s>>>(P, DK, DV, hk, grp, ik, rows, g, scale);
-    else
-      attention_bwd_dkdv_reduce<128><<<rgrid, dim3(kThreads), 0, s>>>(P, DK, DV, hk, grp, ik, rows, g, scale);
-    if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv_reduce");
-    return INTENT_HIP_OK;
-  }
+  const int c = causal ? 1 : 0;
   if (d == 64)
-    attention_bwd_dkdv<64, false><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, nullptr, hk, grp,
-                                                                  iq, ik, g, scale, c, k_blocks);
-  else
-    attention_bwd_dkdv<128, false><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, G, lse, delta, DK, DV, nullptr, hk, grp,
-                                                                   iq, ik, g, scale, c, k_blocks);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv");
-  return INTENT_HIP_OK;
+    return run_dkdv<64>(Q, K, V, G, lse, delta, DK, DV, P, use_split, batch, kv_heads, head_group, sq, sk, g, scale,
+                        c, s);
+  return run_dkdv<128>(Q, K, V, G, lse, delta, DK, DV, P, use_split, batch, kv_heads, head_group, sq, sk, g, scale, c,
+                       s);
 }
 
 extern "C" int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,

@@ -31,7 +31,7 @@ int gemm_resources(int dtype, int64_t m, int64_t n, IntentHipKernelResources *ou
 int gemm_f32_resources(int64_t m, int64_t n, IntentHipKernelResources *out);
 int attention_resources(int dtype, int64_t sq, int64_t d, IntentHipKernelResources *out);
 int spmv_resources(int64_t rows, int64_t nnz, IntentHipKernelResources *out);
-int attention_bwd_resources(int64_t which, int64_t d, IntentHipKernelResources *out);
+int attention_bwd_resources(int64_t which, int64_t rows, int64_t d, IntentHipKernelResources *out);
 int decode_resources(int64_t which, int64_t d, int64_t group, IntentHipKernelResources *out);
 int spmm_resources(int64_t features, IntentHipKernelResources *out);
 

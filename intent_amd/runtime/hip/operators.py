@@ -329,9 +329,12 @@ def _attention_bwd(kind):
         else:
             fn = lib.fn["attention_bwd_dq"]
         op = OP_ATTENTION_BWD_DQ if kind == "dq" else OP_ATTENTION_BWD_DKDV
+        # The kernel variant depends on the rows of the call: batch x query heads x queries for dQ,
+        # batch x key heads x keys for dK/dV.
+        rows = batch * q_heads * sq if kind == "dq" else batch * (q_heads // group) * sk
         return Launch(f"intent_hip_attention_bwd_{kind}", lambda stream: fn(*args, stream), tuple(keep),
                       tuple(before), tuple(after), configuration,
-                      lambda: lib.kernel_resources(op, F16, sq, d))
+                      lambda: lib.kernel_resources(op, F16, rows, d))
     return plan
 
 

@@ -159,3 +159,73 @@ def test_dkdv_split_matches_unsplit_through_the_c_abi(device, shape):
     small = ctypes.c_size_t(0)
     assert lib.fn["attention_bwd_dkdv_workspace_bytes"](4, 32, 4, 4096, 4096, 128, ctypes.byref(small)) == 0
     assert small.value == 0                                     # large grids never split
+
+
+# Calls with at least 256 x 256 rows (batch x heads x sequence) take the 8-wave kernels: dQ with
+# 256-query workgroups, dK/dV as two kernels (dK, then dV) with 256-key workgroups. These shapes
+# reach that bound with short sequences so the oracle stays fast; 260 and 300 leave ragged blocks.
+@pytest.mark.parametrize("shape,causal", [((64, 4, 4, 256, 256, 128), True), ((64, 8, 4, 260, 260, 64), True),
+                                          ((70, 4, 4, 240, 300, 64), False)])
+def test_attention_backward_wide_grids_match_oracle(device, shape, causal):
+    batch, hq, hk, sq, sk, d = shape
+    assert batch * hk * sk >= 256 * 256 and batch * hq * sq >= 256 * 256
+    announce("attention backward, wide grid", shape, causal)
+    q, k, v, o, do, lse = case(sq + sk + d + batch, batch, hq, hk, sq, sk, d)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    program = AttentionBackward.from_jit(lambda defn, **kw: intent.jit(defn, backend="hip", **kw),
+                                         head_group=hq // hk, causal=causal)
+    grad_q, grad_k, grad_v = program.run(t(q), t(k), t(v), t(o), t(do), t(lse), scale)
+    delta = oracle.attention_bwd_delta(o, do)
+    want_dq = oracle.attention_bwd_dq(q, k, v, do, lse, delta, scale, causal, head_group=hq // hk)
+    want_dk, want_dv = oracle.attention_bwd_dkdv(q, k, v, do, lse, delta, scale, causal, head_group=hq // hk)
+    close(grad_q.cpu().numpy(), want_dq)
+    close(grad_k.cpu().numpy(), want_dk)
+    close(grad_v.cpu().numpy(), want_dv)
+
+
+@pytest.mark.parametrize("shape", [(17, 8, 4, 1000, 1000, 64), (17, 4, 4, 1000, 1000, 128)])
+def test_wide_grid_equals_per_batch_calls_through_the_c_abi(device, shape):
+    """Batch elements are independent, and every kernel variant gives each output element the same
+    arithmetic in the same order: the whole batch (8-wave kernels) must equal, bit for bit, one
+    call per batch element (4-wave kernels, dK and dV together; no workspace, so no head split)."""
+    import ctypes
+
+    from intent_amd.runtime.hip.library import library
+
+    batch, hq, hk, sq, sk, d = shape
+    assert batch * hk * sk >= 256 * 256 and hq * sq < 256 * 256
+    announce("attention backward wide vs per-batch", shape)
+    q, k, v, o, do, lse = case(sum(shape), batch, hq, hk, sq, sk, d)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    tq, tk, tv, tdo, tlse = t(q), t(k), t(v), t(do), t(lse)
+    tdelta = t(oracle.attention_bwd_delta(o, do))
+    lib = library()
+    scale = float(np.float32(d ** -0.5))
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(sl):
+        a = [x[sl] for x in (tq, tk, tv, tdo, tlse, tdelta)]
+        dq, dk, dv = torch.empty_like(a[0]), torch.empty_like(a[1]), torch.empty_like(a[2])
+        base = [s for x in a[:4] for s in x.stride()] + list(a[4].stride()) + list(a[5].stride())
+        st_q = (ctypes.c_int64 * 26)(*base, *dq.stride())
+        st_k = (ctypes.c_int64 * 30)(*base, *dk.stride(), *dv.stride())
+        n = a[0].shape[0]
+        ptrs = [x.data_ptr() for x in a]
+        assert lib.fn["attention_bwd_dq"](*ptrs, dq.data_ptr(), n, hq, hq // hk, sq, sk, d, st_q, scale, 1,
+                                          stream) == 0
+        assert lib.fn["attention_bwd_dkdv"](*ptrs, dk.data_ptr(), dv.data_ptr(), n, hq, hq // hk, sq, sk, d, st_k,
+                                            scale, 1, stream) == 0
+        return dq, dk, dv
+
+    whole = run(slice(None))
+    parts = [run(slice(i, i + 1)) for i in range(batch)]
+    torch.cuda.synchronize()
+    for j, name in enumerate(("dq", "dk", "dv")):
+        joined = torch.cat([p[j] for p in parts])
+        assert torch.equal(whole[j], joined), name
+    delta_np = tdelta.cpu().numpy()
+    want_dk, want_dv = oracle.attention_bwd_dkdv(q[:1], k[:1], v[:1], do[:1], lse[:1], delta_np[:1], scale, True,
+                                                 head_group=hq // hk)
+    close(whole[1][:1].cpu().numpy(), want_dk)
+    close(whole[2][:1].cpu().numpy(), want_dv)
