@@ -59,8 +59,8 @@ template <> struct Elem<__bf16> {
 
 template <typename E>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<E>(lo))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<E>(hi))) << 16);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(hi))) << 16);
 }
 
 constexpr int kD = 128;

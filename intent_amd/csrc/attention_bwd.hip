@@ -81,8 +81,8 @@ __device__ __forceinline__ uint4 select(bool keep, uint4 v) {
 }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<_Float16>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<_Float16>(hi))) << 16);
 }
 
 // Element strides of the backward operands (batch, head, row, col for 4-D; batch, head, row for
@@ -253,7 +253,7 @@ __device__ __forceinline__ void attention_bwd_dq_body(
         const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
         const bool valid = key < sk && (!causal || key <= lane_q);
         const float p = valid ? __builtin_amdgcn_exp2f(fmaf(s[e], c1, -lse2)) : 0.0f;
-        dsf[e >> 3][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dlt) : 0.0f);
+        dsf[e >> 3][e & 7] = round_to<_Float16>(valid ? p * (dp[e] - dlt) : 0.0f);
       }
       // This half's 32 keys are 16-key slices 2 st and 2 st + 1 of the tile.
       __builtin_amdgcn_s_setprio(1);
@@ -419,7 +419,7 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
           const bool valid = q < sq && (!causal || lane_k <= q);
           const float p = valid ? __builtin_amdgcn_exp2f(fmaf(s[e], c1, -lv[j] * kLog2e)) : 0.0f;
           if constexpr (kDoV) pf[e >> 3][e & 7] = static_cast<_Float16>(p);
-          if constexpr (kDoK) dsf[e >> 3][e & 7] = static_cast<_Float16>(valid ? p * (dp[e] - dv[j]) : 0.0f);
+          if constexpr (kDoK) dsf[e >> 3][e & 7] = round_to<_Float16>(valid ? p * (dp[e] - dv[j]) : 0.0f);
         }
       }
       // This half's 32 queries are 16-query slices 2 st and 2 st + 1 of the tile.

@@ -84,6 +84,16 @@ __device__ __forceinline__ float to_f32(bf16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
 }
 
+// f32 -> _Float16 or __bf16, rounded to nearest even. The empty asm makes v opaque, so
+// instruction selection cannot fuse the conversion with the f32 product or FMA that produced v:
+// v_fma_mixlo_f16 would round once, straight to 16 bits, where the definitions round the f32
+// result and then cast. It emits no instruction.
+template <typename E>
+__device__ __forceinline__ E round_to(float v) {
+  asm("" : "+v"(v));
+  return static_cast<E>(v);
+}
+
 template <typename T>
 __device__ __forceinline__ T from_f32(float v);
 template <>
@@ -91,7 +101,7 @@ __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
   // v_cvt_f16_f32 rounds to nearest even; finite overflow gives infinity.
-  return f16_t{__builtin_bit_cast(uint16_t, static_cast<_Float16>(v))};
+  return f16_t{__builtin_bit_cast(uint16_t, round_to<_Float16>(v))};
 }
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {

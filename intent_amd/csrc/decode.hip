@@ -268,7 +268,7 @@ __global__ __launch_bounds__(64) void splitk_reduce_f32_to_f16(const float *__re
     float num = 0.0f;
 #pragma unroll 8
     for (int s = 0; s < splits; ++s) num = fmaf(expf(lse[s * g.lse[2]] - top), prow[s * g.q[2] + c], num);
-    OUT[b * g.out[0] + h * g.out[1] + c] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(num * inv));
+    OUT[b * g.out[0] + h * g.out[1] + c] = __builtin_bit_cast(uint16_t, round_to<_Float16>(num * inv));
   }
 }
 

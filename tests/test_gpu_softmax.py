@@ -138,6 +138,32 @@ def test_softmax_bwd_f16(device, shape):
     assert np.all(np.abs(dx.astype(np.float64) - want) <= 2 ** -9 * np.abs(want.astype(np.float64)) + spread + 6e-8)
 
 
+def test_softmax_bwd_f16_rounds_like_the_definition(device):
+    """Inputs on which every product, the whole projection sum and dy - proj are exact in f32
+    (p = k 2^-12 with k < 2048 at 128 places per row, dy = j 2^-3 with |j| < 32), so the
+    summation order cannot matter and dx must equal the oracle bit for bit. The definition
+    rounds p * (dy - proj) to f32 and then casts to f16; on these rows 31 elements differ from
+    a single rounding straight to f16 (a multiply fused with the conversion), so such a fusion
+    fails here."""
+    announce("softmax_bwd_f16 exact-rounding rows")
+    rng = np.random.default_rng(7)
+    rows, cols, nz = 4096, 4096, 128
+    k = np.zeros((rows, cols), np.int64)
+    for r in range(rows):
+        k[r, rng.choice(cols, nz, replace=False)] = rng.integers(1, 2048, nz)
+    p = (k * 2.0 ** -12).astype(np.float16)
+    dy = (rng.integers(-31, 32, (rows, cols)) * 2.0 ** -3).astype(np.float16)
+    p64 = p.astype(np.float64)
+    product = p64 * (dy.astype(np.float64) - (p64 * dy.astype(np.float64)).sum(axis=1, keepdims=True))
+    once = product.astype(np.float16)
+    want = oracle.softmax_bwd(p, dy)
+    assert np.array_equal(want.view(np.uint16), product.astype(np.float32).astype(np.float16).view(np.uint16))
+    assert (want.view(np.uint16) != once.view(np.uint16)).sum() > 0     # the rows discriminate
+    dx = intent.jit(softmax_backward_f16, backend="hip").run(torch.from_numpy(p).to(device),
+                                                            torch.from_numpy(dy).to(device)).cpu().numpy()
+    assert np.array_equal(dx.view(np.uint16), want.view(np.uint16))
+
+
 def test_softmax_bwd_golden(device, golden):
     announce("softmax_bwd golden")
     g = golden("softmax_bwd")
