@@ -10,10 +10,11 @@
 // Design: one wavefront owns one row, two rows per workgroup. The row is loaded once with
 // 128-bit loads (lane l of chunk c reads columns [(64c + l) * V, +V)), held in registers,
 // reduced with DPP (no LDS, no barrier), and written once: one HBM read and one write per
-// element, the minimum. Rows longer than the register-resident limit, or rows whose
-// layout rules out 128-bit access, use a scalar variant; rows longer than 64 * 64
-// scalar elements use a streaming variant that re-reads the row (3 passes forward,
-// 2 backward).
+// element, the minimum. f16 rows are held as their raw 16-bit words where that frees registers
+// (x until its exponentials replace it, dy throughout), which raises the waves per SIMD.
+// Rows longer than the register-resident limit, or rows whose layout rules out 128-bit
+// access, use a scalar variant; rows longer than 64 * 64 scalar elements use a streaming
+// variant that re-reads the row (3 passes forward, 2 backward).
 #include <math.h>
 
 #include <type_traits>
@@ -97,6 +98,17 @@ __device__ __forceinline__ float quotient(float e, float s, float r) {
   return fmaf(fmaf(-q, s, e), r, q);
 }
 
+// ---------------------------------------------------------------- raw 16-bit rows
+// The raw 16-bit words of one 16-byte chunk (8 elements), read once, and element i widened.
+__device__ __forceinline__ u32x4_t load_words(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+}
+template <typename T>
+__device__ __forceinline__ float widen(const u32x4_t &w, int i) {
+  const uint32_t word = w[i >> 1];
+  return to_f32(T{static_cast<uint16_t>((i & 1) ? (word >> 16) : (word & 0xffffu))});
+}
+
 // ---------------------------------------------------------------- forward, register resident
 template <typename T, int V, int CHUNKS>
 __global__ __launch_bounds__(kBlock) void softmax_fwd_wave(const T *x, T *y, int64_t rows, int cols,
@@ -105,6 +117,47 @@ __global__ __launch_bounds__(kBlock) void softmax_fwd_wave(const T *x, T *y, int
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;  // wave-uniform
   const T *xr = x + row * xs;
+  if constexpr (std::is_same<T, f16_t>::value && V == 8) {
+    // x stays in its raw f16 words until the exponentials replace it: 79 VGPRs instead of 90,
+    // six waves per SIMD instead of five (forward of the 16384 x 4096 step, bit-identical:
+    // 51.2 against 53.4 us). Loads are unconditional, as in the backward.
+    u32x4_t xw[CHUNKS];
+    float m = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int col = (c * kWave + lane) * V;
+      const bool live = col < cols;
+      xw[c] = load_words(xr + (live ? col : 0));
+#pragma unroll
+      for (int i = 0; i < V; ++i) m = live ? fmaxf(m, widen<T>(xw[c], i)) : m;
+    }
+    m = wave_max(m);
+    float v[CHUNKS][V];
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const bool live = (c * kWave + lane) * V < cols;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        v[c][i] = live ? shifted_exp<T>(widen<T>(xw[c], i), m) : 0.0f;
+        s += v[c][i];
+      }
+    }
+    s = wave_sum(s);
+    const float r = 1.0f / s;
+    T *yr = y + row * ys;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      const int col = (c * kWave + lane) * V;
+      if (col < cols) {
+        float o[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) o[i] = quotient(v[c][i], s, r);
+        store_row_chunk<T, V, false>(yr + col, o);
+      }
+    }
+    return;
+  }
   float v[CHUNKS][V];
   float m = -INFINITY;
 #pragma unroll
@@ -168,16 +221,6 @@ __global__ __launch_bounds__(kBlock) void softmax_fwd_stream(const T *x, T *y, i
 }
 
 // ---------------------------------------------------------------- backward, register resident
-// The raw 16-bit words of one 16-byte chunk (8 elements), read once, and element i widened.
-__device__ __forceinline__ u32x4_t load_words(const void *p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
-}
-template <typename T>
-__device__ __forceinline__ float widen(const u32x4_t &w, int i) {
-  const uint32_t word = w[i >> 1];
-  return to_f32(T{static_cast<uint16_t>((i & 1) ? (word >> 16) : (word & 0xffffu))});
-}
-
 template <typename T, int V, int CHUNKS>
 __global__ __launch_bounds__(kBlock) void softmax_bwd_wave(const T *p, const T *dy, T *dx, int64_t rows,
                                                            int cols, int64_t ps, int64_t dys,
