@@ -78,8 +78,9 @@ class Flush:
 
 
 def graph_median_ms(launch, flush, replays=33):
-    """Reference protocol (runtime/triton/cuda.py:18-44): warm up, capture, replay with a flush
-    before each timed replay, drop the first sample, report the median."""
+    """Graph replays with a flush before each, HIP events recorded around graph.replay(); drops
+    the first sample and reports the median. The interval includes the replay's own launch path
+    (about 7 us more than operator_ms on a 6 us kernel)."""
     import torch
 
     launch()
@@ -102,6 +103,47 @@ def graph_median_ms(launch, flush, replays=33):
         end.synchronize()
         samples.append(start.elapsed_time(end))
     return statistics.median(samples[1:])
+
+
+# graph-replay time of the last operator_ms call, attached to its operator's record
+_LAST_GRAPH_MS = {}
+
+
+def operator_ms(launch, flush, replays=33):
+    """Median duration of one call's kernels, cold, as the reference measures it.
+
+    The reference (runtime/triton/cuda.py:18-44 with the hooks of runtime/triton/program.py:47-63)
+    captures zero-fill, start.record(), the launch and end.record() in one graph, so its events
+    bracket the kernels and not the graph launch. ROCm's torch refuses event records inside a
+    capture ("External events are disallowed in rocm"). Here the 512 MiB flush (about 200 us of
+    GPU work) is enqueued first, then start, the eager launch and end: the launches reach the
+    queue while the flush still runs, so the events again bracket only the kernels. The graph
+    replay time (events around graph.replay()) is sampled in the same loop, alternating with the
+    eager samples so both see the same clocks, and kept beside it."""
+    import torch
+
+    launch()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            launch()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    eager, replayed = [], []
+    for _ in range(replays):
+        for samples, body in ((eager, launch), (replayed, graph.replay)):
+            flush()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            body()
+            end.record()
+            end.synchronize()
+            samples.append(start.elapsed_time(end))
+    _LAST_GRAPH_MS["graph_ms"] = statistics.median(replayed[1:])
+    return statistics.median(eager[1:])
 
 
 def events_ms(launch, count):
@@ -193,13 +235,13 @@ def box_reference(device, flush):
 
     src = torch.ones(512 << 20, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
-    copy_ms = graph_median_ms(lambda: dst.copy_(src), flush)
+    copy_ms = operator_ms(lambda: dst.copy_(src), flush)
     del src, dst
     g = torch.Generator(device="cpu").manual_seed(0)
     a = (torch.rand((8192, 8192), generator=g) * 2 - 1).to(torch.bfloat16).to(device)
     b = (torch.rand((8192, 8192), generator=g) * 2 - 1).to(torch.bfloat16).to(device)
     c = torch.empty((8192, 8192), dtype=torch.bfloat16, device=device)
-    gemm_ms = graph_median_ms(lambda: torch.matmul(a, b, out=c), flush)
+    gemm_ms = operator_ms(lambda: torch.matmul(a, b, out=c), flush)
     return {"torch_copy_gbs": round(2 * (512 << 20) / copy_ms / 1e6, 1),
             "hipblaslt_bf16_gemm_8192_tflops": round(2 * 8192 ** 3 / gemm_ms / 1e9, 1),
             "hipblaslt_bf16_gemm_8192_ms": round(gemm_ms, 4)}
@@ -215,7 +257,7 @@ def op_softmax_f32(device, flush, cpu):
 
     x = inputs.softmax_f32()
     call = intent.jit(stable_softmax, backend="hip").prepare(torch.from_numpy(x).to(device))
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     nbytes = 2 * 4 * x.size
     out = {"config": "softmax fwd f32 4096x1024 (config 1)", "median_ms": round(ms, 5),
            "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
@@ -238,7 +280,7 @@ def op_gemm(device, flush, cpu):
     m = n = k = 8192
     a, b = inputs.gemm_bf16()
     call = intent.jit(bf16_gemm, backend="hip").prepare(to_bf16_tensor(a, device), to_bf16_tensor(b, device))
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     flops = 2 * m * n * k
     out = {"config": "GEMM bf16 8192^3, fp32 accumulate (config 3)", "median_ms": round(ms, 4),
            "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
@@ -265,7 +307,7 @@ def op_attention(device, flush, cpu):
     t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
     call = intent.jit(flash_attention_fwd, backend="hip", constexprs={"CAUSAL": True}).prepare(
         t(q), t(k), t(v), scale)
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     b, h, s, d = q.shape
     flops = 4 * b * h * s * s * d // 2
     out = {"config": "causal attention fwd f16 B4 H32 S4096 D128 (config 4)", "median_ms": round(ms, 4),
@@ -293,7 +335,7 @@ def op_spmv(device, flush, cpu):
     offsets, columns, values, x = inputs.spmv_f32()
     t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
     call = intent.jit(csr_spmv, backend="hip").prepare(t(offsets), t(columns), t(values), t(x))
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     rows, nnz = offsets.shape[0] - 1, int(offsets[-1])
     nbytes = 4 * (rows + 1) + 8 * nnz + 4 * x.shape[0] + 4 * rows
     out = {"config": f"CSR SpMV f32 {rows}^2, {nnz} nnz, rank-law Zipf(1.5) rows (config 5)",
@@ -322,7 +364,7 @@ def op_gemm_f16_relu(device, flush, cpu):
     b = inputs.uniform(rng, (k, n), -1.0, 1.0, "f16")
     call = intent.jit(gemm, backend="hip", constexprs={"ACTIVATION": Activation.RELU}).prepare(
         torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     flops = 2 * m * n * k
     out = {"config": "gemm f16 8192^3, ACTIVATION=RELU, fp32 accumulate", "median_ms": round(ms, 4),
            "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
@@ -352,7 +394,7 @@ def _op_f32(device, flush, cpu, transpose_b):
     b = inputs.uniform(rng, (n, k) if transpose_b else (k, n), -1.0, 1.0)
     defn = linear_f32 if transpose_b else gemm_f32
     call = intent.jit(defn, backend="hip").prepare(torch.from_numpy(a).to(device), torch.from_numpy(b).to(device))
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     flops = 2 * m * n * k
     out = {"config": f"{defn.__name__} M=4096 K=4096 N=14336, f32", "median_ms": round(ms, 4),
            "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
@@ -399,7 +441,7 @@ def _op_attention_grouped(device, flush, cpu, bf16):
     defn = flash_attention_bf16_fwd if bf16 else flash_gqa_attention_fwd
     call = intent.jit(defn, backend="hip", constexprs={"HEAD_GROUP": group, "CAUSAL": True}).prepare(
         conv(q), conv(k), conv(v), scale)
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     flops = 4 * b * hq * s * s * d // 2
     name = ("causal attention fwd bf16 B4 H32 S4096 D128 (flash_attention_bf16_fwd)" if bf16 else
             "causal GQA attention fwd f16 B4 HQ32 HK8 S4096 D128 (flash_gqa_attention_fwd)")
@@ -448,7 +490,7 @@ def _op_attention_bwd(device, flush, cpu, large):
     program = AttentionBackward.from_jit(lambda defn, **kw: intent.jit(defn, backend="hip", **kw),
                                          head_group=hq // hk, causal=True)
     call = program.prepare(t(q), t(k), t(v), t(o), t(do), t(lse), scale)
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     flops = 14 * b * hq * s * s * d // 2          # dQ: 3 products, dK/dV: 4 products, causal half
     out = {"config": f"causal attention backward f16 B{b} HQ{hq} HK{hk} S{s} D{d} (delta + dK/dV + dQ)",
            "median_ms": round(ms, 4), "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
@@ -499,7 +541,7 @@ def op_paged_decode(device, flush, cpu):
     program = PagedDecode.from_jit(lambda defn, **kw: intent.jit(defn, backend="hip", **kw), page_size=page_size,
                                    head_group=hq // hk, splits=splits)
     call = program.prepare(*(t(a) for a in arrays), scale)
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     partials, merge = call.calls
     partial_ms, merge_ms = sequence_kernel_ms(partials.launch, merge.launch, 50)
     tokens = int(lengths.astype(np.int64).sum())
@@ -541,7 +583,7 @@ def op_spmm(device, flush, cpu):
     offsets, columns, values, dense = inputs.csr_spmm()
     t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
     call = intent.jit(csr_spmm, backend="hip").prepare(t(offsets), t(columns), t(values), t(dense))
-    ms = graph_median_ms(call.launch, flush)
+    ms = operator_ms(call.launch, flush)
     rows, nnz = offsets.shape[0] - 1, int(offsets[-1])
     cols, features = dense.shape
     nbytes = 4 * (rows + 1) + 8 * nnz + 4 * cols * features + 4 * rows * features
@@ -681,6 +723,9 @@ def main():
             log(f"operator {name}")
             try:
                 operators.append(OPERATORS[name](device, flush, not args.no_cpu_baseline))
+                graph_ms = _LAST_GRAPH_MS.pop("graph_ms", None)
+                if graph_ms is not None:
+                    operators[-1]["graph_ms"] = round(graph_ms, 5)
             except intent.CompilationStageError as error:
                 operators.append({"config": name, "status": "unsupported", "error": str(error)})
             log(json.dumps(operators[-1]))
