@@ -6,9 +6,11 @@ backward in f16 storage with f32 math, 16384 x 4096 — one step = stable_softma
 then softmax_backward_f16 through prepared intent.jit calls; throughput = algorithmic
 bytes (fwd 4*M*N + bwd 6*M*N = 671,088,640 B) / measured step time (K eager steps between HIP
 events; the same step as hipGraph replays is reported beside it), inputs resident in HBM. `roofline` is the dominant kernel (the backward), timed with HIP events on the launch
-stream between the launches of the real fwd/bwd sequence. `operators` carries every other configuration (median of 33 graph replays,
-first dropped, 512 MiB write-then-read flush of the 256 MB MALL before each), and
-`cpu_baseline` the oracle on a bounded sample on this host.
+stream between the launches of the real fwd/bwd sequence. `operators` carries every other configuration: the median
+of 33 cold calls (first dropped, 512 MiB write-then-read flush of the 256 MB MALL before each), events around the
+launches queued behind the flush so that they bracket the kernels as the reference's in-graph events do
+(operator_ms); the median of graph replays timed around graph.replay() is kept beside it as graph_ms. `cpu_baseline`
+is the oracle on a bounded sample on this host.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-operators] [--no-cpu-baseline]
 """
@@ -229,8 +231,8 @@ def headline_cpu_baseline(x, dy):
 
 def box_reference(device, flush):
     """Figures of the box itself, beside the kernels' rooflines: a torch device copy of 512 MiB
-    (read + write GB/s) and torch.matmul bf16 8192^3 (hipBLASLt), both median graph replays
-    after the flush."""
+    (read + write GB/s) and torch.matmul bf16 8192^3 (hipBLASLt), both timed like the operators
+    (operator_ms)."""
     import torch
 
     src = torch.ones(512 << 20, dtype=torch.uint8, device=device)
