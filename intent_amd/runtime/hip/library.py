@@ -11,7 +11,7 @@ from pathlib import Path
 
 from ...diagnostics import CompilationStageError
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 LIBRARY_NAME = "libintent_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parents[2] / LIBRARY_NAME
 
