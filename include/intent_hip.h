@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 6
+#define INTENT_HIP_ABI_VERSION 7
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -177,6 +177,23 @@ int intent_hip_attention_bwd_dq(const void *q, const void *k, const void *v, con
                                 int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
                                 const int64_t strides[26], float scale, int causal, void *stream);
 
+/* The same with a caller-owned device workspace. When the call has fewer than 256 * 256 rows
+ * (batch * q_heads * sq) and the grid above would hold fewer than 256 workgroups
+ * (batch * q_heads * ceil(sq / 128)), the key tiles of each query block are divided into up to 8
+ * ranges (enough for about 512 workgroups) with a workgroup each, which write unscaled f32 partial sums to the workspace
+ * ([splits][batch * q_heads][sq][d]); a second kernel folds them in range order, scales and
+ * casts. intent_hip_attention_bwd_dq_workspace_bytes gives the size (0 when the split is not
+ * taken; the workspace may then be NULL, and a NULL workspace always selects the unsplit kernel).
+ * The workspace must be 16-byte aligned. No counterpart in the reference: the reference's single
+ * kernel launch (backward/attention.py:171-211) has no workspace. */
+int intent_hip_attention_bwd_dq_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_group,
+                                                int64_t sq, int64_t sk, int64_t d, size_t *bytes);
+int intent_hip_attention_bwd_dq_ws(const void *q, const void *k, const void *v, const void *dout,
+                                   const float *lse, const float *delta, void *dq, int64_t batch,
+                                   int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                                   const int64_t strides[26], float scale, int causal, void *workspace,
+                                   size_t workspace_bytes, void *stream);
+
 /* dk = f16(scale * sum_q f16(ds) q), dv = f16(sum_q f16(p) dout), summed over the head_group query
  * heads of each key head: attention_backward_dkdv (:87-137) with summarize_key_value_gradients
  * (:47-79). strides[30]: q, k, v, dout (4 each), lse[3], delta[3], dk[4], dv[4]. */
@@ -186,11 +203,12 @@ int intent_hip_attention_bwd_dkdv(const void *q, const void *k, const void *v, c
                                   int64_t sk, int64_t d, const int64_t strides[30], float scale,
                                   int causal, void *stream);
 
-/* The same with a caller-owned device workspace. When head_group > 1 and the grid above would
- * hold fewer than 256 workgroups (batch * kv_heads * ceil(sk / 128)), each query head of the
- * group gets its own workgroups, which write unscaled f32 partial sums to the workspace
- * ([2][head_group][batch][kv_heads][sk][d]: dK, then dV); a second kernel folds them over the
- * group in head order, scales dK and casts. intent_hip_attention_bwd_dkdv_workspace_bytes gives
+/* The same with a caller-owned device workspace. When the grid above would hold fewer than 256
+ * workgroups (batch * kv_heads * ceil(sk / 128)), each query head of the group, and each of up to
+ * 8 ranges of its query tiles (qsplits, enough for about 512 workgroups), gets its own workgroups, which write unscaled f32
+ * partial sums to the workspace ([2][head_group * qsplits][batch][kv_heads][sk][d]: dK, then dV);
+ * a second kernel folds them in (head, range) order, scales dK and casts. With head_group == 1
+ * the split is taken only when qsplits > 1. intent_hip_attention_bwd_dkdv_workspace_bytes gives
  * the size (0 when the split is not taken; the workspace may then be NULL, and a NULL workspace
  * always selects the unsplit kernel). The workspace must be 16-byte aligned. No counterpart in
  * the reference: the reference's single kernel launch (backward/attention.py:87-137) has no

@@ -153,22 +153,27 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_delta(const uint16_t *
 }
 
 // ---------------------------------------------------------------- dQ
-// kW waves of 32 queries per workgroup (4 or 8).
+// kW waves of 32 queries per workgroup (4 or 8). With splits > 1 the key tiles of each query
+// block are divided into `splits` consecutive ranges, one workgroup each, which write unscaled
+// f32 partial sums to `partial` ([split][batch * heads][sq][D]); attention_bwd_dq_reduce folds
+// them in split order. Used when too few workgroups would run.
 template <int D, int kW>
 __device__ __forceinline__ void attention_bwd_dq_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
-    uint16_t *__restrict__ DQ, int heads, int head_group, int sq, int sk, BwdGeometry g, float scale, int causal,
-    int q_blocks, uint4 *lds) {
+    uint16_t *__restrict__ DQ, float *__restrict__ partial, int heads, int head_group, int sq, int sk,
+    BwdGeometry g, float scale, int causal, int q_blocks, int splits, uint4 *lds) {
   constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one K (or V) tile
   constexpr int kDma = kChunks / (kW * 64);        // per thread per operand
   constexpr int kQRows = kW * 32;
   static_assert(kDma * kW * 64 == kChunks, "DMA split");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bh_count = gridDim.x / q_blocks;
-  const int qb = q_blocks - 1 - static_cast<int>(blockIdx.x) / bh_count;   // heaviest blocks first
-  const int bh = static_cast<int>(blockIdx.x) % bh_count;
+  const int split = static_cast<int>(blockIdx.x) % splits;
+  const int item = static_cast<int>(blockIdx.x) / splits;
+  const int bh_count = gridDim.x / (q_blocks * splits);
+  const int qb = q_blocks - 1 - item / bh_count;   // heaviest blocks first
+  const int bh = item % bh_count;
   const int b = bh / heads, h = bh % heads, kh = h / head_group;
   const uint16_t *kbase = K + b * g.k[0] + kh * g.k[1];
   const uint16_t *vbase = V + b * g.v[0] + kh * g.v[1];
@@ -195,11 +200,13 @@ __device__ __forceinline__ void attention_bwd_dq_body(
 
   const int q_last_block = min(qb * kQRows + kQRows, sq) - 1;
   const int k_end = causal ? min(sk, q_last_block + 1) : sk;
-  const int tiles = (k_end + kTile - 1) / kTile;
+  const int all_tiles = (k_end + kTile - 1) / kTile;
+  const int t_begin = split * all_tiles / splits, t_end = (split + 1) * all_tiles / splits;
   const int wave_q_last = min(wq0 + 31, sq - 1);
 
+  // Key tile kt goes to stage (kt - t_begin) % kStages.
   auto issue = [&](int kt) {
-    uint4 *stage = lds + (kt % kStages) * 2 * kChunks;
+    uint4 *stage = lds + ((kt - t_begin) % kStages) * 2 * kChunks;
     const int key0 = kt * kTile;
 #pragma unroll
     for (int i = 0; i < kDma; ++i) {
@@ -225,14 +232,14 @@ __device__ __forceinline__ void attention_bwd_dq_body(
   const int t_row = 4 * (g16 >> 1) + (i16 >> 2);
   const int t_col = 16 * (g16 & 1) + 4 * (i16 & 3);
 
-  for (int kt = 0; kt < kStages - 1 && kt < tiles; ++kt) issue(kt);
-  for (int kt = 0; kt < tiles; ++kt) {
-    wait_tiles_after<2 * kDma>(min(tiles - 1 - kt, kStages - 2));
+  for (int kt = t_begin; kt < t_begin + kStages - 1 && kt < t_end; ++kt) issue(kt);
+  for (int kt = t_begin; kt < t_end; ++kt) {
+    wait_tiles_after<2 * kDma>(min(t_end - 1 - kt, kStages - 2));
     __syncthreads();          // tile kt is in LDS; every wave is done with tile kt - 1
-    if (kt + kStages - 1 < tiles) issue(kt + kStages - 1);   // into tile kt - 1's stage
+    if (kt + kStages - 1 < t_end) issue(kt + kStages - 1);   // into tile kt - 1's stage
     const int key0 = kt * kTile;
     if ((causal && key0 > wave_q_last) || wq0 >= sq) continue;   // wave-uniform
-    const uint4 *ktile = lds + (kt % kStages) * 2 * kChunks;
+    const uint4 *ktile = lds + ((kt - t_begin) % kStages) * 2 * kChunks;
     const uint4 *vtile = ktile + kChunks;
     const uint16_t *kt16 = reinterpret_cast<const uint16_t *>(ktile);
 #pragma unroll
@@ -266,6 +273,16 @@ __device__ __forceinline__ void attention_bwd_dq_body(
   }
 
   if (!q_ok) return;
+  if (partial != nullptr) {
+    float *prow = partial + ((static_cast<int64_t>(split) * bh_count + bh) * sq + lane_q) * D;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        *reinterpret_cast<float4 *>(prow + mt * 32 + 8 * gq + 4 * half) =
+            make_float4(acc[mt][4 * gq], acc[mt][4 * gq + 1], acc[mt][4 * gq + 2], acc[mt][4 * gq + 3]);
+    return;
+  }
   uint16_t *orow = DQ + b * g.out0[0] + h * g.out0[1] + static_cast<int64_t>(lane_q) * g.out0[2];
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt)
@@ -280,24 +297,48 @@ template <int D, int kW>
 __global__ __launch_bounds__(kW * 64, 1) void attention_bwd_dq(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
-    uint16_t *__restrict__ DQ, int heads, int head_group, int sq, int sk, BwdGeometry g, float scale, int causal,
-    int q_blocks) {
+    uint16_t *__restrict__ DQ, float *__restrict__ partial, int heads, int head_group, int sq, int sk,
+    BwdGeometry g, float scale, int causal, int q_blocks, int splits) {
   constexpr int kChunks = kTile * D / 8;
   __shared__ uint4 lds[kStages * 2 * kChunks];
-  attention_bwd_dq_body<D, kW>(Q, K, V, G, LSE, DELTA, DQ, heads, head_group, sq, sk, g, scale, causal, q_blocks, lds);
+  attention_bwd_dq_body<D, kW>(Q, K, V, G, LSE, DELTA, DQ, partial, heads, head_group, sq, sk, g, scale, causal,
+                               q_blocks, splits, lds);
+}
+
+// dQ = f16(scale * sum over the splits of the partial dQ), in split order; four columns per thread.
+template <int D>
+__global__ __launch_bounds__(kThreads) void attention_bwd_dq_reduce(const float *__restrict__ partial,
+                                                                    uint16_t *__restrict__ DQ, int heads, int sq,
+                                                                    int splits, int64_t rows, BwdGeometry g,
+                                                                    float scale) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (t >= rows * (D / 4)) return;
+  const int64_t row = t / (D / 4);
+  const int col = static_cast<int>(t % (D / 4)) * 4;
+  const int64_t q = row % sq, bh = row / sq;
+  const int64_t b = bh / heads, h = bh % heads;
+  float4 s4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int i = 0; i < splits; ++i) {
+    const float4 a = *reinterpret_cast<const float4 *>(partial + (i * rows + row) * D + col);
+    s4 = make_float4(s4.x + a.x, s4.y + a.y, s4.z + a.z, s4.w + a.w);
+  }
+  uint16_t *qrow = DQ + b * g.out0[0] + h * g.out0[1] + q * g.out0[2];
+  *reinterpret_cast<uint2 *>(qrow + col) =
+      make_uint2(pack_f16x2(s4.x * scale, s4.y * scale), pack_f16x2(s4.z * scale, s4.w * scale));
 }
 
 // ---------------------------------------------------------------- dK / dV
-// kSplit: the workgroup takes one query head of the group (grid x head_group) and writes its
-// unscaled f32 dK and dV sums to `partial` ([group][batch][kv_heads][sk][D], dK then dV), which
-// attention_bwd_dkdv_reduce folds over the group. Used when too few workgroups would run.
+// kSplit: the workgroup takes one query head of the group and one of `qsplits` consecutive
+// ranges of its query tiles (grid x head_group x qsplits) and writes its unscaled f32 dK and dV
+// sums to `partial` ([head_group * qsplits][batch][kv_heads][sk][D], dK then dV), which
+// attention_bwd_dkdv_reduce folds. Used when too few workgroups would run.
 // kPart: dK and dV together, or one of them (DkdvPart); kW: waves of 32 keys per workgroup.
 template <int D, bool kSplit, int kPart, int kW>
 __device__ __forceinline__ void attention_bwd_dkdv_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, float *__restrict__ partial, int kv_heads,
-    int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks, uint4 *lds) {
+    int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks, int qsplits, uint4 *lds) {
   constexpr int kChunks = kTile * D / 8;          // 16-byte chunks of one Q (or dO) tile
   constexpr int kDma = kChunks / (kW * 64);
   constexpr int kKRows = kW * 32;
@@ -309,8 +350,10 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   const int bh_count = gridDim.x / k_blocks;
   const int kb = static_cast<int>(blockIdx.x) / bh_count;   // causal: first key blocks see the most queries
   const int bhs = static_cast<int>(blockIdx.x) % bh_count;
-  const int split = kSplit ? bhs % head_group : 0;          // the query head of the group (split mode)
-  const int bh = kSplit ? bhs / head_group : bhs;
+  const int qs = kSplit ? bhs % qsplits : 0;                 // the query-tile range (split mode)
+  const int rest = kSplit ? bhs / qsplits : bhs;
+  const int split = kSplit ? rest % head_group : 0;          // the query head of the group (split mode)
+  const int bh = kSplit ? rest / head_group : rest;
   const int b = bh / kv_heads, kh = bh % kv_heads;
 
   const int wk0 = kb * kKRows + wave * 32;
@@ -335,8 +378,10 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   // Query tiles: for each of the head_group query heads, the 64-query tiles that can hold a valid
   // pair for this workgroup's keys (causal: queries >= its first key).
   const int q_tiles = (sq + kTile - 1) / kTile;
-  const int first = causal ? min(kb * kKRows / kTile, q_tiles) : 0;
-  const int per_head = q_tiles - first;
+  const int first_all = causal ? min(kb * kKRows / kTile, q_tiles) : 0;
+  const int span = q_tiles - first_all;
+  const int first = first_all + (kSplit ? qs * span / qsplits : 0);
+  const int per_head = kSplit ? first_all + (qs + 1) * span / qsplits - first : span;
   const int tiles = (kSplit ? 1 : head_group) * per_head;
 
   auto tile_head = [&](int t) { return kh * head_group + (kSplit ? split : t / per_head); };
@@ -437,10 +482,11 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
 
   if (!k_ok) return;
   if constexpr (kSplit) {
-    const int64_t rows = static_cast<int64_t>(gridDim.x / (k_blocks * head_group)) * sk;   // batch * kv_heads * sk
+    const int64_t rows = static_cast<int64_t>(gridDim.x / (k_blocks * head_group * qsplits)) * sk;   // batch * kv_heads * sk
     const int64_t row = (static_cast<int64_t>(b) * kv_heads + kh) * sk + lane_k;
-    float *pk = partial + (static_cast<int64_t>(split) * rows + row) * D;
-    float *pv = partial + (static_cast<int64_t>(head_group + split) * rows + row) * D;
+    const int parts = head_group * qsplits, part = split * qsplits + qs;
+    float *pk = partial + (static_cast<int64_t>(part) * rows + row) * D;
+    float *pv = partial + (static_cast<int64_t>(parts + part) * rows + row) * D;
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
@@ -477,20 +523,20 @@ __global__ __launch_bounds__(kW * 64, 1) void attention_bwd_dkdv(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
     const uint16_t *__restrict__ G, const float *__restrict__ LSE, const float *__restrict__ DELTA,
     uint16_t *__restrict__ DK, uint16_t *__restrict__ DV, float *__restrict__ partial, int kv_heads,
-    int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks) {
+    int head_group, int sq, int sk, BwdGeometry g, float scale, int causal, int k_blocks, int qsplits) {
   constexpr int kStage = 2 * (kTile * D / 8) + 2 * (kTile / 4);
   __shared__ uint4 lds[kStages * kStage];
   attention_bwd_dkdv_body<D, kSplit, kPart, kW>(Q, K, V, G, LSE, DELTA, DK, DV, partial, kv_heads, head_group, sq, sk, g,
-                                     scale, causal, k_blocks, lds);
+                                     scale, causal, k_blocks, qsplits, lds);
 }
 
-// dK = f16(scale * sum over the group of the partial dK), dV = f16(sum of the partial dV); four
-// columns per thread, in group order.
+// dK = f16(scale * sum of the `parts` partial dK), dV = f16(sum of the partial dV); four columns
+// per thread, in part order (query head of the group, then query-tile range).
 template <int D>
 __global__ __launch_bounds__(kThreads) void attention_bwd_dkdv_reduce(const float *__restrict__ partial,
                                                                       uint16_t *__restrict__ DK,
                                                                       uint16_t *__restrict__ DV, int kv_heads,
-                                                                      int head_group, int sk, int64_t rows,
+                                                                      int parts, int sk, int64_t rows,
                                                                       BwdGeometry g, float scale) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (t >= rows * (D / 4)) return;
@@ -499,9 +545,9 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_dkdv_reduce(const floa
   const int64_t k = row % sk, bh = row / sk;
   const int64_t b = bh / kv_heads, kh = bh % kv_heads;
   float4 sk4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), sv4 = sk4;
-  for (int i = 0; i < head_group; ++i) {
+  for (int i = 0; i < parts; ++i) {
     const float4 a = *reinterpret_cast<const float4 *>(partial + (i * rows + row) * D + col);
-    const float4 c = *reinterpret_cast<const float4 *>(partial + ((head_group + i) * rows + row) * D + col);
+    const float4 c = *reinterpret_cast<const float4 *>(partial + ((parts + i) * rows + row) * D + col);
     sk4 = make_float4(sk4.x + a.x, sk4.y + a.y, sk4.z + a.z, sk4.w + a.w);
     sv4 = make_float4(sv4.x + c.x, sv4.y + c.y, sv4.z + c.z, sv4.w + c.w);
   }
@@ -628,18 +674,71 @@ extern "C" int intent_hip_attention_bwd_delta(const void *o, const void *dout, f
 
 namespace {
 
-// attention_bwd_dq<D, kW> over every (batch, query head) and block of 32 kW queries.
+// Narrow grids split their work over more workgroups, which write f32 partial sums to a
+// caller-owned workspace that a second kernel folds: with fewer than kSplitBelow workgroups of
+// the 4-wave kernel, CUs stay idle while one workgroup walks the longest range of tiles alone.
+// The split aims at kSplitTarget workgroups (two per CU fit at D = 64), at most kMaxSplits ranges.
+// Reference example (B2 HQ8 HK2 S1024 D64 causal, delta + dK/dV + dQ): 88.8 us unsplit except by
+// head, 64.3 us aiming at 256 workgroups with up to 4 ranges, 61.5 us with 512 and 8.
+constexpr int64_t kSplitBelow = 256;
+constexpr int64_t kSplitTarget = 512;
+constexpr int64_t kMaxSplits = 8;
+
+// dQ: the number of key-tile ranges per query block (1 = no split).
+int dq_splits(int64_t batch, int64_t q_heads, int64_t sq, int64_t sk) {
+  if (batch <= 0 || q_heads <= 0 || sq <= 0 || sk <= 0 || batch * q_heads * sq >= kWideRows) return 1;
+  const int64_t blocks = batch * q_heads * ((sq + kRows - 1) / kRows);
+  if (blocks >= kSplitBelow) return 1;
+  int64_t splits = (kSplitTarget + blocks - 1) / blocks;
+  splits = splits < kMaxSplits ? splits : kMaxSplits;
+  const int64_t key_tiles = (sk + kTile - 1) / kTile;
+  return static_cast<int>(splits < key_tiles ? splits : key_tiles);
+}
+
+int64_t dq_workspace(int splits, int64_t batch, int64_t q_heads, int64_t sq, int64_t d) {
+  return splits > 1 ? splits * batch * q_heads * sq * d * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+// dK/dV: split by query head of the group and by query-tile range; returns the number of ranges
+// per head (0 = no split).
+int dkdv_qsplits(int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk) {
+  if (batch <= 0 || q_heads <= 0 || sq <= 0 || sk <= 0) return 0;
+  const int64_t blocks = batch * (q_heads / head_group) * ((sk + kRows - 1) / kRows);
+  if (blocks >= kSplitBelow) return 0;
+  int64_t qsplits = (kSplitTarget + blocks * head_group - 1) / (blocks * head_group);
+  qsplits = qsplits < kMaxSplits ? qsplits : kMaxSplits;
+  const int64_t query_tiles = (sq + kTile - 1) / kTile;
+  qsplits = qsplits < query_tiles ? qsplits : query_tiles;
+  if (head_group == 1 && qsplits <= 1) return 0;
+  return static_cast<int>(qsplits < 1 ? 1 : qsplits);
+}
+
+int64_t dkdv_workspace(int qsplits, int64_t batch, int64_t q_heads, int64_t head_group, int64_t sk, int64_t d) {
+  return qsplits > 0 ? 2 * head_group * qsplits * batch * (q_heads / head_group) * sk * d *
+                           static_cast<int64_t>(sizeof(float))
+                     : 0;
+}
+
+// attention_bwd_dq<D, kW> over every (batch, query head), block of 32 kW queries and key range;
+// with splits > 1 the partial sums in `partial` are then folded by attention_bwd_dq_reduce.
 template <int D, int kW>
 int launch_dq(const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *G, const float *lse,
-              const float *delta, uint16_t *DQ, int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
-              int64_t sk, const BwdGeometry &g, float scale, int causal, hipStream_t s) {
+              const float *delta, uint16_t *DQ, float *partial, int splits, int64_t batch, int64_t q_heads,
+              int64_t head_group, int64_t sq, int64_t sk, const BwdGeometry &g, float scale, int causal,
+              hipStream_t s) {
   const int q_blocks = static_cast<int>((sq + kW * 32 - 1) / (kW * 32));
-  const int64_t blocks = batch * q_heads * q_blocks;
+  const int64_t blocks = batch * q_heads * q_blocks * splits;
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
   attention_bwd_dq<D, kW><<<dim3(static_cast<unsigned>(blocks)), dim3(kW * 64), 0, s>>>(
-      Q, K, V, G, lse, delta, DQ, static_cast<int>(q_heads), static_cast<int>(head_group), static_cast<int>(sq),
-      static_cast<int>(sk), g, scale, causal, q_blocks);
+      Q, K, V, G, lse, delta, DQ, splits > 1 ? partial : nullptr, static_cast<int>(q_heads),
+      static_cast<int>(head_group), static_cast<int>(sq), static_cast<int>(sk), g, scale, causal, q_blocks, splits);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dq");
+  if (splits == 1) return INTENT_HIP_OK;
+  const int64_t rows = batch * q_heads * sq;
+  const dim3 rgrid(static_cast<unsigned>((rows * (D / 4) + kThreads - 1) / kThreads));
+  attention_bwd_dq_reduce<D><<<rgrid, dim3(kThreads), 0, s>>>(partial, DQ, static_cast<int>(q_heads),
+                                                              static_cast<int>(sq), splits, rows, g, scale);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dq_reduce");
   return INTENT_HIP_OK;
 }
 
@@ -649,54 +748,63 @@ template <int D, bool kSplit, int kPart, int kW>
 int launch_dkdv(const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *G, const float *lse,
                 const float *delta, uint16_t *DK, uint16_t *DV, float *partial, int64_t batch, int64_t kv_heads,
                 int64_t head_group, int64_t sq, int64_t sk, const BwdGeometry &g, float scale, int causal,
-                hipStream_t s) {
+                int qsplits, hipStream_t s) {
   const int k_blocks = static_cast<int>((sk + kW * 32 - 1) / (kW * 32));
-  const int64_t blocks = batch * kv_heads * k_blocks * (kSplit ? head_group : 1);
+  const int64_t blocks = batch * kv_heads * k_blocks * (kSplit ? head_group * qsplits : 1);
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many workgroups");
   attention_bwd_dkdv<D, kSplit, kPart, kW><<<dim3(static_cast<unsigned>(blocks)), dim3(kW * 64), 0, s>>>(
       Q, K, V, G, lse, delta, DK, DV, partial, static_cast<int>(kv_heads), static_cast<int>(head_group),
-      static_cast<int>(sq), static_cast<int>(sk), g, scale, causal, k_blocks);
+      static_cast<int>(sq), static_cast<int>(sk), g, scale, causal, k_blocks, qsplits);
   if (hipPeekAtLastError() != hipSuccess)
     return launch_status(kPart == kOnlyDk ? "attention_bwd_dk" : kPart == kOnlyDv ? "attention_bwd_dv" : "attention_bwd_dkdv");
   return INTENT_HIP_OK;
 }
 
-// dK and dV of one call: split by query head with a workspace (then folded), as two 8-wave
-// kernels on wide grids, or as one 4-wave kernel.
+// dK and dV of one call: split by query head and query-tile range with a workspace (qsplits > 0;
+// then folded), as two 8-wave kernels on wide grids, or as one 4-wave kernel.
 template <int D>
 int run_dkdv(const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *G, const float *lse,
-             const float *delta, uint16_t *DK, uint16_t *DV, float *partial, bool use_split, int64_t batch,
+             const float *delta, uint16_t *DK, uint16_t *DV, float *partial, int qsplits, int64_t batch,
              int64_t kv_heads, int64_t head_group, int64_t sq, int64_t sk, const BwdGeometry &g, float scale,
              int causal, hipStream_t s) {
-  if (use_split) {
+  if (qsplits > 0) {
     if (int rc = launch_dkdv<D, true, kBoth, 4>(Q, K, V, G, lse, delta, DK, DV, partial, batch, kv_heads, head_group,
-                                                sq, sk, g, scale, causal, s))
+                                                sq, sk, g, scale, causal, qsplits, s))
       return rc;
     const int64_t rows = batch * kv_heads * sk;
     const dim3 rgrid(static_cast<unsigned>((rows * (D / 4) + kThreads - 1) / kThreads));
     attention_bwd_dkdv_reduce<D><<<rgrid, dim3(kThreads), 0, s>>>(partial, DK, DV, static_cast<int>(kv_heads),
-                                                                  static_cast<int>(head_group), static_cast<int>(sk),
-                                                                  rows, g, scale);
+                                                                  static_cast<int>(head_group * qsplits),
+                                                                  static_cast<int>(sk), rows, g, scale);
     if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_bwd_dkdv_reduce");
     return INTENT_HIP_OK;
   }
   if (batch * kv_heads * sk >= kWideRows) {
     if (int rc = launch_dkdv<D, false, kOnlyDk, 8>(Q, K, V, G, lse, delta, DK, DV, nullptr, batch, kv_heads,
-                                                   head_group, sq, sk, g, scale, causal, s))
+                                                   head_group, sq, sk, g, scale, causal, 1, s))
       return rc;
     return launch_dkdv<D, false, kOnlyDv, 8>(Q, K, V, G, lse, delta, DK, DV, nullptr, batch, kv_heads, head_group, sq,
-                                             sk, g, scale, causal, s);
+                                             sk, g, scale, causal, 1, s);
   }
   return launch_dkdv<D, false, kBoth, 4>(Q, K, V, G, lse, delta, DK, DV, nullptr, batch, kv_heads, head_group, sq, sk,
-                                         g, scale, causal, s);
+                                         g, scale, causal, 1, s);
 }
 
 }  // namespace
 
-extern "C" int intent_hip_attention_bwd_dq(const void *q, const void *k, const void *v, const void *dout,
-                                           const float *lse, const float *delta, void *dq, int64_t batch,
-                                           int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
-                                           const int64_t *strides, float scale, int causal, void *stream) {
+extern "C" int intent_hip_attention_bwd_dq_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_group,
+                                                           int64_t sq, int64_t sk, int64_t d, size_t *bytes) {
+  if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
+  if (const int rc = check_common(batch, q_heads, head_group, sq, sk, d)) return rc;
+  *bytes = static_cast<size_t>(dq_workspace(dq_splits(batch, q_heads, sq, sk), batch, q_heads, sq, d));
+  return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_attention_bwd_dq_ws(const void *q, const void *k, const void *v, const void *dout,
+                                              const float *lse, const float *delta, void *dq, int64_t batch,
+                                              int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                                              const int64_t *strides, float scale, int causal, void *workspace,
+                                              size_t workspace_bytes, void *stream) {
   if (const int rc = check_common(batch, q_heads, head_group, sq, sk, d)) return rc;
   if (batch == 0 || q_heads == 0 || sq == 0) return INTENT_HIP_OK;
   if (strides == nullptr || q == nullptr || dout == nullptr || lse == nullptr || delta == nullptr || dq == nullptr ||
@@ -709,47 +817,44 @@ extern "C" int intent_hip_attention_bwd_dq(const void *q, const void *k, const v
   if (int rc = check_operand(dq, strides + 22, 1, "grad_q")) return rc;
   BwdGeometry g{};
   load_geometry(g, strides, false);
+  int splits = dq_splits(batch, q_heads, sq, sk);
+  const int64_t need = dq_workspace(splits, batch, q_heads, sq, d);
+  if (need > 0 && workspace != nullptr && (workspace_bytes < static_cast<size_t>(need) || !aligned(workspace, 16)))
+    return fail(INTENT_HIP_ERR_WORKSPACE, "dQ needs %lld 16-byte aligned workspace bytes, got %zu",
+                static_cast<long long>(need), workspace_bytes);
+  if (workspace == nullptr) splits = 1;
   const auto *Q = static_cast<const uint16_t *>(q);
   const auto *K = static_cast<const uint16_t *>(k);
   const auto *V = static_cast<const uint16_t *>(v);
   const auto *G = static_cast<const uint16_t *>(dout);
   auto *DQ = static_cast<uint16_t *>(dq);
+  auto *P = static_cast<float *>(workspace);
   const bool wide = batch * q_heads * sq >= kWideRows;
   const int c = causal ? 1 : 0;
   const hipStream_t s = as_stream(stream);
   if (d == 64)
-    return wide ? launch_dq<64, 8>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s)
-                : launch_dq<64, 4>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s);
-  return wide ? launch_dq<128, 8>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s)
-              : launch_dq<128, 4>(Q, K, V, G, lse, delta, DQ, batch, q_heads, head_group, sq, sk, g, scale, c, s);
+    return wide ? launch_dq<64, 8>(Q, K, V, G, lse, delta, DQ, P, 1, batch, q_heads, head_group, sq, sk, g, scale, c, s)
+                : launch_dq<64, 4>(Q, K, V, G, lse, delta, DQ, P, splits, batch, q_heads, head_group, sq, sk, g, scale,
+                                   c, s);
+  return wide ? launch_dq<128, 8>(Q, K, V, G, lse, delta, DQ, P, 1, batch, q_heads, head_group, sq, sk, g, scale, c, s)
+              : launch_dq<128, 4>(Q, K, V, G, lse, delta, DQ, P, splits, batch, q_heads, head_group, sq, sk, g, scale,
+                                  c, s);
 }
 
-namespace {
-
-// dK/dV split by query head: taken when head_group > 1 and fewer than kSplitBelow workgroups of
-// the unsplit kernel would run (the first key block then walks head_group times the query tiles
-// alone). The workspace holds the unscaled f32 partial sums, dK then dV.
-constexpr int64_t kSplitBelow = 256;
-
-bool dkdv_split(int64_t batch, int64_t q_heads, int64_t head_group, int64_t sk) {
-  if (head_group < 2 || batch <= 0 || q_heads <= 0 || sk <= 0) return false;
-  const int64_t blocks = batch * (q_heads / head_group) * ((sk + kRows - 1) / kRows);
-  return blocks < kSplitBelow;
+extern "C" int intent_hip_attention_bwd_dq(const void *q, const void *k, const void *v, const void *dout,
+                                           const float *lse, const float *delta, void *dq, int64_t batch,
+                                           int64_t q_heads, int64_t head_group, int64_t sq, int64_t sk, int64_t d,
+                                           const int64_t *strides, float scale, int causal, void *stream) {
+  return intent_hip_attention_bwd_dq_ws(q, k, v, dout, lse, delta, dq, batch, q_heads, head_group, sq, sk, d, strides,
+                                        scale, causal, nullptr, 0, stream);
 }
-
-int64_t dkdv_workspace(int64_t batch, int64_t q_heads, int64_t head_group, int64_t sk, int64_t d) {
-  return 2 * head_group * batch * (q_heads / head_group) * sk * d * static_cast<int64_t>(sizeof(float));
-}
-
-}  // namespace
 
 extern "C" int intent_hip_attention_bwd_dkdv_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_group,
                                                              int64_t sq, int64_t sk, int64_t d, size_t *bytes) {
   if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
   if (const int rc = check_common(batch, q_heads, head_group, sq, sk, d)) return rc;
-  *bytes = dkdv_split(batch, q_heads, head_group, sk)
-               ? static_cast<size_t>(dkdv_workspace(batch, q_heads, head_group, sk, d))
-               : 0;
+  *bytes = static_cast<size_t>(
+      dkdv_workspace(dkdv_qsplits(batch, q_heads, head_group, sq, sk), batch, q_heads, head_group, sk, d));
   return INTENT_HIP_OK;
 }
 
@@ -772,12 +877,12 @@ extern "C" int intent_hip_attention_bwd_dkdv_ws(const void *q, const void *k, co
   BwdGeometry g{};
   load_geometry(g, strides, true);
   const int64_t kv_heads = q_heads / head_group;
-  const bool split = dkdv_split(batch, q_heads, head_group, sk);
-  const int64_t need = split ? dkdv_workspace(batch, q_heads, head_group, sk, d) : 0;
-  if (split && workspace != nullptr && (workspace_bytes < static_cast<size_t>(need) || !aligned(workspace, 16)))
+  int qsplits = dkdv_qsplits(batch, q_heads, head_group, sq, sk);
+  const int64_t need = dkdv_workspace(qsplits, batch, q_heads, head_group, sk, d);
+  if (need > 0 && workspace != nullptr && (workspace_bytes < static_cast<size_t>(need) || !aligned(workspace, 16)))
     return fail(INTENT_HIP_ERR_WORKSPACE, "dK/dV needs %lld 16-byte aligned workspace bytes, got %zu",
                 static_cast<long long>(need), workspace_bytes);
-  const bool use_split = split && workspace != nullptr;
+  if (workspace == nullptr) qsplits = 0;
   const auto *Q = static_cast<const uint16_t *>(q);
   const auto *K = static_cast<const uint16_t *>(k);
   const auto *V = static_cast<const uint16_t *>(v);
@@ -788,9 +893,9 @@ extern "C" int intent_hip_attention_bwd_dkdv_ws(const void *q, const void *k, co
   const hipStream_t s = as_stream(stream);
   const int c = causal ? 1 : 0;
   if (d == 64)
-    return run_dkdv<64>(Q, K, V, G, lse, delta, DK, DV, P, use_split, batch, kv_heads, head_group, sq, sk, g, scale,
+    return run_dkdv<64>(Q, K, V, G, lse, delta, DK, DV, P, qsplits, batch, kv_heads, head_group, sq, sk, g, scale,
                         c, s);
-  return run_dkdv<128>(Q, K, V, G, lse, delta, DK, DV, P, use_split, batch, kv_heads, head_group, sq, sk, g, scale, c,
+  return run_dkdv<128>(Q, K, V, G, lse, delta, DK, DV, P, qsplits, batch, kv_heads, head_group, sq, sk, g, scale, c,
                        s);
 }
 

@@ -11,7 +11,7 @@ from pathlib import Path
 
 from ...diagnostics import CompilationStageError
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 LIBRARY_NAME = "libintent_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parents[2] / LIBRARY_NAME
 
@@ -66,6 +66,10 @@ SIGNATURES = {
     "intent_hip_splitk_reduce_f32_to_f16": (_int, (_p, _p, _p, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64), _p)),
     "intent_hip_attention_bwd_dkdv_workspace_bytes": (_int, (_i64, _i64, _i64, _i64, _i64, _i64,
                                                               ctypes.POINTER(_sz))),
+    "intent_hip_attention_bwd_dq_workspace_bytes": (_int, (_i64, _i64, _i64, _i64, _i64, _i64,
+                                                            ctypes.POINTER(_sz))),
+    "intent_hip_attention_bwd_dq_ws": (_int, (_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                              ctypes.POINTER(_i64), _f32, _int, _p, _sz, _p)),
     "intent_hip_attention_bwd_dkdv_ws": (_int, (_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                                 ctypes.POINTER(_i64), _f32, _int, _p, _sz, _p)),
     "intent_hip_csr_spmv_workspace_bytes": (_int, (_i64, _i64, ctypes.POINTER(_sz))),

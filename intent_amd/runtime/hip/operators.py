@@ -310,24 +310,21 @@ def _attention_bwd(kind):
                 int(causal))
         configuration = (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq), ("sk", sk),
                          ("d", d), ("causal", causal))
-        if kind == "dkdv":
-            # Small grids split the query heads of a group over workgroups; the f32 partial sums
-            # need a workspace, allocated here once per prepared call.
-            import ctypes
+        # Small grids split their work over more workgroups; the f32 partial sums need a
+        # workspace, allocated here once per prepared call.
+        import ctypes
 
-            import torch
+        import torch
 
-            size = ctypes.c_size_t(0)
-            lib.check(lib.fn["attention_bwd_dkdv_workspace_bytes"](batch, q_heads, group, sq, sk, d,
-                                                                  ctypes.byref(size)), "provider_preparation")
-            workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
-            if workspace is not None:
-                keep.append(workspace)
-            fn = lib.fn["attention_bwd_dkdv_ws"]
-            args = (*args, workspace.data_ptr() if workspace is not None else None, size.value)
-            configuration += (("workspace_bytes", size.value),)
-        else:
-            fn = lib.fn["attention_bwd_dq"]
+        size = ctypes.c_size_t(0)
+        lib.check(lib.fn[f"attention_bwd_{kind}_workspace_bytes"](batch, q_heads, group, sq, sk, d,
+                                                                 ctypes.byref(size)), "provider_preparation")
+        workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
+        if workspace is not None:
+            keep.append(workspace)
+        fn = lib.fn[f"attention_bwd_{kind}_ws"]
+        args = (*args, workspace.data_ptr() if workspace is not None else None, size.value)
+        configuration += (("workspace_bytes", size.value),)
         op = OP_ATTENTION_BWD_DQ if kind == "dq" else OP_ATTENTION_BWD_DKDV
         # The kernel variant depends on the rows of the call: batch x query heads x queries for dQ,
         # batch x key heads x keys for dK/dV.

@@ -111,12 +111,13 @@ def test_authored_softmax_backward_autograd(device):
     assert torch.allclose(x.grad, reference.grad, rtol=1e-4, atol=1e-6)
 
 
-@pytest.mark.parametrize("shape", [(2, 8, 2, 1024, 1024, 64), (1, 6, 3, 300, 200, 128)])
+@pytest.mark.parametrize("shape", [(2, 8, 2, 1024, 1024, 64), (1, 6, 3, 300, 200, 128), (1, 4, 4, 300, 300, 64)])
 def test_dkdv_split_matches_unsplit_through_the_c_abi(device, shape):
-    """intent_hip_attention_bwd_dkdv_ws with a workspace (query heads split over workgroups, f32
-    partials folded by a second kernel) against the same entry with no workspace (one workgroup
-    walks every head of the group): the sums differ only in association, so within 2 f16 ulp plus
-    1e-3 of the largest magnitude; both against the oracle."""
+    """intent_hip_attention_bwd_dkdv_ws with a workspace (query heads and ranges of their query
+    tiles split over workgroups, f32 partials folded by a second kernel) against the same entry
+    with no workspace (one workgroup walks every head of the group): the sums differ only in
+    association, so within 2 f16 ulp plus 1e-3 of the largest magnitude; both against the
+    oracle. The third shape has one query head per key head, split by query range alone."""
     import ctypes
 
     from intent_amd.runtime.hip.library import library
@@ -131,7 +132,8 @@ def test_dkdv_split_matches_unsplit_through_the_c_abi(device, shape):
     lib = library()
     size = ctypes.c_size_t(0)
     assert lib.fn["attention_bwd_dkdv_workspace_bytes"](batch, hq, hq // hk, sq, sk, d, ctypes.byref(size)) == 0
-    assert size.value == 2 * hq * batch * sk * d * 4            # the split is taken for these grids
+    per_range = 2 * hq * batch * sk * d * 4                     # dK and dV partials of one range per head
+    assert size.value > 0 and size.value % per_range == 0 and size.value // per_range <= 8
     workspace = torch.empty(size.value, dtype=torch.uint8, device=device)
     results = []
     for ws in (workspace, None):
@@ -229,3 +231,48 @@ def test_wide_grid_equals_per_batch_calls_through_the_c_abi(device, shape):
                                                  head_group=hq // hk)
     close(whole[1][:1].cpu().numpy(), want_dk)
     close(whole[2][:1].cpu().numpy(), want_dv)
+
+
+@pytest.mark.parametrize("shape,causal", [((2, 8, 2, 1024, 1024, 64), True), ((1, 3, 1, 200, 700, 128), False),
+                                          ((1, 2, 2, 130, 130, 64), True)])
+def test_dq_split_matches_unsplit_through_the_c_abi(device, shape, causal):
+    """intent_hip_attention_bwd_dq_ws with a workspace (each query block's key tiles divided over
+    up to 8 workgroups, f32 partials folded in range order) against the same entry with no
+    workspace: within 2 f16 ulp plus 1e-3 of the largest magnitude; both against the oracle."""
+    import ctypes
+
+    from intent_amd.runtime.hip.library import library
+
+    batch, hq, hk, sq, sk, d = shape
+    announce("dQ split vs unsplit", shape, causal)
+    q, k, v, o, do, lse = case(sum(shape), batch, hq, hk, sq, sk, d)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    tq, tk, tv, tdo, tlse = t(q), t(k), t(v), t(do), t(lse)
+    delta_np = oracle.attention_bwd_delta(o, do)
+    tdelta = t(delta_np)
+    lib = library()
+    size = ctypes.c_size_t(0)
+    assert lib.fn["attention_bwd_dq_workspace_bytes"](batch, hq, hq // hk, sq, sk, d, ctypes.byref(size)) == 0
+    per_range = batch * hq * sq * d * 4
+    assert size.value > 0 and size.value % per_range == 0 and 2 <= size.value // per_range <= 8
+    workspace = torch.empty(size.value, dtype=torch.uint8, device=device)
+    scale = float(np.float32(d ** -0.5))
+    results = []
+    for ws in (workspace, None):
+        dq = torch.empty_like(tq)
+        st = [x for a in (tq, tk, tv, tdo) for x in a.stride()] + list(tlse.stride()) + list(tdelta.stride()) + \
+            list(dq.stride())
+        strides = (ctypes.c_int64 * 26)(*st)
+        rc = lib.fn["attention_bwd_dq_ws"](tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), tdo.data_ptr(), tlse.data_ptr(),
+                                           tdelta.data_ptr(), dq.data_ptr(), batch, hq, hq // hk, sq, sk, d, strides,
+                                           scale, int(causal), ws.data_ptr() if ws is not None else None,
+                                           size.value if ws is not None else 0, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        results.append(dq.cpu().numpy().astype(np.float64))
+    torch.cuda.synchronize()
+    split, unsplit = results
+    assert np.all(np.abs(split - unsplit) <= 2 * 2.0 ** -10 * np.abs(unsplit) + 1e-3 * np.abs(unsplit).max())
+    close(split, oracle.attention_bwd_dq(q, k, v, do, lse, delta_np, scale, causal, head_group=hq // hk))
+    large = ctypes.c_size_t(0)
+    assert lib.fn["attention_bwd_dq_workspace_bytes"](4, 32, 4, 4096, 4096, 128, ctypes.byref(large)) == 0
+    assert large.value == 0                                     # large grids never split
