@@ -9,7 +9,7 @@
 // The key axis is folded in 64-key chunks; the running maximum replaces the chunk maximum
 // before P is rounded (online softmax), which the 16-bit tolerance covers.
 //
-// Design (d = dv = 128):
+// Design (d = dv = 128 or 64):
 //   * a workgroup owns 256 query rows of one (batch, head): 8 waves x 32 rows, two per SIMD;
 //     key tiles of 64 keys stream through LDS in two stages (K: 16 KB, V: 16 KB per stage),
 //     written by global_load_lds_dwordx4 while the previous tile is consumed. Each K/V tile
@@ -63,14 +63,25 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(hi))) << 16);
 }
 
-constexpr int kD = 128;
 constexpr int kBQ = 256;     // query rows per workgroup
 constexpr int kBK = 64;      // keys per tile
 constexpr int kThreads = 512;
-constexpr int kKChunks = kBK * kD / 8;      // 16-byte chunks of a K tile (row = key, 16 chunks)
-constexpr int kVChunks = kBK * kD / 8;      // 16-byte chunks of a V tile (row = key, 16 chunks)
-constexpr int kStageChunks = kKChunks + kVChunks;
 constexpr float kLog2e = 1.4426950408889634f;
+
+// LDS layouts of the K and V tiles: rows of D / 8 16-byte chunks, logical chunk c of row r stored
+// at c ^ swz(r). D = 128: K rows at c ^ (r & 15), V rows at c ^ 4 (r & 3). D = 64 (two rows per
+// 64-bank row): both at c ^ ((r >> 1) & 7) in the bit order below, a bijection of the 8 chunk
+// slots over each 16 consecutive rows (the K fragment reads) that also sends the transposing V
+// reads of 4 consecutive rows to 4 distinct chunk groups. Plain functions of d (constant after
+// inlining), not templates: called as swz<D>(...) from the lambdas of the kernel template, hipcc
+// (ROCm 7.2) compiled the device code but silently emitted no host stubs for the kernel, so the
+// library failed to load with undefined kernel symbols.
+__host__ __device__ __forceinline__ int swz_k(int d, int row) {
+  return d == 128 ? (row & 15) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+}
+__host__ __device__ __forceinline__ int swz_v(int d, int row) {
+  return d == 128 ? 4 * (row & 3) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+}
 
 __device__ __forceinline__ uint4 select(bool keep, uint4 v) {
   return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
@@ -91,14 +102,20 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // raised when a tile's maximum exceeds it by more than this, so weights stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename E>
-__global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t *__restrict__ Q,
+template <typename E, int D>
+__global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__restrict__ Q,
                                                                   const uint16_t *__restrict__ K,
                                                                   const uint16_t *__restrict__ V,
                                                                   uint16_t *__restrict__ O, int heads,
                                                                   int head_group, int sq, int sk, Geometry g,
                                                                   float scale, int causal, int q_blocks) {
   typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
+  constexpr int kD = D;
+  constexpr int kRowChunks = kD / 8;          // 16-byte chunks per K or V row
+  constexpr int kKChunks = kBK * kRowChunks;  // 16-byte chunks of a K tile (row = key)
+  constexpr int kVChunks = kBK * kRowChunks;  // 16-byte chunks of a V tile (row = key)
+  constexpr int kStageChunks = kKChunks + kVChunks;
+  static_assert(kKChunks % kThreads == 0, "DMA split");
   __shared__ uint4 lds[2 * kStageChunks];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in a scalar register
@@ -132,29 +149,29 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
   const int tiles = (k_end + kBK - 1) / kBK;
   const int wave_q_last = min(wq0 + 31, sq - 1);
 
-  // DMA roles: each wave moves 4 x 64 chunks of K and of V per tile. LDS chunk slot p of a
-  // tile is row p / 16 (a key), physical chunk p % 16; K rows store logical chunk
-  // pc ^ (key & 15), V rows pc ^ 4 (key & 3). Keys beyond sk read row sk - 1 (finite data
-  // that the mask zeroes out; V tail rows are cleared in LDS below).
+  // DMA roles: each wave moves D / 32 x 64 chunks of K and of V per tile. LDS chunk slot p of a
+  // tile is row p / (D / 8) (a key), physical chunk p % (D / 8); rows store logical chunk
+  // pc ^ swz(key). Keys beyond sk read row sk - 1 (finite data that the mask zeroes out; V tail
+  // rows are cleared in LDS below).
   auto issue = [&](int kt) {
     uint4 *stage = lds + (kt & 1) * kStageChunks;
     const int key0 = kt * kBK;
 #pragma unroll
     for (int i = 0; i < kKChunks / kThreads; ++i) {
       const int p = (wave * (kKChunks / kThreads) + i) * 64 + lane;
-      const int row = p >> 4, pc = p & 15;
+      const int row = p / kRowChunks, pc = p % kRowChunks;
       const int key = min(key0 + row, sk - 1);
-      __builtin_amdgcn_global_load_lds(kbase + static_cast<int64_t>(key) * g.ks[2] + (pc ^ (row & 15)) * 8,
+      __builtin_amdgcn_global_load_lds(kbase + static_cast<int64_t>(key) * g.ks[2] + (pc ^ swz_k(D, row)) * 8,
                                        (lds_void_t *)(stage + (wave * (kKChunks / kThreads) + i) * 64), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + static_cast<int64_t>(key) * g.vs[2] + (pc ^ (4 * (row & 3))) * 8,
+      __builtin_amdgcn_global_load_lds(vbase + static_cast<int64_t>(key) * g.vs[2] + (pc ^ swz_v(D, row)) * 8,
                                        (lds_void_t *)(stage + kKChunks + (wave * (kKChunks / kThreads) + i) * 64), 16,
                                        0, 0);
     }
   };
 
-  f32x16_t acc[4];   // O^T: dv tile mt (32 dv) x 32 queries
+  f32x16_t acc[kD / 32];   // O^T: dv tile mt (32 dv) x 32 queries
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < kD / 32; ++mt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[mt][e] = 0.0f;
   float row_max = -INFINITY;   // running maximum of valid scaled scores (exp2 domain)
@@ -177,8 +194,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
     if (key0 + kBK > sk) {
       // Tail tile: clear the V rows past the last key so masked weights meet zeros.
       uint4 *vt = const_cast<uint4 *>(sk_tile + kKChunks);
-      for (int c = tid; c < kBK * 16; c += kThreads)
-        if (key0 + (c >> 4) >= sk) vt[c] = make_uint4(0, 0, 0, 0);
+      for (int c = tid; c < kBK * kRowChunks; c += kThreads)
+        if (key0 + c / kRowChunks >= sk) vt[c] = make_uint4(0, 0, 0, 0);
       __syncthreads();
     }
     const bool active = !causal || key0 <= wave_q_last;      // wave-uniform
@@ -196,7 +213,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
           const int row = st * 32 + frag_row;
-          kf[buf][st] = __builtin_bit_cast(f16x8_t, sk_tile[row * 16 + ((ks * 2 + half) ^ (row & 15))]);
+          kf[buf][st] = __builtin_bit_cast(f16x8_t, sk_tile[row * kRowChunks + ((ks * 2 + half) ^ swz_k(D, row))]);
         }
       };
       read_k(0, 0);
@@ -237,7 +254,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
       row_max = new_max;
       row_den *= alpha;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < kD / 32; ++mt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[mt][e] *= alpha;
     }
@@ -255,16 +272,16 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
     // [key][dv] layout through ds_read_b64_tr_b16: read r of slice sl gives the lane keys
     // 16 sl + 8 r + 4 half + 0..3 of its dv.
     {
-      f16x8_t vf[2][4];
+      f16x8_t vf[2][kD / 32];
       auto read_v = [&](int sl, int buf) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < kD / 32; ++mt) {
           i16x4_t parts[2];
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
             const int key = sl * 16 + 8 * r + v_key;
             const int dv = mt * 32 + v_dv;
-            const int chunk = (dv >> 3) ^ (4 * (key & 3));
+            const int chunk = (dv >> 3) ^ swz_v(D, key);
             parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kD + chunk * 8 + (dv & 7)));
           }
           vf[buf][mt] = __builtin_bit_cast(f16x8_t, parts);
@@ -276,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
       for (int sl = 0; sl < 4; ++sl) {
         if (sl + 1 < 4) read_v(sl + 1, (sl + 1) & 1);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < kD / 32; ++mt)
           acc[mt] = Elem<E>::mma(vf[sl & 1][mt], pf[sl], acc[mt]);
       }
       __builtin_amdgcn_s_setprio(0);
@@ -290,7 +307,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
   const float inv = valid ? __builtin_amdgcn_rcpf(den) : 0.0f;
   uint16_t *orow = obase + static_cast<int64_t>(lane_q) * g.os[2];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < kD / 32; ++mt)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const uint32_t w0 = pack2<E>(acc[mt][4 * gq] * inv, acc[mt][4 * gq + 1] * inv);
@@ -303,12 +320,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_d128(const uint16_t
 
 int attention_resources(int dtype, int64_t sq, int64_t d, IntentHipKernelResources *out) {
   (void)sq;
-  (void)d;
+  const auto describe = [out](const void *kernel, const char *name) { return describe_kernel(kernel, name, kThreads, out); };
   if (dtype == INTENT_HIP_BF16)
-    return describe_kernel(reinterpret_cast<const void *>(&attention_fwd_d128<__bf16>), "attention_fwd_d128<bf16>",
-                           kThreads, out);
-  return describe_kernel(reinterpret_cast<const void *>(&attention_fwd_d128<_Float16>), "attention_fwd_d128<f16>",
-                         kThreads, out);
+    return d == 64 ? describe(reinterpret_cast<const void *>(&attention_fwd<__bf16, 64>), "attention_fwd<bf16,64>")
+                   : describe(reinterpret_cast<const void *>(&attention_fwd<__bf16, 128>), "attention_fwd<bf16,128>");
+  return d == 64 ? describe(reinterpret_cast<const void *>(&attention_fwd<_Float16, 64>), "attention_fwd<f16,64>")
+                 : describe(reinterpret_cast<const void *>(&attention_fwd<_Float16, 128>), "attention_fwd<f16,128>");
 }
 
 }  // namespace intent_hip
@@ -328,8 +345,8 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   if (dtype != INTENT_HIP_F16 && dtype != INTENT_HIP_BF16)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "attention dtype code %d (1 = f16, 2 = bf16)", dtype);
   if (batch == 0 || heads == 0 || sq == 0 || dv == 0) return INTENT_HIP_OK;
-  if (d != kD || dv != kD)
-    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernel supports head dimension 128 (got d=%lld, dv=%lld)",
+  if ((d != 64 && d != 128) || dv != d)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernel supports D = DV = 64 or 128 (got d=%lld, dv=%lld)",
                 static_cast<long long>(d), static_cast<long long>(dv));
   if (strides == nullptr || q == nullptr || o == nullptr || (sk > 0 && (k == nullptr || v == nullptr)))
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
@@ -358,15 +375,20 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   auto *Op = static_cast<uint16_t *>(o);
   const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
   const hipStream_t s = as_stream(stream);
-  if (dtype == INTENT_HIP_BF16)
-    attention_fwd_d128<__bf16><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, static_cast<int>(heads),
-                                                      static_cast<int>(head_group), static_cast<int>(sq),
-                                                      static_cast<int>(sk), g, scale, causal ? 1 : 0, q_blocks);
-  else
-    attention_fwd_d128<_Float16><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, static_cast<int>(heads),
-                                                        static_cast<int>(head_group), static_cast<int>(sq),
-                                                        static_cast<int>(sk), g, scale, causal ? 1 : 0, q_blocks);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd_d128");
+  const int h = static_cast<int>(heads), grp = static_cast<int>(head_group);
+  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk), c = causal ? 1 : 0;
+  if (dtype == INTENT_HIP_BF16) {
+    if (d == 64)
+      attention_fwd<__bf16, 64><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+    else
+      attention_fwd<__bf16, 128><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+  } else {
+    if (d == 64)
+      attention_fwd<_Float16, 64><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+    else
+      attention_fwd<_Float16, 128><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+  }
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd");
   return INTENT_HIP_OK;
 }
 

@@ -75,9 +75,27 @@ def test_attention_strided_views(device):
     assert_16bit(odd.cpu().numpy(), oracle.attention_fwd_f16(q, k, v, scale, True))
 
 
+@pytest.mark.parametrize("shape,sk,causal", [((1, 2, 300, 64), 300, True), ((2, 3, 129, 64), 200, False),
+                                             ((1, 1, 64, 64), 64, True), ((1, 2, 257, 64), 257, False)])
+def test_attention_head_dim_64_matches_oracle(device, shape, sk, causal):
+    """D = DV = 64 (the reference's own streaming example uses it), its own LDS layout."""
+    announce("attention d=64", shape, sk, causal)
+    b, h, s, d = shape
+    rng = np.random.default_rng(s + sk + h)
+    q = inputs.normal(rng, (b, h, s, d), "f16")
+    k = inputs.normal(rng, (b, h, sk, d), "f16")
+    v = inputs.normal(rng, (b, h, sk, d), "f16")
+    scale = float(np.float32(1 / np.sqrt(d)))
+    o = run(device, q, k, v, scale, causal)
+    assert not np.isnan(o).any()
+    assert_16bit(o, oracle.attention_fwd_f16(q, k, v, scale, causal))
+    if causal:
+        assert (o[:, :, 0, :] == v[:, :, 0, :]).all()        # one valid key: exactly v[0]
+
+
 def test_attention_unsupported_head_dim(device):
-    announce("attention d=64")
-    q, k, v, scale = inputs.attention_f16(seed=1, batch=1, heads=1, seq=64, dim=64)
+    announce("attention d=96")
+    q, k, v, scale = inputs.attention_f16(seed=1, batch=1, heads=1, seq=64, dim=96)
     with pytest.raises(intent.CompilationStageError):
         run(device, q, k, v, scale, True)
 

@@ -209,6 +209,34 @@ def test_attention_bf16_matches_oracle(device, shape, group, causal):
         assert (o[:, :, 0, :] == v[:, heads, 0, :]).all()   # one valid key: exactly v[0]
 
 
+def test_reference_streaming_example_attention(device):
+    """The reference's streaming example (examples/programs/streaming.py:15-21):
+    flash_attention_bf16_fwd with HEAD_GROUP 4, causal, q (2, 8, 256, 64), k and v (2, 2, 256, 64),
+    scale 64 ** -0.5."""
+    announce("reference streaming example attention")
+    rng = np.random.default_rng(21)
+    q = inputs.normal(rng, (2, 8, 256, 64), "bf16")
+    k = inputs.normal(rng, (2, 2, 256, 64), "bf16")
+    v = inputs.normal(rng, (2, 2, 256, 64), "bf16")
+    scale = float(np.float32(64 ** -0.5))
+    o = run_attention(device, flash_attention_bf16_fwd, q, k, v, scale, 4, True, True)
+    want = oracle.attention_fwd(q, k, v, scale, True, head_group=4, storage="bf16")
+    assert_16bit(bf16_to_f32(o), bf16_to_f32(want), rel=4e-2, abs_=2e-2)
+    assert (o[:, :, 0, :] == v[:, np.arange(8) // 4, 0, :]).all()
+
+
+def test_gqa_head_dim_64_matches_oracle(device):
+    announce("gqa d=64")
+    rng = np.random.default_rng(64)
+    q = inputs.normal(rng, (1, 6, 333, 64), "f16")
+    k = inputs.normal(rng, (1, 2, 400, 64), "f16")
+    v = inputs.normal(rng, (1, 2, 400, 64), "f16")
+    scale = float(np.float32(0.125))
+    for causal in (True, False):
+        o = run_attention(device, flash_gqa_attention_fwd, q, k, v, scale, 3, causal, False)
+        assert_16bit(o, oracle.attention_fwd(q, k, v, scale, causal, head_group=3))
+
+
 def test_gqa_head_mismatch_is_value_error(device):
     announce("gqa head mismatch")
     q = torch.zeros(1, 6, 8, 128, dtype=torch.float16, device=device)
