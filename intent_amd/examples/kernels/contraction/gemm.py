@@ -4,6 +4,12 @@
 import intent_amd as intent
 import intent_amd.language as I
 
+# The reference's example extents (contraction/gemm.py:5-7), kept as module constants for callers
+# that import them; the definitions below take any extents.
+M = 4096
+K = 4096
+N = 14336
+
 
 class Activation(I.Enum):
     """Epilogue activation of `gemm` (gemm.py:10-12)."""

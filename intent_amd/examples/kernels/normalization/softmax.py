@@ -6,6 +6,11 @@ hand-written kernel for each definition and never executes a body."""
 import intent_amd as intent
 import intent_amd.language as I
 
+# The reference's example extents (normalization/softmax.py:4-5), kept as module constants for
+# callers that import them; the definitions below take any extents.
+ROWS = 8192
+COLUMNS = 8192
+
 ROW_MAJOR_NOALIAS = I.constraints(strides=(None, 1), noalias=True)
 
 

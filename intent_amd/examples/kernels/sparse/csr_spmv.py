@@ -7,6 +7,13 @@ matrix; R1 = R + 1 is checked (and R derived from it) by the hip binder."""
 import intent_amd as intent
 import intent_amd.language as I
 
+# The reference's static extents (csr_spmv.py:5-8), kept as module constants for callers that
+# import them (examples/programs/irregular.py:14-33); the definition below takes any extents.
+ROWS = 32768
+COLUMNS = 32768
+NONZEROS_PER_ROW = 32
+NONZEROS = ROWS * NONZEROS_PER_ROW
+
 
 @intent.kernel
 def csr_spmv(

@@ -10,8 +10,18 @@ A region fold over key chunks keeps, per query row, a summary record
   merge:   m = maximum_num of the valid maxima; each side scaled by exp2(m_side - m)
   output:  acc * approx_reciprocal(den) for valid rows, 0 otherwise; cast to f16
 """
+import math
+
 import intent_amd as intent
 import intent_amd.language as I
+
+# The reference's example extents (streaming/attention.py:7-11), kept as module constants for
+# callers that import them; the definitions below take any extents.
+BATCH = 4
+HEADS = 32
+SEQUENCE = 4096
+HEAD_DIMENSION = 128
+SCALE = 1.0 / math.sqrt(HEAD_DIMENSION)
 
 
 @intent.fn

@@ -76,6 +76,29 @@ def test_spmv_random_lengths(device, seed, rows, max_len):
     assert (run(device, offsets, columns, ival, ix) == oracle.csr_spmv(offsets, columns, ival, ix)).all()
 
 
+def test_spmv_reference_example_unsorted_columns(device):
+    """The reference's irregular example (examples/programs/irregular.py:27-33): 32 nonzeros per row
+    at the definition's constants (csr_spmv.py:5-8), columns drawn with replacement, so unsorted
+    within a row and repeated. A few rows of 5000 nonzeros spread over every column exercise the
+    single-row placement with unsorted columns. Placement only chooses which workgroup runs a
+    block, so the bars are those of sorted matrices; small integers make every sum exact."""
+    from intent_amd.examples.kernels.sparse.csr_spmv import COLUMNS, NONZEROS_PER_ROW, ROWS
+
+    announce("spmv reference example, unsorted columns")
+    rng = np.random.default_rng(33)
+    lengths = np.full(ROWS, NONZEROS_PER_ROW, np.int64)
+    lengths[rng.integers(0, ROWS, 5)] = 5000
+    offsets = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
+    columns = rng.integers(0, COLUMNS, int(offsets[-1])).astype(np.int32)
+    assert (np.diff(columns[:NONZEROS_PER_ROW]) < 0).any()            # unsorted in the first row
+    values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
+    x = inputs.uniform(rng, COLUMNS, -1, 1)
+    check(device, offsets, columns, values, x)
+    ival = rng.integers(-3, 4, values.shape).astype(np.float32)
+    ix = rng.integers(-3, 4, x.shape).astype(np.float32)
+    assert (run(device, offsets, columns, ival, ix) == oracle.csr_spmv(offsets, columns, ival, ix)).all()
+
+
 def test_spmv_block_boundaries(device):
     """Rows whose ends fall exactly on, just before and just after workgroup boundaries."""
     announce("spmv block boundaries")

@@ -284,3 +284,22 @@ def test_generated_program_save_load_roundtrip(tmp_path):
     with pytest.raises(intent.CompilationStageError) as error:
         intent.GeneratedProgram.load(path)
     assert error.value.stage == "generated_program_loading"
+
+
+def test_definition_modules_export_the_reference_extents():
+    """The reference's examples import the extent constants of the definition modules
+    (examples/programs/irregular.py:14-15 imports ROWS, COLUMNS, NONZEROS, NONZEROS_PER_ROW from
+    csr_spmv); the same names carry the same values here."""
+    import math
+
+    from intent_amd.examples.kernels.contraction import gemm
+    from intent_amd.examples.kernels.normalization import softmax
+    from intent_amd.examples.kernels.sparse import csr_spmv
+    from intent_amd.examples.kernels.streaming import attention
+
+    assert (csr_spmv.ROWS, csr_spmv.COLUMNS, csr_spmv.NONZEROS_PER_ROW) == (32768, 32768, 32)
+    assert csr_spmv.NONZEROS == 32768 * 32
+    assert (softmax.ROWS, softmax.COLUMNS) == (8192, 8192)
+    assert (gemm.M, gemm.K, gemm.N) == (4096, 4096, 14336)
+    assert (attention.BATCH, attention.HEADS, attention.SEQUENCE, attention.HEAD_DIMENSION) == (4, 32, 4096, 128)
+    assert attention.SCALE == 1.0 / math.sqrt(128)
