@@ -20,8 +20,13 @@
 //
 // Design (both kernels memory-bound):
 //   * partials: one workgroup per (job, key head), 4 waves taking 64-token chunks in turn. Per
-//     chunk, lane t scores token t against the group's queries (f16 in LDS, read as broadcasts);
-//     chunk maxima and sums are wave reductions; P goes through LDS to the P @ V phase, where
+//     chunk, groups of up to 4 query heads load K as V is loaded below (16 bytes per lane, D / 8
+//     lanes per token row, non-temporal) with this lane's 8 dimensions of every query in
+//     registers, and fold the lanes' partial dot products by a reduce-scatter over the lane bits
+//     (DPP and ds_swizzle), so each lane ends with the full scores of one token. Larger groups
+//     score lane t = token t against the queries in LDS (read as broadcasts), each lane reading
+//     its own K row. Chunk maxima and sums are wave reductions; P goes through LDS to the P @ V
+//     phase, where
 //     each lane loads 16 bytes of a V row (D / 8 lanes per token, the chunk's loads in flight
 //     together) and accumulates 8 output dimensions. Lanes sharing dimensions are folded once per
 //     job, then the four waves' states are merged in wave order.
@@ -45,6 +50,15 @@ struct DecodeGeometry {
   int64_t q[3], k[4], v[4], lse[3], out[4];
 };
 
+// The value of lane (lane ^ m), m in {1, 2, 4, 8}: quad permutes and row_ror:8 (DPP, within 16-lane
+// rows) for 1, 2 and 8; ds_swizzle in bit mode (xor within 32 lanes) for 4. Every lane active.
+__device__ __forceinline__ float lane_xor(float v, int m) {
+  if (m == 1) return dpp_move<0xB1>(v);
+  if (m == 2) return dpp_move<0x4E>(v);
+  if (m == 8) return dpp_move<0x128>(v);
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));
+}
+
 // kG bounds the query heads per key head (the group runs 1..kG; register arrays are sized by kG
 // and every loop over them is unrolled with a uniform guard, so nothing is indexed dynamically).
 template <int D, int kG>
@@ -64,6 +78,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kG <= 
   __shared__ float m_s[kWaves][kG], den_s[kWaves][kG];
   __shared__ float acc_s[kWaves][kG][D];
   __shared__ int valid_s[kWaves];
+  // Groups of up to four query heads score with coalesced K loads (kLanesPerToken lanes per token
+  // row, 16 bytes each) and fold the lanes' partial dot products by a reduce-scatter in registers.
+  constexpr bool kCoalesced = kG <= 4;
+  __shared__ int64_t key_s[kWaves][kCoalesced ? kChunk : 1];   // per token: K row offset, -1 if inactive
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -98,6 +116,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kG <= 
     for (int e = 0; e < 8; ++e) acc[gq][e] = 0.0f;
   }
   bool valid = false;
+  uint4 qr[kCoalesced ? kG : 1];   // this lane's 8 dimensions of each query head of the group
+  if constexpr (kCoalesced) {
+#pragma unroll
+    for (int gq = 0; gq < kG; ++gq)
+      qr[gq] = gq < group ? *reinterpret_cast<const uint4 *>(q_s + gq * D + dim0) : make_uint4(0, 0, 0, 0);
+  }
 
   for (int c0 = wave * kChunk; c0 < tokens; c0 += kWaves * kChunk) {
     // Scores: lane t <-> token c0 + t.
@@ -117,32 +141,105 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kG <= 
       key_row = physical * g.k[0] + offset * g.k[1] + kh * g.k[2];
       row_s[wave][lane] = physical * g.v[0] + offset * g.v[1] + kh * g.v[2];
     }
-    if (active) {                                  // inactive tokens are never read for scores
-      // q.k with v_dot2_f32_f16 (products of f16 pairs summed in f32), half a row at a time.
-      const uint4 *krow = reinterpret_cast<const uint4 *>(KC + key_row);
+    int mine = lane;                               // the chunk token whose scores this lane holds
+    if constexpr (kCoalesced) {
+      key_s[wave][lane] = active ? key_row : -1;
+      if (!__any(active)) continue;
+      __builtin_amdgcn_wave_barrier();
+      // Slot j of a lane is token j * kTokensPerLoad + token_lane, dimensions dim0 .. dim0 + 8. The
+      // kSlots loads go in kNB batches of kB. Each batch's partial sums are folded over the lane
+      // bits below kB: at each step a lane keeps the half of its slots that its lane bit selects
+      // and adds the partner's sums for them. The batches are then folded the same way over the
+      // lane bits kB .. kSlots / 2. Lane (token_lane, dc) ends with the full scores of slot dc,
+      // i.e. of token dc * kTokensPerLoad + token_lane (measured against 2 batches of 8 and one
+      // of 16: 52.0, 53.1 and 73.5 us at the B8 HQ32 HK8 D128 decode shape).
+      constexpr int kNB = 4;
+      constexpr int kB = kSlots / kNB;
+      float red[kNB][kG];
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        uint4 kv[D / 16];
+      for (int h = 0; h < kNB; ++h) {
+        uint4 kv[kB];
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) kv[c] = krow[half * (D / 16) + c];
+        for (int j = 0; j < kB; ++j) {
+          const int64_t r = key_s[wave][(h * kB + j) * kTokensPerLoad + token_lane];
+          kv[j] = make_uint4(0, 0, 0, 0);
+          if (r >= 0) kv[j] = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const f16x8_t *>(KC + r + dim0)));
+        }
+        float v[kB][kG];
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
+        for (int j = 0; j < kB; ++j)
 #pragma unroll
           for (int gq = 0; gq < kG; ++gq) {
+            float t = 0.0f;
             if (gq < group) {
-              const uint4 qv = *reinterpret_cast<const uint4 *>(q_s + gq * D + (half * (D / 16) + c) * 8);
-              float t = s[gq];
-              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.x), __builtin_bit_cast(f16x2_t, kv[c].x), t, false);
-              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.y), __builtin_bit_cast(f16x2_t, kv[c].y), t, false);
-              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.z), __builtin_bit_cast(f16x2_t, kv[c].z), t, false);
-              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.w), __builtin_bit_cast(f16x2_t, kv[c].w), t, false);
-              s[gq] = t;
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qr[gq].x), __builtin_bit_cast(f16x2_t, kv[j].x), t, false);
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qr[gq].y), __builtin_bit_cast(f16x2_t, kv[j].y), t, false);
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qr[gq].z), __builtin_bit_cast(f16x2_t, kv[j].z), t, false);
+              t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qr[gq].w), __builtin_bit_cast(f16x2_t, kv[j].w), t, false);
+            }
+            v[j][gq] = t;
+          }
+#pragma unroll
+        for (int n = kB; n > 1; n /= 2) {
+          const bool upper = (lane & (n / 2)) != 0;
+#pragma unroll
+          for (int j = 0; j < n / 2; ++j)
+#pragma unroll
+            for (int gq = 0; gq < kG; ++gq)
+              if (gq < group) {
+                const float keep = upper ? v[j + n / 2][gq] : v[j][gq];
+                const float give = upper ? v[j][gq] : v[j + n / 2][gq];
+                v[j][gq] = keep + lane_xor(give, n / 2);
+              }
+        }
+#pragma unroll
+        for (int gq = 0; gq < kG; ++gq) red[h][gq] = v[0][gq];
+      }
+#pragma unroll
+      for (int n = kNB; n > 1; n /= 2) {
+        const bool upper = (lane & (kB * n / 2)) != 0;
+#pragma unroll
+        for (int h = 0; h < n / 2; ++h)
+#pragma unroll
+          for (int gq = 0; gq < kG; ++gq)
+            if (gq < group) {
+              const float keep = upper ? red[h + n / 2][gq] : red[h][gq];
+              const float give = upper ? red[h][gq] : red[h + n / 2][gq];
+              red[h][gq] = keep + lane_xor(give, kB * n / 2);
+            }
+      }
+#pragma unroll
+      for (int gq = 0; gq < kG; ++gq) s[gq] = red[0][gq];
+      mine = (lane % kLanesPerToken) * kTokensPerLoad + token_lane;
+      active = key_s[wave][mine] >= 0;
+    } else {
+      if (active) {                                  // inactive tokens are never read for scores
+        // q.k with v_dot2_f32_f16 (products of f16 pairs summed in f32), half a row at a time.
+        const uint4 *krow = reinterpret_cast<const uint4 *>(KC + key_row);
+  #pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          uint4 kv[D / 16];
+  #pragma unroll
+          for (int c = 0; c < D / 16; ++c) kv[c] = krow[half * (D / 16) + c];
+  #pragma unroll
+          for (int c = 0; c < D / 16; ++c) {
+  #pragma unroll
+            for (int gq = 0; gq < kG; ++gq) {
+              if (gq < group) {
+                const uint4 qv = *reinterpret_cast<const uint4 *>(q_s + gq * D + (half * (D / 16) + c) * 8);
+                float t = s[gq];
+                t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.x), __builtin_bit_cast(f16x2_t, kv[c].x), t, false);
+                t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.y), __builtin_bit_cast(f16x2_t, kv[c].y), t, false);
+                t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.z), __builtin_bit_cast(f16x2_t, kv[c].z), t, false);
+                t = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qv.w), __builtin_bit_cast(f16x2_t, kv[c].w), t, false);
+                s[gq] = t;
+              }
             }
           }
         }
       }
+      if (!__any(active)) continue;
     }
-    if (!__any(active)) continue;                  // wave-uniform: no active token in this chunk
     valid = true;
     // Chunk summary as the definition forms it: weights against the chunk's own maximum, rounded
     // to f16 for P @ V; the chunk joins the running state with exp2 factors (left for the state,
@@ -161,7 +258,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kG <= 
         const float right = __builtin_amdgcn_exp2f(chunk_max - next);
         m[gq] = next;
         den[gq] = left[gq] * den[gq] + right * chunk_den;
-        p_s[wave][gq][lane] = right * static_cast<float>(static_cast<_Float16>(p));
+        p_s[wave][gq][mine] = right * static_cast<float>(static_cast<_Float16>(p));
       }
     }
 #pragma unroll
