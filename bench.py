@@ -725,9 +725,9 @@ def main():
             log(f"operator {name}")
             try:
                 operators.append(OPERATORS[name](device, flush, not args.no_cpu_baseline))
-                graph_ms = _LAST_GRAPH_MS.pop("graph_ms", None)
-                if graph_ms is not None:
-                    operators[-1]["graph_ms"] = round(graph_ms, 5)
+                operator_graph_ms = _LAST_GRAPH_MS.pop("graph_ms", None)
+                if operator_graph_ms is not None:
+                    operators[-1]["graph_ms"] = round(operator_graph_ms, 5)
             except intent.CompilationStageError as error:
                 operators.append({"config": name, "status": "unsupported", "error": str(error)})
             log(json.dumps(operators[-1]))
