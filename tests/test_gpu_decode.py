@@ -85,6 +85,12 @@ CASES = {
                         lengths=(700,), splits=2, shuffle=True),
     "group8_d128": dict(kind="uniform", batch=2, query_heads=16, kv_heads=2, dim=128, page_size=64,
                         lengths=(3000, 129), splits=4, shuffle=True),
+    # groups of up to 4 score with coalesced K loads folded across lanes: a group of 2 at D 64 with
+    # one-token and page-boundary lengths, and one split holding a whole sequence at D 128
+    "group2_d64_short": dict(kind="uniform", batch=3, query_heads=4, kv_heads=2, dim=64, page_size=32,
+                             lengths=(513, 64, 1), splits=3, shuffle=True),
+    "group4_d128_one_split": dict(kind="uniform", batch=1, query_heads=8, kv_heads=2, dim=128, page_size=64,
+                                  lengths=(4097,), splits=1, shuffle=True),
     "ragged_empty": dict(kind="ragged", batch=3, query_heads=6, kv_heads=2, dim=64, ps=16,
                          lengths=(0, 37, 300), splits=4, pages_per_sequence=20, page_size=16),
     "logical_page_larger": dict(kind="ragged", batch=2, query_heads=4, kv_heads=1, dim=128, ps=16,
