@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kG <= 
   }
 
   for (int c0 = wave * kChunk; c0 < tokens; c0 += kWaves * kChunk) {
-    // Scores: lane t <-> token c0 + t.
+    // Addresses: lane t <-> token c0 + t (its K row offset, and its V row offset for P @ V).
     const int flat = c0 + lane;
     bool active = false;
     float s[kG];
