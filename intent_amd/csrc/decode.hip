@@ -26,10 +26,9 @@
 //     (DPP and ds_swizzle), so each lane ends with the full scores of one token. Larger groups
 //     score lane t = token t against the queries in LDS (read as broadcasts), each lane reading
 //     its own K row. Chunk maxima and sums are wave reductions; P goes through LDS to the P @ V
-//     phase, where
-//     each lane loads 16 bytes of a V row (D / 8 lanes per token, the chunk's loads in flight
-//     together) and accumulates 8 output dimensions. Lanes sharing dimensions are folded once per
-//     job, then the four waves' states are merged in wave order.
+//     phase, where each lane loads 16 bytes of a V row (D / 8 lanes per token, the chunk's loads
+//     in flight together) and accumulates 8 output dimensions. Lanes sharing dimensions are
+//     folded once per job, then the four waves' states are merged in wave order.
 //   * merge: one single-wave workgroup per (batch, head) row; lanes own output dimensions, the
 //     split loop is unrolled so its loads overlap.
 #include "common.hpp"
