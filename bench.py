@@ -628,7 +628,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(every operator shards by rows / (batch, head) with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(softmax, SpMV and attention would shard by rows or (batch, head) with no exchange, "
+              "the GEMM by M-panels of A with B replicated)", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
