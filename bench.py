@@ -277,7 +277,7 @@ def op_gemm(device, flush, cpu):
     import intent_amd as intent
     from intent_amd.examples import inputs
     from intent_amd.examples.kernels.contraction.gemm import bf16_gemm
-    from tests.gpu_util import to_bf16_tensor
+    from intent_amd.examples.inputs import bf16_tensor as to_bf16_tensor
 
     m = n = k = 8192
     a, b = inputs.gemm_bf16()
@@ -428,7 +428,7 @@ def _op_attention_grouped(device, flush, cpu, bf16):
     import intent_amd as intent
     from intent_amd.examples import inputs
     from intent_amd.examples.kernels.streaming.attention import flash_attention_bf16_fwd, flash_gqa_attention_fwd
-    from tests.gpu_util import to_bf16_tensor
+    from intent_amd.examples.inputs import bf16_tensor as to_bf16_tensor
 
     b, hq, s, d = 4, 32, 4096, 128
     group = 1 if bf16 else 4

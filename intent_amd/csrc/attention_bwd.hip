@@ -127,6 +127,97 @@ __device__ __forceinline__ f16x8_t tr_frag(const uint16_t *tile, int sl, int mt,
   return __builtin_bit_cast(f16x8_t, parts);
 }
 
+// ---------------------------------------------------------------- excluded pairs
+// The reference leaves causally excluded pairs (and rows past the end) out of the gradient
+// products even when their operands are non-finite (masked_gradient_product,
+// backward/attention.py:37-44). The MFMA path gives an excluded pair a zero weight, which is
+// exact for finite operand rows, but 0 * inf or 0 * NaN would reach the gradient. So a tile that
+// holds excluded pairs and whose operand rows (K for dQ; Q for dK; dO for dV) hold an inf or NaN
+// is left out of the MFMA loop, and after that loop the wave folds it again one pair at a time,
+// from global memory, skipping the excluded pairs. The check costs a few LDS reads per edge tile;
+// the scalar fold runs only for such inputs. It sits after the loop, not in it: inside the tile
+// loop, its code raised the 8-wave D = 128 kernels to 256 VGPRs with spills in the hot path.
+
+// Nonzero when either f16 half of w has an all-ones exponent (inf or NaN): 0x7C00 + 0x0400 sets
+// bit 15 of that half, smaller exponents do not, and no carry crosses into the upper half.
+__device__ __forceinline__ uint32_t nonfinite_halves(uint32_t w) {
+  return ((w & 0x7C007C00u) + 0x04000400u) & 0x80008000u;
+}
+
+__device__ __forceinline__ uint32_t nonfinite_chunk(uint4 w) {
+  return nonfinite_halves(w.x) | nonfinite_halves(w.y) | nonfinite_halves(w.z) | nonfinite_halves(w.w);
+}
+
+// True (for the whole wave) when an element of the 64 rows of an LDS tile is inf or NaN. Lane l
+// reads half of rows l % 32 and 32 + l % 32; the lane pair (l, l ^ 32) covers both rows.
+template <int D>
+__device__ __forceinline__ bool tile_nonfinite(const uint4 *tile, int lane) {
+  const int half = lane >> 5;
+  uint32_t bad = 0;
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    const int row = st * 32 + (lane & 31);
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) bad |= nonfinite_chunk(tile[row * (D / 8) + ((ks * 2 + half) ^ swz<D>(row))]);
+  }
+  return __any(bad != 0);
+}
+
+// The same test on rows [first, first + 64) of a tensor in global memory (row r at base + r * ld,
+// rows past `last` read row `last`, as the tile DMA does).
+template <int D>
+__device__ __forceinline__ bool rows_nonfinite(const uint16_t *base, int64_t ld, int first, int last, int lane) {
+  const int half = lane >> 5;
+  uint32_t bad = 0;
+#pragma unroll 1
+  for (int st = 0; st < 2; ++st) {
+    const uint16_t *row = base + static_cast<int64_t>(min(first + st * 32 + (lane & 31), last)) * ld;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) bad |= nonfinite_chunk(*reinterpret_cast<const uint4 *>(row + ks * 16 + half * 8));
+  }
+  return __any(bad != 0);
+}
+
+// Dot product of this lane's half of a row held in registers (D / 16 fragments of 8 f16, columns
+// 16 ks + 8 half + 0..7) with the same columns of a row in global memory, completed across the lane
+// pair. Packed f16 dot products (v_dot2_f32_f16) take the fragments as they are.
+template <int D>
+__device__ __forceinline__ float pair_dot(const f16x8_t (&frag)[D / 16], const uint16_t *row, int half) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  float sum = 0.0f;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    const uint4 x = *reinterpret_cast<const uint4 *>(row + ks * 16 + half * 8);
+    const uint4 f = __builtin_bit_cast(uint4, frag[ks]);
+    sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, f.x), __builtin_bit_cast(f16x2_t, x.x), sum, false);
+    sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, f.y), __builtin_bit_cast(f16x2_t, x.y), sum, false);
+    sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, f.z), __builtin_bit_cast(f16x2_t, x.z), sum, false);
+    sum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, f.w), __builtin_bit_cast(f16x2_t, x.w), sum, false);
+  }
+  return sum + __shfl_xor(sum, 32);
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint32_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xFFFFu)));
+}
+
+// acc (MFMA accumulator order: slot 4 gq + j of tile mt is column 32 mt + 8 gq + 4 half + j) +=
+// w * the lane's columns of a row in global memory; each product is rounded once into the sum
+// (fmaf), as in the MFMA.
+template <int D>
+__device__ __forceinline__ void add_row(f32x16_t (&acc)[D / 32], float w, const uint16_t *row, int half) {
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const uint2 x = *reinterpret_cast<const uint2 *>(row + mt * 32 + gq * 8 + half * 4);
+      acc[mt][4 * gq + 0] = fmaf(w, f16_bits_to_float(x.x), acc[mt][4 * gq + 0]);
+      acc[mt][4 * gq + 1] = fmaf(w, f16_bits_to_float(x.x >> 16), acc[mt][4 * gq + 1]);
+      acc[mt][4 * gq + 2] = fmaf(w, f16_bits_to_float(x.y), acc[mt][4 * gq + 2]);
+      acc[mt][4 * gq + 3] = fmaf(w, f16_bits_to_float(x.y >> 16), acc[mt][4 * gq + 3]);
+    }
+}
+
 // ---------------------------------------------------------------- delta
 // D / 8 lanes per row, 8 elements (one 16-byte load of o and of do) per lane.
 template <int D>
@@ -232,6 +323,10 @@ __device__ __forceinline__ void attention_bwd_dq_body(
   const int t_row = 4 * (g16 >> 1) + (i16 >> 2);
   const int t_col = 16 * (g16 & 1) + 4 * (i16 & 3);
 
+  // Tiles holding excluded pairs: keys past this wave's first query (causal) or past the end.
+  auto edge_tile = [&](int key0) { return (causal && key0 + kTile - 1 > wq0) || key0 + kTile > sk; };
+  bool skipped = false;   // wave-uniform: some edge tile was left for the masked fold
+
   for (int kt = t_begin; kt < t_begin + kStages - 1 && kt < t_end; ++kt) issue(kt);
   for (int kt = t_begin; kt < t_end; ++kt) {
     wait_tiles_after<2 * kDma>(min(t_end - 1 - kt, kStages - 2));
@@ -242,6 +337,10 @@ __device__ __forceinline__ void attention_bwd_dq_body(
     const uint4 *ktile = lds + ((kt - t_begin) % kStages) * 2 * kChunks;
     const uint4 *vtile = ktile + kChunks;
     const uint16_t *kt16 = reinterpret_cast<const uint16_t *>(ktile);
+    if (edge_tile(key0) && tile_nonfinite<D>(ktile, lane)) {   // folded after the loop
+      skipped = true;
+      continue;
+    }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       f16x8_t dsf[2];
@@ -269,6 +368,27 @@ __device__ __forceinline__ void attention_bwd_dq_body(
 #pragma unroll
         for (int mt = 0; mt < D / 32; ++mt) acc[mt] = mma(tr_frag<D>(kt16, st * 2 + h2, mt, t_row, t_col), dsf[h2], acc[mt]);
       __builtin_amdgcn_s_setprio(0);
+    }
+  }
+
+  // Edge tiles left out above (K rows with an inf or NaN): fold their valid keys one by one.
+  if (skipped) {
+#pragma unroll 1
+    for (int kt = t_begin; kt < t_end; ++kt) {
+      const int key0 = kt * kTile;
+      if ((causal && key0 > wave_q_last) || !edge_tile(key0) || !rows_nonfinite<D>(kbase, g.k[2], key0, sk - 1, lane))
+        continue;
+      const int last = (causal ? min(sk - 1, lane_q) : sk - 1) - key0;   // last valid tile row of this query
+#pragma unroll 1
+      for (int j = 0; j < kTile; ++j) {
+        const int key = min(key0 + j, sk - 1);
+        const uint16_t *krow = kbase + static_cast<int64_t>(key) * g.k[2];
+        const float s = pair_dot<D>(qf, krow, half);
+        const float dp = pair_dot<D>(of, vbase + static_cast<int64_t>(key) * g.v[2], half);
+        if (j > last) continue;
+        const float p = __builtin_amdgcn_exp2f(fmaf(s, c1, -lse2));
+        add_row<D>(acc, static_cast<float>(round_to<_Float16>(p * (dp - dlt))), krow, half);
+      }
     }
   }
 
@@ -421,6 +541,10 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
   const int t_row = 4 * (g16 >> 1) + (i16 >> 2);
   const int t_col = 16 * (g16 & 1) + 4 * (i16 & 3);
 
+  // Tiles holding excluded pairs: queries before this wave's last key (causal) or past the end.
+  auto edge_tile = [&](int q0) { return (causal && q0 < wk0 + 31) || q0 + kTile > sq; };
+  bool skipped = false;   // wave-uniform: some edge tile was left for the masked fold
+
   for (int t = 0; t < kStages - 1 && t < tiles; ++t) issue(t);
   for (int t = 0; t < tiles; ++t) {
     // Waves 0 and 1 also move lse and delta: one more DMA instruction per tile.
@@ -438,6 +562,10 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
     // lse_s[i] / dlt_s[i] hold row q0 + i (the last row for i past the end, excluded by the mask).
     const uint16_t *q16 = reinterpret_cast<const uint16_t *>(qtile);
     const uint16_t *g16p = reinterpret_cast<const uint16_t *>(gtile);
+    if (edge_tile(q0) && ((kDoK && tile_nonfinite<D>(qtile, lane)) || (kDoV && tile_nonfinite<D>(gtile, lane)))) {
+      skipped = true;   // folded after the loop
+      continue;
+    }
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       f16x8_t pf[2], dsf[2];
@@ -477,6 +605,39 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
           if constexpr (kDoK) acc_k[mt] = mma(tr_frag<D>(q16, st * 2 + h2, mt, t_row, t_col), dsf[h2], acc_k[mt]);
         }
       __builtin_amdgcn_s_setprio(0);
+    }
+  }
+
+  // Edge tiles left out above (Q or dO rows with an inf or NaN): fold their valid queries one by one.
+  if (skipped) {
+#pragma unroll 1
+    for (int t = 0; t < tiles; ++t) {
+      const int q0 = tile_q0(t);
+      if ((causal && q0 + kTile - 1 < wk0) || !edge_tile(q0)) continue;
+      const int hq = tile_head(t);
+      const uint16_t *qbase = Q + b * g.q[0] + hq * g.q[1];
+      const uint16_t *gbase = G + b * g.dout[0] + hq * g.dout[1];
+      if (!((kDoK && rows_nonfinite<D>(qbase, g.q[2], q0, sq - 1, lane)) ||
+            (kDoV && rows_nonfinite<D>(gbase, g.dout[2], q0, sq - 1, lane))))
+        continue;
+      const int first = causal ? lane_k - q0 : 0, last = sq - 1 - q0;   // valid tile rows of this key
+#pragma unroll 1
+      for (int j = 0; j < kTile; ++j) {
+        const int q = min(q0 + j, sq - 1);
+        const uint16_t *qrow = qbase + static_cast<int64_t>(q) * g.q[2];
+        const uint16_t *grow = gbase + static_cast<int64_t>(q) * g.dout[2];
+        const float s = pair_dot<D>(kf, qrow, half);
+        float dp = 0.0f;
+        if constexpr (kDoK) dp = pair_dot<D>(vf, grow, half);
+        if (j < first || j > last) continue;
+        const float p = __builtin_amdgcn_exp2f(
+            fmaf(s, c1, -LSE[b * g.lse[0] + hq * g.lse[1] + static_cast<int64_t>(q) * g.lse[2]] * kLog2e));
+        if constexpr (kDoV) add_row<D>(acc_v, static_cast<float>(static_cast<_Float16>(p)), grow, half);
+        if constexpr (kDoK) {
+          const float dl = DELTA[b * g.delta[0] + hq * g.delta[1] + static_cast<int64_t>(q) * g.delta[2]];
+          add_row<D>(acc_k, static_cast<float>(round_to<_Float16>(p * (dp - dl))), qrow, half);
+        }
+      }
     }
   }
 

@@ -24,6 +24,25 @@ def _bf16_bits(values_f32: np.ndarray) -> np.ndarray:
     return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
 
 
+def bf16_to_f32(bits) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32 values (exact)."""
+    return (np.asarray(bits).astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_tensor(bits, device):
+    """bf16 bit patterns (uint16 array) -> a torch.bfloat16 tensor on `device`."""
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).astype(np.uint16).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def bf16_tensor_bits(tensor) -> np.ndarray:
+    """A torch.bfloat16 tensor -> its bit patterns as a host uint16 array."""
+    import torch
+
+    return tensor.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
 def normal(rng, shape, dtype: str = "f32", scale=None) -> np.ndarray:
     """float32/float16 array, or uint16 bf16 bits for dtype="bf16"."""
     sample = rng.standard_normal(shape, dtype=np.float32)

@@ -40,17 +40,6 @@ def f16_ulp_distance(a, b):
     return np.abs(ia - ib)
 
 
-def bf16_to_f32(bits):
-    return (np.asarray(bits).astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
-
-
-def to_bf16_tensor(bits, device):
-    import torch
-
-    return torch.from_numpy(np.ascontiguousarray(bits).astype(np.uint16).view(np.int16)).view(torch.bfloat16).to(device)
-
-
-def bf16_tensor_bits(tensor):
-    import torch
-
-    return tensor.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+# bf16 conversions live beside the input generators (bench.py and smoke() use them too).
+from intent_amd.examples.inputs import bf16_tensor as to_bf16_tensor  # noqa: E402,F401
+from intent_amd.examples.inputs import bf16_tensor_bits, bf16_to_f32  # noqa: E402,F401
