@@ -343,7 +343,7 @@ def op_spmv(device, flush, cpu):
     out = {"config": f"CSR SpMV f32 {rows}^2, {nnz} nnz, rank-law Zipf(1.5) rows (config 5)",
            "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
            "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
-           "traffic": read_traffic("spmv_merge_config5")}
+           "traffic": read_traffic("spmv_config5")}
     if cpu:
         import oracle
 

@@ -256,8 +256,11 @@ int intent_hip_splitk_reduce_f32_to_f16(const float *partial, const float *lse, 
                                         void *stream);
 
 /* CSR SpMV y = A x, f32 values, i32 indices.
- * csr_spmv (python/intent/examples/kernels/sparse/csr_spmv.py:11-29), with dynamic extents.
- * The workspace (device memory, caller-owned) must hold intent_hip_csr_spmv_workspace_bytes(). */
+ * csr_spmv (python/intent/examples/kernels/sparse/csr_spmv.py:11-29), with dynamic extents. Row r
+ * covers the absolute positions [row_offsets[r], row_offsets[r + 1]) of column_indices and values
+ * (nnz entries each), so the offsets may start above 0 and end below nnz.
+ * The workspace (device memory, caller-owned, 256-byte aligned) must hold
+ * intent_hip_csr_spmv_workspace_bytes(rows, nnz): at most about 1.13 bytes per nonzero. */
 int intent_hip_csr_spmv_workspace_bytes(int64_t rows, int64_t nnz, size_t *bytes);
 int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t *column_indices,
                             const float *values, const float *x, float *y, int64_t rows,

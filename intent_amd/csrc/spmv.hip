@@ -2,281 +2,660 @@
 //
 // Semantics (python/intent/examples/kernels/sparse/csr_spmv.py:11-29): for every row,
 // acc = 0.0f; for nz in [off[r], off[r+1]) in order: acc = acc + values[nz] * x[col[nz]];
-// y[r] = acc. Index traversal is exact; the product is rounded to f32 before the add
-// (no fused multiply-add), so any row that one thread folds alone reproduces the
-// ordered loop bit for bit. Longer rows are split and their partial sums combined in a
-// fixed, data-independent order (left part + right part), which reassociates the fold.
+// y[r] = acc. Positions are absolute, so off[0] may be above 0 and off[R] below nnz (a row slice
+// of a larger CSR). Index traversal is exact. Rows of up to 8 nonzeros are folded by one lane in
+// order, with each product rounded before the add (no fused multiply-add): that reproduces the
+// ordered loop bit for bit. Longer rows are split into pieces whose partial sums are combined in a
+// fixed, data-independent order, a reassociation of the fold.
 //
-// Design: merge-path partition (Merrill & Garland, "Merge-based parallel sparse
-// matrix-vector multiplication", SC'16). The work items are the R row ends merged with
-// the NNZ nonzeros; every workgroup takes exactly kBlockItems of them and every thread
-// kItems, whatever the row-length distribution (4M rows of length 1 next to rows of
-// 65536). Launches:
-//   1. partition: one thread per row writes the row that contains each workgroup's
-//      starting diagonal (no searches in global memory);
-//   2. placement (place, place_fill): logical workgroups inside one long row are
-//      mapped to the XCD whose L2 serves their column window; the rest fill free slots;
-//   3. merge: a workgroup stages its row ends and its products values*x[col] in LDS
-//      (coalesced non-temporal col/value loads that do not evict x from L2, gathers of
-//      x), each thread searches its diagonal in LDS and folds kItems items in order;
-//      partial rows are combined by a segmented scan across the workgroup; the partial
-//      row left open at the workgroup's end goes to the workspace;
-//   4. fixup: the first workgroup of each run of equal open rows adds the run's
-//      partials (in workgroup order) to y.
-// Placement changes only which hardware workgroup runs a logical block, never what the
-// block computes, so results do not depend on it.
+// Design. The cost of this operator is the gather of x, one per nonzero. A gather that hits L2 is
+// still one L2 request: at config 5 (67M nonzeros), gathers confined to an L2-resident window of
+// x took 300 us of a 450 us merge-path kernel, and the real gathers (61% L2 hits) 470 us of 615.
+// Rows are therefore classed by length:
+//   * up to 4 nonzeros: one lane per row, ordered fold (spmv_rows, four rows per thread with
+//     their loads issued together);
+//   * 5 to 127: 16 lanes per row (spmv_rows);
+//   * medium (128 to big - 1): the row is cut at the boundaries of 8 column windows of C / 8
+//     columns, the share of x one XCD's 4 MB L2 holds, and the piece in window w runs on XCD w
+//     (hardware workgroup h runs on XCD h % 8), so its gathers hit that L2 (spmv_pieces<false>);
+//   * large (big = max(128, 16 S) or more): the row is cut at the boundaries of S slices of 16384
+//     columns; a workgroup stages one slice of x (64 KB) in LDS and runs that slice's piece of
+//     many large rows, gathering from LDS (spmv_pieces<true>).
+// The medium and large row lists are built without atomics: spmv_count counts each 1024-row
+// block's rows of each class, spmv_scan (one workgroup) turns the counts into list offsets, and
+// spmv_rows writes each block's rows at its offset in row order. (Wave-level atomics on two list
+// counters cost 115 us at config 5.) spmv_bounds estimates each cut by interpolation search and
+// makes the cuts of a row non-decreasing with a prefix maximum, so the pieces partition the row
+// for any estimate and any column order; an entry outside its window or slice only reads x from
+// another place. spmv_combine adds the pieces of each medium or large row in window or slice order.
 #include "common.hpp"
 
 namespace intent_hip {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kItems = 8;
-constexpr int kBlockItems = kThreads * kItems;
+constexpr int kLaneRow = 4;         // rows of up to 4 nonzeros: one lane, exact ordered fold
+constexpr int kGroupRow = 128;      // rows below 128 nonzeros: 16 lanes
+constexpr int kGroup = 16;
+constexpr int kRowsPerThread = 4;   // spmv_count / spmv_rows: 1024 rows per 256-thread workgroup
+constexpr int kBlockRows = 256 * kRowsPerThread;
+constexpr int kWindows = 8;         // one column window per XCD
+constexpr int kSliceCols = 16384;   // 64 KB of x in LDS per workgroup
+constexpr int kTargetTiles = 1024;  // slice workgroups per launch (four per CU)
+constexpr int kWindowTiles = 64;    // medium-row tiles per window (two per CU of the XCD)
+constexpr int kSearchSteps = 8;     // interpolation steps per cut
 
 inline size_t align256(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
 
-struct Workspace {
-  int32_t *splits;      // [blocks + 1]: row of each workgroup's starting diagonal
-  int32_t *carry_rows;  // [blocks]: row left open at the workgroup's end, -1 if none
-  float *carry_values;  // [blocks]: its partial sum
-  int32_t *perm;        // [blocks]: logical block run by hardware workgroup h
-  int32_t *overflow;    // [blocks]: logical blocks not placed on their XCD
-  int32_t *counters;    // [64]: per-XCD fill counts, overflow count
+// Row classes and the workspace carved for them.
+struct Plan {
+  int32_t *counters;      // [64]: [0] medium rows, [1] large rows
+  int32_t *block_counts;  // [blocks][2]: medium and large rows of each 1024-row block
+  int32_t *block_first;   // [blocks][2]: their first list index (exclusive scan)
+  int32_t *mid_rows;      // [cap_mid] row ids of medium rows, in row order
+  int32_t *big_rows;      // [cap_big]
+  int32_t *mid_cuts;      // [cap_mid][9]: piece w is [cut w, cut w + 1)
+  float *mid_parts;       // [cap_mid][8]
+  int32_t *big_cuts;      // [cap_big][slices + 1]
+  float *big_parts;       // [cap_big][slices]
+  int32_t cap_mid, cap_big, slices, big, blocks;
 };
 
-size_t workspace_bytes(int64_t blocks) {
-  return align256(4 * static_cast<size_t>(blocks + 1)) + 4 * align256(4 * static_cast<size_t>(blocks)) + 256;
+int64_t slice_count(int64_t cols) { return cols > 0 ? (cols + kSliceCols - 1) / kSliceCols : 1; }
+int64_t big_length(int64_t slices) { return slices * 16 > kGroupRow ? slices * 16 : kGroupRow; }
+int64_t mid_capacity(int64_t rows, int64_t nnz) { return nnz / kGroupRow < rows ? nnz / kGroupRow : rows; }
+int64_t big_capacity(int64_t rows, int64_t nnz, int64_t slices) {
+  const int64_t by_nnz = nnz / big_length(slices);
+  return by_nnz < rows ? by_nnz : rows;
+}
+int64_t block_count(int64_t rows) { return (rows + kBlockRows - 1) / kBlockRows; }
+// Entries (cuts plus parts plus row ids) of the large-row region: cap_big * (2 S + 2) <= 18 nnz / 128
+// for every slice count S, so the bound below holds whatever the column count.
+int64_t big_entries_bound(int64_t nnz) { return (18 * nnz + 127) / 128 + 64; }
+
+size_t workspace_bytes(int64_t rows, int64_t nnz) {
+  const int64_t cap_mid = mid_capacity(rows, nnz);
+  return 256 + 2 * align256(8 * static_cast<size_t>(block_count(rows))) + align256(4 * static_cast<size_t>(cap_mid)) +
+         align256(36 * static_cast<size_t>(cap_mid)) + align256(32 * static_cast<size_t>(cap_mid)) +
+         align256(4 * static_cast<size_t>(big_entries_bound(nnz))) + 1024;
 }
 
-Workspace carve(void *base, int64_t blocks) {
-  char *p = static_cast<char *>(base);
-  Workspace w;
-  w.splits = reinterpret_cast<int32_t *>(p);
-  p += align256(4 * static_cast<size_t>(blocks + 1));
-  w.carry_rows = reinterpret_cast<int32_t *>(p);
-  p += align256(4 * static_cast<size_t>(blocks));
-  w.carry_values = reinterpret_cast<float *>(p);
-  p += align256(4 * static_cast<size_t>(blocks));
-  w.perm = reinterpret_cast<int32_t *>(p);
-  p += align256(4 * static_cast<size_t>(blocks));
-  w.overflow = reinterpret_cast<int32_t *>(p);
-  p += align256(4 * static_cast<size_t>(blocks));
-  w.counters = reinterpret_cast<int32_t *>(p);
-  return w;
+Plan carve(void *base, int64_t rows, int64_t cols, int64_t nnz) {
+  Plan p;
+  p.slices = static_cast<int32_t>(slice_count(cols));
+  p.big = static_cast<int32_t>(big_length(p.slices));
+  p.cap_mid = static_cast<int32_t>(mid_capacity(rows, nnz));
+  p.cap_big = static_cast<int32_t>(big_capacity(rows, nnz, p.slices));
+  p.blocks = static_cast<int32_t>(block_count(rows));
+  char *c = static_cast<char *>(base);
+  p.counters = reinterpret_cast<int32_t *>(c);
+  c += 256;
+  p.block_counts = reinterpret_cast<int32_t *>(c);
+  c += align256(8 * static_cast<size_t>(p.blocks));
+  p.block_first = reinterpret_cast<int32_t *>(c);
+  c += align256(8 * static_cast<size_t>(p.blocks));
+  p.mid_rows = reinterpret_cast<int32_t *>(c);
+  c += align256(4 * static_cast<size_t>(p.cap_mid));
+  p.mid_cuts = reinterpret_cast<int32_t *>(c);
+  c += align256(36 * static_cast<size_t>(p.cap_mid));
+  p.mid_parts = reinterpret_cast<float *>(c);
+  c += align256(32 * static_cast<size_t>(p.cap_mid));
+  p.big_rows = reinterpret_cast<int32_t *>(c);
+  c += align256(4 * static_cast<size_t>(p.cap_big));
+  p.big_cuts = reinterpret_cast<int32_t *>(c);
+  c += align256(4 * static_cast<size_t>(p.cap_big) * (p.slices + 1));
+  p.big_parts = reinterpret_cast<float *>(c);
+  return p;
 }
 
-constexpr int kXcds = 8;
+__device__ __forceinline__ int32_t clamp_col(int32_t c, int32_t cols) {
+  return static_cast<uint32_t>(c) < static_cast<uint32_t>(cols) ? c : cols - 1;
+}
 
-// Hardware workgroup h runs on XCD h % 8. A logical block whose items all lie inside one row
-// gathers x from a narrow column window (columns are sorted within a row); it is placed on the
-// XCD that owns that eighth of the columns, so its gathers come from that XCD's L2. Other blocks
-// fill the remaining slots. Each logical block computes the same result wherever it runs.
-__global__ __launch_bounds__(kThreads) void spmv_place(const int32_t *__restrict__ col, int32_t cols,
-                                                       int32_t blocks, int64_t total, int64_t nnz,
-                                                       Workspace ws) {
-  // Slots are reserved per workgroup: LDS atomics rank the threads, then one global atomic
-  // per XCD (and one for the overflow list) reserves the workgroup's range.
-  __shared__ int32_t s_count[kXcds + 1];
-  __shared__ int32_t s_base[kXcds + 1];
-  const int t = threadIdx.x;
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + t;
-  if (t <= kXcds) s_count[t] = 0;
-  __syncthreads();
-  int xcd = -1;
-  if (g < blocks) {
-    const int32_t x0 = ws.splits[g], x1 = ws.splits[g + 1];
-    const int64_t y0 = g * kBlockItems - x0;
-    const int64_t d1 = (g + 1) * kBlockItems < total ? (g + 1) * kBlockItems : total;
-    const int64_t y1 = d1 - x1;
-    if (x1 - x0 <= 1 && y1 - y0 >= kBlockItems / 2 && y0 >= 0 && y1 <= nnz) {
-      const int64_t mid = (y0 + y1) / 2;
-      xcd = static_cast<int>((static_cast<int64_t>(col[mid]) * kXcds) / cols);
-      xcd = xcd < 0 ? 0 : (xcd >= kXcds ? kXcds - 1 : xcd);
+// Row r's nonzeros [begin, end), clamped into [0, nnz] (valid CSR never needs the clamp).
+__device__ __forceinline__ void row_span(const int32_t *off, int64_t r, int64_t nnz, int32_t &begin, int32_t &end) {
+  const int64_t b = off[r], e = off[r + 1];
+  const int64_t cb = b < 0 ? 0 : (b > nnz ? nnz : b);
+  const int64_t ce = e < cb ? cb : (e > nnz ? nnz : e);
+  begin = static_cast<int32_t>(cb);
+  end = static_cast<int32_t>(ce);
+}
+
+__device__ __forceinline__ float group16_sum(float v) {
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 1);
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+  return v;
+}
+
+// Medium and large rows of every 1024-row block (rows base + tid + 256 k).
+__global__ __launch_bounds__(256) void spmv_count(const int32_t *__restrict__ off, int32_t rows, int64_t nnz,
+                                                  Plan plan) {
+  __shared__ int s_part[2][4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kBlockRows;
+  int mid = 0, big = 0;
+#pragma unroll
+  for (int k = 0; k < kRowsPerThread; ++k) {
+    const int64_t r = base + threadIdx.x + 256 * k;
+    if (r < rows) {
+      int32_t b, e;
+      row_span(off, r, nnz, b, e);
+      mid += (e - b >= kGroupRow && e - b < plan.big) ? 1 : 0;
+      big += (e - b >= plan.big) ? 1 : 0;
     }
   }
-  const int32_t local = xcd >= 0 ? atomicAdd(&s_count[xcd], 1) : 0;
-  __syncthreads();
-  if (t < kXcds) s_base[t] = s_count[t] > 0 ? atomicAdd(&ws.counters[t], s_count[t]) : 0;
-  __syncthreads();
-  bool spill = g < blocks;
-  if (xcd >= 0) {
-    const int32_t capacity = (blocks - xcd + kXcds - 1) / kXcds;   // slots h = xcd + 8 i < blocks
-    const int32_t slot = s_base[xcd] + local;
-    if (slot < capacity) {
-      ws.perm[xcd + kXcds * slot] = static_cast<int32_t>(g);
-      spill = false;
-    }
+  mid = wave_sum_int(mid);
+  big = wave_sum_int(big);
+  if ((threadIdx.x & 63) == 0) {
+    s_part[0][threadIdx.x >> 6] = mid;
+    s_part[1][threadIdx.x >> 6] = big;
   }
-  const int32_t rank = spill ? atomicAdd(&s_count[kXcds], 1) : 0;
   __syncthreads();
-  if (t == 0) s_base[kXcds] = s_count[kXcds] > 0 ? atomicAdd(&ws.counters[kXcds], s_count[kXcds]) : 0;
-  __syncthreads();
-  if (spill) ws.overflow[s_base[kXcds] + rank] = static_cast<int32_t>(g);
+  if (threadIdx.x < 2)
+    plan.block_counts[2 * blockIdx.x + threadIdx.x] =
+        s_part[threadIdx.x][0] + s_part[threadIdx.x][1] + s_part[threadIdx.x][2] + s_part[threadIdx.x][3];
 }
 
-__global__ __launch_bounds__(kThreads) void spmv_place_fill(int32_t blocks, Workspace ws) {
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (j >= ws.counters[kXcds]) return;
-  // Free slots of XCD e are i in [filled_e, capacity_e); enumerate them XCD by XCD.
-  int64_t rank = j;
-  for (int e = 0; e < kXcds; ++e) {
-    const int32_t capacity = (blocks - e + kXcds - 1) / kXcds;
-    const int32_t filled = min(ws.counters[e], capacity);
-    const int32_t free_slots = capacity - filled;
-    if (rank < free_slots) {
-      ws.perm[e + kXcds * (filled + rank)] = ws.overflow[j];
-      return;
+// Exclusive prefix sums of the block counts (one workgroup of 1024 threads); totals to counters.
+__global__ __launch_bounds__(1024) void spmv_scan(Plan plan) {
+  __shared__ int s_wave[2][16];
+  __shared__ int s_carry[2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < 2) s_carry[tid] = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < plan.blocks; b0 += 1024) {
+    const int b = b0 + tid;
+    int v[2];
+    int incl[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      v[c] = b < plan.blocks ? plan.block_counts[2 * b + c] : 0;
+      incl[c] = v[c];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int up = __shfl_up(incl[c], d);
+        incl[c] += lane >= d ? up : 0;
+      }
+      if (lane == 63) s_wave[c][wave] = incl[c];
     }
-    rank -= free_slots;
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      int before = s_carry[c];
+      for (int w = 0; w < wave; ++w) before += s_wave[c][w];
+      if (b < plan.blocks) plan.block_first[2 * b + c] = before + incl[c] - v[c];
+    }
+    __syncthreads();
+    if (tid < 2) {
+      int total = s_carry[tid];
+      for (int w = 0; w < 16; ++w) total += s_wave[tid][w];
+      s_carry[tid] = total;
+    }
+    __syncthreads();
+  }
+  if (tid < 2) plan.counters[tid] = s_carry[tid];
+}
+
+// Short rows and the row lists. Rows base + tid + 256 k of the block: rows of up to 4 nonzeros are
+// folded by their lane (the loads of the thread's four rows issued together); rows of 5..127 by a
+// 16-lane group (four rows per wave at a time); medium and large rows are written to their lists
+// at the block's scanned offset, in row order.
+__global__ __launch_bounds__(256) void spmv_rows(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
+                                                 const float *__restrict__ val, const float *__restrict__ x,
+                                                 float *__restrict__ y, int32_t rows, int32_t cols, int64_t nnz,
+                                                 Plan plan) {
+  __shared__ int s_wave[2][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kBlockRows;
+  int32_t begin[kRowsPerThread], length[kRowsPerThread];
+#pragma unroll
+  for (int k = 0; k < kRowsPerThread; ++k) {
+    const int64_t r = base + threadIdx.x + 256 * k;
+    int32_t b = 0, e = 0;
+    if (r < rows) row_span(off, r, nnz, b, e);
+    begin[k] = b;
+    length[k] = r < rows ? e - b : -1;
+  }
+  // Lane rows: all column and value loads, then all gathers, then the ordered folds.
+  {
+    int32_t c[kRowsPerThread][kLaneRow];
+    float v[kRowsPerThread][kLaneRow], xs[kRowsPerThread][kLaneRow];
+#pragma unroll
+    for (int k = 0; k < kRowsPerThread; ++k)
+#pragma unroll
+      for (int j = 0; j < kLaneRow; ++j) {
+        const bool ok = length[k] <= kLaneRow && j < length[k];
+        c[k][j] = ok ? col[begin[k] + j] : 0;
+        v[k][j] = ok ? val[begin[k] + j] : 0.0f;
+      }
+#pragma unroll
+    for (int k = 0; k < kRowsPerThread; ++k)
+#pragma unroll
+      for (int j = 0; j < kLaneRow; ++j)
+        xs[k][j] = (length[k] <= kLaneRow && j < length[k]) ? x[clamp_col(c[k][j], cols)] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRowsPerThread; ++k) {
+      // hipcc would otherwise fuse each product and add into one FMA, which rounds once.
+#pragma clang fp contract(off)
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kLaneRow; ++j)
+        if (j < length[k]) acc = acc + v[k][j] * xs[k][j];
+      if (length[k] >= 0 && length[k] <= kLaneRow) y[base + threadIdx.x + 256 * k] = acc;
+    }
+  }
+  // Lists: rank of each medium / large row within the block, in row order (k, then thread).
+  int first[2] = {plan.block_first[2 * blockIdx.x], plan.block_first[2 * blockIdx.x + 1]};
+#pragma unroll
+  for (int k = 0; k < kRowsPerThread; ++k) {
+    const bool is_mid = length[k] >= kGroupRow && length[k] < plan.big;
+    const bool is_big = length[k] >= plan.big;
+    const uint64_t m_mid = __ballot(is_mid), m_big = __ballot(is_big);
+    if (lane == 0) {
+      s_wave[0][wave] = __builtin_popcountll(m_mid);
+      s_wave[1][wave] = __builtin_popcountll(m_big);
+    }
+    __syncthreads();
+    int before[2] = {first[0], first[1]};
+    for (int w = 0; w < wave; ++w) {
+      before[0] += s_wave[0][w];
+      before[1] += s_wave[1][w];
+    }
+    const uint64_t below = (1ull << lane) - 1;
+    const int32_t r = static_cast<int32_t>(base + threadIdx.x + 256 * k);
+    if (is_mid) {
+      const int at = before[0] + __builtin_popcountll(m_mid & below);
+      if (at < plan.cap_mid) plan.mid_rows[at] = r;
+    }
+    if (is_big) {
+      const int at = before[1] + __builtin_popcountll(m_big & below);
+      if (at < plan.cap_big) plan.big_rows[at] = r;
+    }
+    first[0] += s_wave[0][0] + s_wave[0][1] + s_wave[0][2] + s_wave[0][3];
+    first[1] += s_wave[1][0] + s_wave[1][1] + s_wave[1][2] + s_wave[1][3];
+    __syncthreads();
+  }
+  // Rows of 5..127 nonzeros: group g (16 lanes) takes the g-th pending row of the wave.
+  const int g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+  for (int k = 0; k < kRowsPerThread; ++k) {
+    uint64_t pending = __ballot(length[k] > kLaneRow && length[k] < kGroupRow);
+    while (pending != 0) {   // wave-uniform
+      uint64_t m = pending;
+      for (int q = 0; q < g; ++q) m &= m - 1;   // drop the g lowest pending rows
+      const bool has = m != 0;
+      const int from = has ? __builtin_ctzll(m) : lane;
+      const int32_t gb = __shfl(begin[k], from), ge = gb + __shfl(length[k], from);
+      float acc = 0.0f;
+      if (has) {   // at most 8 nonzeros per lane, all loads issued together
+        constexpr int kPer = kGroupRow / kGroup;
+        int32_t c[kPer];
+        float v[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+          const int32_t p = gb + l16 + kGroup * q;
+          c[q] = p < ge ? col[p] : 0;
+          v[q] = p < ge ? val[p] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < kPer; ++q)
+          if (gb + l16 + kGroup * q < ge) acc = fmaf(v[q], x[clamp_col(c[q], cols)], acc);
+      }
+      acc = group16_sum(acc);
+      if (has && l16 == 0) y[base + from + (threadIdx.x & ~63) + 256 * k] = acc;
+      for (int q = 0; q < 4 && pending != 0; ++q) pending &= pending - 1;   // four rows consumed
+    }
   }
 }
 
-// Row r owns the diagonals [off[r] + r, off[r+1] + r + 1): its nonzeros, then its end.
-// It records itself as the split of every workgroup boundary g * kBlockItems inside that range.
-// Workgroup 0 also clears the placement counters (a store, not a memset node, so the launch
-// sequence can be captured in a graph).
-__global__ __launch_bounds__(kThreads) void spmv_partition(const int32_t *__restrict__ off, int32_t rows,
-                                                           int32_t blocks, int32_t *__restrict__ splits,
-                                                           int32_t *__restrict__ counters) {
-  if (blockIdx.x == 0 && threadIdx.x < 64) counters[threadIdx.x] = 0;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (r > rows) return;
-  if (r == rows) {
-    splits[blocks] = rows;
+// Cuts of one row by a group of G lanes (gl: lane in the group, gbase: its first lane). Cut k
+// estimates the lower bound of column k * spacing among the row's columns (cut 0 is the row start;
+// a threshold at or past `cols` gives the row end) by interpolation search: at most kSearchSteps
+// probes, each placed where a uniform spread of the columns between the known bracket values
+// would put the threshold. That converges in a few steps on sorted columns. A prefix maximum over
+// the group then makes the cuts non-decreasing, so the pieces partition the row for any estimate
+// and any column order (an entry outside its window or slice only reads x from another place).
+// `rounds` (cuts per lane, rounded up) must be the same for every lane of the wave.
+template <int G>
+__device__ __forceinline__ void cut_row(const int32_t *__restrict__ col, int32_t begin, int32_t end, int n_cuts,
+                                        int rounds, int64_t spacing, int32_t cols, int gl, int gbase,
+                                        int32_t *__restrict__ out) {
+  int32_t carry = begin;   // running maximum of the cuts of earlier rounds
+  for (int u0 = 0; u0 < rounds; u0 += 4) {
+    int32_t lo[4], hi[4];
+    int64_t thr[4], vlo[4], vhi[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = gl + G * (u0 + u);
+      thr[u] = static_cast<int64_t>(k) * spacing;
+      lo[u] = begin;
+      hi[u] = end;
+      vlo[u] = -1;
+      vhi[u] = cols;
+      if (k == 0 || thr[u] >= cols) lo[u] = hi[u] = k == 0 ? begin : end;
+    }
+    for (int step = 0; step < kSearchSteps; ++step) {
+      int32_t at[4], cv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t span = hi[u] - lo[u] + 1, rise = vhi[u] - vlo[u];
+        int64_t guess = lo[u] - 1 + ((thr[u] - vlo[u]) * span + rise / 2) / (rise > 0 ? rise : 1);
+        guess = guess < lo[u] ? lo[u] : (guess > hi[u] - 1 ? hi[u] - 1 : guess);
+        at[u] = static_cast<int32_t>(guess);
+        cv[u] = lo[u] < hi[u] ? col[at[u]] : 0;
+      }
+      bool open = false;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (lo[u] < hi[u]) {
+          if (static_cast<int64_t>(cv[u]) < thr[u]) {
+            lo[u] = at[u] + 1;
+            vlo[u] = cv[u];
+          } else {
+            hi[u] = at[u];
+            vhi[u] = cv[u];
+          }
+        }
+        open |= lo[u] < hi[u];
+      }
+      if (!open) break;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      // Prefix maximum in cut order: lanes gl within this round, after the earlier rounds.
+      int32_t cut = lo[u] > carry ? lo[u] : carry;
+#pragma unroll
+      for (int d = 1; d < G; d <<= 1) {
+        const int32_t up = __shfl(cut, gbase + (gl >= d ? gl - d : gl), 64);
+        cut = up > cut ? up : cut;
+      }
+      const int k = gl + G * (u0 + u);
+      if (k < n_cuts) out[k] = cut;
+      carry = __shfl(cut, gbase + G - 1, 64);
+    }
+  }
+}
+
+// Cuts of the listed rows: one wave per large row (slices + 1 cuts), then one 16-lane group per
+// medium row (9 cuts: the starts of windows 0..8).
+__global__ __launch_bounds__(256) void spmv_bounds(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
+                                                   int32_t cols, int64_t nnz, Plan plan) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n_mid = min(plan.counters[0], plan.cap_mid), n_big = min(plan.counters[1], plan.cap_big);
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+  const int big_cuts = plan.slices + 1;
+  for (int64_t i = wave; i < n_big; i += waves) {   // wave-uniform
+    int32_t b, e;
+    row_span(off, plan.big_rows[i], nnz, b, e);
+    cut_row<64>(col, b, e, big_cuts, (big_cuts + 63) / 64, kSliceCols, cols, lane, 0, plan.big_cuts + i * big_cuts);
+  }
+  const int64_t window = (static_cast<int64_t>(cols) + kWindows - 1) / kWindows;
+  const int g = lane >> 4;
+  for (int64_t i0 = wave * 4; i0 < n_mid; i0 += waves * 4) {   // wave-uniform: four rows per wave
+    const int64_t i = i0 + g;
+    const bool ok = i < n_mid;
+    int32_t b = 0, e = 0;
+    if (ok) row_span(off, plan.mid_rows[i], nnz, b, e);
+    cut_row<16>(col, b, e, ok ? kWindows + 1 : 0, 1, window, cols, lane & 15, g * 16,
+                plan.mid_cuts + (ok ? i : 0) * (kWindows + 1));
+  }
+}
+
+// Pieces of listed rows for one part (a window of the medium rows, or a slice of the large rows),
+// run by a workgroup "tile" over the list rows i = k + K j. Per batch of up to 1024 rows the pieces
+// are laid end to end (prefix sums in LDS) and the 8 waves take equal ranges of that stream, 64
+// consecutive nonzeros per chunk and 8 chunks per step, so loads are coalesced and many are in
+// flight whatever the row structure. A wave-uniform cursor gives every lane its row: each step
+// reads the next 8 row starts once, and a lane counts the starts at or below its position. Each
+// lane accumulates the products of the wave's current row; a row's sum is one wave reduction when
+// the wave leaves the row. Sums of rows that end inside the wave's range are written at once; the
+// pieces of rows that cross a range boundary are added in wave order after the batch.
+// kLds: the slice's columns of x are staged in LDS (large rows); otherwise x is read from global
+// memory, and workgroup h runs on XCD h % 8, whose L2 holds window h % 8 (medium rows).
+constexpr int kTileThreads = 512;
+constexpr int kTileWaves = kTileThreads / 64;
+constexpr int kBatchRows = 1024;
+constexpr int kStep = 8;
+
+template <bool kLds>
+__global__ __launch_bounds__(kTileThreads, 2) void spmv_pieces(const int32_t *__restrict__ col,
+                                                               const float *__restrict__ val,
+                                                               const float *__restrict__ x, int32_t cols,
+                                                               const int32_t *__restrict__ cuts, int cut_stride,
+                                                               float *__restrict__ parts, int part_stride,
+                                                               const int32_t *__restrict__ count, int capacity) {
+  __shared__ float sx[kLds ? kSliceCols : 1];
+  __shared__ int32_t s_begin[kBatchRows + 1];
+  __shared__ int32_t s_pre[kBatchRows + 1];
+  __shared__ int32_t s_wave_total[kTileWaves];
+  __shared__ int32_t s_piece_row[kTileWaves][2];
+  __shared__ float s_piece_sum[kTileWaves][2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = kLds ? static_cast<int>(gridDim.x) / part_stride : static_cast<int>(gridDim.x) / kWindows;
+  const int part = kLds ? static_cast<int>(blockIdx.x) / K : static_cast<int>(blockIdx.x % kWindows);
+  const int k = kLds ? static_cast<int>(blockIdx.x) % K : static_cast<int>(blockIdx.x / kWindows);
+  const int n_rows = min(*count, capacity);
+  if (n_rows <= k) return;   // workgroup-uniform
+  const int64_t c0 = kLds ? static_cast<int64_t>(part) * kSliceCols : 0;
+  const int width = kLds ? static_cast<int>(min(static_cast<int64_t>(kSliceCols), cols - c0)) : 0;
+  if constexpr (kLds) {   // every load of the slice is issued before the first store to LDS
+    constexpr int kPer = kSliceCols / kTileThreads;
+    float staged[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int c = tid + kTileThreads * q;
+      staged[q] = c < width ? x[c0 + c] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) sx[tid + kTileThreads * q] = staged[q];
+  }
+  auto xval = [&](int32_t c) {
+    if constexpr (kLds) {
+      const int64_t local = static_cast<int64_t>(c) - c0;
+      if (static_cast<uint64_t>(local) < static_cast<uint64_t>(width)) return sx[local];
+    }
+    return x[clamp_col(c, cols)];
+  };
+  auto slot = [&](int64_t t) { return (k + static_cast<int64_t>(K) * t) * part_stride + part; };
+  const int n_tile = (n_rows - k + K - 1) / K;
+  for (int t0 = 0; t0 < n_tile; t0 += kBatchRows) {
+    const int nb = min(kBatchRows, n_tile - t0);
+    __syncthreads();   // the previous batch is done with the LDS arrays
+    // Piece lengths (two rows per thread) and their exclusive prefix sums.
+    int len2[2] = {0, 0};
+    int32_t cb[2], ce[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {   // both rows' cuts are loaded before either is used
+      const int j = 2 * tid + h;
+      const int64_t i = k + static_cast<int64_t>(K) * (t0 + min(j, nb - 1));
+      cb[h] = cuts[i * cut_stride + part];
+      ce[h] = cuts[i * cut_stride + part + 1];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * tid + h;
+      if (j < nb) {
+        s_begin[j] = cb[h];
+        len2[h] = ce[h] - cb[h];
+        if (ce[h] == cb[h]) parts[slot(t0 + j)] = 0.0f;   // an empty piece
+      }
+    }
+    int incl = len2[0] + len2[1];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int up = __shfl_up(incl, d);
+      incl += lane >= d ? up : 0;
+    }
+    if (lane == 63) s_wave_total[wave] = incl;
+    __syncthreads();
+    int wave_base = 0;
+    for (int w = 0; w < wave; ++w) wave_base += s_wave_total[w];
+    const int excl = wave_base + incl - len2[0] - len2[1];
+    if (2 * tid < nb) s_pre[2 * tid] = excl;
+    if (2 * tid + 1 < nb) s_pre[2 * tid + 1] = excl + len2[0];
+    if (tid == kTileThreads - 1) {
+      s_pre[nb] = wave_base + incl;   // the total
+      s_begin[nb] = 0;
+    }
+    if (lane < 2) s_piece_row[wave][lane] = -1;
+    __syncthreads();
+    const int total = s_pre[nb];
+    const int v0 = static_cast<int>(static_cast<int64_t>(total) * wave / kTileWaves);
+    const int v1 = static_cast<int>(static_cast<int64_t>(total) * (wave + 1) / kTileWaves);
+    if (v0 < v1) {   // wave-uniform
+      // The row holding v0: the last j with s_pre[j] <= v0 (skips empty pieces).
+      int lo = 0, hi = nb;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_pre[mid] <= v0) lo = mid;
+        else hi = mid - 1;
+      }
+      int cur = lo;     // wave-uniform: row of the running per-lane sums
+      int crow = lo;    // wave-uniform: row holding the first position of the step
+      float acc = 0.0f;
+      auto flush = [&](int j, float sum) {   // wave-uniform
+        const bool before = s_pre[j] < v0, after = s_pre[j + 1] > v1;
+        if (lane == 0) {
+          if (before || after) {
+            s_piece_row[wave][before ? 0 : 1] = j;
+            s_piece_sum[wave][before ? 0 : 1] = sum;
+          } else {
+            parts[slot(t0 + j)] = sum;
+          }
+        }
+      };
+      for (int vs = v0; vs < v1; vs += 64 * kStep) {
+        // Starts of rows crow + 1 .. crow + 8, and position-to-address offsets of rows crow .. crow + 8.
+        int32_t start[kStep], delta[kStep + 1];
+#pragma unroll
+        for (int m = 0; m <= kStep; ++m) {
+          const int j = crow + m;
+          delta[m] = j < nb ? __builtin_amdgcn_readfirstlane(s_begin[j] - s_pre[j]) : 0;
+          if (m > 0) start[m - 1] = j <= nb ? __builtin_amdgcn_readfirstlane(s_pre[j]) : INT32_MAX;
+        }
+        int rows_u[kStep];
+        int32_t cols_u[kStep];
+        float vals_u[kStep];
+#pragma unroll
+        for (int u = 0; u < kStep; ++u) {
+          const int v = vs + 64 * u + lane;
+          const bool ok = v < v1;
+          int m = 0;
+#pragma unroll
+          for (int q = 0; q < kStep; ++q) m += start[q] <= v ? 1 : 0;
+          int row = crow + m;
+          int32_t off;
+          if (m == kStep && ok) {   // more than eight rows begin in this step: walk on (rare)
+            while (s_pre[row + 1] <= v) ++row;
+            off = s_begin[row] - s_pre[row];
+          } else {
+            off = delta[0];
+#pragma unroll
+            for (int q = 1; q <= kStep; ++q) off = m == q ? delta[q] : off;
+          }
+          rows_u[u] = ok ? row : -1;
+          const int32_t p = ok ? v + off : 0;
+          cols_u[u] = ok ? __builtin_nontemporal_load(col + p) : 0;
+          vals_u[u] = ok ? __builtin_nontemporal_load(val + p) : 0.0f;
+        }
+        {   // the row holding the next step's first position
+          const int next = vs + 64 * kStep;
+          int m = 0;
+#pragma unroll
+          for (int q = 0; q < kStep; ++q) m += start[q] <= next ? 1 : 0;
+          crow += m;
+          if (m == kStep)
+            while (crow < nb && __builtin_amdgcn_readfirstlane(s_pre[crow + 1]) <= next) ++crow;
+        }
+#pragma unroll
+        for (int u = 0; u < kStep; ++u) {
+          if (vs + 64 * u >= v1) break;   // wave-uniform
+          const float prod = rows_u[u] >= 0 ? vals_u[u] * xval(cols_u[u]) : 0.0f;
+          const int first_row = __builtin_amdgcn_readfirstlane(rows_u[u]);
+          const int last_row = __builtin_amdgcn_readlane(rows_u[u], min(63, v1 - 1 - (vs + 64 * u)));
+          if (first_row == last_row) {   // the whole chunk in one row
+            if (first_row != cur) {
+              flush(cur, wave_sum(acc));
+              cur = first_row;
+              acc = 0.0f;
+            }
+            acc += prod;
+          } else {
+            for (int j = first_row; j <= last_row; ++j) {   // wave-uniform
+              const bool mine = rows_u[u] == j;
+              if (__ballot(mine) == 0) continue;
+              if (j != cur) {
+                flush(cur, wave_sum(acc));
+                cur = j;
+                acc = 0.0f;
+              }
+              acc += mine ? prod : 0.0f;
+            }
+          }
+        }
+      }
+      flush(cur, wave_sum(acc));
+    }
+    __syncthreads();
+    // Pieces of rows that cross a wave range boundary, added in wave order.
+    if (tid == 0) {
+      int run = -1;
+      float sum = 0.0f;
+      for (int w = 0; w < kTileWaves; ++w)
+        for (int h = 0; h < 2; ++h) {
+          const int j = s_piece_row[w][h];
+          if (j < 0) continue;
+          if (j == run) {
+            sum += s_piece_sum[w][h];
+          } else {
+            if (run >= 0) parts[slot(t0 + run)] = sum;
+            run = j;
+            sum = s_piece_sum[w][h];
+          }
+        }
+      if (run >= 0) parts[slot(t0 + run)] = sum;
+    }
+  }
+}
+
+// y of every medium row (thread per row: windows 0..7 in order) and large row (wave per row: lane
+// l sums slices l, l + 64, ... in order, then a fixed reduction tree).
+__global__ __launch_bounds__(256) void spmv_combine(float *__restrict__ y, Plan plan) {
+  const int64_t n_mid = min(plan.counters[0], plan.cap_mid), n_big = min(plan.counters[1], plan.cap_big);
+  const int half = gridDim.x / 2;
+  if (static_cast<int>(blockIdx.x) < half) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n_mid;
+         i += static_cast<int64_t>(half) * 256) {
+      const float4 a = *reinterpret_cast<const float4 *>(plan.mid_parts + i * kWindows);
+      const float4 b = *reinterpret_cast<const float4 *>(plan.mid_parts + i * kWindows + 4);
+      y[plan.mid_rows[i]] = ((((((a.x + a.y) + a.z) + a.w) + b.x) + b.y) + b.z) + b.w;
+    }
     return;
   }
-  const int64_t begin = static_cast<int64_t>(off[r]) + r;
-  const int64_t end = static_cast<int64_t>(off[r + 1]) + r + 1;
-  int64_t g = (begin + kBlockItems - 1) / kBlockItems;
-  int64_t last = (end - 1) / kBlockItems;
-  if (g < 0) g = 0;
-  if (last > blocks - 1) last = blocks - 1;
-  for (; g <= last; ++g) splits[g] = static_cast<int32_t>(r);
-}
-
-__global__ __launch_bounds__(kThreads) void spmv_merge(const int32_t *__restrict__ off,
-                                                       const int32_t *__restrict__ col,
-                                                       const float *__restrict__ val,
-                                                       const float *__restrict__ x, float *__restrict__ y,
-                                                       int32_t rows, int32_t cols, int64_t total,
-                                                       Workspace ws) {
-  __shared__ int32_t s_end[kBlockItems + 1];  // row ends of this workgroup, relative to y0
-  __shared__ float s_prod[kBlockItems];       // values * x[col] of this workgroup's nonzeros
-  __shared__ int32_t s_key[kThreads];
-  __shared__ float s_val[kThreads];
-
-  const int t = threadIdx.x;
-  const int32_t placed = ws.perm[blockIdx.x];  // a permutation of [0, gridDim.x) by construction
-  const int64_t g = placed < 0 ? 0 : (placed >= static_cast<int32_t>(gridDim.x) ? gridDim.x - 1 : placed);
-  const int64_t d0 = g * kBlockItems;
-  const int64_t d1 = d0 + kBlockItems < total ? d0 + kBlockItems : total;
-  const int32_t x0 = ws.splits[g];
-  const int32_t x1 = ws.splits[g + 1];
-  const int64_t y0 = d0 - x0;
-  // Row ends completed inside this workgroup (local rows 0..n_ends-1) and nonzeros.
-  int32_t n_ends = x1 - x0;
-  int32_t n_nz = static_cast<int32_t>((d1 - x1) - y0);
-  // Defensive clamps: valid CSR input always satisfies them.
-  n_ends = n_ends < 0 ? 0 : (n_ends > kBlockItems ? kBlockItems : n_ends);
-  n_nz = n_nz < 0 ? 0 : (n_nz > kBlockItems ? kBlockItems : n_nz);
-
-  for (int i = t; i < n_ends; i += kThreads) s_end[i] = static_cast<int32_t>(off[x0 + i + 1] - y0);
-  {
-    int32_t c[kItems];
-    float v[kItems];
-#pragma unroll
-    for (int k = 0; k < kItems; ++k) {
-      const int i = t + k * kThreads;
-      const bool live = i < n_nz;
-      c[k] = live ? __builtin_nontemporal_load(col + y0 + i) : 0;
-      v[k] = live ? __builtin_nontemporal_load(val + y0 + i) : 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < kItems; ++k) {
-      const int i = t + k * kThreads;
-      if (i < n_nz) {
-        const uint32_t column = static_cast<uint32_t>(c[k]) < static_cast<uint32_t>(cols) ? c[k] : cols - 1;
-        s_prod[i] = __fmul_rn(v[k], x[column]);
-      }
-    }
-  }
-  __syncthreads();
-
-  // This thread's local diagonal range and its starting merge coordinate.
-  const int32_t items = n_ends + n_nz;
-  const int32_t dt = t * kItems < items ? t * kItems : items;
-  const int32_t dt_end = dt + kItems < items ? dt + kItems : items;
-  int32_t lo = dt - n_nz > 0 ? dt - n_nz : 0;
-  int32_t hi = dt < n_ends ? dt : n_ends;
-  while (lo < hi) {
-    const int32_t mid = (lo + hi) >> 1;
-    if (s_end[mid] <= dt - mid - 1) lo = mid + 1;
-    else hi = mid;
-  }
-  int32_t xt = lo;
-  int32_t yt = dt - lo;
-
-  float acc = 0.0f;
-  float head = 0.0f;
-  int32_t head_row = -1;
-  for (int32_t d = dt; d < dt_end; ++d) {
-    if (xt < n_ends && s_end[xt] <= yt) {
-      if (head_row < 0) {
-        head_row = xt;
-        head = acc;
-      } else {
-        y[x0 + xt] = acc;
-      }
-      acc = 0.0f;
-      ++xt;
-    } else if (yt < n_nz) {
-      acc = __fadd_rn(acc, s_prod[yt]);
-      ++yt;
-    }
-  }
-
-  // Segmented inclusive scan of the open-row partials (keys are non-decreasing).
-  s_key[t] = xt;
-  s_val[t] = acc;
-  float scanned = acc;
-  for (int offset = 1; offset < kThreads; offset <<= 1) {
-    __syncthreads();
-    const float add = (t >= offset && s_key[t - offset] == xt) ? s_val[t - offset] : 0.0f;
-    __syncthreads();
-    scanned = __fadd_rn(scanned, add);
-    s_val[t] = scanned;
-  }
-  __syncthreads();
-  if (head_row >= 0) {
-    const float carry = t > 0 ? s_val[t - 1] : 0.0f;
-    y[x0 + head_row] = __fadd_rn(carry, head);
-  }
-  if (t == kThreads - 1) {
-    const int64_t open_row = static_cast<int64_t>(x0) + xt;
-    ws.carry_rows[g] = open_row < rows ? static_cast<int32_t>(open_row) : -1;
-    ws.carry_values[g] = scanned;
+  const int lane = threadIdx.x & 63;
+  const int S = plan.slices;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x - half) * 4 + (threadIdx.x >> 6); i < n_big;
+       i += static_cast<int64_t>(half) * 4) {   // uniform within a wave
+    float acc = 0.0f;
+    for (int s = lane; s < S; s += 64) acc += plan.big_parts[i * S + s];
+    const float sum = wave_sum(acc);
+    if (lane == 0) y[plan.big_rows[i]] = sum;
   }
 }
-
-__global__ __launch_bounds__(kThreads) void spmv_fixup(float *__restrict__ y, int32_t blocks, Workspace ws) {
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (g >= blocks) return;
-  const int32_t r = ws.carry_rows[g];
-  if (r < 0 || (g > 0 && ws.carry_rows[g - 1] == r)) return;
-  float sum = ws.carry_values[g];
-  for (int64_t h = g + 1; h < blocks && ws.carry_rows[h] == r; ++h) sum = __fadd_rn(sum, ws.carry_values[h]);
-  y[r] = __fadd_rn(sum, y[r]);
-}
-
-int64_t block_count(int64_t rows, int64_t nnz) { return (rows + nnz + kBlockItems - 1) / kBlockItems; }
 
 }  // namespace
 
 int spmv_resources(int64_t rows, int64_t nnz, IntentHipKernelResources *out) {
   (void)rows;
   (void)nnz;
-  return describe_kernel(reinterpret_cast<const void *>(&spmv_merge), "spmv_merge", kThreads, out);
+  return describe_kernel(reinterpret_cast<const void *>(&spmv_pieces<true>), "spmv_pieces<true>", kTileThreads, out);
 }
 
 }  // namespace intent_hip
@@ -286,7 +665,7 @@ using namespace intent_hip;
 extern "C" int intent_hip_csr_spmv_workspace_bytes(int64_t rows, int64_t nnz, size_t *bytes) {
   if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
   if (rows < 0 || nnz < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
-  *bytes = workspace_bytes(block_count(rows, nnz));
+  *bytes = workspace_bytes(rows, nnz);
   return INTENT_HIP_OK;
 }
 
@@ -295,31 +674,36 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
                                        int64_t cols, int64_t nnz, void *workspace, size_t workspace_size,
                                        void *stream) {
   if (rows < 0 || cols < 0 || nnz < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
-  if (rows + nnz > INT32_MAX)
-    return fail(INTENT_HIP_ERR_UNSUPPORTED, "rows + nnz must stay below 2^31 (32-bit CSR indices)");
+  if (rows + nnz > INT32_MAX || cols > INT32_MAX)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "rows + nnz and cols must stay below 2^31 (32-bit CSR indices)");
   if (rows == 0) return INTENT_HIP_OK;
   if (nnz > 0 && cols == 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "nonzeros in a matrix with no columns");
   if (row_offsets == nullptr || y == nullptr || (nnz > 0 && (column_indices == nullptr || values == nullptr || x == nullptr)))
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null tensor pointer");
-  const int64_t blocks = block_count(rows, nnz);
-  if (workspace == nullptr || workspace_size < workspace_bytes(blocks))
-    return fail(INTENT_HIP_ERR_WORKSPACE, "SpMV needs %zu workspace bytes, got %zu", workspace_bytes(blocks),
-                workspace_size);
-  const Workspace ws = carve(workspace, blocks);
+  if (workspace == nullptr || workspace_size < workspace_bytes(rows, nnz) || !aligned(workspace, 256))
+    return fail(INTENT_HIP_ERR_WORKSPACE, "SpMV needs %zu workspace bytes (256-byte aligned), got %zu",
+                workspace_bytes(rows, nnz), workspace_size);
+  const Plan plan = carve(workspace, rows, cols, nnz);
   const hipStream_t s = as_stream(stream);
-  const int32_t r32 = static_cast<int32_t>(rows), b32 = static_cast<int32_t>(blocks);
-  const int32_t c32 = cols > INT32_MAX ? INT32_MAX : static_cast<int32_t>(cols);
-  const int64_t total = rows + nnz;
-  spmv_partition<<<dim3(static_cast<unsigned>((rows + 1 + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(
-      row_offsets, r32, b32, ws.splits, ws.counters);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_partition");
-  spmv_place<<<dim3(static_cast<unsigned>((blocks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(
-      column_indices, c32 > 0 ? c32 : 1, b32, total, nnz, ws);
-  spmv_place_fill<<<dim3(static_cast<unsigned>((blocks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(b32, ws);
-  spmv_merge<<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s>>>(row_offsets, column_indices, values, x,
-                                                                             y, r32, c32, total, ws);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_merge");
-  spmv_fixup<<<dim3(static_cast<unsigned>((blocks + kThreads - 1) / kThreads)), dim3(kThreads), 0, s>>>(y, b32, ws);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_fixup");
+  const int32_t r32 = static_cast<int32_t>(rows), c32 = static_cast<int32_t>(cols > 0 ? cols : 1);
+  const dim3 row_grid(static_cast<unsigned>(plan.blocks));
+  spmv_count<<<row_grid, dim3(256), 0, s>>>(row_offsets, r32, nnz, plan);
+  spmv_scan<<<1, 1024, 0, s>>>(plan);
+  spmv_rows<<<row_grid, dim3(256), 0, s>>>(row_offsets, column_indices, values, x, y, r32, c32, nnz, plan);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_rows");
+  if (plan.cap_mid == 0 && plan.cap_big == 0) return INTENT_HIP_OK;   // no row can be medium or large
+  spmv_bounds<<<dim3(1024), dim3(256), 0, s>>>(row_offsets, column_indices, c32, nnz, plan);
+  if (plan.cap_mid > 0)
+    spmv_pieces<false><<<dim3(kWindows * kWindowTiles), dim3(kTileThreads), 0, s>>>(
+        column_indices, values, x, c32, plan.mid_cuts, kWindows + 1, plan.mid_parts, kWindows, plan.counters + 0,
+        plan.cap_mid);
+  if (plan.cap_big > 0) {
+    const int K = static_cast<int>((kTargetTiles + plan.slices - 1) / plan.slices);
+    spmv_pieces<true><<<dim3(static_cast<unsigned>(plan.slices) * static_cast<unsigned>(K)), dim3(kTileThreads), 0,
+                        s>>>(column_indices, values, x, c32, plan.big_cuts, plan.slices + 1, plan.big_parts,
+                             plan.slices, plan.counters + 1, plan.cap_big);
+  }
+  spmv_combine<<<dim3(128), dim3(256), 0, s>>>(y, plan);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_combine");
   return INTENT_HIP_OK;
 }

@@ -1,10 +1,11 @@
-"""GPU parity of the CSR SpMV kernel.
+"""GPU parity of the CSR SpMV kernels.
 
 Bars: index traversal bit-exact (probes with ones, one-hot x and small integers give
-exact results in any summation order); rows folded by one thread equal the oracle's
-strict left fold bit for bit (every length-1 row, always); all rows within the
-backward-error bound |y - y64| <= 1e-5 * sum|a_i x_i| against float64, and within
-(1e-5 + 2 (L-1) 2^-24) * sum|a_i x_i| against the oracle."""
+exact results in any summation order); rows folded by one lane (up to 4 nonzeros) equal the
+oracle's strict left fold bit for bit; all rows within the backward-error bound
+|y - y64| <= 1e-5 * sum|a_i x_i| against float64, and within (1e-5 + 2 (L-1) 2^-24) *
+sum|a_i x_i| against the oracle. The cases reach every row class: one lane, 16-lane groups,
+medium rows cut at 8 column windows, and large rows cut at 16384-column slices (x in LDS)."""
 import numpy as np
 import pytest
 import torch
@@ -24,15 +25,18 @@ def run(device, offsets, columns, values, x):
 
 
 def reference64(offsets, columns, values, x):
+    """float64 row sums and magnitudes over each row's absolute range [off[r], off[r+1])."""
     rows = offsets.shape[0] - 1
-    lengths = np.diff(offsets.astype(np.int64))
+    starts, ends = offsets[:-1].astype(np.int64), offsets[1:].astype(np.int64)
+    lengths = ends - starts
     products = values.astype(np.float64) * x[columns].astype(np.float64)
     y64, mag = np.zeros(rows), np.zeros(rows)
     nonempty = lengths > 0
-    starts = offsets[:-1].astype(np.int64)[nonempty]
-    if products.size:
-        y64[nonempty] = np.add.reduceat(products, starts)
-        mag[nonempty] = np.add.reduceat(np.abs(products), starts)
+    if nonempty.any():
+        padded = np.concatenate((products, [0.0]))      # an end index may equal the array length
+        cuts = np.stack((starts[nonempty], ends[nonempty]), axis=1).ravel()
+        y64[nonempty] = np.add.reduceat(padded, cuts)[::2]
+        mag[nonempty] = np.add.reduceat(np.abs(padded), cuts)[::2]
     return y64, mag, lengths
 
 
@@ -43,8 +47,8 @@ def check(device, offsets, columns, values, x):
     assert np.all(np.abs(y - y64) <= 1e-5 * mag + 1e-38), "backward error vs float64"
     bound = (1e-5 + 2 * np.maximum(lengths - 1, 0) * 2.0 ** -24) * mag + 1e-38
     assert np.all(np.abs(y.astype(np.float64) - want) <= bound), "vs oracle"
-    single = lengths == 1
-    assert (y[single] == want[single]).all(), "length-1 rows must be bit-exact"
+    lane_rows = lengths <= 4
+    assert (y[lane_rows] == want[lane_rows]).all(), "rows of up to 4 nonzeros must be bit-exact"
     assert (y[lengths == 0] == 0).all()
     return y, want
 
@@ -141,3 +145,54 @@ def test_spmv_shape_errors(device):
         out = torch.empty(3, device=device)
         kernel(t(np.array([0, 1], np.int32)), t(np.array([0], np.int32)), t(np.zeros(1, np.float32)),
                t(np.zeros(2, np.float32)), out)
+
+
+def test_spmv_offsets_inside_larger_arrays(device):
+    """Row offsets that start above 0 and end below the length of the column and value arrays (a
+    row slice of a larger CSR): rows read their absolute ranges, nothing outside is touched."""
+    announce("spmv offsets inside larger arrays")
+    rng = np.random.default_rng(11)
+    for first, lengths in ((3000, [1, 1]), (0, [1, 0, 0]), (777, [5, 0, 300, 9, 2000, 1, 40])):
+        nnz = first + int(np.sum(lengths)) + 1234
+        offsets = (first + np.concatenate(([0], np.cumsum(lengths)))).astype(np.int32)
+        columns = rng.integers(0, 6000, nnz).astype(np.int32)
+        values = inputs.uniform(rng, nnz, -1, 1)
+        x = inputs.uniform(rng, 6000, -1, 1)
+        check(device, offsets, columns, values, x)
+
+
+@pytest.mark.parametrize("sort", [True, False])
+def test_spmv_medium_and_large_rows(device, sort):
+    """300000 columns give 19 slices, so rows of 128..303 nonzeros are medium (cut at 8 column
+    windows) and longer rows large (cut at slices); with unsorted columns the cuts still partition
+    each row and entries outside their window or slice read x from global memory."""
+    announce("spmv medium and large rows", sort)
+    rng = np.random.default_rng(21 + sort)
+    cols = 300_000
+    lengths = np.concatenate((rng.integers(128, 304, 3000), rng.integers(304, 20000, 300), rng.integers(0, 128, 3000),
+                              [127, 128, 303, 304, 0, 1, 8, 9]))
+    rng.shuffle(lengths)
+    offsets, columns = inputs.csr_matrix(rng, lengths, cols)
+    if not sort:
+        for r in np.nonzero(lengths >= 128)[0]:
+            rng.shuffle(columns[offsets[r]:offsets[r + 1]])
+    values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
+    x = inputs.uniform(rng, cols, -1, 1)
+    check(device, offsets, columns, values, x)
+    ival = rng.integers(-3, 4, values.shape).astype(np.float32)
+    ix = rng.integers(-3, 4, x.shape).astype(np.float32)
+    assert (run(device, offsets, columns, ival, ix) == oracle.csr_spmv(offsets, columns, ival, ix)).all()
+
+
+def test_spmv_large_rows_over_several_batches(device):
+    """More than 1024 large rows per slice workgroup (16.8M columns give 1025 slices, one workgroup
+    per slice): the slice kernel walks its rows in several LDS batches."""
+    announce("spmv large rows over several batches")
+    rng = np.random.default_rng(31)
+    cols = 1025 * 16384
+    lengths = np.full(1300, 16400, np.int64)
+    lengths[::13] = 0                                   # 1200 large rows, and empty ones among them
+    offsets, columns = inputs.csr_matrix(rng, lengths, cols)
+    values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
+    x = inputs.uniform(rng, cols, -1, 1)
+    check(device, offsets, columns, values, x)

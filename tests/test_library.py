@@ -45,6 +45,10 @@ def test_argument_validation_without_gpu():
     assert lib.fn["softmax_fwd"](0, None, None, 0, 4, 4, 4, None) == 0
     size = ctypes.c_size_t(0)
     assert lib.fn["csr_spmv_workspace_bytes"](4_194_304, 67_108_855, ctypes.byref(size)) == 0
-    assert 0 < size.value < 1 << 20
+    # worst case (every nonzero in rows of 128 or in large rows): about 1.13 bytes per nonzero
+    assert 0 < size.value <= 1.13 * 67_108_855 + 4096
+    small = ctypes.c_size_t(0)
+    assert lib.fn["csr_spmv_workspace_bytes"](1000, 127, ctypes.byref(small)) == 0
+    assert small.value <= 4096                      # no row can be medium or large
     assert lib.fn["csr_spmv_f32"](1, 1, 1, 1, 1, 10, 10, 10, None, 0, None) == 5
     assert lib.fn["csr_spmv_f32"](1, 1, 1, 1, 1, 2**31 - 5, 10, 10, 1, 1 << 30, None) == 2
