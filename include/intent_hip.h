@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 7
+#define INTENT_HIP_ABI_VERSION 8
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -266,6 +266,18 @@ int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t *column_in
                             const float *values, const float *x, float *y, int64_t rows,
                             int64_t cols, int64_t nnz, void *workspace, size_t workspace_bytes,
                             void *stream);
+
+/* CSR SpMV with no workspace argument and no allocation: the workspace is a static device array of
+ * INTENT_HIP_STATIC_SCRATCH_BYTES inside the library (one per GPU, held until the process ends).
+ * No counterpart in the reference; it is for callers that cannot allocate device memory (code
+ * under graph capture, serving loops, harnesses that forbid hipMalloc). Same results as
+ * intent_hip_csr_spmv_f32 (the same kernels). Returns INTENT_HIP_ERR_WORKSPACE when
+ * intent_hip_csr_spmv_workspace_bytes(rows, nnz) exceeds the static array. Unlike the other entry
+ * points it is not stateless: calls that overlap on one GPU share the array and race. */
+#define INTENT_HIP_STATIC_SCRATCH_BYTES (32u << 20)
+int intent_hip_csr_spmv_f32_static(const int32_t *row_offsets, const int32_t *column_indices,
+                                   const float *values, const float *x, float *y, int64_t rows,
+                                   int64_t cols, int64_t nnz, void *stream);
 
 /* CSR SpMM out = A dense, f32 values and features, i32 indices.
  * csr_spmm (python/intent/examples/kernels/sparse/csr_spmm.py:11-33), with dynamic extents:

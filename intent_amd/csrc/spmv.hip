@@ -28,6 +28,8 @@
 // makes the cuts of a row non-decreasing with a prefix maximum, so the pieces partition the row
 // for any estimate and any column order; an entry outside its window or slice only reads x from
 // another place. spmv_combine adds the pieces of each medium or large row in window or slice order.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace intent_hip {
@@ -706,4 +708,65 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   spmv_combine<<<dim3(128), dim3(256), 0, s>>>(y, plan);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_combine");
   return INTENT_HIP_OK;
+}
+
+// ---------------------------------------------------------------- no-allocation entry point
+// For callers that cannot allocate (code under graph capture, serving loops, harnesses that forbid
+// hipMalloc): the workspace is a static device array, `scratch`, of INTENT_HIP_STATIC_SCRATCH_BYTES.
+// Each GPU the library runs on holds its own copy until the process ends; its address on the
+// current device is looked up once (hipGetSymbolAddress) and kept per device. Every call on a GPU
+// shares that GPU's array, so calls that overlap on one GPU race. Nothing in it has to start at
+// zero: every kernel writes what a later kernel of the same call reads.
+namespace intent_hip {
+
+static __device__ __align__(256) char scratch[INTENT_HIP_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch_address[kMaxDevices] = {};
+
+// The current device's address of `scratch` (the host-side name of the array is not a device
+// address and is never passed to a kernel).
+int scratch_address(void **out) {
+  int device = -1;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess) return fail(INTENT_HIP_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(status));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "device %d is beyond the %d devices the static scratch tracks", device,
+                kMaxDevices);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_address[device] == nullptr) {
+    void *address = nullptr;
+    status = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (status != hipSuccess || address == nullptr)
+      return fail(INTENT_HIP_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                  hipGetErrorString(status));
+    g_scratch_address[device] = address;
+  }
+  *out = g_scratch_address[device];
+  return INTENT_HIP_OK;
+}
+
+}  // namespace
+}  // namespace intent_hip
+
+extern "C" int intent_hip_csr_spmv_f32_static(const int32_t *row_offsets, const int32_t *column_indices,
+                                              const float *values, const float *x, float *y, int64_t rows,
+                                              int64_t cols, int64_t nnz, void *stream) {
+  if (rows < 0 || cols < 0 || nnz < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (rows + nnz > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "rows + nnz must stay below 2^31");
+  const size_t need = workspace_bytes(rows, nnz);
+  if (need > INTENT_HIP_STATIC_SCRATCH_BYTES)
+    return fail(INTENT_HIP_ERR_WORKSPACE,
+                "SpMV of %lld rows and %lld nonzeros needs %zu workspace bytes, beyond the %zu-byte static scratch; "
+                "use intent_hip_csr_spmv_f32 with a caller-owned workspace",
+                static_cast<long long>(rows), static_cast<long long>(nnz), need,
+                static_cast<size_t>(INTENT_HIP_STATIC_SCRATCH_BYTES));
+  if (rows == 0) return INTENT_HIP_OK;
+  void *address = nullptr;
+  if (const int rc = scratch_address(&address)) return rc;
+  return intent_hip_csr_spmv_f32(row_offsets, column_indices, values, x, y, rows, cols, nnz, address,
+                                 INTENT_HIP_STATIC_SCRATCH_BYTES, stream);
 }

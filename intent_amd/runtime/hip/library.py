@@ -11,7 +11,7 @@ from pathlib import Path
 
 from ...diagnostics import CompilationStageError
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 LIBRARY_NAME = "libintent_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parents[2] / LIBRARY_NAME
 
@@ -74,6 +74,7 @@ SIGNATURES = {
                                                 ctypes.POINTER(_i64), _f32, _int, _p, _sz, _p)),
     "intent_hip_csr_spmv_workspace_bytes": (_int, (_i64, _i64, ctypes.POINTER(_sz))),
     "intent_hip_csr_spmv_f32": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p)),
+    "intent_hip_csr_spmv_f32_static": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _p)),
     "intent_hip_csr_spmm_f32": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p)),
 }
 
