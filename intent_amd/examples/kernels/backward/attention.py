@@ -1,14 +1,26 @@
-"""Attention backward definitions (interface and semantics of the reference's
-`python/intent/examples/kernels/backward/attention.py:17-211`): delta, dK/dV and dQ of a
-grouped-query attention with f16 storage and f32 arithmetic.
+"""Attention backward definitions: attention_backward_delta, attention_backward_dkdv and
+attention_backward_dq, for grouped-query attention with f16 storage and f32 arithmetic. Names,
+signatures and example extents are the reference's
+(`python/intent/examples/kernels/backward/attention.py:17-211`).
 
-  delta[b,h,q] = sum_d o * do
-  p  = exp2(s * scale * log2(e) - lse * log2(e)), s = q . k  (approximate, flush-to-zero),
-       lse the natural log of the forward's softmax denominator; causal pairs need q >= k
-  dv = sum_q f16(p) * do;  dp = do . v;  ds = p * (dp - delta)
-  dk = scale * sum_q f16(ds) * q;  dq = scale * sum_k f16(ds) * k
-Causally excluded pairs contribute nothing, even with non-finite operands; the summed axes are
-region folds combined by addition. Key head of query head h: h // HEAD_GROUP.
+For query head h (key head h // HEAD_GROUP), query row i and key row j:
+
+  delta_i  = sum_d f32(out_id) * f32(dout_id)
+  taken    = every pair, or with CAUSAL the pairs j <= i
+  P_ij     = exp2(s_ij * scale * log2(e) - lse_i * log2(e)) with s_ij = q_i . k_j
+             (approximate exp2, subnormals flushed); lse is the natural log of the forward's
+             softmax denominator
+  dS_ij    = P_ij * (dout_i . v_j - delta_i)
+  dQ_i     = scale * sum_j f16(dS_ij) k_j
+  dK_j     = scale * sum_(h, i) f16(dS_ij) q_i,   dV_j = sum_(h, i) f16(P_ij) dout_i
+
+The (h, i) sums run over every query row of the HEAD_GROUP query heads that share key j's head.
+Every sum includes only the pairs that are taken. A pair that is not taken adds nothing, even when a row it would
+touch holds inf or NaN (a zero weight times inf would give NaN). All sums are f32. The kernels add
+in their own order, so results match any order of the same sum to f32 rounding.
+
+The bodies state this one head at a time. The hip provider recognises a definition by name and
+signature and runs its own kernels.
 """
 import math
 
@@ -24,50 +36,41 @@ HEAD_DIMENSION = 64
 SCALE = 1.0 / math.sqrt(HEAD_DIMENSION)
 
 
+@intent.fn
+def taken_pairs(query_count, key_count, causal):
+    rows, cols = I.indices(I.domain(0, query_count)), I.indices(I.domain(0, key_count))
+    if causal:
+        return rows[:, None] >= cols[None, :]
+    return I.full((query_count, key_count), fill=True, dtype=I.bool)
+
+
+@intent.fn
+def pair_weights(q_rows, k_rows, lse_rows, scale, taken):
+    """P of one query head against one key head, 0 on pairs that are not taken."""
+    s = I.matmul(q_rows, k_rows, transpose_rhs=True, acc_dtype=I.f32)
+    return I.select(taken, I.exp2(s * (scale * I.LOG2E) - lse_rows[:, None] * I.LOG2E, approximate=True,
+                                  flush_to_zero=True), 0.0)
+
+
+@intent.fn
+def taken_sum(weights, rows, taken):
+    """out[a, :] = sum over b with taken[a, b] of f32(weights[a, b]) * f32(rows[b, :]).
+    A pair that is not taken is left out of the sum, not multiplied by zero."""
+    terms = I.cast(weights, I.f32)[:, :, None] * I.cast(rows, I.f32)[None, :, :]
+    return I.reduce.sum(I.select(taken[:, :, None], terms, 0.0), axis=1)
+
+
 @intent.kernel
 def attention_backward_delta(
     output: I.In[I.f16, ("B", "HQ", "Q", "D")],
     grad_output: I.In[I.f16, ("B", "HQ", "Q", "D")],
     delta: I.Out[I.f32, ("B", "HQ", "Q")],
 ):
-    B, HQ, Q, _ = output.shape
-    rows = I.domain(0, Q)
-    for batch in I.parallel(I.domain(0, B)):
-        for head in I.parallel(I.domain(0, HQ)):
-            delta[batch, head, rows] = I.reduce.sum(
-                I.cast(output[batch, head, rows, :], I.f32) * I.cast(grad_output[batch, head, rows, :], I.f32),
-                axis=1)
-
-
-@intent.fn
-def masked_gradient_product(weights, operands, valid):
-    products = I.cast(weights, I.f32)[:, :, None] * I.cast(operands, I.f32)[None, :, :]
-    return I.reduce.sum(I.mask(products, valid=valid[:, :, None], fill=0.0), axis=1)
-
-
-@intent.fn
-def summarize_key_value_gradients(queries, grad_outputs, lse, delta, query_coordinates,
-                                  keys, values, key_coordinates, scale, causal):
-    scores = I.matmul(keys, queries, transpose_rhs=True, acc_dtype=I.f32)
-    weights = I.exp2(scores * (scale * I.LOG2E) - lse[None, :] * I.LOG2E, approximate=True, flush_to_zero=True)
-    if causal:
-        valid = key_coordinates[:, None] <= query_coordinates[None, :]
-        weights = I.mask(weights, valid=valid, fill=0.0)
-        grad_values = masked_gradient_product(I.cast(weights, I.f16), grad_outputs, valid)
-    else:
-        grad_values = I.matmul(I.cast(weights, I.f16), grad_outputs, acc_dtype=I.f32)
-    grad_weights = I.matmul(values, grad_outputs, transpose_rhs=True, acc_dtype=I.f32)
-    grad_scores = weights * (grad_weights - delta[None, :])
-    if causal:
-        grad_keys = masked_gradient_product(I.cast(grad_scores, I.f16), queries, valid)
-    else:
-        grad_keys = I.matmul(I.cast(grad_scores, I.f16), queries, acc_dtype=I.f32)
-    return I.record(grad_k=grad_keys, grad_v=grad_values)
-
-
-@intent.fn
-def merge_key_value_gradients(lhs, rhs):
-    return I.record(grad_k=lhs.grad_k + rhs.grad_k, grad_v=lhs.grad_v + rhs.grad_v)
+    B, HQ = output.shape[0], output.shape[1]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, HQ)):
+            delta[b, h, :] = I.reduce.sum(I.cast(output[b, h, :, :], I.f32) * I.cast(grad_output[b, h, :, :], I.f32),
+                                          axis=1)
 
 
 @intent.kernel
@@ -84,46 +87,22 @@ def attention_backward_dkdv(
     HEAD_GROUP: I.Constexpr[int],
     CAUSAL: I.Constexpr[bool],
 ):
-    B, HQ, Q, D = q.shape
-    _, HK, K, _ = k.shape
-    keys = I.domain(0, K)
-    group = I.domain(0, HEAD_GROUP * Q)
-    for batch in I.parallel(I.domain(0, B)):
-        for key_head in I.parallel(I.domain(0, HK)):
-            member = I.indices(group)
-            heads = key_head * HEAD_GROUP + member // Q
-            rows = member % Q
-            summary = I.region_fold(
-                source=(q[batch, heads, rows, :], grad_output[batch, heads, rows, :], lse[batch, heads, rows],
-                        delta[batch, heads, rows], rows),
-                axis=0,
-                summarize=summarize_key_value_gradients,
-                combine=merge_key_value_gradients,
-                identity=I.record(grad_k=I.zeros((K, D), dtype=I.f32), grad_v=I.zeros((K, D), dtype=I.f32)),
-                operands=(k[batch, key_head, keys, :], v[batch, key_head, keys, :], I.indices(keys), scale, CAUSAL),
-            )
-            grad_k[batch, key_head, keys, :] = I.cast(summary.grad_k * scale, I.f16)
-            grad_v[batch, key_head, keys, :] = I.cast(summary.grad_v, I.f16)
-
-
-@intent.fn
-def summarize_query_gradients(keys, values, key_coordinates, queries, grad_outputs, lse, delta,
-                              query_coordinates, scale, causal):
-    scores = I.matmul(queries, keys, transpose_rhs=True, acc_dtype=I.f32)
-    weights = I.exp2(scores * (scale * I.LOG2E) - lse[:, None] * I.LOG2E, approximate=True, flush_to_zero=True)
-    if causal:
-        valid = query_coordinates[:, None] >= key_coordinates[None, :]
-        weights = I.mask(weights, valid=valid, fill=0.0)
-    grad_weights = I.matmul(grad_outputs, values, transpose_rhs=True, acc_dtype=I.f32)
-    grad_scores = weights * (grad_weights - delta[:, None])
-    if causal:
-        return masked_gradient_product(I.cast(grad_scores, I.f16), keys, valid)
-    return I.matmul(I.cast(grad_scores, I.f16), keys, acc_dtype=I.f32)
-
-
-@intent.fn
-def merge_query_gradients(lhs, rhs):
-    return lhs + rhs
+    B, Q, D = q.shape[0], q.shape[2], q.shape[3]
+    HK, K = k.shape[1], k.shape[2]
+    taken = taken_pairs(Q, K, CAUSAL)                                     # [Q, K]
+    for b in I.parallel(I.domain(0, B)):
+        for kv in I.parallel(I.domain(0, HK)):
+            keys, values = k[b, kv, :, :], v[b, kv, :, :]
+            dk, dv = I.zeros((K, D), dtype=I.f32), I.zeros((K, D), dtype=I.f32)
+            for member in range(HEAD_GROUP):
+                h = kv * HEAD_GROUP + member
+                queries, upstream = q[b, h, :, :], grad_output[b, h, :, :]
+                p = pair_weights(queries, keys, lse[b, h, :], scale, taken)                 # [Q, K]
+                ds = p * (I.matmul(upstream, values, transpose_rhs=True, acc_dtype=I.f32) - delta[b, h, :][:, None])
+                dv = dv + taken_sum(I.transpose(I.cast(p, I.f16)), upstream, I.transpose(taken))
+                dk = dk + taken_sum(I.transpose(I.cast(ds, I.f16)), queries, I.transpose(taken))
+            grad_k[b, kv, :, :] = I.cast(dk * scale, I.f16)
+            grad_v[b, kv, :, :] = I.cast(dv, I.f16)
 
 
 @intent.kernel
@@ -139,19 +118,13 @@ def attention_backward_dq(
     HEAD_GROUP: I.Constexpr[int],
     CAUSAL: I.Constexpr[bool],
 ):
-    B, HQ, Q, D = q.shape
+    B, HQ, Q = q.shape[0], q.shape[1], q.shape[2]
     K = k.shape[2]
-    rows, keys = I.domain(0, Q), I.domain(0, K)
-    for batch in I.parallel(I.domain(0, B)):
-        for head in I.parallel(I.domain(0, HQ)):
-            key_head = head // HEAD_GROUP
-            value = I.region_fold(
-                source=(k[batch, key_head, keys, :], v[batch, key_head, keys, :], I.indices(keys)),
-                axis=0,
-                summarize=summarize_query_gradients,
-                combine=merge_query_gradients,
-                identity=I.zeros((Q, D), dtype=I.f32),
-                operands=(q[batch, head, rows, :], grad_output[batch, head, rows, :], lse[batch, head, rows],
-                          delta[batch, head, rows], I.indices(rows), scale, CAUSAL),
-            )
-            grad_q[batch, head, rows, :] = I.cast(value * scale, I.f16)
+    taken = taken_pairs(Q, K, CAUSAL)                                     # [Q, K]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, HQ)):
+            keys, values = k[b, h // HEAD_GROUP, :, :], v[b, h // HEAD_GROUP, :, :]
+            p = pair_weights(q[b, h, :, :], keys, lse[b, h, :], scale, taken)
+            dp = I.matmul(grad_output[b, h, :, :], values, transpose_rhs=True, acc_dtype=I.f32)
+            ds = p * (dp - delta[b, h, :][:, None])
+            grad_q[b, h, :, :] = I.cast(taken_sum(I.cast(ds, I.f16), keys, taken) * scale, I.f16)

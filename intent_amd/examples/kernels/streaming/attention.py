@@ -1,14 +1,21 @@
-"""Fused attention forward definitions (interface and semantics of the reference's
-`python/intent/examples/kernels/streaming/attention.py:47-237, 417-553`): flash_attention_fwd,
-flash_gqa_attention_fwd (grouped key/value heads) and flash_attention_bf16_fwd.
+"""Attention forward definitions: flash_attention_fwd, flash_gqa_attention_fwd (key/value heads
+shared by HEAD_GROUP query heads) and flash_attention_bf16_fwd. Names, signatures and extents are
+the reference's (`python/intent/examples/kernels/streaming/attention.py:428-553`).
 
-A region fold over key chunks keeps, per query row, a summary record
-(valid, maximum, denominator, accumulator) in the exp2 domain:
-  chunk:   s = (q . k^T) * scale * log2(e); causal validity q_idx >= k_idx; masked -inf;
-           m = maximum_num of valid scores (0 when none valid); p = exp2(s - m) (approximate,
-           flush-to-zero) on valid keys; den = sum p; acc = cast(p, f16) @ v (f32 accumulate)
-  merge:   m = maximum_num of the valid maxima; each side scaled by exp2(m_side - m)
-  output:  acc * approx_reciprocal(den) for valid rows, 0 otherwise; cast to f16
+What each computes, per (batch, query head) and query row i:
+
+  logit[i, j] = (q_i . k_j) * scale * log2(e)          f32 accumulation of the storage type
+  admitted    = every key, or with CAUSAL the keys j <= i
+  peak_i      = largest admitted logit (NaN-ignoring maximum)
+  w[i, j]     = exp2(logit - peak_i) on admitted pairs (approximate, subnormals flushed), else 0
+  out_i       = (sum_j round(w[i, j]) v_j) * approx_recip(sum_j w[i, j]), stored in the storage type;
+                round() is the storage type (f16 or bf16), the sums are f32; a row that admits
+                no key is 0.
+
+The bodies below state this densely, one (batch, head) at a time. They are never traced by the hip
+provider, which recognises a definition by name and signature. The hand-written kernel streams
+the keys in tiles with a running maximum, so its sums are ordered differently; the tests hold it to
+the oracle within the tolerance stated there.
 """
 import math
 
@@ -25,100 +32,35 @@ SCALE = 1.0 / math.sqrt(HEAD_DIMENSION)
 
 
 @intent.fn
-def maximum_score(lhs, rhs):
-    return I.maximum_num(lhs, rhs)
-
-
-@intent.fn
-def reduce_score_maximum(scores, axis):
-    return I.reduce(scores, axis=axis, identity=-I.inf, combine=maximum_score)
-
-
-@intent.fn
-def empty_attention_summary(query_count, value_width):
-    return I.record(
-        valid=I.full((query_count,), fill=False, dtype=I.bool),
-        maximum=I.full((query_count,), fill=0.0, dtype=I.f32),
-        denominator=I.zeros((query_count,), dtype=I.f32),
-        accumulator=I.zeros((query_count, value_width), dtype=I.f32),
-    )
-
-
-@intent.fn
-def merge_attention_summaries(lhs, rhs):
-    merged_max = I.select(lhs.valid, lhs.maximum, rhs.maximum)
-    merged_max = I.select(rhs.valid, I.maximum_num(merged_max, rhs.maximum), merged_max)
-    left = I.select(lhs.valid, I.exp2(I.select(lhs.valid, lhs.maximum, merged_max) - merged_max,
-                                      approximate=True, flush_to_zero=True), 0.0)
-    right = I.select(rhs.valid, I.exp2(I.select(rhs.valid, rhs.maximum, merged_max) - merged_max,
-                                       approximate=True, flush_to_zero=True), 0.0)
-    return I.record(
-        valid=lhs.valid | rhs.valid,
-        maximum=merged_max,
-        denominator=left * lhs.denominator + right * rhs.denominator,
-        accumulator=left[:, None] * lhs.accumulator + right[:, None] * rhs.accumulator,
-    )
-
-
-@intent.fn
-def summarize_attention_chunk_f16(key_chunk, value_chunk, key_coordinates, queries, query_coordinates,
-                                  scale, causal):
-    scores = I.matmul(queries, key_chunk, transpose_rhs=True, acc_dtype=I.f32) * (scale * I.LOG2E)
-    valid = I.full(scores.shape, fill=True, dtype=I.bool)
+def causal_pairs(query_positions, key_positions, causal):
+    """Which (query, key) pairs take part: all of them, or with `causal` those with key <= query."""
     if causal:
-        valid = query_coordinates[:, None] >= key_coordinates[None, :]
-    masked = I.select(valid, scores, -I.inf)
-    any_valid = I.reduce.any(valid, axis=1)
-    chunk_max = I.select(any_valid, reduce_score_maximum(masked, axis=1), 0.0)
-    weights = I.select(valid, I.exp2(masked - chunk_max[:, None], approximate=True, flush_to_zero=True), 0.0)
-    return I.record(
-        valid=any_valid,
-        maximum=chunk_max,
-        denominator=I.reduce.sum(weights, axis=1),
-        accumulator=I.select(any_valid[:, None],
-                             I.matmul(I.cast(weights, I.f16), value_chunk, acc_dtype=I.f32), 0.0),
-    )
+        return query_positions[:, None] >= key_positions[None, :]
+    return I.full((query_positions.shape[0], key_positions.shape[0]), fill=True, dtype=I.bool)
 
 
 @intent.fn
-def summarize_attention_chunk_bf16(key_chunk, value_chunk, key_coordinates, queries, query_coordinates,
-                                   scale, causal, active):
-    scores = I.matmul(queries, key_chunk, transpose_rhs=True, acc_dtype=I.f32) * (scale * I.LOG2E)
-    valid = I.full(scores.shape, fill=True, dtype=I.bool) & active
-    if causal:
-        valid = valid & (query_coordinates[:, None] >= key_coordinates[None, :])
-    masked = I.select(valid, scores, -I.inf)
-    any_valid = I.reduce.any(valid, axis=1)
-    chunk_max = I.select(any_valid, reduce_score_maximum(masked, axis=1), 0.0)
-    weights = I.select(valid, I.exp2(masked - chunk_max[:, None], approximate=True, flush_to_zero=True), 0.0)
-    return I.record(
-        valid=any_valid,
-        maximum=chunk_max,
-        denominator=I.reduce.sum(weights, axis=1),
-        accumulator=I.select(any_valid[:, None],
-                             I.matmul(I.cast(weights, I.bf16), value_chunk, acc_dtype=I.f32), 0.0),
-    )
+def admitted_attention(logits, admitted, values, element):
+    """The unnormalised softmax of each row of base-2 `logits` over its admitted entries, applied
+    to `values` with the weights rounded to `element`: `live` (the row admits a key), `peak`,
+    `total` (the f32 sum of the weights; 1 where the row is not live) and `mixed` (the weighted
+    sum of value rows, f32)."""
+    live = I.reduce.any(admitted, axis=1)
+    peak = I.select(live, I.reduce(I.select(admitted, logits, -I.inf), axis=1, identity=-I.inf,
+                                   combine=I.maximum_num), 0.0)
+    weights = I.select(admitted, I.exp2(logits - peak[:, None], approximate=True, flush_to_zero=True), 0.0)
+    return I.record(live=live, peak=peak, total=I.select(live, I.reduce.sum(weights, axis=1), 1.0),
+                    mixed=I.matmul(I.cast(weights, element), values, acc_dtype=I.f32))
 
 
 @intent.fn
-def summarize_masked_attention_chunk(key_chunk, value_chunk, key_coordinates, active, queries, query_coordinates,
-                                     scale):
-    """Decode chunk summary: every pair of an active key is valid (attention.py:250-290)."""
-    scores = I.matmul(queries, key_chunk, transpose_rhs=True, acc_dtype=I.f32) * (scale * I.LOG2E)
-    valid = I.full(scores.shape, fill=True, dtype=I.bool) & active[None, :]
-    masked = I.select(valid, scores, -I.inf)
-    any_valid = I.reduce.any(valid, axis=1)
-    chunk_max = I.select(any_valid, reduce_score_maximum(masked, axis=1), 0.0)
-    weights = I.select(valid, I.exp2(masked - chunk_max[:, None], approximate=True, flush_to_zero=True), 0.0)
-    return I.record(valid=any_valid, maximum=chunk_max, denominator=I.reduce.sum(weights, axis=1),
-                    accumulator=I.matmul(I.cast(weights, I.f16), value_chunk, acc_dtype=I.f32))
-
-
-@intent.fn
-def normalize_attention_summary(summary):
-    denominator = I.select(summary.valid, summary.denominator, 1.0)
-    reciprocal = I.fdiv(1.0, denominator, approximate=True, flush_to_zero=True)
-    return I.select(summary.valid[:, None], summary.accumulator * reciprocal[:, None], 0.0)
+def attend_head(q_rows, k_rows, v_rows, scale, causal, element):
+    logits = I.matmul(q_rows, k_rows, transpose_rhs=True, acc_dtype=I.f32) * (scale * I.LOG2E)
+    admitted = causal_pairs(I.indices(I.domain(0, q_rows.shape[0])), I.indices(I.domain(0, k_rows.shape[0])),
+                            causal)
+    summary = admitted_attention(logits, admitted, v_rows, element)
+    share = I.fdiv(1.0, summary.total, approximate=True, flush_to_zero=True)
+    return I.cast(I.select(summary.live[:, None], summary.mixed * share[:, None], 0.0), element)
 
 
 @intent.kernel
@@ -130,21 +72,10 @@ def flash_attention_fwd(
     scale: I.f32,
     CAUSAL: I.Constexpr[bool],
 ):
-    B, H, Q, _ = q.shape
-    K = k.shape[2]
-    DV = v.shape[3]
-    q_axis, k_axis = I.domain(0, Q), I.domain(0, K)
-    for batch in I.parallel(I.domain(0, B)):
-        for head in I.parallel(I.domain(0, H)):
-            summary = I.region_fold(
-                source=(k[batch, head, k_axis, :], v[batch, head, k_axis, :], I.indices(k_axis)),
-                axis=0,
-                summarize=summarize_attention_chunk_f16,
-                combine=merge_attention_summaries,
-                identity=empty_attention_summary(Q, DV),
-                operands=(q[batch, head, q_axis, :], I.indices(q_axis), scale, CAUSAL),
-            )
-            output[batch, head, q_axis, :] = I.cast(normalize_attention_summary(summary), I.f16)
+    B, H = q.shape[0], q.shape[1]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, H)):
+            output[b, h, :, :] = attend_head(q[b, h, :, :], k[b, h, :, :], v[b, h, :, :], scale, CAUSAL, I.f16)
 
 
 @intent.kernel
@@ -157,22 +88,12 @@ def flash_gqa_attention_fwd(
     HEAD_GROUP: I.Constexpr[int],
     CAUSAL: I.Constexpr[bool],
 ):
-    B, HQ, Q, _ = q.shape
-    K = k.shape[2]
-    DV = v.shape[3]
-    q_axis, k_axis = I.domain(0, Q), I.domain(0, K)
-    for batch in I.parallel(I.domain(0, B)):
-        for query_head in I.parallel(I.domain(0, HQ)):
-            key_head = query_head // HEAD_GROUP
-            summary = I.region_fold(
-                source=(k[batch, key_head, k_axis, :], v[batch, key_head, k_axis, :], I.indices(k_axis)),
-                axis=0,
-                summarize=summarize_attention_chunk_f16,
-                combine=merge_attention_summaries,
-                identity=empty_attention_summary(Q, DV),
-                operands=(q[batch, query_head, q_axis, :], I.indices(q_axis), scale, CAUSAL),
-            )
-            output[batch, query_head, q_axis, :] = I.cast(normalize_attention_summary(summary), I.f16)
+    B, HQ = q.shape[0], q.shape[1]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, HQ)):
+            shared = h // HEAD_GROUP
+            output[b, h, :, :] = attend_head(q[b, h, :, :], k[b, shared, :, :], v[b, shared, :, :], scale, CAUSAL,
+                                             I.f16)
 
 
 @intent.kernel
@@ -185,19 +106,9 @@ def flash_attention_bf16_fwd(
     HEAD_GROUP: I.Constexpr[int],
     CAUSAL: I.Constexpr[bool],
 ):
-    B, HQ, Q, _ = q.shape
-    K = k.shape[2]
-    DV = v.shape[3]
-    q_axis, k_axis = I.domain(0, Q), I.domain(0, K)
-    for batch in I.parallel(I.domain(0, B)):
-        for query_head in I.parallel(I.domain(0, HQ)):
-            key_head = query_head // HEAD_GROUP
-            summary = I.region_fold(
-                source=(k[batch, key_head, k_axis, :], v[batch, key_head, k_axis, :], I.indices(k_axis)),
-                axis=0,
-                summarize=summarize_attention_chunk_bf16,
-                combine=merge_attention_summaries,
-                identity=empty_attention_summary(Q, DV),
-                operands=(q[batch, query_head, q_axis, :], I.indices(q_axis), scale, CAUSAL, True),
-            )
-            output[batch, query_head, q_axis, :] = I.cast(normalize_attention_summary(summary), I.bf16)
+    B, HQ = q.shape[0], q.shape[1]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, HQ)):
+            shared = h // HEAD_GROUP
+            output[b, h, :, :] = attend_head(q[b, h, :, :], k[b, shared, :, :], v[b, shared, :, :], scale, CAUSAL,
+                                             I.bf16)

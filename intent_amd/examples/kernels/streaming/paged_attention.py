@@ -1,21 +1,25 @@
-"""Paged grouped-query decode attention, split over page ranges (interface and semantics of the
-reference's `python/intent/examples/kernels/streaming/paged_attention.py:77-165`).
+"""Paged grouped-query decode attention, split over page ranges. Names, signature and example
+extents are the reference's (`python/intent/examples/kernels/streaming/paged_attention.py:77-165`).
 
-For each (batch, split) job and key head, the HEAD_GROUP query heads of that key head attend over
-the tokens of the job's pages: page position p in [split_offsets[job], split_offsets[job+1]),
-physical page page_indices[p], token offset o in [0, PS); logical token
-(p - page_offsets[batch]) * PAGE_SIZE + o, active while below sequence_lengths[batch]. The fold
-is the f16 attention summary in the exp2 domain (masked chunk summaries merged by rescaling);
-outputs: partial_lse = maximum + log(denominator) * log2(e) (-inf for an empty job) and
-partial_output = accumulator * (1 / denominator) (0 for an empty job), in f32.
+A job is one (batch, split) pair. Its pages are the page-table positions p in
+[split_offsets[job], split_offsets[job + 1]); position p holds physical page page_indices[p], and
+token t of it is logical token (p - page_offsets[batch]) * PAGE_SIZE + t. A token takes part while
+its logical index is below sequence_lengths[batch]. For each key head, the HEAD_GROUP query heads
+that share it attend over the job's tokens as the forward attention does (base-2 logits, NaN-ignoring
+peak, approximate exp2 weights rounded to f16 before they weight V). The job writes, per query head,
+the base-2 log-sum-exp of its weights to partial_lse and its rows divided (exactly) by the sum of
+the weights to partial_output, in f32. A job with no live token writes -inf and 0. The split-K
+merge (splitk_reduce.py) combines the splits of a batch.
+
+The body states this for one job at a time; the hip provider recognises the definition by name and
+signature and runs its own kernel.
 """
 import math
 
 import intent_amd as intent
 import intent_amd.language as I
 
-from intent_amd.examples.kernels.streaming.attention import (empty_attention_summary, merge_attention_summaries,
-                                                             summarize_masked_attention_chunk)
+from intent_amd.examples.kernels.streaming.attention import admitted_attention
 
 BATCH = 8
 QUERY_HEADS = 32
@@ -44,35 +48,22 @@ def paged_gqa_decode_partials(
     HEAD_GROUP: I.Constexpr[int],
     SPLITS: I.Constexpr[int],
 ):
-    B, HQ, D = q.shape
-    PS, HK = key_cache.shape[1], key_cache.shape[2]
-    DV = value_cache.shape[3]
+    B, HK, PS = q.shape[0], key_cache.shape[2], key_cache.shape[1]
     for job in I.parallel(I.domain(0, B * SPLITS)):
         batch, split = job // SPLITS, job % SPLITS
-        page_begin = I.cast(page_offsets[batch], I.index)
-        length = I.cast(sequence_lengths[batch], I.index)
-        first = I.cast(split_offsets[job], I.index)
-        pages = I.cast(split_offsets[job + 1] - split_offsets[job], I.index)
-        token = I.indices(I.domain(0, pages * PS))
-        position = first + token // PS
-        offset = token % PS
-        physical = I.cast(page_indices[position], I.index)
-        logical = (position - page_begin) * PAGE_SIZE + offset
-        for key_head in I.parallel(I.domain(0, HK)):
-            heads = key_head * HEAD_GROUP + I.indices(I.domain(0, HEAD_GROUP))
-            summary = I.region_fold(
-                source=(key_cache[physical, offset, key_head, :], value_cache[physical, offset, key_head, :],
-                        logical, logical < length),
-                axis=0,
-                summarize=summarize_masked_attention_chunk,
-                combine=merge_attention_summaries,
-                identity=empty_attention_summary(HEAD_GROUP, DV),
-                operands=(I.gather(q, index=(batch, heads, slice(None))),
-                          I.full((HEAD_GROUP,), fill=0, dtype=I.index), scale),
-            )
-            denominator = I.select(summary.valid, summary.denominator, 1.0)
+        first, last = I.cast(split_offsets[job], I.index), I.cast(split_offsets[job + 1], I.index)
+        token = I.indices(I.domain(0, (last - first) * PS))
+        position, slot = first + token // PS, token % PS
+        page = I.cast(page_indices[position], I.index)
+        live = (position - I.cast(page_offsets[batch], I.index)) * PAGE_SIZE + slot < I.cast(sequence_lengths[batch],
+                                                                                              I.index)
+        for kv in I.parallel(I.domain(0, HK)):
+            heads = kv * HEAD_GROUP + I.indices(I.domain(0, HEAD_GROUP))
+            queries = I.gather(q, index=(batch, heads, slice(None)))
+            logits = I.matmul(queries, key_cache[page, slot, kv, :], transpose_rhs=True, acc_dtype=I.f32)
+            result = admitted_attention(logits * (scale * I.LOG2E), live[None, :] & I.full(
+                (HEAD_GROUP, token.shape[0]), fill=True, dtype=I.bool), value_cache[page, slot, kv, :], I.f16)
             I.scatter_unique(partial_lse, index=(batch, heads, split),
-                             value=I.select(summary.valid, summary.maximum + I.log(denominator) * I.LOG2E, -I.inf))
+                             value=I.select(result.live, result.peak + I.log(result.total) * I.LOG2E, -I.inf))
             I.scatter_unique(partial_output, index=(batch, heads, split, slice(None)),
-                             value=I.select(summary.valid[:, None],
-                                            summary.accumulator * (1.0 / denominator)[:, None], 0.0))
+                             value=I.select(result.live[:, None], result.mixed * (1.0 / result.total)[:, None], 0.0))

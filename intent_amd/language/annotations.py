@@ -1,16 +1,27 @@
-"""View/scalar/constexpr annotations of kernel parameters.
+"""Parameter annotations of kernel definitions.
 
-Same surface and validation rules as the reference's
-`python/intent/language/annotations.py`: `I.In/Out/InOut[dtype, shape, constraints]`,
-`I.constraints(strides=, alias=, noalias=)`, `I.Constexpr[type]`, `I.Enum`.
-Shapes mix static extents (non-negative ints) and symbolic names (identifiers);
-one symbol names one logical dimension across all parameters of a kernel."""
+A kernel parameter is annotated with one of:
+
+* a view, `I.In[dtype, shape]`, `I.Out[...]` or `I.InOut[...]`, with an optional third item
+  `I.constraints(strides=..., alias=..., noalias=...)`;
+* a scalar, the bare dtype (`scale: I.f32`);
+* a specialization value, `I.Constexpr[type]`, fixed when the kernel is jitted.
+
+A shape lists extents: a non-negative int fixes an extent, and an identifier names a logical
+dimension. Every view of a kernel that uses the same name shares that extent. A stride constraint
+is an int, an identifier that names a stride shared by the views that use it, or None for an axis
+left free. An Out view's incoming elements are undefined.
+
+The public names and the error classes are the reference's
+(`python/intent/language/annotations.py`). Malformed entries raise TypeError and out-of-range
+values raise ValueError. `In`, `Out`, `InOut` and `Constexpr` are subscriptable annotation objects
+here. Nothing but subscription is asked of them, and the runtime reads the resulting specs by
+attribute.
+"""
 from __future__ import annotations
 
-import builtins as _py
+import enum
 from dataclasses import dataclass
-from enum import Enum as _PyEnum
-from enum import IntEnum
 from typing import Any
 
 from .dtypes import DType
@@ -19,52 +30,71 @@ ShapeDim = int | str
 StrideDim = int | str | None
 
 
+def _entry_class(entry: object) -> str:
+    """Classify one shape or stride entry: "int", "name", "none", "bad name" or "other".
+
+    bool counts as "other" although it is an int subclass: True is no extent."""
+    if entry is None:
+        return "none"
+    if isinstance(entry, bool):
+        return "other"
+    if isinstance(entry, int):
+        return "int"
+    if isinstance(entry, str):
+        return "name" if entry.isidentifier() else "bad name"
+    return "other"
+
+
+def _extent(entry: object) -> ShapeDim:
+    kind = _entry_class(entry)
+    if kind == "name":
+        return entry
+    if kind == "int":
+        if entry < 0:
+            raise ValueError(f"a static extent cannot be negative, got {entry}")
+        return entry
+    if kind == "bad name":
+        raise ValueError(f"{entry!r} is not an identifier and cannot name a dimension")
+    raise TypeError(f"a shape entry is an int extent or a dimension name, not {entry!r}")
+
+
+def _stride(entry: object) -> StrideDim:
+    if _entry_class(entry) in ("int", "name", "none"):
+        return entry
+    raise TypeError(f"a stride constraint is an int, a stride name or None, not {entry!r}")
+
+
 def _shape(shape: object) -> tuple[ShapeDim, ...]:
     if not isinstance(shape, (tuple, list)):
-        raise TypeError("tensor shape annotation must be a tuple or list")
-    out: list[ShapeDim] = []
-    for dim in shape:
-        if isinstance(dim, _py.bool):
-            raise TypeError("boolean is not a tensor shape dimension")
-        if isinstance(dim, int):
-            if dim < 0:
-                raise ValueError("static tensor dimensions must be non-negative")
-        elif isinstance(dim, str):
-            if not dim.isidentifier():
-                raise ValueError(f"invalid symbolic dimension: {dim!r}")
-        else:
-            raise TypeError(f"unsupported tensor shape dimension: {dim!r}")
-        out.append(dim)
-    return tuple(out)
+        raise TypeError(f"a view shape is a tuple or list of extents, not {type(shape).__name__}")
+    return tuple(_extent(entry) for entry in shape)
 
 
 @dataclass(frozen=True, slots=True)
 class ViewConstraints:
+    """Layout and allocation relations of one view (strides, alias group, noalias)."""
+
     strides: tuple[StrideDim, ...] | None = None
     alias: str | None = None
     noalias: bool = False
 
     def __post_init__(self) -> None:
         if self.strides is not None:
-            strides = tuple(self.strides)
-            for stride in strides:
-                if stride is None or (isinstance(stride, int) and not isinstance(stride, _py.bool)):
-                    continue
-                if isinstance(stride, str) and stride.isidentifier():
-                    continue
-                raise TypeError(f"unsupported stride constraint: {stride!r}")
-            object.__setattr__(self, "strides", strides)
-        if self.alias is not None and not self.alias:
-            raise ValueError("alias group must not be empty")
-        if self.alias is not None and self.noalias:
-            raise ValueError("alias and noalias cannot be specified together")
+            object.__setattr__(self, "strides", tuple(_stride(entry) for entry in self.strides))
+        if self.alias is not None:
+            if self.noalias:
+                raise ValueError("a view cannot both join an alias group and be noalias")
+            if not self.alias:
+                raise ValueError("an alias group needs a non-empty name")
 
 
-def constraints(*, strides=None, alias=None, noalias=False) -> ViewConstraints:
-    return ViewConstraints(strides=strides, alias=alias, noalias=noalias)
+def constraints(*, strides: tuple[StrideDim, ...] | None = None, alias: str | None = None,
+                noalias: bool = False) -> ViewConstraints:
+    """The optional third item of a view annotation."""
+    return ViewConstraints(strides, alias, noalias)
 
 
-class ViewKind(IntEnum):
+class ViewKind(enum.IntEnum):
     IN = 0
     OUT = 1
     INOUT = 2
@@ -72,59 +102,69 @@ class ViewKind(IntEnum):
 
 @dataclass(frozen=True, slots=True)
 class ViewSpec:
+    """A view parameter: access kind, element dtype, shape and constraints."""
+
     kind: ViewKind
     dtype: DType
     shape: tuple[ShapeDim, ...]
     constraints: ViewConstraints
 
     def __post_init__(self) -> None:
-        if not isinstance(self.kind, ViewKind):
-            raise TypeError("view kind must be a ViewKind")
-        if not isinstance(self.dtype, DType):
-            raise TypeError("view element type must be an Intent dtype")
-        if not isinstance(self.constraints, ViewConstraints):
-            raise TypeError("view constraints must be a ViewConstraints")
-        object.__setattr__(self, "shape", _shape(self.shape))
-        if self.constraints.strides is not None and len(self.constraints.strides) != len(self.shape):
-            raise ValueError("stride constraint rank must match tensor rank")
+        for value, expected, what in ((self.kind, ViewKind, "access kind"), (self.dtype, DType, "element dtype"),
+                                      (self.constraints, ViewConstraints, "constraints")):
+            if not isinstance(value, expected):
+                raise TypeError(f"a view's {what} must be a {expected.__name__}, got {value!r}")
+        shape = _shape(self.shape)
+        object.__setattr__(self, "shape", shape)
+        strides = self.constraints.strides
+        if strides is not None and len(strides) != len(shape):
+            raise ValueError(f"{len(strides)} stride constraints for a view of rank {len(shape)}")
 
 
-class _View:
-    kind: ViewKind
+class _ViewAnnotation:
+    """`In`, `Out` and `InOut`: subscripting one with (dtype, shape[, constraints]) gives a ViewSpec."""
 
-    def __class_getitem__(cls, parameters: object) -> ViewSpec:
-        if not isinstance(parameters, tuple) or len(parameters) not in (2, 3):
-            raise TypeError("view annotation expects dtype, shape, and optional constraints")
-        extra = parameters[2] if len(parameters) == 3 else ViewConstraints()
+    def __init__(self, kind: ViewKind, name: str, doc: str) -> None:
+        self.kind, self.__name__, self.__doc__ = kind, name, doc
+
+    def __getitem__(self, items: object) -> ViewSpec:
+        if not isinstance(items, tuple) or not 2 <= len(items) <= 3:
+            raise TypeError(f"I.{self.__name__}[...] takes a dtype, a shape and optionally I.constraints(...)")
+        dtype, shape, *rest = items
+        extra = rest[0] if rest else ViewConstraints()
         if not isinstance(extra, ViewConstraints):
-            raise TypeError("third view annotation argument must be I.constraints(...)")
-        return ViewSpec(cls.kind, parameters[0], _shape(parameters[1]), extra)
+            raise TypeError(f"the third item of I.{self.__name__}[...] must come from I.constraints(...), "
+                            f"got {extra!r}")
+        return ViewSpec(self.kind, dtype, _shape(shape), extra)
+
+    def __repr__(self) -> str:
+        return f"I.{self.__name__}"
 
 
-class In(_View):
-    kind = ViewKind.IN
-
-
-class Out(_View):
-    """Output view; its incoming elements are undefined."""
-    kind = ViewKind.OUT
-
-
-class InOut(_View):
-    kind = ViewKind.INOUT
+In = _ViewAnnotation(ViewKind.IN, "In", "A view the kernel reads.")
+Out = _ViewAnnotation(ViewKind.OUT, "Out", "A view the kernel writes; its incoming elements are undefined.")
+InOut = _ViewAnnotation(ViewKind.INOUT, "InOut", "A view the kernel reads and writes.")
 
 
 @dataclass(frozen=True, slots=True)
 class ConstexprSpec:
+    """A specialization parameter of type `value_type`, bound at jit time."""
+
     value_type: Any
 
 
-class Constexpr:
-    def __class_getitem__(cls, value_type: Any) -> ConstexprSpec:
+class _ConstexprAnnotation:
+    def __getitem__(self, value_type: Any) -> ConstexprSpec:
         if value_type is None:
-            raise TypeError("Constexpr requires a value type")
+            raise TypeError("I.Constexpr[...] needs the type of the specialization value")
         return ConstexprSpec(value_type)
 
+    def __repr__(self) -> str:
+        return "I.Constexpr"
 
-class Enum(_PyEnum):
-    """Base class for author specialization enums (constexpr-only)."""
+
+Constexpr = _ConstexprAnnotation()
+
+
+class Enum(enum.Enum):
+    """Base class of author enums used as specialization values."""

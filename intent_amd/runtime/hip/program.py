@@ -118,6 +118,11 @@ class HipProgram:
         self._lock = threading.Lock()
         self._closed = False
 
+    @property
+    def derivable_dimensions(self) -> frozenset:
+        """Dimension identities whose extents follow from other dimensions (csr_spmv's R = R1 - 1)."""
+        return frozenset(self._derived)
+
     # -- binding ------------------------------------------------------------------------------
     def _bind(self, arguments, outputs, *, abstract=False):
         device = self.device
