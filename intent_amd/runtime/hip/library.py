@@ -12,6 +12,8 @@ from pathlib import Path
 from ...diagnostics import CompilationStageError
 
 ABI_VERSION = 8
+# INTENT_HIP_STATIC_SCRATCH_BYTES: the static scratch of intent_hip_csr_spmv_f32_static.
+STATIC_SCRATCH_BYTES = 32 << 20
 LIBRARY_NAME = "libintent_hip.so"
 LIBRARY_PATH = Path(__file__).resolve().parents[2] / LIBRARY_NAME
 

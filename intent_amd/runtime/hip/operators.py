@@ -35,11 +35,13 @@ buffer copied back after the kernel.
 """
 from __future__ import annotations
 
+import contextlib
+import contextvars
 from dataclasses import dataclass, field
 from typing import Callable
 
 from ...diagnostics import CompilationStageError
-from .library import (BF16, F16, F32, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
+from .library import (BF16, F16, F32, STATIC_SCRATCH_BYTES, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
                       OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32,
                       OP_CSR_SPMM_F32, OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
@@ -74,6 +76,26 @@ def _view(access, dtype, rank):
     return ("view", access, dtype, rank)
 
 
+# ------------------------------------------------------------------------------ workspace policy
+# The target's backend_options["workspace"]: "prepare" lets a plan allocate device memory once per
+# prepared call (staging copies, SpMV plan, split partial sums); "static" forbids it.
+_WORKSPACE = contextvars.ContextVar("intent_hip_workspace", default="prepare")
+
+
+@contextlib.contextmanager
+def workspace_policy(policy: str):
+    """Plans made inside this block follow `policy` ("prepare" or "static")."""
+    token = _WORKSPACE.set(policy)
+    try:
+        yield
+    finally:
+        _WORKSPACE.reset(token)
+
+
+def _static_workspace() -> bool:
+    return _WORKSPACE.get() == "static"
+
+
 # ------------------------------------------------------------------------------ layout helpers
 def _aligned(tensor, vector: int) -> bool:
     """Unit inner stride, outer strides multiples of `vector` elements, 16-byte aligned start."""
@@ -94,6 +116,7 @@ def _readable(tensor, keep, before, vector: int = 1):
     (unit inner stride; with `vector`, also aligned for 16-byte loads)."""
     if _aligned(tensor, vector):
         return tensor
+    _refuse_staging(tensor, vector)
     staged = tensor.new_empty(tensor.shape)
     keep.append(staged)
     before.append(lambda: staged.copy_(tensor))
@@ -103,10 +126,19 @@ def _readable(tensor, keep, before, vector: int = 1):
 def _writable(tensor, keep, after, vector: int = 1):
     if _aligned(tensor, vector):
         return tensor
+    _refuse_staging(tensor, vector)
     staged = tensor.new_empty(tensor.shape)
     keep.append(staged)
     after.append(lambda: tensor.copy_(staged))
     return staged
+
+
+def _refuse_staging(tensor, vector: int) -> None:
+    if _static_workspace():
+        need = "unit inner stride" + (f", outer strides in multiples of {vector} and a 16-byte aligned start"
+                                      if vector > 1 else "")
+        raise ValueError(f"with backend_options workspace='static' the provider does not stage views; this "
+                         f"kernel needs {need}, got strides {tuple(tensor.stride())}")
 
 
 def _row_stride(tensor):
@@ -317,8 +349,9 @@ def _attention_bwd(kind):
         import torch
 
         size = ctypes.c_size_t(0)
-        lib.check(lib.fn[f"attention_bwd_{kind}_workspace_bytes"](batch, q_heads, group, sq, sk, d,
-                                                                 ctypes.byref(size)), "provider_preparation")
+        if not _static_workspace():
+            lib.check(lib.fn[f"attention_bwd_{kind}_workspace_bytes"](batch, q_heads, group, sq, sk, d,
+                                                                     ctypes.byref(size)), "provider_preparation")
         workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
         if workspace is not None:
             keep.append(workspace)
@@ -414,13 +447,22 @@ def _csr_spmv(lib, bound, constexprs, device):
     nnz, cols = values.shape[0], vector.shape[0]
     size = ctypes.c_size_t(0)
     lib.check(lib.fn["csr_spmv_workspace_bytes"](rows, nnz, ctypes.byref(size)), "provider_preparation")
-    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
-    keep.append(workspace)
-    fn = lib.fn["csr_spmv_f32"]
-    args = (ok.data_ptr(), ck.data_ptr(), vk.data_ptr(), xk.data_ptr(), yk.data_ptr(), rows, cols, nnz,
-            workspace.data_ptr(), size.value)
-    return Launch("intent_hip_csr_spmv_f32", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
-                  tuple(after), (("rows", rows), ("cols", cols), ("nnz", nnz), ("workspace_bytes", size.value)),
+    pointers = (ok.data_ptr(), ck.data_ptr(), vk.data_ptr(), xk.data_ptr(), yk.data_ptr(), rows, cols, nnz)
+    facts = (("rows", rows), ("cols", cols), ("nnz", nnz), ("workspace_bytes", size.value))
+    if _static_workspace():
+        if size.value > STATIC_SCRATCH_BYTES:
+            raise CompilationStageError(
+                "provider_preparation", f"csr_spmv of {rows} rows and {nnz} nonzeros needs {size.value} workspace "
+                f"bytes, beyond the {STATIC_SCRATCH_BYTES}-byte static scratch; use workspace='prepare'")
+        fn, entry = lib.fn["csr_spmv_f32_static"], "intent_hip_csr_spmv_f32_static"
+        args = pointers
+        facts += (("workspace", "static"),)
+    else:
+        workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+        keep.append(workspace)
+        fn, entry = lib.fn["csr_spmv_f32"], "intent_hip_csr_spmv_f32"
+        args = (*pointers, workspace.data_ptr(), size.value)
+    return Launch(entry, lambda stream: fn(*args, stream), tuple(keep), tuple(before), tuple(after), facts,
                   lambda: lib.kernel_resources(OP_CSR_SPMV_F32, F32, rows, nnz))
 
 

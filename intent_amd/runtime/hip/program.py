@@ -18,7 +18,7 @@ from ..interface import PublicInterface, ViewParameter
 from ..invocation import bind_arguments
 from ..torch_views import allocate_output, observe_view
 from .library import library
-from .operators import OperatorSpec, recognize
+from .operators import OperatorSpec, recognize, workspace_policy
 
 
 def _symbols(definition, constexprs) -> dict[str, int]:
@@ -110,6 +110,7 @@ class HipProgram:
         import torch
 
         self.spec, self.interface, self.constexprs, self.target = spec, interface, dict(constexprs), target
+        self.workspace = getattr(target, "workspace", "prepare")
         self.device = torch.device("cuda", target.device)
         self.library = library()
         self._derived = {symbols[name]: (symbols[source], offset) for name, source, offset in spec.derived
@@ -155,7 +156,8 @@ class HipProgram:
             raise TypeError("outputs must be a tuple in declared Out order")
         bound = self._bind(arguments, outputs)
         self._check_writable_overlap(bound)
-        launch = self.spec.plan(self.library, bound, self.constexprs, self.device)
+        with workspace_policy(self.workspace):
+            launch = self.spec.plan(self.library, bound, self.constexprs, self.device)
         return HipPreparedCall(self, bound, launch)
 
     def run(self, *arguments):

@@ -23,6 +23,20 @@ INSTALLATION = {
 SUPPORTED_ARCHITECTURES = ("gfx950",)
 
 
+# backend_options={"workspace": ...}: where the device memory a kernel needs beyond its operands
+# comes from.
+#   "prepare" (default)  allocated once per prepared call: the SpMV plan and the split
+#                        partial sums of small attention-backward grids; a view whose layout
+#                        the kernel does not take is staged through a contiguous copy.
+#   "static"             the provider allocates nothing at prepare: SpMV runs on the library's
+#                        static per-GPU scratch (intent_hip_csr_spmv_f32_static, problems up to
+#                        INTENT_HIP_STATIC_SCRATCH_BYTES of plan), the attention backward runs its
+#                        unsplit kernels, and a view that would need staging is rejected
+#                        (ValueError). Out buffers the caller does not pass are still allocated.
+#                        Calls on one GPU that overlap share the SpMV scratch and race.
+WORKSPACE_POLICIES = ("prepare", "static")
+
+
 @dataclass(frozen=True, slots=True)
 class ResolvedHipTarget:
     device: int
@@ -32,6 +46,7 @@ class ResolvedHipTarget:
     lds_per_workgroup: int
     global_memory_bytes: int
     facts: dict = field(default_factory=dict, compare=False)
+    workspace: str = "prepare"
 
     @property
     def provider(self) -> str:
@@ -41,6 +56,11 @@ class ResolvedHipTarget:
 @dataclass(frozen=True, slots=True)
 class HipTarget:
     device: int = 0
+    workspace: str = "prepare"
+
+    def __post_init__(self) -> None:
+        if self.workspace not in WORKSPACE_POLICIES:
+            raise ValueError(f"workspace must be one of {WORKSPACE_POLICIES}, got {self.workspace!r}")
 
     def resolve(self) -> ResolvedHipTarget:
         from ..runtime.hip.library import library
@@ -52,7 +72,7 @@ class HipTarget:
                 "target_resolution", f"device {self.device} is {arch}; the hip provider is built for "
                 f"{', '.join(SUPPORTED_ARCHITECTURES)} only")
         return ResolvedHipTarget(self.device, arch, info["compute_units"], info["wavefront_size"],
-                                 info["lds_per_workgroup"], info["global_memory_bytes"], info)
+                                 info["lds_per_workgroup"], info["global_memory_bytes"], info, self.workspace)
 
 
 def _materialize(target, definition, *, constexprs=None, tuning_config=None, options=None):
@@ -74,5 +94,6 @@ def _environment_checks(target):
 
 PROVIDER = Provider(
     "gpu", HipTarget, None, None, _environment_checks,
-    LocalExecution("cuda", True, frozenset(), partial(indexed_target, HipTarget), indexed_key, torch_storage),
+    LocalExecution("cuda", True, frozenset({"workspace"}), partial(indexed_target, HipTarget), indexed_key,
+                   torch_storage),
     "hip-direct", None, materialize=_materialize)

@@ -375,3 +375,27 @@ def test_benchmarked_shape_matches_autograd_and_oracle(device):
     close(grads[0][:1, :group].cpu().numpy(), want_dq)
     close(grads[1][:1, :1].cpu().numpy(), want_dk)
     close(grads[2][:1, :1].cpu().numpy(), want_dv)
+
+
+@pytest.mark.parametrize("shape,causal", [((1, 2, 1, 128, 128, 64), True), ((1, 4, 2, 300, 300, 128), True),
+                                          ((1, 2, 2, 200, 333, 64), False)])
+def test_static_workspace_option_runs_the_unsplit_kernels(device, shape, causal):
+    """backend_options={"workspace": "static"}: prepare allocates no partial-sum workspace, so small grids
+    run unsplit; the results hold the same bar against the oracle."""
+    batch, hq, hk, sq, sk, d = shape
+    announce("attention backward workspace=static", shape, causal)
+    q, k, v, o, do, lse = case(sq * 7 + d, batch, hq, hk, sq, sk, d)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    jit = lambda defn, **kw: intent.jit(defn, backend="hip", backend_options={"workspace": "static"}, **kw)  # noqa: E731
+    prepared = AttentionBackward.from_jit(jit, head_group=hq // hk, causal=causal).prepare(
+        t(q), t(k), t(v), t(o), t(do), t(lse), scale)
+    for call in prepared.calls[1:]:
+        assert dict(call.inspect_configurations()[0].configuration)["workspace_bytes"] == 0
+    prepared.launch()
+    grad_q, grad_k, grad_v = prepared.result()
+    delta = oracle.attention_bwd_delta(o, do)
+    want_dk, want_dv = oracle.attention_bwd_dkdv(q, k, v, do, lse, delta, scale, causal, head_group=hq // hk)
+    close(grad_q.cpu().numpy(), oracle.attention_bwd_dq(q, k, v, do, lse, delta, scale, causal, head_group=hq // hk))
+    close(grad_k.cpu().numpy(), want_dk)
+    close(grad_v.cpu().numpy(), want_dv)

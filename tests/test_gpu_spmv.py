@@ -196,3 +196,30 @@ def test_spmv_large_rows_over_several_batches(device):
     values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
     x = inputs.uniform(rng, cols, -1, 1)
     check(device, offsets, columns, values, x)
+
+
+def test_static_workspace_option(device):
+    """backend_options={"workspace": "static"} runs csr_spmv through the no-allocation entry point
+    (static per-GPU scratch): bit-identical to the default path; problems beyond the scratch are
+    refused at prepare."""
+    announce("spmv workspace=static")
+    rng = np.random.default_rng(77)
+    lengths = np.concatenate((rng.integers(0, 5, 20000), rng.integers(5, 300, 3000), rng.integers(300, 9000, 40)))
+    offsets, columns = inputs.csr_matrix(rng, lengths[rng.permutation(lengths.shape[0])], 60000)
+    values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
+    x = inputs.uniform(rng, 60000, -1, 1)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    args = (t(offsets), t(columns), t(values), t(x))
+    static = intent.jit(csr_spmv, backend="hip", backend_options={"workspace": "static"})
+    call = static.prepare(*args)
+    call.launch()
+    assert call.observation.entry == "intent_hip_csr_spmv_f32_static"
+    want = intent.jit(csr_spmv, backend="hip").run(*args)
+    assert torch.equal(call.result(), want)
+    big_rows, big_nnz = 1_000_000, 30_000_000
+    huge = (torch.zeros(big_rows + 1, dtype=torch.int32, device=device),
+            torch.zeros(big_nnz, dtype=torch.int32, device=device),
+            torch.zeros(big_nnz, dtype=torch.float32, device=device), torch.zeros(16, device=device))
+    with pytest.raises(intent.CompilationStageError) as error:
+        static.prepare(*huge)
+    assert error.value.stage == "provider_preparation"

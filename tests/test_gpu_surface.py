@@ -142,3 +142,24 @@ def test_saved_program_runs_like_jit(device, tmp_path):
     call = softmax.prepare(x, outputs=(out,))
     call.launch()
     assert call.result() is out and torch.equal(out, want)
+
+
+def test_static_workspace_refuses_staging(device):
+    """With backend_options={"workspace": "static"} the provider allocates nothing at prepare, so a
+    view the kernel cannot read in place (here a vector of stride 2) is refused instead of staged
+    through a copy, as the default policy does."""
+    announce("workspace=static staging")
+    from intent_amd.examples.kernels.sparse.csr_spmv import csr_spmv
+
+    offsets = torch.tensor([0, 2, 3, 3, 5], dtype=torch.int32, device=device)
+    columns = torch.tensor([0, 3, 1, 2, 3], dtype=torch.int32, device=device)
+    values = torch.tensor([1.0, 2.0, 3.0, 4.0, 5.0], device=device)
+    strided = torch.arange(8.0, device=device)[::2]                      # x = [0, 2, 4, 6]
+    with pytest.raises(ValueError):
+        intent.jit(csr_spmv, backend="hip", backend_options={"workspace": "static"}).run(
+            offsets, columns, values, strided)
+    y = intent.jit(csr_spmv, backend="hip").run(offsets, columns, values, strided)
+    assert y.cpu().tolist() == [12.0, 6.0, 0.0, 46.0]
+    with pytest.raises(ValueError):
+        intent.jit(csr_spmv, backend="hip", backend_options={"workspace": "pinned"}).run(
+            offsets, columns, values, strided.contiguous())

@@ -286,3 +286,24 @@ def test_attention_backward_program_order_and_outputs():
     assert [entry[3] for entry in log] == [("ws",), ("gk", "gv"), ("gq",)]
     with pytest.raises(TypeError):
         program.prepare("q", "k", "v", "o", "do", "lse", 0.125, outputs=("gq",))
+
+
+# ------------------------------------------------------------------------------ backend options
+def test_workspace_option_values_and_staging_refusal():
+    from intent_amd.runtime.hip import operators
+    from intent_amd.targets.hip import HipTarget
+
+    assert HipTarget(0).workspace == "prepare" and HipTarget(0, "static").workspace == "static"
+    with pytest.raises(ValueError):
+        HipTarget(0, "pinned")
+    transposed = torch.zeros(4, 6).t()
+    keep, before = [], []
+    assert operators._readable(transposed, keep, before) is not transposed and len(before) == 1
+    with operators.workspace_policy("static"):
+        with pytest.raises(ValueError):
+            operators._readable(transposed, [], [])
+        with pytest.raises(ValueError):
+            operators._writable(transposed, [], [])
+        plain = torch.zeros(4, 6)
+        assert operators._readable(plain, [], []) is plain
+    assert not operators._static_workspace()
