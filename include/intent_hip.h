@@ -50,7 +50,7 @@ enum IntentHipOperator {
   INTENT_HIP_OP_CSR_SPMV_F32 = 4,
   INTENT_HIP_OP_GEMM = 5,              /* dtype F16 or BF16 */
   INTENT_HIP_OP_GEMM_F32 = 6,
-  INTENT_HIP_OP_ATTENTION_FWD = 7,     /* dtype F16 or BF16 */
+  INTENT_HIP_OP_ATTENTION_FWD = 7,     /* dtype F16 or BF16; for both forward ops cols = d, or d | dv << 16 */
   INTENT_HIP_OP_ATTENTION_BWD_DELTA = 8, /* cols = head dimension */
   INTENT_HIP_OP_ATTENTION_BWD_DQ = 9,    /* rows = batch * query heads * queries, cols = head dimension */
   INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10, /* rows = batch * key heads * keys, cols = head dimension */
@@ -139,7 +139,7 @@ int intent_hip_gemm_f32(const float *a, const float *b, float *c, int64_t m, int
  * normalize_attention_summary (:417-425).
  * q [b,h,sq,d], k [b,h,sk,d], v [b,h,sk,dv], o [b,h,sq,dv]; strides[16] holds the four
  * element strides of q, k, v, o in that order (the last of each must be 1).
- * causal: key j is valid for query i iff i >= j (absolute indices). Supports d = dv = 64 or 128. */
+ * causal: key j is valid for query i iff i >= j (absolute indices). d and dv are each 64 or 128. */
 int intent_hip_attention_fwd_f16(const void *q, const void *k, const void *v, void *o,
                                  int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d,
                                  int64_t dv, const int64_t strides[16], float scale, int causal,

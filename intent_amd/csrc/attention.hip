@@ -9,7 +9,7 @@
 // The key axis is folded in 64-key chunks; the running maximum replaces the chunk maximum
 // before P is rounded (online softmax), which the 16-bit tolerance covers.
 //
-// Design (d = dv = 128 or 64):
+// Design (d and dv each 64 or 128, independently):
 //   * a workgroup owns 256 query rows of one (batch, head): 8 waves x 32 rows, two per SIMD;
 //     key tiles of 64 keys stream through LDS in two stages (K: 16 KB, V: 16 KB per stage),
 //     written by global_load_lds_dwordx4 while the previous tile is consumed. Each K/V tile
@@ -102,7 +102,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // raised when a tile's maximum exceeds it by more than this, so weights stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename E, int D>
+template <typename E, int D, int DV>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__restrict__ Q,
                                                                   const uint16_t *__restrict__ K,
                                                                   const uint16_t *__restrict__ V,
@@ -110,12 +110,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
                                                                   int head_group, int sq, int sk, Geometry g,
                                                                   float scale, int causal, int q_blocks) {
   typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
-  constexpr int kD = D;
-  constexpr int kRowChunks = kD / 8;          // 16-byte chunks per K or V row
-  constexpr int kKChunks = kBK * kRowChunks;  // 16-byte chunks of a K tile (row = key)
-  constexpr int kVChunks = kBK * kRowChunks;  // 16-byte chunks of a V tile (row = key)
+  constexpr int kD = D, kDV = DV;
+  constexpr int kKRow = kD / 8;               // 16-byte chunks per K row
+  constexpr int kVRow = kDV / 8;              // 16-byte chunks per V row
+  constexpr int kKChunks = kBK * kKRow;       // 16-byte chunks of a K tile (row = key)
+  constexpr int kVChunks = kBK * kVRow;       // 16-byte chunks of a V tile (row = key)
   constexpr int kStageChunks = kKChunks + kVChunks;
-  static_assert(kKChunks % kThreads == 0, "DMA split");
+  static_assert(kKChunks % kThreads == 0 && kVChunks % kThreads == 0, "DMA split");
   __shared__ uint4 lds[2 * kStageChunks];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in a scalar register
@@ -149,29 +150,35 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const int tiles = (k_end + kBK - 1) / kBK;
   const int wave_q_last = min(wq0 + 31, sq - 1);
 
-  // DMA roles: each wave moves D / 32 x 64 chunks of K and of V per tile. LDS chunk slot p of a
-  // tile is row p / (D / 8) (a key), physical chunk p % (D / 8); rows store logical chunk
-  // pc ^ swz(key). Keys beyond sk read row sk - 1 (finite data that the mask zeroes out; V tail
-  // rows are cleared in LDS below).
+  // DMA roles: each wave moves D / 32 x 64 chunks of K and DV / 32 x 64 chunks of V per tile.
+  // LDS chunk slot p of a tile is row p / (row chunks) (a key), physical chunk p % (row chunks);
+  // rows store logical chunk pc ^ swz(key). Keys beyond sk read row sk - 1 (finite data that the
+  // mask zeroes out; V tail rows are cleared in LDS below).
   auto issue = [&](int kt) {
     uint4 *stage = lds + (kt & 1) * kStageChunks;
     const int key0 = kt * kBK;
 #pragma unroll
     for (int i = 0; i < kKChunks / kThreads; ++i) {
       const int p = (wave * (kKChunks / kThreads) + i) * 64 + lane;
-      const int row = p / kRowChunks, pc = p % kRowChunks;
+      const int row = p / kKRow, pc = p % kKRow;
       const int key = min(key0 + row, sk - 1);
       __builtin_amdgcn_global_load_lds(kbase + static_cast<int64_t>(key) * g.ks[2] + (pc ^ swz_k(D, row)) * 8,
                                        (lds_void_t *)(stage + (wave * (kKChunks / kThreads) + i) * 64), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + static_cast<int64_t>(key) * g.vs[2] + (pc ^ swz_v(D, row)) * 8,
-                                       (lds_void_t *)(stage + kKChunks + (wave * (kKChunks / kThreads) + i) * 64), 16,
+    }
+#pragma unroll
+    for (int i = 0; i < kVChunks / kThreads; ++i) {
+      const int p = (wave * (kVChunks / kThreads) + i) * 64 + lane;
+      const int row = p / kVRow, pc = p % kVRow;
+      const int key = min(key0 + row, sk - 1);
+      __builtin_amdgcn_global_load_lds(vbase + static_cast<int64_t>(key) * g.vs[2] + (pc ^ swz_v(DV, row)) * 8,
+                                       (lds_void_t *)(stage + kKChunks + (wave * (kVChunks / kThreads) + i) * 64), 16,
                                        0, 0);
     }
   };
 
-  f32x16_t acc[kD / 32];   // O^T: dv tile mt (32 dv) x 32 queries
+  f32x16_t acc[kDV / 32];   // O^T: dv tile mt (32 dv) x 32 queries
 #pragma unroll
-  for (int mt = 0; mt < kD / 32; ++mt)
+  for (int mt = 0; mt < kDV / 32; ++mt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[mt][e] = 0.0f;
   float row_max = -INFINITY;   // running maximum of valid scaled scores (exp2 domain)
@@ -194,8 +201,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     if (key0 + kBK > sk) {
       // Tail tile: clear the V rows past the last key so masked weights meet zeros.
       uint4 *vt = const_cast<uint4 *>(sk_tile + kKChunks);
-      for (int c = tid; c < kBK * kRowChunks; c += kThreads)
-        if (key0 + c / kRowChunks >= sk) vt[c] = make_uint4(0, 0, 0, 0);
+      for (int c = tid; c < kVChunks; c += kThreads)
+        if (key0 + c / kVRow >= sk) vt[c] = make_uint4(0, 0, 0, 0);
       __syncthreads();
     }
     const bool active = !causal || key0 <= wave_q_last;      // wave-uniform
@@ -213,7 +220,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
           const int row = st * 32 + frag_row;
-          kf[buf][st] = __builtin_bit_cast(f16x8_t, sk_tile[row * kRowChunks + ((ks * 2 + half) ^ swz_k(D, row))]);
+          kf[buf][st] = __builtin_bit_cast(f16x8_t, sk_tile[row * kKRow + ((ks * 2 + half) ^ swz_k(D, row))]);
         }
       };
       read_k(0, 0);
@@ -254,7 +261,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
       row_max = new_max;
       row_den *= alpha;
 #pragma unroll
-      for (int mt = 0; mt < kD / 32; ++mt)
+      for (int mt = 0; mt < kDV / 32; ++mt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[mt][e] *= alpha;
     }
@@ -272,17 +279,17 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     // [key][dv] layout through ds_read_b64_tr_b16: read r of slice sl gives the lane keys
     // 16 sl + 8 r + 4 half + 0..3 of its dv.
     {
-      f16x8_t vf[2][kD / 32];
+      f16x8_t vf[2][kDV / 32];
       auto read_v = [&](int sl, int buf) {
 #pragma unroll
-        for (int mt = 0; mt < kD / 32; ++mt) {
+        for (int mt = 0; mt < kDV / 32; ++mt) {
           i16x4_t parts[2];
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
             const int key = sl * 16 + 8 * r + v_key;
             const int dv = mt * 32 + v_dv;
-            const int chunk = (dv >> 3) ^ swz_v(D, key);
-            parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kD + chunk * 8 + (dv & 7)));
+            const int chunk = (dv >> 3) ^ swz_v(DV, key);
+            parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kDV + chunk * 8 + (dv & 7)));
           }
           vf[buf][mt] = __builtin_bit_cast(f16x8_t, parts);
         }
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
       for (int sl = 0; sl < 4; ++sl) {
         if (sl + 1 < 4) read_v(sl + 1, (sl + 1) & 1);
 #pragma unroll
-        for (int mt = 0; mt < kD / 32; ++mt)
+        for (int mt = 0; mt < kDV / 32; ++mt)
           acc[mt] = Elem<E>::mma(vf[sl & 1][mt], pf[sl], acc[mt]);
       }
       __builtin_amdgcn_s_setprio(0);
@@ -307,7 +314,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const float inv = valid ? __builtin_amdgcn_rcpf(den) : 0.0f;
   uint16_t *orow = obase + static_cast<int64_t>(lane_q) * g.os[2];
 #pragma unroll
-  for (int mt = 0; mt < kD / 32; ++mt)
+  for (int mt = 0; mt < kDV / 32; ++mt)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       const uint32_t w0 = pack2<E>(acc[mt][4 * gq] * inv, acc[mt][4 * gq + 1] * inv);
@@ -318,14 +325,24 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
 
 }  // namespace
 
-int attention_resources(int dtype, int64_t sq, int64_t d, IntentHipKernelResources *out) {
+// The kernel of a (dtype, d, dv) triple; d and dv are each 64 or 128 (checked by the callers).
+template <typename E>
+const void *attention_kernel(int64_t d, int64_t dv) {
+  if (d == 64) return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 64, 64>)
+                               : reinterpret_cast<const void *>(&attention_fwd<E, 64, 128>);
+  return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 128, 64>)
+                  : reinterpret_cast<const void *>(&attention_fwd<E, 128, 128>);
+}
+
+int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, IntentHipKernelResources *out) {
   (void)sq;
-  const auto describe = [out](const void *kernel, const char *name) { return describe_kernel(kernel, name, kThreads, out); };
-  if (dtype == INTENT_HIP_BF16)
-    return d == 64 ? describe(reinterpret_cast<const void *>(&attention_fwd<__bf16, 64>), "attention_fwd<bf16,64>")
-                   : describe(reinterpret_cast<const void *>(&attention_fwd<__bf16, 128>), "attention_fwd<bf16,128>");
-  return d == 64 ? describe(reinterpret_cast<const void *>(&attention_fwd<_Float16, 64>), "attention_fwd<f16,64>")
-                 : describe(reinterpret_cast<const void *>(&attention_fwd<_Float16, 128>), "attention_fwd<f16,128>");
+  if ((d != 64 && d != 128) || (dv != 64 && dv != 128))
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernels take d, dv in {64, 128}");
+  char name[48];
+  snprintf(name, sizeof name, "attention_fwd<%s,%d,%d>", dtype == INTENT_HIP_BF16 ? "bf16" : "f16",
+           static_cast<int>(d), static_cast<int>(dv));
+  const void *kernel = dtype == INTENT_HIP_BF16 ? attention_kernel<__bf16>(d, dv) : attention_kernel<_Float16>(d, dv);
+  return describe_kernel(kernel, name, kThreads, out);
 }
 
 }  // namespace intent_hip
@@ -333,6 +350,13 @@ int attention_resources(int dtype, int64_t sq, int64_t d, IntentHipKernelResourc
 using namespace intent_hip;
 
 namespace {
+
+template <typename E, int D, int DV>
+void launch_fwd(dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O,
+                int heads, int head_group, int sq, int sk, const Geometry &g, float scale, int causal, int q_blocks) {
+  attention_fwd<E, D, DV><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, O, heads, head_group, sq, sk, g, scale, causal,
+                                                          q_blocks);
+}
 
 int launch_attention(int dtype, const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
                      int64_t head_group, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
@@ -345,8 +369,8 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   if (dtype != INTENT_HIP_F16 && dtype != INTENT_HIP_BF16)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "attention dtype code %d (1 = f16, 2 = bf16)", dtype);
   if (batch == 0 || heads == 0 || sq == 0 || dv == 0) return INTENT_HIP_OK;
-  if ((d != 64 && d != 128) || dv != d)
-    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernel supports D = DV = 64 or 128 (got d=%lld, dv=%lld)",
+  if ((d != 64 && d != 128) || (dv != 64 && dv != 128))
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernels take D and DV in {64, 128} (got d=%lld, dv=%lld)",
                 static_cast<long long>(d), static_cast<long long>(dv));
   if (strides == nullptr || q == nullptr || o == nullptr || (sk > 0 && (k == nullptr || v == nullptr)))
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
@@ -373,20 +397,24 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   const auto *Kp = static_cast<const uint16_t *>(k);
   const auto *Vp = static_cast<const uint16_t *>(v);
   auto *Op = static_cast<uint16_t *>(o);
-  const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+  const dim3 grid(static_cast<unsigned>(blocks));
   const hipStream_t s = as_stream(stream);
   const int h = static_cast<int>(heads), grp = static_cast<int>(head_group);
   const int iq = static_cast<int>(sq), ik = static_cast<int>(sk), c = causal ? 1 : 0;
   if (dtype == INTENT_HIP_BF16) {
     if (d == 64)
-      attention_fwd<__bf16, 64><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+      dv == 64 ? launch_fwd<__bf16, 64, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
+               : launch_fwd<__bf16, 64, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
     else
-      attention_fwd<__bf16, 128><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+      dv == 64 ? launch_fwd<__bf16, 128, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
+               : launch_fwd<__bf16, 128, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
   } else {
     if (d == 64)
-      attention_fwd<_Float16, 64><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+      dv == 64 ? launch_fwd<_Float16, 64, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
+               : launch_fwd<_Float16, 64, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
     else
-      attention_fwd<_Float16, 128><<<grid, block, 0, s>>>(Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
+      dv == 64 ? launch_fwd<_Float16, 128, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
+               : launch_fwd<_Float16, 128, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
   }
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd");
   return INTENT_HIP_OK;

@@ -250,9 +250,9 @@ def _attention_f16(lib, bound, constexprs, device):
     args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, heads, sq, sk, d, dv, strides,
             float(scale), int(causal))
     return Launch("intent_hip_attention_fwd_f16", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
-                  tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("sk", sk), ("d", d),
+                  tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("sk", sk), ("d", d), ("dv", dv),
                                  ("causal", causal)),
-                  lambda: lib.kernel_resources(OP_ATTENTION_FWD_F16, F16, sq, d))
+                  lambda: lib.kernel_resources(OP_ATTENTION_FWD_F16, F16, sq, d | (dv << 16)))
 
 
 def _attention_grouped(dtype_code):
@@ -281,8 +281,8 @@ def _attention_grouped(dtype_code):
                 sk, d, dv, strides, float(scale), int(causal))
         return Launch("intent_hip_attention_fwd", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
                       tuple(after), (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq),
-                                     ("sk", sk), ("d", d), ("causal", causal)),
-                      lambda: lib.kernel_resources(OP_ATTENTION_FWD, dtype_code, sq, d))
+                                     ("sk", sk), ("d", d), ("dv", dv), ("causal", causal)),
+                      lambda: lib.kernel_resources(OP_ATTENTION_FWD, dtype_code, sq, d | (dv << 16)))
     return plan
 
 

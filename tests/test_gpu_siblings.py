@@ -244,3 +244,39 @@ def test_gqa_head_mismatch_is_value_error(device):
     with pytest.raises(ValueError):
         intent.jit(flash_gqa_attention_fwd, backend="hip", constexprs={"HEAD_GROUP": 2, "CAUSAL": True}).run(
             q, k, k, 1.0)
+
+
+@pytest.mark.parametrize("d,dv", [(128, 64), (64, 128)])
+@pytest.mark.parametrize("kind,group,causal", [("f16", 1, True), ("f16", 3, False), ("bf16", 2, True),
+                                               ("bf16", 1, False)])
+def test_attention_value_width_differs_from_key_width(device, d, dv, kind, group, causal):
+    """D and DV chosen independently from {64, 128} (flash_attention_fwd, flash_gqa_attention_fwd and
+    flash_attention_bf16_fwd declare them as separate symbols): against the oracle, and with DV = 128
+    split along the value columns, bit for bit against the DV = 64 kernel on each half (the weights do
+    not depend on V)."""
+    from intent_amd.examples.kernels.streaming.attention import flash_attention_fwd
+
+    announce("attention d != dv", d, dv, kind, group, causal)
+    rng = np.random.default_rng(d * 7 + dv + group)
+    hq = 6 if group == 3 else 4
+    q = inputs.normal(rng, (2, hq, 300, d), kind)
+    k = inputs.normal(rng, (2, hq // group, 333, d), kind)
+    v = inputs.normal(rng, (2, hq // group, 333, dv), kind)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    bf16 = kind == "bf16"
+    defn = flash_attention_bf16_fwd if bf16 else flash_gqa_attention_fwd
+    o = run_attention(device, defn, q, k, v, scale, group, causal, bf16)
+    assert o.shape == (2, hq, 300, dv)
+    want = oracle.attention_fwd(q, k, v, scale, causal, head_group=group, storage="bf16" if bf16 else None)
+    if bf16:
+        assert_16bit(bf16_to_f32(o), bf16_to_f32(want), rel=4e-2, abs_=2e-2)
+    else:
+        assert_16bit(o, want)
+    if group == 1 and not bf16:
+        plain = intent.jit(flash_attention_fwd, backend="hip", constexprs={"CAUSAL": causal}).run(
+            t(q, device), t(k, device), t(v, device), scale).cpu().numpy()
+        assert (plain.view(np.uint16) == o.view(np.uint16)).all()
+    if dv == 128:
+        for part in (slice(0, 64), slice(64, 128)):
+            piece = run_attention(device, defn, q, k, np.ascontiguousarray(v[..., part]), scale, group, causal, bf16)
+            assert (piece.view(np.uint16) == o[..., part].view(np.uint16)).all()

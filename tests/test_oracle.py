@@ -317,6 +317,35 @@ def test_attention_grouped_equals_repeated_heads():
     assert (wrong.view(np.uint16) != grouped.view(np.uint16)).any()         # the head mapping matters
 
 
+@pytest.mark.parametrize("d,dv", [(128, 64), (64, 128)])
+@pytest.mark.parametrize("storage", [None, "bf16"])
+def test_attention_value_width_independent_of_key_width(d, dv, storage):
+    """DV != D: against float64 softmax attention, and split along the value columns. The weights do
+    not depend on V, so the first 64 columns of an output with DV = 128 equal, bit for bit, the
+    output with V cut to its first 64 columns (and the same for the last 64)."""
+    g = np.random.default_rng(d + 3 * dv + (storage is None))
+    kind = storage or "f16"
+    q = inputs.normal(g, (1, 4, 37, d), kind)
+    k = inputs.normal(g, (1, 2, 45, d), kind)
+    v = inputs.normal(g, (1, 2, 45, dv), kind)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    o = oracle.attention_fwd(q, k, v, scale, True, head_group=2, storage=storage)
+    assert o.shape == (1, 4, 37, dv)
+    as64 = (lambda a: oracle.bf16_bits_to_float(a).astype(np.float64)) if storage else (lambda a: a.astype(np.float64))
+    heads = np.arange(4) // 2
+    s = np.einsum("bhqd,bhkd->bhqk", as64(q), as64(k)[:, heads]) * scale
+    s[..., np.triu_indices(37, 1, 45)[0], np.triu_indices(37, 1, 45)[1]] = -np.inf
+    w = np.exp(s - s.max(-1, keepdims=True))
+    want = np.einsum("bhqk,bhkd->bhqd", w / w.sum(-1, keepdims=True), as64(v)[:, heads])
+    tol = (4e-2, 2e-2) if storage else (2e-2, 1e-2)
+    assert np.all(np.abs(as64(o) - want) <= tol[0] * np.abs(want) + tol[1])
+    if dv == 128:
+        for part in (slice(0, 64), slice(64, 128)):
+            piece = oracle.attention_fwd(q, k, np.ascontiguousarray(v[..., part]), scale, True, head_group=2,
+                                         storage=storage)
+            assert (piece.view(np.uint16) == o[..., part].view(np.uint16)).all()
+
+
 def test_attention_bf16_first_causal_row():
     g = np.random.default_rng(15)
     q, k, v = (inputs.normal(g, (1, 2, 20, 128), "bf16") for _ in range(3))
