@@ -6,7 +6,8 @@ backward in f16 storage with f32 math, 16384 x 4096 — one step = stable_softma
 then softmax_backward_f16 through prepared intent.jit calls; throughput = algorithmic
 bytes (fwd 4*M*N + bwd 6*M*N = 671,088,640 B) / measured step time (K eager steps between HIP
 events; the same step as hipGraph replays is reported beside it), inputs resident in HBM. `roofline` is the dominant kernel (the backward), timed with HIP events on the launch
-stream between the launches of the real fwd/bwd sequence. `operators` carries every other configuration: the median
+stream between the launches of the real fwd/bwd sequence, with the same kernel timed cold (after a MALL flush)
+beside it as `cold_backward`. `operators` carries every other configuration: the median
 of 33 cold calls (first dropped, 512 MiB write-then-read flush of the 256 MB MALL before each), events around the
 launches queued behind the flush so that they bracket the kernels as the reference's in-graph events do
 (operator_ms); the median of graph replays timed around graph.replay() is kept beside it as graph_ms. `cpu_baseline`
@@ -718,6 +719,13 @@ def main():
                                "frac": round(fwd_bytes / fwd_ms / 1e6 / HBM_PEAK_GBS, 4),
                                "traffic": read_traffic("softmax_fwd_f16_16384x4096")}}
     log(f"bwd kernel {bwd_ms:.4f} ms ({achieved:.1f} GB/s), fwd kernel {fwd_ms:.4f} ms")
+    # The same backward launch cold: a 512 MiB write-then-read flush of the MALL before each call, so
+    # y and dy come from HBM rather than from the MALL lines the forward just wrote.
+    cold_ms = operator_ms(bwd.launch, Flush(device))
+    roofline["cold_backward"] = {"avg_launch_ms": round(cold_ms, 5), "achieved": round(bwd_bytes / cold_ms / 1e6, 1),
+                                 "frac": round(bwd_bytes / cold_ms / 1e6 / HBM_PEAK_GBS, 4),
+                                 "timing": "median of cold calls, 512 MiB flush before each"}
+    log(f"bwd kernel cold {cold_ms:.4f} ms ({bwd_bytes / cold_ms / 1e6:.1f} GB/s)")
 
     operators = []
     if not args.no_operators:
