@@ -3,7 +3,7 @@
 // Semantics (python/intent/examples/kernels/sparse/csr_spmv.py:11-29): for every row,
 // acc = 0.0f; for nz in [off[r], off[r+1]) in order: acc = acc + values[nz] * x[col[nz]];
 // y[r] = acc. Positions are absolute, so off[0] may be above 0 and off[R] below nnz (a row slice
-// of a larger CSR). Index traversal is exact. Rows of up to 8 nonzeros are folded by one lane in
+// of a larger CSR). Index traversal is exact. Rows of up to 4 nonzeros are folded by one lane in
 // order, with each product rounded before the add (no fused multiply-add): that reproduces the
 // ordered loop bit for bit. Longer rows are split into pieces whose partial sums are combined in a
 // fixed, data-independent order, a reassociation of the fold.
@@ -17,10 +17,11 @@
 //   * 5 to 127: 16 lanes per row (spmv_rows);
 //   * medium (128 to big - 1): the row is cut at the boundaries of 8 column windows of C / 8
 //     columns, the share of x one XCD's 4 MB L2 holds, and the piece in window w runs on XCD w
-//     (hardware workgroup h runs on XCD h % 8), so its gathers hit that L2 (spmv_pieces<false>);
-//   * large (big = max(128, 16 S) or more): the row is cut at the boundaries of S slices of 16384
-//     columns; a workgroup stages one slice of x (64 KB) in LDS and runs that slice's piece of
-//     many large rows, gathering from LDS (spmv_pieces<true>).
+//     (hardware workgroup h runs on XCD h % 8), so its gathers hit that L2 (spmv_slices<false>);
+//   * large (big = max(128, 32 S) or more): the row is cut at the boundaries of S slices of 32768
+//     columns; a workgroup stages one slice of x (128 KB) in LDS and runs that slice's piece of
+//     many large rows, gathering from LDS (spmv_slices<true>).
+// Each piece runs on one wave: coalesced loads of its columns and values, one reduction per piece.
 // The medium and large row lists are built without atomics: spmv_count counts each 1024-row
 // block's rows of each class, spmv_scan (one workgroup) turns the counts into list offsets, and
 // spmv_rows writes each block's rows at its offset in row order. (Wave-level atomics on two list
@@ -41,9 +42,9 @@ constexpr int kGroup = 16;
 constexpr int kRowsPerThread = 4;   // spmv_count / spmv_rows: 1024 rows per 256-thread workgroup
 constexpr int kBlockRows = 256 * kRowsPerThread;
 constexpr int kWindows = 8;         // one column window per XCD
-constexpr int kSliceCols = 16384;   // 64 KB of x in LDS per workgroup
-constexpr int kTargetTiles = 1024;  // slice workgroups per launch (four per CU)
-constexpr int kWindowTiles = 64;    // medium-row tiles per window (two per CU of the XCD)
+constexpr int kSliceCols = 32768;   // 128 KB of x in LDS per workgroup
+constexpr int kSliceTiles = 256;    // slice workgroups per launch: one per CU, all resident at once
+constexpr int kWindowTiles = 32;    // medium-row workgroups per window (one per CU of the XCD)
 constexpr int kSearchSteps = 8;     // interpolation steps per cut
 
 inline size_t align256(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
@@ -63,7 +64,8 @@ struct Plan {
 };
 
 int64_t slice_count(int64_t cols) { return cols > 0 ? (cols + kSliceCols - 1) / kSliceCols : 1; }
-int64_t big_length(int64_t slices) { return slices * 16 > kGroupRow ? slices * 16 : kGroupRow; }
+// Rows of at least big = max(128, 32 S) nonzeros (32 per slice on average) are large.
+int64_t big_length(int64_t slices) { const int64_t l = slices * (kSliceCols / 1024); return l > kGroupRow ? l : kGroupRow; }
 int64_t mid_capacity(int64_t rows, int64_t nnz) { return nnz / kGroupRow < rows ? nnz / kGroupRow : rows; }
 int64_t big_capacity(int64_t rows, int64_t nnz, int64_t slices) {
   const int64_t by_nnz = nnz / big_length(slices);
@@ -410,220 +412,101 @@ __global__ __launch_bounds__(256) void spmv_bounds(const int32_t *__restrict__ o
   }
 }
 
-// Pieces of listed rows for one part (a window of the medium rows, or a slice of the large rows),
-// run by a workgroup "tile" over the list rows i = k + K j. Per batch of up to 1024 rows the pieces
-// are laid end to end (prefix sums in LDS) and the 8 waves take equal ranges of that stream, 64
-// consecutive nonzeros per chunk and 8 chunks per step, so loads are coalesced and many are in
-// flight whatever the row structure. A wave-uniform cursor gives every lane its row: each step
-// reads the next 8 row starts once, and a lane counts the starts at or below its position. Each
-// lane accumulates the products of the wave's current row; a row's sum is one wave reduction when
-// the wave leaves the row. Sums of rows that end inside the wave's range are written at once; the
-// pieces of rows that cross a range boundary are added in wave order after the batch.
-// kLds: the slice's columns of x are staged in LDS (large rows); otherwise x is read from global
-// memory, and workgroup h runs on XCD h % 8, whose L2 holds window h % 8 (medium rows).
-constexpr int kTileThreads = 512;
-constexpr int kTileWaves = kTileThreads / 64;
-constexpr int kBatchRows = 1024;
-constexpr int kStep = 8;
-
+// Pieces of listed rows for one part: a slice of the large rows (kLds, workgroups part * K + k; the
+// slice's kSliceCols columns of x are staged in LDS) or a window of the medium rows (workgroup h
+// takes window h % 8 and runs on XCD h % 8, whose L2 holds that window of x). Wave w takes the
+// pieces of list rows i = k + K t for t = w, w + 16, ..., one piece at a time: lanes stride the
+// piece 64 nonzeros at a time, kUnroll strides loaded together (coalesced), and the piece's sum is
+// one wave reduction in a fixed order. While a piece is summed, the next piece's cuts and first
+// kUnroll strides are already in flight. An entry outside the staged slice (possible with an
+// inexact cut) reads x from global memory.
+constexpr int kSliceThreads = 1024;
+constexpr int kSliceWaves = kSliceThreads / 64;
+constexpr int kUnroll = 4;    // 64-nonzero strides of a piece loaded together
 template <bool kLds>
-__global__ __launch_bounds__(kTileThreads, 2) void spmv_pieces(const int32_t *__restrict__ col,
-                                                               const float *__restrict__ val,
-                                                               const float *__restrict__ x, int32_t cols,
-                                                               const int32_t *__restrict__ cuts, int cut_stride,
-                                                               float *__restrict__ parts, int part_stride,
-                                                               const int32_t *__restrict__ count, int capacity) {
+__global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__restrict__ col,
+                                                            const float *__restrict__ val,
+                                                            const float *__restrict__ x, int32_t cols,
+                                                            const int32_t *__restrict__ cuts, int cut_stride,
+                                                            float *__restrict__ parts, int part_stride,
+                                                            const int32_t *__restrict__ count, int capacity) {
   __shared__ float sx[kLds ? kSliceCols : 1];
-  __shared__ int32_t s_begin[kBatchRows + 1];
-  __shared__ int32_t s_pre[kBatchRows + 1];
-  __shared__ int32_t s_wave_total[kTileWaves];
-  __shared__ int32_t s_piece_row[kTileWaves][2];
-  __shared__ float s_piece_sum[kTileWaves][2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int K = kLds ? static_cast<int>(gridDim.x) / part_stride : static_cast<int>(gridDim.x) / kWindows;
-  const int part = kLds ? static_cast<int>(blockIdx.x) / K : static_cast<int>(blockIdx.x % kWindows);
-  const int k = kLds ? static_cast<int>(blockIdx.x) % K : static_cast<int>(blockIdx.x / kWindows);
+  const int K = static_cast<int>(gridDim.x) / part_stride;
+  // Slices: workgroups part * K + k. Windows: part = h % 8, so window w's pieces run on XCD w.
+  const int part = kLds ? static_cast<int>(blockIdx.x) / K : static_cast<int>(blockIdx.x % part_stride);
+  const int k = kLds ? static_cast<int>(blockIdx.x) % K : static_cast<int>(blockIdx.x / part_stride);
   const int n_rows = min(*count, capacity);
   if (n_rows <= k) return;   // workgroup-uniform
   const int64_t c0 = kLds ? static_cast<int64_t>(part) * kSliceCols : 0;
   const int width = kLds ? static_cast<int>(min(static_cast<int64_t>(kSliceCols), cols - c0)) : 0;
-  if constexpr (kLds) {   // every load of the slice is issued before the first store to LDS
-    constexpr int kPer = kSliceCols / kTileThreads;
+  if constexpr (kLds) {
+    constexpr int kPer = kSliceCols / kSliceThreads;
     float staged[kPer];
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
-      const int c = tid + kTileThreads * q;
+      const int c = tid + kSliceThreads * q;
       staged[q] = c < width ? x[c0 + c] : 0.0f;
     }
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) sx[tid + kTileThreads * q] = staged[q];
+    for (int q = 0; q < kPer; ++q) sx[tid + kSliceThreads * q] = staged[q];
   }
-  auto xval = [&](int32_t c) {
-    if constexpr (kLds) {
-      const int64_t local = static_cast<int64_t>(c) - c0;
-      if (static_cast<uint64_t>(local) < static_cast<uint64_t>(width)) return sx[local];
-    }
-    return x[clamp_col(c, cols)];
-  };
-  auto slot = [&](int64_t t) { return (k + static_cast<int64_t>(K) * t) * part_stride + part; };
+  if constexpr (kLds) __syncthreads();
   const int n_tile = (n_rows - k + K - 1) / K;
-  for (int t0 = 0; t0 < n_tile; t0 += kBatchRows) {
-    const int nb = min(kBatchRows, n_tile - t0);
-    __syncthreads();   // the previous batch is done with the LDS arrays
-    // Piece lengths (two rows per thread) and their exclusive prefix sums.
-    int len2[2] = {0, 0};
-    int32_t cb[2], ce[2];
+  auto cut_at = [&](int t, int side) {
+    return __builtin_amdgcn_readfirstlane(cuts[(k + static_cast<int64_t>(K) * t) * cut_stride + part + side]);
+  };
+  auto load_block = [&](int32_t p0, int32_t e, int32_t (&cu)[kUnroll], float (&vu)[kUnroll]) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {   // both rows' cuts are loaded before either is used
-      const int j = 2 * tid + h;
-      const int64_t i = k + static_cast<int64_t>(K) * (t0 + min(j, nb - 1));
-      cb[h] = cuts[i * cut_stride + part];
-      ce[h] = cuts[i * cut_stride + part + 1];
+    for (int u = 0; u < kUnroll; ++u) {
+      const int32_t p = p0 + 64 * u + lane;
+      const bool ok = p < e;
+      cu[u] = ok ? __builtin_nontemporal_load(col + p) : static_cast<int32_t>(c0);
+      vu[u] = ok ? __builtin_nontemporal_load(val + p) : 0.0f;
     }
+  };
+  auto add_block = [&](const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], float acc) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = 2 * tid + h;
-      if (j < nb) {
-        s_begin[j] = cb[h];
-        len2[h] = ce[h] - cb[h];
-        if (ce[h] == cb[h]) parts[slot(t0 + j)] = 0.0f;   // an empty piece
+    for (int u = 0; u < kUnroll; ++u) {
+      float xv;
+      if constexpr (kLds) {
+        const int64_t local = static_cast<int64_t>(cu[u]) - c0;
+        xv = static_cast<uint64_t>(local) < static_cast<uint64_t>(width) ? sx[local] : x[clamp_col(cu[u], cols)];
+      } else {
+        xv = x[clamp_col(cu[u], cols)];
       }
+      acc = fmaf(vu[u], xv, acc);
     }
-    int incl = len2[0] + len2[1];
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int up = __shfl_up(incl, d);
-      incl += lane >= d ? up : 0;
+    return acc;
+  };
+  int t = wave;
+  if (t >= n_tile) return;
+  int32_t b = cut_at(t, 0), e = cut_at(t, 1);
+  int32_t cu[kUnroll], ncu[kUnroll];
+  float vu[kUnroll], nvu[kUnroll];
+  load_block(b, e, cu, vu);
+  int32_t nb = 0, ne = 0;
+  if (t + kSliceWaves < n_tile) { nb = cut_at(t + kSliceWaves, 0); ne = cut_at(t + kSliceWaves, 1); }
+  while (true) {   // wave-uniform
+    const int tn = t + kSliceWaves;
+    const bool more = tn < n_tile;
+    if (more) load_block(nb, ne, ncu, nvu);   // the next piece's first block, in flight during this one
+    int32_t nnb = 0, nne = 0;
+    if (tn + kSliceWaves < n_tile) { nnb = cut_at(tn + kSliceWaves, 0); nne = cut_at(tn + kSliceWaves, 1); }
+    float acc = add_block(cu, vu, 0.0f);
+    for (int32_t p0 = b + 64 * kUnroll; p0 < e; p0 += 64 * kUnroll) {   // wave-uniform: rest of the piece
+      int32_t cr[kUnroll];
+      float vr[kUnroll];
+      load_block(p0, e, cr, vr);
+      acc = add_block(cr, vr, acc);
     }
-    if (lane == 63) s_wave_total[wave] = incl;
-    __syncthreads();
-    int wave_base = 0;
-    for (int w = 0; w < wave; ++w) wave_base += s_wave_total[w];
-    const int excl = wave_base + incl - len2[0] - len2[1];
-    if (2 * tid < nb) s_pre[2 * tid] = excl;
-    if (2 * tid + 1 < nb) s_pre[2 * tid + 1] = excl + len2[0];
-    if (tid == kTileThreads - 1) {
-      s_pre[nb] = wave_base + incl;   // the total
-      s_begin[nb] = 0;
-    }
-    if (lane < 2) s_piece_row[wave][lane] = -1;
-    __syncthreads();
-    const int total = s_pre[nb];
-    const int v0 = static_cast<int>(static_cast<int64_t>(total) * wave / kTileWaves);
-    const int v1 = static_cast<int>(static_cast<int64_t>(total) * (wave + 1) / kTileWaves);
-    if (v0 < v1) {   // wave-uniform
-      // The row holding v0: the last j with s_pre[j] <= v0 (skips empty pieces).
-      int lo = 0, hi = nb;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_pre[mid] <= v0) lo = mid;
-        else hi = mid - 1;
-      }
-      int cur = lo;     // wave-uniform: row of the running per-lane sums
-      int crow = lo;    // wave-uniform: row holding the first position of the step
-      float acc = 0.0f;
-      auto flush = [&](int j, float sum) {   // wave-uniform
-        const bool before = s_pre[j] < v0, after = s_pre[j + 1] > v1;
-        if (lane == 0) {
-          if (before || after) {
-            s_piece_row[wave][before ? 0 : 1] = j;
-            s_piece_sum[wave][before ? 0 : 1] = sum;
-          } else {
-            parts[slot(t0 + j)] = sum;
-          }
-        }
-      };
-      for (int vs = v0; vs < v1; vs += 64 * kStep) {
-        // Starts of rows crow + 1 .. crow + 8, and position-to-address offsets of rows crow .. crow + 8.
-        int32_t start[kStep], delta[kStep + 1];
+    const float sum = wave_sum(acc);
+    if (lane == 0) parts[(k + static_cast<int64_t>(K) * t) * part_stride + part] = sum;
+    if (!more) break;
+    t = tn;
+    b = nb; e = ne; nb = nnb; ne = nne;
 #pragma unroll
-        for (int m = 0; m <= kStep; ++m) {
-          const int j = crow + m;
-          delta[m] = j < nb ? __builtin_amdgcn_readfirstlane(s_begin[j] - s_pre[j]) : 0;
-          if (m > 0) start[m - 1] = j <= nb ? __builtin_amdgcn_readfirstlane(s_pre[j]) : INT32_MAX;
-        }
-        int rows_u[kStep];
-        int32_t cols_u[kStep];
-        float vals_u[kStep];
-#pragma unroll
-        for (int u = 0; u < kStep; ++u) {
-          const int v = vs + 64 * u + lane;
-          const bool ok = v < v1;
-          int m = 0;
-#pragma unroll
-          for (int q = 0; q < kStep; ++q) m += start[q] <= v ? 1 : 0;
-          int row = crow + m;
-          int32_t off;
-          if (m == kStep && ok) {   // more than eight rows begin in this step: walk on (rare)
-            while (s_pre[row + 1] <= v) ++row;
-            off = s_begin[row] - s_pre[row];
-          } else {
-            off = delta[0];
-#pragma unroll
-            for (int q = 1; q <= kStep; ++q) off = m == q ? delta[q] : off;
-          }
-          rows_u[u] = ok ? row : -1;
-          const int32_t p = ok ? v + off : 0;
-          cols_u[u] = ok ? __builtin_nontemporal_load(col + p) : 0;
-          vals_u[u] = ok ? __builtin_nontemporal_load(val + p) : 0.0f;
-        }
-        {   // the row holding the next step's first position
-          const int next = vs + 64 * kStep;
-          int m = 0;
-#pragma unroll
-          for (int q = 0; q < kStep; ++q) m += start[q] <= next ? 1 : 0;
-          crow += m;
-          if (m == kStep)
-            while (crow < nb && __builtin_amdgcn_readfirstlane(s_pre[crow + 1]) <= next) ++crow;
-        }
-#pragma unroll
-        for (int u = 0; u < kStep; ++u) {
-          if (vs + 64 * u >= v1) break;   // wave-uniform
-          const float prod = rows_u[u] >= 0 ? vals_u[u] * xval(cols_u[u]) : 0.0f;
-          const int first_row = __builtin_amdgcn_readfirstlane(rows_u[u]);
-          const int last_row = __builtin_amdgcn_readlane(rows_u[u], min(63, v1 - 1 - (vs + 64 * u)));
-          if (first_row == last_row) {   // the whole chunk in one row
-            if (first_row != cur) {
-              flush(cur, wave_sum(acc));
-              cur = first_row;
-              acc = 0.0f;
-            }
-            acc += prod;
-          } else {
-            for (int j = first_row; j <= last_row; ++j) {   // wave-uniform
-              const bool mine = rows_u[u] == j;
-              if (__ballot(mine) == 0) continue;
-              if (j != cur) {
-                flush(cur, wave_sum(acc));
-                cur = j;
-                acc = 0.0f;
-              }
-              acc += mine ? prod : 0.0f;
-            }
-          }
-        }
-      }
-      flush(cur, wave_sum(acc));
-    }
-    __syncthreads();
-    // Pieces of rows that cross a wave range boundary, added in wave order.
-    if (tid == 0) {
-      int run = -1;
-      float sum = 0.0f;
-      for (int w = 0; w < kTileWaves; ++w)
-        for (int h = 0; h < 2; ++h) {
-          const int j = s_piece_row[w][h];
-          if (j < 0) continue;
-          if (j == run) {
-            sum += s_piece_sum[w][h];
-          } else {
-            if (run >= 0) parts[slot(t0 + run)] = sum;
-            run = j;
-            sum = s_piece_sum[w][h];
-          }
-        }
-      if (run >= 0) parts[slot(t0 + run)] = sum;
-    }
+    for (int u = 0; u < kUnroll; ++u) { cu[u] = ncu[u]; vu[u] = nvu[u]; }
   }
 }
 
@@ -657,7 +540,7 @@ __global__ __launch_bounds__(256) void spmv_combine(float *__restrict__ y, Plan 
 int spmv_resources(int64_t rows, int64_t nnz, IntentHipKernelResources *out) {
   (void)rows;
   (void)nnz;
-  return describe_kernel(reinterpret_cast<const void *>(&spmv_pieces<true>), "spmv_pieces<true>", kTileThreads, out);
+  return describe_kernel(reinterpret_cast<const void *>(&spmv_slices<true>), "spmv_slices<true>", kSliceThreads, out);
 }
 
 }  // namespace intent_hip
@@ -696,14 +579,14 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   if (plan.cap_mid == 0 && plan.cap_big == 0) return INTENT_HIP_OK;   // no row can be medium or large
   spmv_bounds<<<dim3(1024), dim3(256), 0, s>>>(row_offsets, column_indices, c32, nnz, plan);
   if (plan.cap_mid > 0)
-    spmv_pieces<false><<<dim3(kWindows * kWindowTiles), dim3(kTileThreads), 0, s>>>(
+    spmv_slices<false><<<dim3(kWindows * kWindowTiles), dim3(kSliceThreads), 0, s>>>(
         column_indices, values, x, c32, plan.mid_cuts, kWindows + 1, plan.mid_parts, kWindows, plan.counters + 0,
         plan.cap_mid);
   if (plan.cap_big > 0) {
-    const int K = static_cast<int>((kTargetTiles + plan.slices - 1) / plan.slices);
-    spmv_pieces<true><<<dim3(static_cast<unsigned>(plan.slices) * static_cast<unsigned>(K)), dim3(kTileThreads), 0,
-                        s>>>(column_indices, values, x, c32, plan.big_cuts, plan.slices + 1, plan.big_parts,
-                             plan.slices, plan.counters + 1, plan.cap_big);
+    const int K = static_cast<int>((kSliceTiles + plan.slices - 1) / plan.slices);
+    spmv_slices<true><<<dim3(static_cast<unsigned>(plan.slices) * static_cast<unsigned>(K)), dim3(kSliceThreads), 0,
+                  s>>>(column_indices, values, x, c32, plan.big_cuts, plan.slices + 1, plan.big_parts,
+                       plan.slices, plan.counters + 1, plan.cap_big);
   }
   spmv_combine<<<dim3(128), dim3(256), 0, s>>>(y, plan);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_combine");
