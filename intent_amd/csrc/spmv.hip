@@ -465,19 +465,25 @@ __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__re
       vu[u] = ok ? __builtin_nontemporal_load(val + p) : 0.0f;
     }
   };
-  auto add_block = [&](const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], float acc) {
+  // Products of one block into acc; with kLds, those of entries outside the slice (possible with an
+  // inexact cut) go to `stray` instead, read from global x. The two reads stay separate: written as
+  // one select of an LDS and a global load, hipcc merged them into a generic flat load, which sent
+  // every gather through the vector memory path (125 against 105 us for the large rows).
+  auto add_block = [&](const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], float &acc, float &stray) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      float xv;
       if constexpr (kLds) {
         const int64_t local = static_cast<int64_t>(cu[u]) - c0;
-        xv = static_cast<uint64_t>(local) < static_cast<uint64_t>(width) ? sx[local] : x[clamp_col(cu[u], cols)];
+        const bool in = static_cast<uint64_t>(local) < static_cast<uint64_t>(width);
+        const float xl = sx[in ? local : 0];
+        acc = fmaf(vu[u], in ? xl : 0.0f, acc);
+        if (__builtin_expect(__any(!in), 0)) {   // wave-uniform
+          if (!in) stray = fmaf(vu[u], __builtin_nontemporal_load(x + clamp_col(cu[u], cols)), stray);
+        }
       } else {
-        xv = x[clamp_col(cu[u], cols)];
+        acc = fmaf(vu[u], x[clamp_col(cu[u], cols)], acc);
       }
-      acc = fmaf(vu[u], xv, acc);
     }
-    return acc;
   };
   int t = wave;
   if (t >= n_tile) return;
@@ -493,14 +499,15 @@ __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__re
     if (more) load_block(nb, ne, ncu, nvu);   // the next piece's first block, in flight during this one
     int32_t nnb = 0, nne = 0;
     if (tn + kSliceWaves < n_tile) { nnb = cut_at(tn + kSliceWaves, 0); nne = cut_at(tn + kSliceWaves, 1); }
-    float acc = add_block(cu, vu, 0.0f);
+    float acc = 0.0f, stray = 0.0f;
+    add_block(cu, vu, acc, stray);
     for (int32_t p0 = b + 64 * kUnroll; p0 < e; p0 += 64 * kUnroll) {   // wave-uniform: rest of the piece
       int32_t cr[kUnroll];
       float vr[kUnroll];
       load_block(p0, e, cr, vr);
-      acc = add_block(cr, vr, acc);
+      add_block(cr, vr, acc, stray);
     }
-    const float sum = wave_sum(acc);
+    const float sum = wave_sum(acc + stray);
     if (lane == 0) parts[(k + static_cast<int64_t>(K) * t) * part_stride + part] = sum;
     if (!more) break;
     t = tn;
