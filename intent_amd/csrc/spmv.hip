@@ -431,7 +431,10 @@ __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__re
                                                             float *__restrict__ parts, int part_stride,
                                                             const int32_t *__restrict__ count, int capacity) {
   __shared__ float sx[kLds ? kSliceCols : 1];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // Wave-uniform in a scalar register, so the cuts below are scalar loads (counted by lgkmcnt):
+  // a vector load of them, waited with vmcnt, also waits for the prefetched strides.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = static_cast<int>(gridDim.x) / part_stride;
   // Slices: workgroups part * K + k. Windows: part = h % 8, so window w's pieces run on XCD w.
   const int part = kLds ? static_cast<int>(blockIdx.x) / K : static_cast<int>(blockIdx.x % part_stride);
@@ -456,64 +459,94 @@ __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__re
   auto cut_at = [&](int t, int side) {
     return __builtin_amdgcn_readfirstlane(cuts[(k + static_cast<int64_t>(K) * t) * cut_stride + part + side]);
   };
+  // kUnroll strides of a piece [p0, e). With kLds they load raw: every lane loads (lanes past the end
+  // re-read the piece's last entry, or entry 0 of an empty piece), and add_block masks them where it
+  // uses them. Masked here with a select, hipcc put each load behind a branch on the lane mask, or
+  // placed the masking right after the loads; either way the compiler waited for every load in
+  // flight (vmcnt 0), the next piece's prefetched strides included, before the first gather
+  // (large rows 117 against 104 us). The medium rows' short pieces keep the select, so lanes past
+  // the end load nothing (92 against 98 us).
   auto load_block = [&](int32_t p0, int32_t e, int32_t (&cu)[kUnroll], float (&vu)[kUnroll]) {
+    const int32_t last = e > 0 ? e - 1 : 0;
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int32_t p = p0 + 64 * u + lane;
-      const bool ok = p < e;
-      cu[u] = ok ? __builtin_nontemporal_load(col + p) : static_cast<int32_t>(c0);
-      vu[u] = ok ? __builtin_nontemporal_load(val + p) : 0.0f;
-    }
-  };
-  // Products of one block into acc; with kLds, those of entries outside the slice (possible with an
-  // inexact cut) go to `stray` instead, read from global x. The two reads stay separate: written as
-  // one select of an LDS and a global load, hipcc merged them into a generic flat load, which sent
-  // every gather through the vector memory path (125 against 105 us for the large rows).
-  auto add_block = [&](const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], float &acc, float &stray) {
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
       if constexpr (kLds) {
-        const int64_t local = static_cast<int64_t>(cu[u]) - c0;
-        const bool in = static_cast<uint64_t>(local) < static_cast<uint64_t>(width);
-        const float xl = sx[in ? local : 0];
-        acc = fmaf(vu[u], in ? xl : 0.0f, acc);
-        if (__builtin_expect(__any(!in), 0)) {   // wave-uniform
-          if (!in) stray = fmaf(vu[u], __builtin_nontemporal_load(x + clamp_col(cu[u], cols)), stray);
-        }
-      } else {
-        acc = fmaf(vu[u], x[clamp_col(cu[u], cols)], acc);
+        const int32_t at = p < e ? p : last;
+        cu[u] = __builtin_nontemporal_load(col + at);
+        vu[u] = __builtin_nontemporal_load(val + at);
+      } else {   // short pieces: lanes past the end load nothing
+        cu[u] = p < e ? __builtin_nontemporal_load(col + p) : 0;
+        vu[u] = p < e ? __builtin_nontemporal_load(val + p) : 0.0f;
       }
     }
   };
+  // Products of the block loaded for [p0, e) into acc; with kLds, those of entries outside the slice
+  // (possible with an inexact cut) go to `stray`, read from global x. The LDS and global reads stay
+  // separate: written as one select of an LDS and a global load, hipcc merged them into a generic
+  // flat load, which sent every gather through the vector memory path (125 against 117 us).
+  auto add_block = [&](int32_t p0, int32_t e, const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], float &acc,
+                       float &stray) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const bool ok = p0 + 64 * u + lane < e;
+      const float v = ok ? vu[u] : 0.0f;
+      if constexpr (kLds) {
+        const int32_t local = cu[u] - static_cast<int32_t>(c0);
+        const bool in = !ok || static_cast<uint32_t>(local) < static_cast<uint32_t>(width);
+        const float xl = sx[ok && in ? local : 0];
+        acc = fmaf(v, in ? xl : 0.0f, acc);   // an entry outside the slice adds into stray only
+        if (__builtin_expect(__any(!in), 0)) {   // wave-uniform
+          if (!in) stray = fmaf(v, __builtin_nontemporal_load(x + clamp_col(cu[u], cols)), stray);
+        }
+      } else {
+        acc = fmaf(v, x[clamp_col(ok ? cu[u] : 0, cols)], acc);
+      }
+    }
+  };
+  // This wave's pieces t = wave + 16 i. Two register sets alternate: while piece t is summed from
+  // one, the next piece's first strides load into the other, and the cuts of the piece after next
+  // load (scalar). The loop is unrolled by two so that no set is ever copied into the other, which
+  // would wait for the loads in flight.
   int t = wave;
   if (t >= n_tile) return;
-  int32_t b = cut_at(t, 0), e = cut_at(t, 1);
-  int32_t cu[kUnroll], ncu[kUnroll];
-  float vu[kUnroll], nvu[kUnroll];
-  load_block(b, e, cu, vu);
-  int32_t nb = 0, ne = 0;
-  if (t + kSliceWaves < n_tile) { nb = cut_at(t + kSliceWaves, 0); ne = cut_at(t + kSliceWaves, 1); }
-  while (true) {   // wave-uniform
-    const int tn = t + kSliceWaves;
-    const bool more = tn < n_tile;
-    if (more) load_block(nb, ne, ncu, nvu);   // the next piece's first block, in flight during this one
-    int32_t nnb = 0, nne = 0;
-    if (tn + kSliceWaves < n_tile) { nnb = cut_at(tn + kSliceWaves, 0); nne = cut_at(tn + kSliceWaves, 1); }
+  int32_t b0 = cut_at(t, 0), e0 = cut_at(t, 1);
+  int32_t b1 = 0, e1 = 0;
+  if (t + kSliceWaves < n_tile) { b1 = cut_at(t + kSliceWaves, 0); e1 = cut_at(t + kSliceWaves, 1); }
+  int32_t cu0[kUnroll], cu1[kUnroll];
+  float vu0[kUnroll], vu1[kUnroll];
+  load_block(b0, e0, cu0, vu0);
+  // Piece t: [b, e) summed from (cu, vu). Before that, the next piece's block [nb, ne) starts loading
+  // into (ncu, nvu), and the cuts of piece t + 32 into (fb, fe). Returns whether a next piece exists.
+  auto piece = [&](int32_t b, int32_t e, const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], int32_t nb,
+                   int32_t ne, int32_t (&ncu)[kUnroll], float (&nvu)[kUnroll], int32_t &fb, int32_t &fe) {
+    const bool more = t + kSliceWaves < n_tile;   // wave-uniform
+    if (more) load_block(nb, ne, ncu, nvu);
+    if (t + 2 * kSliceWaves < n_tile) {
+      fb = cut_at(t + 2 * kSliceWaves, 0);
+      fe = cut_at(t + 2 * kSliceWaves, 1);
+    }
     float acc = 0.0f, stray = 0.0f;
-    add_block(cu, vu, acc, stray);
+    add_block(b, e, cu, vu, acc, stray);
     for (int32_t p0 = b + 64 * kUnroll; p0 < e; p0 += 64 * kUnroll) {   // wave-uniform: rest of the piece
       int32_t cr[kUnroll];
       float vr[kUnroll];
       load_block(p0, e, cr, vr);
-      add_block(cr, vr, acc, stray);
+      add_block(p0, e, cr, vr, acc, stray);
     }
     const float sum = wave_sum(acc + stray);
     if (lane == 0) parts[(k + static_cast<int64_t>(K) * t) * part_stride + part] = sum;
-    if (!more) break;
-    t = tn;
-    b = nb; e = ne; nb = nnb; ne = nne;
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) { cu[u] = ncu[u]; vu[u] = nvu[u]; }
+    return more;
+  };
+  while (true) {   // wave-uniform
+    // Piece t in set 0 (cuts b0, e0), piece t + 16 loading into set 1 (cuts b1, e1); the cuts of
+    // piece t + 32 replace b0, e0.
+    if (!piece(b0, e0, cu0, vu0, b1, e1, cu1, vu1, b0, e0)) break;
+    t += kSliceWaves;
+    // Piece t in set 1 (b1, e1), piece t + 16 loading into set 0 (b0, e0); piece t + 32's cuts
+    // replace b1, e1.
+    if (!piece(b1, e1, cu1, vu1, b0, e0, cu0, vu0, b1, e1)) break;
+    t += kSliceWaves;
   }
 }
 
