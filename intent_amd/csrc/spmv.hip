@@ -489,18 +489,21 @@ __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__re
                        float &stray) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
+      // Masked lanes leave the sums as they were (a select after the FMA): multiplying their
+      // stand-in x by zero would turn an inf or NaN elsewhere in x into a NaN here.
       const bool ok = p0 + 64 * u + lane < e;
-      const float v = ok ? vu[u] : 0.0f;
       if constexpr (kLds) {
         const int32_t local = cu[u] - static_cast<int32_t>(c0);
         const bool in = !ok || static_cast<uint32_t>(local) < static_cast<uint32_t>(width);
         const float xl = sx[ok && in ? local : 0];
-        acc = fmaf(v, in ? xl : 0.0f, acc);   // an entry outside the slice adds into stray only
+        const float sum = fmaf(vu[u], xl, acc);
+        acc = ok && in ? sum : acc;   // an entry outside the slice adds into stray only
         if (__builtin_expect(__any(!in), 0)) {   // wave-uniform
-          if (!in) stray = fmaf(v, __builtin_nontemporal_load(x + clamp_col(cu[u], cols)), stray);
+          if (!in) stray = fmaf(vu[u], __builtin_nontemporal_load(x + clamp_col(cu[u], cols)), stray);
         }
       } else {
-        acc = fmaf(v, x[clamp_col(ok ? cu[u] : 0, cols)], acc);
+        const float sum = fmaf(vu[u], x[clamp_col(ok ? cu[u] : 0, cols)], acc);
+        acc = ok ? sum : acc;
       }
     }
   };

@@ -103,6 +103,40 @@ def test_spmv_reference_example_unsorted_columns(device):
     assert (run(device, offsets, columns, ival, ix) == oracle.csr_spmv(offsets, columns, ival, ix)).all()
 
 
+def test_spmv_special_values_stay_in_their_rows(device):
+    """inf, -inf and NaN in x reach only the rows that reference them. They sit at every column a
+    lane past a piece's end can stand in with (column 0, the last column, each 32768-column slice
+    start, each column-window start), and every row class runs beside them: masked lanes must not
+    multiply those entries by zero. A few rows do reference them; their inf or NaN follows IEEE
+    addition in any order."""
+    announce("spmv special values in x")
+    rng = np.random.default_rng(41)
+    cols = 300_000
+    lengths = np.concatenate((rng.integers(1, 5, 2000), rng.integers(5, 128, 2000), rng.integers(128, 304, 1500),
+                              rng.integers(304, 20000, 150)))
+    rng.shuffle(lengths)
+    offsets, columns = inputs.csr_matrix(rng, lengths, cols)
+    window = -(-cols // 8)
+    poison = np.unique(np.concatenate(([0, cols - 1], np.arange(0, cols, 32768), np.arange(0, cols, window))))
+    hit = np.isin(columns, poison)
+    columns[hit] = np.where(columns[hit] == cols - 1, cols - 2, columns[hit] + 1)   # no row references them
+    chosen = rng.choice(np.nonzero(lengths > 0)[0], 60, replace=False)
+    columns[offsets[chosen] + rng.integers(0, lengths[chosen])] = rng.choice(poison, 60)
+    values = inputs.uniform(rng, int(offsets[-1]), -1, 1)
+    x = inputs.uniform(rng, cols, -1, 1)
+    x[poison] = np.resize(np.array([np.inf, -np.inf, np.nan], np.float32), poison.size)
+    y = run(device, offsets, columns, values, x)
+    want = oracle.csr_spmv(offsets, columns, values, x)
+    assert (np.isnan(y) == np.isnan(want)).all()
+    special = ~np.isfinite(want)
+    assert special.sum() >= 40 and (y[special & ~np.isnan(want)] == want[special & ~np.isnan(want)]).all()
+    clean_x = np.where(np.isfinite(x), x, 0).astype(np.float32)
+    y64, mag, rows_len = reference64(offsets, columns, values, clean_x)
+    finite = ~special
+    assert np.isfinite(y[finite]).all()
+    assert np.all(np.abs(y[finite] - y64[finite]) <= 1e-5 * mag[finite] + 1e-38)
+
+
 def test_spmv_block_boundaries(device):
     """Rows whose ends fall exactly on, just before and just after workgroup boundaries."""
     announce("spmv block boundaries")
