@@ -50,7 +50,7 @@ def parse():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
-                                "attention_bwd,attention_bwd_large,paged_decode,spmm")
+                                "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -470,6 +470,46 @@ def op_attention_bf16(device, flush, cpu):
     return _op_attention_grouped(device, flush, cpu, True)
 
 
+def op_varlen_prefill(device, flush, cpu):
+    """flash_varlen_gqa_prefill: 16 packed sequences of 1..4096 rows (uniform, seed 5), 32 query heads
+    over 8 key/value heads, D = 128, causal. FLOPs count each sequence's causal half, as config 4."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.streaming.attention import flash_varlen_gqa_prefill
+
+    rng = np.random.default_rng(5)
+    lengths = rng.integers(1, 4097, 16).astype(np.int32)
+    cu = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
+    total, hq, hk, d = int(cu[-1]), 32, 8, 128
+    q = inputs.normal(rng, (total, hq, d), "f16")
+    k = inputs.normal(rng, (total, hk, d), "f16")
+    v = inputs.normal(rng, (total, hk, d), "f16")
+    scale = float(np.float32(1 / np.sqrt(d)))
+    dev = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    call = intent.jit(flash_varlen_gqa_prefill, backend="hip", constexprs={"HEAD_GROUP": hq // hk}).prepare(
+        dev(q), dev(k), dev(v), dev(lengths), dev(cu), scale)
+    ms = operator_ms(call.launch, flush)
+    flops = int(sum(4 * hq * int(n) * int(n) * d // 2 for n in lengths))
+    out = {"config": f"causal varlen GQA prefill f16, 16 sequences of 1..4096 rows ({total} in all), HQ{hq} HK{hk} "
+                     f"D{d} (flash_varlen_gqa_prefill)", "median_ms": round(ms, 4),
+           "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        first = min(int(lengths[0]), 1024)
+        seconds = cpu_median_seconds(lambda: oracle.attention_varlen_fwd(
+            np.ascontiguousarray(q[:first, :4]), np.ascontiguousarray(k[:first, :1]),
+            np.ascontiguousarray(v[:first, :1]), np.array([0, first], np.int32), scale, True, head_group=4))
+        sample_flops = 4 * 4 * first * first * d // 2
+        out["cpu"] = {"tflops": round(sample_flops / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": f"4 query heads of one key head over the first {first} rows of "
+                                                f"the first sequence"}
+    return out
+
+
 def _op_attention_bwd(device, flush, cpu, large):
     """The three-kernel attention backward (programs/attention_backward.py) as one prepared
     sequence: the reference example's shape (backward/attention.py:7-13: B2, HQ8, HK2, S1024, D64)
@@ -609,7 +649,7 @@ OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_att
              "gemm_f16_relu": op_gemm_f16_relu, "gemm_f32": op_gemm_f32, "linear_f32": op_linear_f32,
              "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
              "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode,
-             "spmm": op_spmm}
+             "spmm": op_spmm, "varlen_prefill": op_varlen_prefill}
 
 
 def read_traffic(name):

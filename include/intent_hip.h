@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 8
+#define INTENT_HIP_ABI_VERSION 9
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -56,7 +56,8 @@ enum IntentHipOperator {
   INTENT_HIP_OP_ATTENTION_BWD_DKDV = 10, /* rows = batch * key heads * keys, cols = head dimension */
   INTENT_HIP_OP_PAGED_DECODE_PARTIALS = 11, /* rows = HEAD_GROUP, cols = head dimension */
   INTENT_HIP_OP_SPLITK_REDUCE = 12,
-  INTENT_HIP_OP_CSR_SPMM_F32 = 13         /* cols = features */
+  INTENT_HIP_OP_CSR_SPMM_F32 = 13,        /* cols = features */
+  INTENT_HIP_OP_ATTENTION_VARLEN = 14     /* packed sequences; dtype F16 or BF16, cols = d | dv << 16 */
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -157,6 +158,24 @@ int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void
                              int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
                              int64_t sk, int64_t d, int64_t dv, const int64_t strides[16],
                              float scale, int causal, void *stream);
+
+/* Fused attention forward over packed sequences: rows cu_seqlens[s] .. cu_seqlens[s+1] of
+ * q [total,hq,d], k [total,hk,d], v [total,hk,dv] and o [total,hq,dv] form sequence s; each
+ * sequence attends within itself (with `causal`, key row <= query row), with the algebra of
+ * intent_hip_attention_fwd.
+ *   flash_varlen_attention_fwd (streaming/attention.py:839-877): hq = hk = 1, CAUSAL constexpr;
+ *   flash_varlen_gqa_prefill   (streaming/attention.py:880-924): key head = query head /
+ *                              head_group, causal.
+ * strides[12]: (row, head, inner) element strides of q, k, v, o; inner must be 1. The offsets are
+ * read on the device (clamped into [0, total]): a one-workgroup kernel lists the
+ * (sequence, query block) work items into the workspace, whose size
+ * intent_hip_attention_varlen_workspace_bytes gives. dtype F16 or BF16; d, dv in {64, 128}. */
+int intent_hip_attention_varlen_workspace_bytes(int64_t sequences, int64_t total, size_t *bytes);
+int intent_hip_attention_varlen_fwd(int dtype, const void *q, const void *k, const void *v,
+                                    const int32_t *cu_seqlens, void *o, int64_t sequences, int64_t total,
+                                    int64_t q_heads, int64_t head_group, int64_t d, int64_t dv,
+                                    const int64_t strides[12], float scale, int causal, void *workspace,
+                                    size_t workspace_bytes, void *stream);
 
 /* Attention backward, f16 storage with f32 arithmetic, head dimension d = 64 or 128
  * (python/intent/examples/kernels/backward/attention.py; the three kernels of

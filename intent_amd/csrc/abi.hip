@@ -98,9 +98,13 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     // cols = d, or d | dv << 16 when dv differs from d.
     case INTENT_HIP_OP_ATTENTION_FWD_F16:
       return attention_resources(INTENT_HIP_F16, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF),
-                                 out);
+                                 false, out);
     case INTENT_HIP_OP_ATTENTION_FWD:
-      return attention_resources(dtype, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), out);
+      return attention_resources(dtype, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), false,
+                                 out);
+    case INTENT_HIP_OP_ATTENTION_VARLEN:
+      return attention_resources(dtype, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), true,
+                                 out);
     case INTENT_HIP_OP_CSR_SPMV_F32: return spmv_resources(rows, cols, out);
     case INTENT_HIP_OP_ATTENTION_BWD_DELTA: return attention_bwd_resources(0, rows, cols, out);
     case INTENT_HIP_OP_ATTENTION_BWD_DQ: return attention_bwd_resources(1, rows, cols, out);

@@ -91,6 +91,16 @@ struct Geometry {
   int64_t qs[4], ks[4], vs[4], os[4];  // element strides (batch, head, row, col)
 };
 
+// Packed sequences (flash_varlen_attention_fwd, flash_varlen_gqa_prefill): rows cu[s] .. cu[s + 1]
+// of q, k, v and the output belong to sequence s. Workgroup item * heads + h runs query head h of
+// items[item] = (sequence, query block); attention_varlen_items writes the items on the device.
+struct Ragged {
+  const int32_t *cu;      // [sequences + 1] row offsets
+  const int2 *items;      // [capacity]
+  const int32_t *count;   // items written
+  int total;              // rows of q, k, v and the output
+};
+
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -102,13 +112,14 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // raised when a tile's maximum exceeds it by more than this, so weights stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename E, int D, int DV>
+template <typename E, int D, int DV, bool kVarlen>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__restrict__ Q,
                                                                   const uint16_t *__restrict__ K,
                                                                   const uint16_t *__restrict__ V,
                                                                   uint16_t *__restrict__ O, int heads,
-                                                                  int head_group, int sq, int sk, Geometry g,
-                                                                  float scale, int causal, int q_blocks) {
+                                                                  int head_group, int sq_all, int sk_all,
+                                                                  Geometry g, float scale, int causal,
+                                                                  int q_blocks, Ragged r) {
   typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
   constexpr int kD = D, kDV = DV;
   constexpr int kKRow = kD / 8;               // 16-byte chunks per K row
@@ -120,15 +131,32 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   __shared__ uint4 lds[2 * kStageChunks];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in a scalar register
-  const int bh_count = gridDim.x / q_blocks;
-  const int qb = q_blocks - 1 - static_cast<int>(blockIdx.x) / bh_count;   // heaviest blocks first
-  const int bh = static_cast<int>(blockIdx.x) % bh_count;
-  const int b = bh / heads, h = bh % heads;
-  const uint16_t *qbase = Q + b * g.qs[0] + h * g.qs[1];
+  int qb, b = 0, h, sq, sk;   // query block, batch entry, query head, rows of q and of k/v
+  int64_t row0 = 0;           // first row of the sequence (packed sequences)
+  if constexpr (kVarlen) {
+    const int item = static_cast<int>(blockIdx.x) / heads;   // the heads of an item are neighbours
+    h = static_cast<int>(blockIdx.x) % heads;
+    if (item >= *r.count) return;                            // the grid covers the item capacity
+    const int2 work = r.items[item];
+    const int start = min(max(r.cu[work.x], 0), r.total);
+    const int end = min(max(r.cu[work.x + 1], start), r.total);
+    qb = work.y;
+    sq = sk = end - start;
+    row0 = start;
+  } else {
+    const int bh_count = gridDim.x / q_blocks;
+    qb = q_blocks - 1 - static_cast<int>(blockIdx.x) / bh_count;   // heaviest blocks first
+    const int bh = static_cast<int>(blockIdx.x) % bh_count;
+    b = bh / heads;
+    h = bh % heads;
+    sq = sq_all;
+    sk = sk_all;
+  }
+  const uint16_t *qbase = Q + b * g.qs[0] + h * g.qs[1] + row0 * g.qs[2];
   const int kh = h / head_group;   // query head h reads key/value head h / head_group
-  const uint16_t *kbase = K + b * g.ks[0] + kh * g.ks[1];
-  const uint16_t *vbase = V + b * g.vs[0] + kh * g.vs[1];
-  uint16_t *obase = O + b * g.os[0] + h * g.os[1];
+  const uint16_t *kbase = K + b * g.ks[0] + kh * g.ks[1] + row0 * g.ks[2];
+  const uint16_t *vbase = V + b * g.vs[0] + kh * g.vs[1] + row0 * g.vs[2];
+  uint16_t *obase = O + b * g.os[0] + h * g.os[1] + row0 * g.os[2];
 
   const int q0 = qb * kBQ;
   const int wq0 = q0 + wave * 32;             // this wave's first query row
@@ -323,25 +351,72 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     }
 }
 
-}  // namespace
-
-// The kernel of a (dtype, d, dv) triple; d and dv are each 64 or 128 (checked by the callers).
-template <typename E>
-const void *attention_kernel(int64_t d, int64_t dv) {
-  if (d == 64) return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 64, 64>)
-                               : reinterpret_cast<const void *>(&attention_fwd<E, 64, 128>);
-  return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 128, 64>)
-                  : reinterpret_cast<const void *>(&attention_fwd<E, 128, 128>);
+// Items of the packed sequences, one workgroup: sequence s has ceil(rows / kBQ) query blocks, listed
+// from the last (the most keys under a causal mask) to the first, sequence after sequence. Offsets
+// are clamped into [0, total] and the list into its capacity, so no offsets can send a later
+// workgroup out of bounds.
+__global__ __launch_bounds__(1024) void attention_varlen_items(const int32_t *__restrict__ cu, int sequences,
+                                                               int total, int2 *__restrict__ items,
+                                                               int32_t *__restrict__ count, int capacity) {
+  __shared__ int s_wave[16];
+  __shared__ int s_carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) s_carry = 0;
+  __syncthreads();
+  for (int s0 = 0; s0 < sequences; s0 += 1024) {
+    const int s = s0 + tid;
+    int blocks = 0;
+    if (s < sequences) {
+      const int start = min(max(cu[s], 0), total);
+      const int end = min(max(cu[s + 1], start), total);
+      blocks = (end - start + kBQ - 1) / kBQ;
+    }
+    int incl = blocks;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int up = __shfl_up(incl, d);
+      incl += lane >= d ? up : 0;
+    }
+    if (lane == 63) s_wave[wave] = incl;
+    __syncthreads();
+    int first = s_carry + incl - blocks;
+    for (int w = 0; w < wave; ++w) first += s_wave[w];
+    for (int j = 0; j < blocks; ++j)
+      if (first + j < capacity) items[first + j] = make_int2(s, blocks - 1 - j);
+    __syncthreads();
+    if (tid == 0) {
+      int sum = s_carry;
+      for (int w = 0; w < 16; ++w) sum += s_wave[w];
+      s_carry = sum;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) *count = min(s_carry, capacity);
 }
 
-int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, IntentHipKernelResources *out) {
+}  // namespace
+
+// The kernel of a (dtype, d, dv, packed) choice; d and dv are each 64 or 128 (checked by the callers).
+template <typename E, bool kVarlen>
+const void *attention_kernel(int64_t d, int64_t dv) {
+  if (d == 64) return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 64, 64, kVarlen>)
+                               : reinterpret_cast<const void *>(&attention_fwd<E, 64, 128, kVarlen>);
+  return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 128, 64, kVarlen>)
+                  : reinterpret_cast<const void *>(&attention_fwd<E, 128, 128, kVarlen>);
+}
+
+int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, bool varlen, IntentHipKernelResources *out) {
   (void)sq;
   if ((d != 64 && d != 128) || (dv != 64 && dv != 128))
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernels take d, dv in {64, 128}");
-  char name[48];
-  snprintf(name, sizeof name, "attention_fwd<%s,%d,%d>", dtype == INTENT_HIP_BF16 ? "bf16" : "f16",
-           static_cast<int>(d), static_cast<int>(dv));
-  const void *kernel = dtype == INTENT_HIP_BF16 ? attention_kernel<__bf16>(d, dv) : attention_kernel<_Float16>(d, dv);
+  char name[64];
+  snprintf(name, sizeof name, "attention_fwd<%s,%d,%d%s>", dtype == INTENT_HIP_BF16 ? "bf16" : "f16",
+           static_cast<int>(d), static_cast<int>(dv), varlen ? ",packed" : "");
+  const void *kernel;
+  if (dtype == INTENT_HIP_BF16)
+    kernel = varlen ? attention_kernel<__bf16, true>(d, dv) : attention_kernel<__bf16, false>(d, dv);
+  else
+    kernel = varlen ? attention_kernel<_Float16, true>(d, dv) : attention_kernel<_Float16, false>(d, dv);
   return describe_kernel(kernel, name, kThreads, out);
 }
 
@@ -351,11 +426,34 @@ using namespace intent_hip;
 
 namespace {
 
-template <typename E, int D, int DV>
+template <typename E, int D, int DV, bool kVarlen>
 void launch_fwd(dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O,
-                int heads, int head_group, int sq, int sk, const Geometry &g, float scale, int causal, int q_blocks) {
-  attention_fwd<E, D, DV><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, O, heads, head_group, sq, sk, g, scale, causal,
-                                                          q_blocks);
+                int heads, int head_group, int sq, int sk, const Geometry &g, float scale, int causal, int q_blocks,
+                const Ragged &r) {
+  attention_fwd<E, D, DV, kVarlen><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, O, heads, head_group, sq, sk, g, scale,
+                                                                   causal, q_blocks, r);
+}
+
+// One launch of the (dtype, d, dv) instantiation.
+template <bool kVarlen>
+void launch_variant(int dtype, int64_t d, int64_t dv, dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K,
+                    const uint16_t *V, uint16_t *O, int heads, int head_group, int sq, int sk, const Geometry &g,
+                    float scale, int causal, int q_blocks, const Ragged &r) {
+  if (dtype == INTENT_HIP_BF16) {
+    if (d == 64)
+      dv == 64 ? launch_fwd<__bf16, 64, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
+               : launch_fwd<__bf16, 64, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+    else
+      dv == 64 ? launch_fwd<__bf16, 128, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
+               : launch_fwd<__bf16, 128, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+  } else {
+    if (d == 64)
+      dv == 64 ? launch_fwd<_Float16, 64, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
+               : launch_fwd<_Float16, 64, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+    else
+      dv == 64 ? launch_fwd<_Float16, 128, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
+               : launch_fwd<_Float16, 128, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+  }
 }
 
 int launch_attention(int dtype, const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
@@ -401,21 +499,7 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   const hipStream_t s = as_stream(stream);
   const int h = static_cast<int>(heads), grp = static_cast<int>(head_group);
   const int iq = static_cast<int>(sq), ik = static_cast<int>(sk), c = causal ? 1 : 0;
-  if (dtype == INTENT_HIP_BF16) {
-    if (d == 64)
-      dv == 64 ? launch_fwd<__bf16, 64, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
-               : launch_fwd<__bf16, 64, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
-    else
-      dv == 64 ? launch_fwd<__bf16, 128, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
-               : launch_fwd<__bf16, 128, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
-  } else {
-    if (d == 64)
-      dv == 64 ? launch_fwd<_Float16, 64, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
-               : launch_fwd<_Float16, 64, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
-    else
-      dv == 64 ? launch_fwd<_Float16, 128, 64>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks)
-               : launch_fwd<_Float16, 128, 128>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks);
-  }
+  launch_variant<false>(dtype, d, dv, grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks, Ragged{});
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd");
   return INTENT_HIP_OK;
 }
@@ -434,4 +518,76 @@ extern "C" int intent_hip_attention_fwd(int dtype, const void *q, const void *k,
                                         void *stream) {
   return launch_attention(dtype, q, k, v, o, batch, q_heads, head_group, sq, sk, d, dv, strides, scale, causal,
                           stream);
+}
+
+// ---------------------------------------------------------------- packed sequences
+namespace {
+
+int64_t varlen_capacity(int64_t sequences, int64_t total) { return (total + kBQ - 1) / kBQ + sequences; }
+size_t varlen_workspace(int64_t sequences, int64_t total) {
+  return 256 + 8 * static_cast<size_t>(varlen_capacity(sequences, total));
+}
+
+}  // namespace
+
+extern "C" int intent_hip_attention_varlen_workspace_bytes(int64_t sequences, int64_t total, size_t *bytes) {
+  if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
+  if (sequences < 0 || total < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  *bytes = varlen_workspace(sequences, total);
+  return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_attention_varlen_fwd(int dtype, const void *q, const void *k, const void *v,
+                                               const int32_t *cu_seqlens, void *o, int64_t sequences, int64_t total,
+                                               int64_t q_heads, int64_t head_group, int64_t d, int64_t dv,
+                                               const int64_t *strides, float scale, int causal, void *workspace,
+                                               size_t workspace_bytes, void *stream) {
+  if (sequences < 0 || total < 0 || q_heads < 0 || d < 0 || dv < 0)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (head_group < 1 || (q_heads > 0 && q_heads % head_group != 0))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "head_group %lld must be positive and divide the %lld query heads",
+                static_cast<long long>(head_group), static_cast<long long>(q_heads));
+  if (dtype != INTENT_HIP_F16 && dtype != INTENT_HIP_BF16)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "attention dtype code %d (1 = f16, 2 = bf16)", dtype);
+  if (sequences == 0 || total == 0 || q_heads == 0 || dv == 0) return INTENT_HIP_OK;
+  if ((d != 64 && d != 128) || (dv != 64 && dv != 128))
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernels take D and DV in {64, 128} (got d=%lld, dv=%lld)",
+                static_cast<long long>(d), static_cast<long long>(dv));
+  if (strides == nullptr || q == nullptr || k == nullptr || v == nullptr || o == nullptr || cu_seqlens == nullptr)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  const int64_t capacity = varlen_capacity(sequences, total);
+  if (total > INT32_MAX / 2 || sequences > INT32_MAX / 2 || capacity * q_heads > INT32_MAX)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "packed attention extents too large for one launch");
+  if (workspace == nullptr || workspace_bytes < varlen_workspace(sequences, total) || !aligned(workspace, 256))
+    return fail(INTENT_HIP_ERR_WORKSPACE, "packed attention needs %zu workspace bytes (256-byte aligned), got %zu",
+                varlen_workspace(sequences, total), workspace_bytes);
+  Geometry g{};   // batch strides stay 0: the sequence start moves the row
+  // strides[] lists (row, head, inner) per tensor; the kernel's geometry is (batch, head, row, col).
+  for (int t = 0; t < 4; ++t) {
+    int64_t *dst = t == 0 ? g.qs : t == 1 ? g.ks : t == 2 ? g.vs : g.os;
+    dst[2] = strides[3 * t];
+    dst[1] = strides[3 * t + 1];
+    dst[3] = strides[3 * t + 2];
+  }
+  if (g.qs[3] != 1 || g.ks[3] != 1 || g.vs[3] != 1 || g.os[3] != 1)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "attention tensors need unit inner stride");
+  for (int i = 1; i < 3; ++i)
+    if (g.qs[i] % 8 || g.ks[i] % 8 || g.vs[i] % 8 || g.os[i] % 4)
+      return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention strides must be multiples of 8 elements");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 8))
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention tensors must be 16-byte aligned");
+  char *ws = static_cast<char *>(workspace);
+  Ragged r{cu_seqlens, reinterpret_cast<const int2 *>(ws + 256), reinterpret_cast<const int32_t *>(ws),
+           static_cast<int>(total)};
+  const hipStream_t s = as_stream(stream);
+  attention_varlen_items<<<1, 1024, 0, s>>>(cu_seqlens, static_cast<int>(sequences), static_cast<int>(total),
+                                            reinterpret_cast<int2 *>(ws + 256), reinterpret_cast<int32_t *>(ws),
+                                            static_cast<int>(capacity));
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_varlen_items");
+  const dim3 grid(static_cast<unsigned>(capacity * q_heads));
+  launch_variant<true>(dtype, d, dv, grid, s, static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
+                       static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), static_cast<int>(q_heads),
+                       static_cast<int>(head_group), 0, 0, g, scale, causal ? 1 : 0, 1, r);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd (packed)");
+  return INTENT_HIP_OK;
 }

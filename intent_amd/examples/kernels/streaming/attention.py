@@ -112,3 +112,43 @@ def flash_attention_bf16_fwd(
             shared = h // HEAD_GROUP
             output[b, h, :, :] = attend_head(q[b, h, :, :], k[b, shared, :, :], v[b, shared, :, :], scale, CAUSAL,
                                              I.bf16)
+
+
+# ------------------------------------------------------------------------------ packed sequences
+# Rows cu_seqlens[s] .. cu_seqlens[s + 1] of q, k, v and output form sequence s, and each sequence
+# attends only within itself, with row positions relative to its start (the reference's
+# I.ragged over cu_seqlens, streaming/attention.py:839-924). `sequence_lengths` gives the sequence
+# count and is otherwise unread, as in the reference; rows outside every sequence are not written.
+@intent.kernel
+def flash_varlen_attention_fwd(
+    q: I.In[I.f16, ("U", "D")],
+    k: I.In[I.f16, ("U", "D")],
+    v: I.In[I.f16, ("U", "DV")],
+    sequence_lengths: I.In[I.i32, ("B",)],
+    cu_seqlens: I.In[I.i32, ("B_PLUS_1",)],
+    output: I.Out[I.f16, ("U", "DV")],
+    scale: I.f32,
+    CAUSAL: I.Constexpr[bool],
+):
+    for s in I.parallel(I.domain(0, sequence_lengths.shape[0])):
+        rows = I.domain(cu_seqlens[s], cu_seqlens[s + 1])
+        output[rows, :] = attend_head(q[rows, :], k[rows, :], v[rows, :], scale, CAUSAL, I.f16)
+
+
+@intent.kernel
+def flash_varlen_gqa_prefill(
+    q: I.In[I.f16, ("U", "HQ", "D")],
+    k: I.In[I.f16, ("U", "HK", "D")],
+    v: I.In[I.f16, ("U", "HK", "DV")],
+    sequence_lengths: I.In[I.i32, ("B",)],
+    cu_seqlens: I.In[I.i32, ("B_PLUS_1",)],
+    output: I.Out[I.f16, ("U", "HQ", "DV")],
+    scale: I.f32,
+    HEAD_GROUP: I.Constexpr[int],
+):
+    for s in I.parallel(I.domain(0, sequence_lengths.shape[0])):
+        rows = I.domain(cu_seqlens[s], cu_seqlens[s + 1])
+        for h in I.parallel(I.domain(0, q.shape[1])):
+            shared = h // HEAD_GROUP
+            output[rows, h, :] = attend_head(q[rows, h, :], k[rows, shared, :], v[rows, shared, :], scale, True,
+                                             I.f16)

@@ -17,6 +17,8 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   flash_attention_fwd     streaming/attention.py:428-466   intent_hip_attention_fwd_f16
   flash_gqa_attention_fwd streaming/attention.py:469-507   intent_hip_attention_fwd (f16, HEAD_GROUP)
   flash_attention_bf16_fwd streaming/attention.py:510-553  intent_hip_attention_fwd (bf16, HEAD_GROUP)
+  flash_varlen_attention_fwd streaming/attention.py:839-877 intent_hip_attention_varlen_fwd (one head, CAUSAL)
+  flash_varlen_gqa_prefill streaming/attention.py:880-924  intent_hip_attention_varlen_fwd (HEAD_GROUP, causal)
   csr_spmv                sparse/csr_spmv.py:11-29         intent_hip_csr_spmv_f32
   attention_backward_delta backward/attention.py:17-34     intent_hip_attention_bwd_delta
   attention_backward_dkdv backward/attention.py:87-137     intent_hip_attention_bwd_dkdv
@@ -42,7 +44,7 @@ from typing import Callable
 
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, STATIC_SCRATCH_BYTES, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
-                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32,
+                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32,
                       OP_CSR_SPMM_F32, OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
@@ -286,6 +288,68 @@ def _attention_grouped(dtype_code):
     return plan
 
 
+def _head_group(constexprs) -> int:
+    group = constexprs["HEAD_GROUP"]
+    if isinstance(group, bool) or not isinstance(group, int) or group < 1:
+        raise CompilationStageError("provider_configuration", f"HEAD_GROUP must be a positive int, got {group!r}")
+    return group
+
+
+def _attention_varlen(grouped: bool):
+    """flash_varlen_attention_fwd (q [U,D], one head, CAUSAL) / flash_varlen_gqa_prefill (q [U,HQ,D],
+    key head = query head // HEAD_GROUP, causal): packed sequences delimited by cu_seqlens
+    (attention.py:839-924). The offsets stay on the device: the kernel's own pre-pass lists the
+    work items into a workspace allocated here, once per prepared call."""
+    def plan(lib, bound, constexprs, device):
+        import ctypes
+
+        import torch
+
+        q, k, v, lengths, cu, o, scale = bound.arguments
+        if grouped:
+            group, causal = _head_group(constexprs), True
+            total, q_heads, d = q.shape
+            if k.shape[1] * group != q_heads or v.shape[1] != k.shape[1]:
+                raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({k.shape[1]}) * HEAD_GROUP "
+                                 f"({group})")
+            dv = v.shape[2]
+        else:
+            group, causal = 1, bool(constexprs["CAUSAL"])
+            (total, d), q_heads, dv = q.shape, 1, v.shape[1]
+        sequences = lengths.shape[0]
+        if cu.shape[0] != sequences + 1:
+            raise ValueError(f"cu_seqlens needs sequence_lengths.shape[0] + 1 = {sequences + 1} entries, "
+                             f"got {cu.shape[0]}")
+        if k.shape[0] != total or v.shape[0] != total:
+            raise ValueError("q, k and v must hold the same packed rows")
+        if _static_workspace():
+            raise CompilationStageError(
+                "provider_preparation", "packed-sequence attention lists its work items in a workspace; "
+                "backend_options workspace='static' has none for it, use workspace='prepare'")
+        keep, before, after = [q, k, v, lengths, cu, o], [], []
+        qk, kk, vk = _readable(q, keep, before, 8), _readable(k, keep, before, 8), _readable(v, keep, before, 8)
+        ok, cuk = _writable(o, keep, after, 8), _readable(cu, keep, before)
+
+        def row_head_inner(t):
+            return (t.stride(0), t.stride(1), t.stride(2)) if t.dim() == 3 else (t.stride(0), 0, t.stride(1))
+
+        strides = (ctypes.c_int64 * 12)(*(x for t in (qk, kk, vk, ok) for x in row_head_inner(t)))
+        size = ctypes.c_size_t(0)
+        lib.check(lib.fn["attention_varlen_workspace_bytes"](sequences, total, ctypes.byref(size)),
+                  "provider_preparation")
+        workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+        keep += [strides, workspace]
+        fn = lib.fn["attention_varlen_fwd"]
+        args = (F16, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), cuk.data_ptr(), ok.data_ptr(), sequences, total,
+                q_heads, group, d, dv, strides, float(scale), int(causal), workspace.data_ptr(), size.value)
+        return Launch("intent_hip_attention_varlen_fwd", lambda stream: fn(*args, stream), tuple(keep),
+                      tuple(before), tuple(after),
+                      (("sequences", sequences), ("total", total), ("q_heads", q_heads), ("head_group", group),
+                       ("d", d), ("dv", dv), ("causal", causal), ("workspace_bytes", size.value)),
+                      lambda: lib.kernel_resources(OP_ATTENTION_VARLEN, F16, total, d | (dv << 16)))
+    return plan
+
+
 # ------------------------------------------------------------------------------ attention backward
 def _strides(*tensors):
     import ctypes
@@ -513,6 +577,14 @@ _SPECS = (
     OperatorSpec("flash_attention_bf16_fwd", (_view(IN, "bf16", 4), _view(IN, "bf16", 4), _view(IN, "bf16", 4),
                                               _view(OUT, "bf16", 4), ("scalar", "f32")), ("HEAD_GROUP", "CAUSAL"),
                  _attention_grouped(BF16)),
+    OperatorSpec("flash_varlen_attention_fwd",
+                 (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(IN, "f16", 2), _view(IN, "i32", 1),
+                  _view(IN, "i32", 1), _view(OUT, "f16", 2), ("scalar", "f32")), ("CAUSAL",),
+                 _attention_varlen(False)),
+    OperatorSpec("flash_varlen_gqa_prefill",
+                 (_view(IN, "f16", 3), _view(IN, "f16", 3), _view(IN, "f16", 3), _view(IN, "i32", 1),
+                  _view(IN, "i32", 1), _view(OUT, "f16", 3), ("scalar", "f32")), ("HEAD_GROUP",),
+                 _attention_varlen(True)),
     OperatorSpec("attention_backward_delta", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(OUT, "f32", 3)), (),
                  _attention_bwd_delta),
     OperatorSpec("attention_backward_dkdv",

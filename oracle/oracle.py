@@ -194,6 +194,27 @@ def attention_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, cau
     return o
 
 
+def attention_varlen_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens: np.ndarray, scale: float,
+                         causal: bool, *, head_group: int = 1, workers: int | None = None) -> np.ndarray:
+    """Packed sequences (flash_varlen_attention_fwd, streaming/attention.py:839-877; with heads,
+    flash_varlen_gqa_prefill, :880-924): rows cu_seqlens[s] .. cu_seqlens[s+1] of q [U,HQ,D] (or
+    [U,D]), k [U,HK,D], v [U,HK,DV] form sequence s, which attends within itself exactly as one
+    batch entry of attention_fwd whose row positions start at 0 (I.ragged over the offsets; causal
+    compares absolute positions of the same sequence, so relative positions give the same pairs).
+    Rows outside every sequence are left 0. Returns float16 like q."""
+    squeeze = q.ndim == 2
+    if squeeze:
+        q, k, v = q[:, None, :], k[:, None, :], v[:, None, :]
+    o = np.zeros((q.shape[0], q.shape[1], v.shape[2]), q.dtype)
+    for s in range(cu_seqlens.shape[0] - 1):
+        lo, hi = int(cu_seqlens[s]), int(cu_seqlens[s + 1])
+        if hi <= lo:
+            continue
+        part = [np.ascontiguousarray(t[lo:hi].transpose(1, 0, 2))[None] for t in (q, k, v)]
+        o[lo:hi] = attention_fwd(*part, scale, causal, head_group=head_group, workers=workers)[0].transpose(1, 0, 2)
+    return o[:, 0, :] if squeeze else o
+
+
 def attention_fwd_f16(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool, *,
                       chunk: int = 64, workers: int | None = None) -> np.ndarray:
     """q [B,H,Q,D], k [B,H,K,D], v [B,H,K,DV] float16; returns o [B,H,Q,DV] float16."""

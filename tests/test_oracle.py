@@ -501,3 +501,66 @@ def test_csr_spmm_against_scipy_float64_and_probes():
         for nz in range(off[r], off[r + 1]):
             expect[r, col[nz]] = val[nz]
     assert (got == expect).all()
+
+
+# ------------------------------------------------------------------------------ packed sequences
+def _varlen64(q, k, v, cu, scale, causal, group):
+    """float64 softmax attention of each packed sequence, written out directly (no oracle call)."""
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    o = np.zeros((q.shape[0], q.shape[1], v.shape[2]))
+    for s in range(len(cu) - 1):
+        lo, hi = cu[s], cu[s + 1]
+        if hi <= lo:
+            continue
+        for h in range(q.shape[1]):
+            logits = q[lo:hi, h] @ k[lo:hi, h // group].T * scale
+            if causal:
+                logits[np.triu_indices(hi - lo, 1)] = -np.inf
+            w = np.exp(logits - logits.max(axis=1, keepdims=True))
+            o[lo:hi, h] = (w / w.sum(axis=1, keepdims=True)) @ v[lo:hi, h // group]
+    return o
+
+
+@pytest.mark.parametrize("causal,group", [(True, 1), (False, 1), (True, 4)])
+def test_attention_varlen_against_float64(causal, group):
+    """Sequences of 0, 1, 63, 64, 65 and 300 rows packed back to back: every row matches float64
+    attention over its own sequence only (a wrong offset, an off-by-one at a boundary or a wrong
+    key head breaks it)."""
+    g = np.random.default_rng(13 + group + causal)
+    lengths = np.array([65, 0, 1, 300, 63, 64], np.int32)
+    cu = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
+    total = int(cu[-1])
+    q = inputs.normal(g, (total, 4 if group > 1 else 2, 64), "f16")
+    hq = q.shape[1]
+    k = inputs.normal(g, (total, hq // group, 64), "f16")
+    v = inputs.normal(g, (total, hq // group, 128), "f16")
+    scale = float(np.float32(1 / 8))
+    o = oracle.attention_varlen_fwd(q, k, v, cu, scale, causal, head_group=group)
+    want = _varlen64(q, k, v, cu, scale, causal, group)
+    assert np.all(np.abs(o.astype(np.float64) - want) <= 2e-2 * np.abs(want) + 1e-2)
+    q2 = q[:, 0, :].copy()
+    o2 = oracle.attention_varlen_fwd(q2, np.ascontiguousarray(k[:, 0, :]), np.ascontiguousarray(v[:, 0, :]), cu,
+                                     scale, causal)
+    assert o2.shape == (total, 128) and (o2.view(np.uint16) == oracle.attention_varlen_fwd(
+        q2[:, None], np.ascontiguousarray(k[:, :1]), np.ascontiguousarray(v[:, :1]), cu, scale,
+        causal)[:, 0].view(np.uint16)).all()
+
+
+def test_attention_varlen_equals_batched_and_isolates_sequences():
+    """Equal lengths: the packed result is the batched oracle's, bit for bit. Changing the rows of
+    one sequence leaves every other sequence's output unchanged."""
+    g = np.random.default_rng(17)
+    batch, seq, heads = 3, 96, 2
+    q, k, v = (inputs.normal(g, (batch, heads, seq, 64), "f16") for _ in range(3))
+    packed = [np.ascontiguousarray(t.transpose(0, 2, 1, 3).reshape(batch * seq, heads, 64)) for t in (q, k, v)]
+    cu = np.arange(0, batch * seq + 1, seq, dtype=np.int32)
+    o = oracle.attention_varlen_fwd(*packed, cu, 0.125, True)
+    want = oracle.attention_fwd(q, k, v, 0.125, True).transpose(0, 2, 1, 3).reshape(batch * seq, heads, 64)
+    assert (o.view(np.uint16) == want.view(np.uint16)).all()
+    changed = [t.copy() for t in packed]
+    for t in changed:
+        t[seq:2 * seq] = inputs.normal(g, t[seq:2 * seq].shape, "f16")
+    o2 = oracle.attention_varlen_fwd(*changed, cu, 0.125, True)
+    keep = np.r_[0:seq, 2 * seq:3 * seq]
+    assert (o2[keep].view(np.uint16) == o[keep].view(np.uint16)).all()
+    assert not (o2[seq:2 * seq].view(np.uint16) == o[seq:2 * seq].view(np.uint16)).all()
