@@ -33,6 +33,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "HBM GB/s (softmax, SpMV) and TFLOP/s (GEMM, attention) vs 1-GPU roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0          # dense bf16 / fp16
+INT8_PEAK_TOPS = 5000.0            # dense int8
 MFMA_F32_PEAK_TFLOPS = 157.3       # dense fp32 MFMA
 FWD_BYTES_PER_ELEMENT, BWD_BYTES_PER_ELEMENT = 4, 6
 
@@ -50,7 +51,7 @@ def parse():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
-                                "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill")
+                                "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill,gemm_i8")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -470,6 +471,38 @@ def op_attention_bf16(device, flush, cpu):
     return _op_attention_grouped(device, flush, cpu, True)
 
 
+def op_gemm_i8(device, flush, cpu):
+    """gemm_i8 at the reference module's extents (contraction/gemm.py:5-7): int8 operands in the
+    full range, int32 bias and output; against the dense int8 MFMA peak."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples.kernels.contraction.gemm import gemm_i8
+
+    m, k, n = 4096, 4096, 14336
+    rng = np.random.default_rng(7)
+    a = rng.integers(-128, 128, (m, k)).astype(np.int8)
+    b = rng.integers(-128, 128, (k, n)).astype(np.int8)
+    bias = rng.integers(-2**20, 2**20, n).astype(np.int32)
+    dev = lambda x: torch.from_numpy(x).to(device)  # noqa: E731
+    call = intent.jit(gemm_i8, backend="hip").prepare(dev(a), dev(b), dev(bias))
+    ms = operator_ms(call.launch, flush)
+    ops = 2 * m * n * k
+    out = {"config": f"gemm_i8 M={m} K={k} N={n}, int8 operands, int32 bias and output", "median_ms": round(ms, 4),
+           "achieved": round(ops / ms / 1e9, 1), "unit": "TOP/s",
+           "roofline_frac": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4), "ops": ops,
+           "bytes": int(m * k + k * n + 4 * n + 4 * m * n)}
+    if cpu:
+        import oracle
+
+        rows, cols = 16, 1024
+        b_part = np.ascontiguousarray(b[:, :cols])
+        seconds = cpu_median_seconds(lambda: oracle.gemm_i8(a[:rows], b_part, bias[:cols]))
+        out["cpu"] = {"tops": round(2 * rows * cols * k / seconds / 1e12, 5), "cores": 1, "kind": "port",
+                      "sample": f"the first {rows} x {cols} block of C (numpy int64 product)"}
+    return out
+
+
 def op_varlen_prefill(device, flush, cpu):
     """flash_varlen_gqa_prefill: 16 packed sequences of 1..4096 rows (uniform, seed 5), 32 query heads
     over 8 key/value heads, D = 128, causal. FLOPs count each sequence's causal half, as config 4."""
@@ -649,7 +682,7 @@ OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_att
              "gemm_f16_relu": op_gemm_f16_relu, "gemm_f32": op_gemm_f32, "linear_f32": op_linear_f32,
              "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
              "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode,
-             "spmm": op_spmm, "varlen_prefill": op_varlen_prefill}
+             "spmm": op_spmm, "varlen_prefill": op_varlen_prefill, "gemm_i8": op_gemm_i8}
 
 
 def read_traffic(name):

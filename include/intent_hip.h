@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 9
+#define INTENT_HIP_ABI_VERSION 10
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -57,7 +57,8 @@ enum IntentHipOperator {
   INTENT_HIP_OP_PAGED_DECODE_PARTIALS = 11, /* rows = HEAD_GROUP, cols = head dimension */
   INTENT_HIP_OP_SPLITK_REDUCE = 12,
   INTENT_HIP_OP_CSR_SPMM_F32 = 13,        /* cols = features */
-  INTENT_HIP_OP_ATTENTION_VARLEN = 14     /* packed sequences; dtype F16 or BF16, cols = d | dv << 16 */
+  INTENT_HIP_OP_ATTENTION_VARLEN = 14,    /* packed sequences; dtype F16 or BF16, cols = d | dv << 16 */
+  INTENT_HIP_OP_GEMM_I8 = 15
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -133,6 +134,13 @@ int intent_hip_gemm(int dtype, int activation, const void *a, const void *b, voi
  * ldb is B's row stride in either layout. */
 int intent_hip_gemm_f32(const float *a, const float *b, float *c, int64_t m, int64_t n, int64_t k,
                         int64_t lda, int64_t ldb, int64_t ldc, int transpose_b, void *stream);
+
+/* int8 GEMM with int32 accumulation and bias, C = A @ B + bias:
+ * gemm_i8 (python/intent/examples/kernels/contraction/gemm.py:41-51). A [m,k] and B [k,n] int8,
+ * bias [n] and C [m,n] int32, row strides lda/ldb/ldc in elements. int32 sums wrap on overflow;
+ * the result is exact, so every shape gives the same bits. */
+int intent_hip_gemm_i8(const void *a, const void *b, const int32_t *bias, int32_t *c, int64_t m,
+                       int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, void *stream);
 
 /* Fused attention forward, f16 in/out, f32 online softmax in the exp2 domain.
  * flash_attention_fwd (python/intent/examples/kernels/streaming/attention.py:428-466) with

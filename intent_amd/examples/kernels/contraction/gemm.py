@@ -1,6 +1,7 @@
 """Dense GEMM definitions (interface of the reference's
-`python/intent/examples/kernels/contraction/gemm.py:10-92`): gemm_f32, linear_f32, the f16
-`gemm` with its ACTIVATION constexpr, and bf16_gemm."""
+`python/intent/examples/kernels/contraction/gemm.py:10-92`): gemm_f32, linear_f32, gemm_i8 (int8
+operands, int32 accumulator and bias), the f16 `gemm` with its ACTIVATION constexpr, and
+bf16_gemm."""
 import intent_amd as intent
 import intent_amd.language as I
 
@@ -38,6 +39,17 @@ def linear_f32(
 ):
     m, n, k = I.domain(0, x.shape[0]), I.domain(0, weight.shape[0]), I.domain(0, x.shape[1])
     output[m, n] = I.matmul(x[m, k], weight[n, k], transpose_rhs=True, acc_dtype=I.f32)
+
+
+@intent.kernel
+def gemm_i8(
+    a: I.In[I.i8, ("M", "K")],
+    b: I.In[I.i8, ("K", "N")],
+    bias: I.In[I.i32, ("N",)],
+    c: I.Out[I.i32, ("M", "N")],
+):
+    m, n, k = I.domain(0, a.shape[0]), I.domain(0, b.shape[1]), I.domain(0, a.shape[1])
+    c[m, n] = I.matmul(a[m, k], b[k, n], acc_dtype=I.i32) + bias[n]
 
 
 @intent.kernel

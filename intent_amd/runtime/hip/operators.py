@@ -12,6 +12,7 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   softmax_backward_f16    f16-storage variant of the same  intent_hip_softmax_bwd (f16)
   gemm_f32                contraction/gemm.py:15-27        intent_hip_gemm_f32 (transpose_b 0)
   linear_f32              contraction/gemm.py:30-38        intent_hip_gemm_f32 (transpose_b 1)
+  gemm_i8                 contraction/gemm.py:41-51        intent_hip_gemm_i8
   gemm                    contraction/gemm.py:54-73        intent_hip_gemm (f16, ACTIVATION)
   bf16_gemm               contraction/gemm.py:76-92        intent_hip_gemm_bf16
   flash_attention_fwd     streaming/attention.py:428-466   intent_hip_attention_fwd_f16
@@ -44,7 +45,7 @@ from typing import Callable
 
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, STATIC_SCRATCH_BYTES, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
-                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32,
+                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8,
                       OP_CSR_SPMM_F32, OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
@@ -233,6 +234,20 @@ def _gemm_f32(transpose_b: bool):
                       tuple(after), (("m", m), ("n", n), ("k", k), ("transpose_b", transpose_b)),
                       lambda: lib.kernel_resources(OP_GEMM_F32, F32, m, n))
     return plan
+
+
+def _gemm_i8(lib, bound, constexprs, device):
+    a, b, bias, c = bound.arguments
+    keep, before, after = [a, b, bias, c], [], []
+    ak, bk, biask, ck = (_readable(a, keep, before), _readable(b, keep, before), _readable(bias, keep, before),
+                         _writable(c, keep, after))
+    m, k = a.shape
+    n = b.shape[1]
+    fn = lib.fn["gemm_i8"]
+    args = (ak.data_ptr(), bk.data_ptr(), biask.data_ptr(), ck.data_ptr(), m, n, k, _row_stride(ak), _row_stride(bk),
+            _row_stride(ck))
+    return Launch("intent_hip_gemm_i8", lambda stream: fn(*args, stream), tuple(keep), tuple(before), tuple(after),
+                  (("m", m), ("n", n), ("k", k)), lambda: lib.kernel_resources(OP_GEMM_I8, 0, m, n))
 
 
 # ------------------------------------------------------------------------------ attention
@@ -565,6 +580,8 @@ _SPECS = (
                  _gemm_f32(False)),
     OperatorSpec("linear_f32", (_view(IN, "f32", 2), _view(IN, "f32", 2), _view(OUT, "f32", 2)), (),
                  _gemm_f32(True)),
+    OperatorSpec("gemm_i8", (_view(IN, "i8", 2), _view(IN, "i8", 2), _view(IN, "i32", 1), _view(OUT, "i32", 2)), (),
+                 _gemm_i8),
     OperatorSpec("gemm", (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(OUT, "f16", 2)), ("ACTIVATION",),
                  _gemm16(F16)),
     OperatorSpec("bf16_gemm", (_view(IN, "bf16", 2), _view(IN, "bf16", 2), _view(OUT, "bf16", 2)), (),

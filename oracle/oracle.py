@@ -194,6 +194,14 @@ def attention_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, cau
     return o
 
 
+def gemm_i8(a: np.ndarray, b: np.ndarray, bias: np.ndarray) -> np.ndarray:
+    """gemm_i8 (contraction/gemm.py:41-51): c = matmul(a, b, acc_dtype=i32) + bias, int8 operands.
+    The products and sums are exact in int64; reducing mod 2^32 afterwards gives what int32
+    arithmetic that wraps on overflow gives, in any summation order."""
+    total = a.astype(np.int64) @ b.astype(np.int64) + bias.astype(np.int64)[None, :]
+    return total.astype(np.uint64).astype(np.uint32).view(np.int32)
+
+
 def attention_varlen_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens: np.ndarray, scale: float,
                          causal: bool, *, head_group: int = 1, workers: int | None = None) -> np.ndarray:
     """Packed sequences (flash_varlen_attention_fwd, streaming/attention.py:839-877; with heads,

@@ -564,3 +564,24 @@ def test_attention_varlen_equals_batched_and_isolates_sequences():
     keep = np.r_[0:seq, 2 * seq:3 * seq]
     assert (o2[keep].view(np.uint16) == o[keep].view(np.uint16)).all()
     assert not (o2[seq:2 * seq].view(np.uint16) == o[seq:2 * seq].view(np.uint16)).all()
+
+
+# ------------------------------------------------------------------------------ int8 GEMM
+def test_gemm_i8_oracle_pinned():
+    """gemm_i8: against a scalar loop on a small case, an identity operand (c = b + bias exactly),
+    and int32 wraparound, where a bias near the int32 limit plus a positive sum must wrap."""
+    g = np.random.default_rng(19)
+    a = g.integers(-128, 128, (5, 7)).astype(np.int8)
+    b = g.integers(-128, 128, (7, 3)).astype(np.int8)
+    bias = g.integers(-1000, 1000, 3).astype(np.int32)
+    c = oracle.gemm_i8(a, b, bias)
+    for i in range(5):
+        for j in range(3):
+            assert c[i, j] == sum(int(a[i, t]) * int(b[t, j]) for t in range(7)) + int(bias[j])
+    eye = np.eye(7, dtype=np.int8)
+    assert (oracle.gemm_i8(eye, b, bias) == b.astype(np.int32) + bias).all()
+    top = np.full(3, 2**31 - 10, np.int32)
+    ones = np.ones((1, 7), np.int8)
+    wrapped = oracle.gemm_i8(ones, np.full((7, 3), 2, np.int8), top)
+    assert (wrapped == np.int32(-2**31 + 4)).all()             # 2^31 - 10 + 14 wraps
+    assert oracle.gemm_i8(np.zeros((2, 0), np.int8), np.zeros((0, 3), np.int8), bias).tolist() == [bias.tolist()] * 2
