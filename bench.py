@@ -51,7 +51,7 @@ def parse():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
-                                "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill,gemm_i8")
+                                "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill,gemm_i8,quantized_gemm")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -503,6 +503,40 @@ def op_gemm_i8(device, flush, cpu):
     return out
 
 
+def op_quantized_gemm(device, flush, cpu):
+    """quantized_gemm at the reference module's extents: f16 operands N(0,1) and N(0,1)/64, bias
+    N(0,1), residual 4 N(0,1), output scales U(0.05, 0.5); int8 output. Against the f16 peak."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples.kernels.contraction.gemm import quantized_gemm
+
+    m, k, n = 4096, 4096, 14336
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((m, k), np.float32).astype(np.float16)
+    b = (rng.standard_normal((k, n), np.float32) / 64).astype(np.float16)
+    bias = rng.standard_normal(n, np.float32)
+    residual = (4 * rng.standard_normal((m, n), np.float32)).astype(np.float16)
+    scale = rng.uniform(0.05, 0.5, n).astype(np.float32)
+    dev = lambda x: torch.from_numpy(x).to(device)  # noqa: E731
+    call = intent.jit(quantized_gemm, backend="hip").prepare(dev(a), dev(b), dev(bias), dev(residual), dev(scale))
+    ms = operator_ms(call.launch, flush)
+    flops = 2 * m * n * k
+    out = {"config": f"quantized_gemm M={m} K={k} N={n}, f16 operands, int8 output", "median_ms": round(ms, 4),
+           "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        rows, cols = 16, 1024
+        b_part, r_part = np.ascontiguousarray(b[:, :cols]), np.ascontiguousarray(residual[:rows, :cols])
+        seconds = cpu_median_seconds(lambda: oracle.quantized_gemm(a[:rows], b_part, bias[:cols], r_part,
+                                                                   scale[:cols]))
+        out["cpu"] = {"tflops": round(2 * rows * cols * k / seconds / 1e12, 5), "cores": 1, "kind": "port",
+                      "sample": f"the first {rows} x {cols} block of the output (numpy float64 product)"}
+    return out
+
+
 def op_varlen_prefill(device, flush, cpu):
     """flash_varlen_gqa_prefill: 16 packed sequences of 1..4096 rows (uniform, seed 5), 32 query heads
     over 8 key/value heads, D = 128, causal. FLOPs count each sequence's causal half, as config 4."""
@@ -682,7 +716,8 @@ OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_att
              "gemm_f16_relu": op_gemm_f16_relu, "gemm_f32": op_gemm_f32, "linear_f32": op_linear_f32,
              "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
              "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode,
-             "spmm": op_spmm, "varlen_prefill": op_varlen_prefill, "gemm_i8": op_gemm_i8}
+             "spmm": op_spmm, "varlen_prefill": op_varlen_prefill, "gemm_i8": op_gemm_i8,
+             "quantized_gemm": op_quantized_gemm}
 
 
 def read_traffic(name):

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 10
+#define INTENT_HIP_ABI_VERSION 11
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -58,7 +58,8 @@ enum IntentHipOperator {
   INTENT_HIP_OP_SPLITK_REDUCE = 12,
   INTENT_HIP_OP_CSR_SPMM_F32 = 13,        /* cols = features */
   INTENT_HIP_OP_ATTENTION_VARLEN = 14,    /* packed sequences; dtype F16 or BF16, cols = d | dv << 16 */
-  INTENT_HIP_OP_GEMM_I8 = 15
+  INTENT_HIP_OP_GEMM_I8 = 15,
+  INTENT_HIP_OP_QUANTIZED_GEMM = 16
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -134,6 +135,16 @@ int intent_hip_gemm(int dtype, int activation, const void *a, const void *b, voi
  * ldb is B's row stride in either layout. */
 int intent_hip_gemm_f32(const float *a, const float *b, float *c, int64_t m, int64_t n, int64_t k,
                         int64_t lda, int64_t ldb, int64_t ldc, int transpose_b, void *stream);
+
+/* f16 GEMM with f32 accumulation and a quantizing epilogue, int8 output:
+ * quantized_gemm (python/intent/examples/kernels/contraction/gemm.py:95-121). Per element, each
+ * step an f32 operation: v = maximum(acc + bias[n], 0) (NaN propagates), v += residual[i][n],
+ * v = v / output_scale[n] (IEEE division), v = minimum(maximum(v, -128), 127), out = i8(v)
+ * truncating toward zero (NaN, an illegal cast input, gives 0). a [m,k], b [k,n], residual [m,n]
+ * f16; bias, output_scale [n] f32; out [m,n] int8; row strides lda/ldb/ldr/ldo in elements. */
+int intent_hip_quantized_gemm(const void *a, const void *b, const float *bias, const void *residual,
+                              const float *output_scale, void *out, int64_t m, int64_t n, int64_t k,
+                              int64_t lda, int64_t ldb, int64_t ldr, int64_t ldo, void *stream);
 
 /* int8 GEMM with int32 accumulation and bias, C = A @ B + bias:
  * gemm_i8 (python/intent/examples/kernels/contraction/gemm.py:41-51). A [m,k] and B [k,n] int8,

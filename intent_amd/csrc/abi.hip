@@ -113,6 +113,7 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     case INTENT_HIP_OP_SPLITK_REDUCE: return decode_resources(1, cols, rows, out);
     case INTENT_HIP_OP_CSR_SPMM_F32: return spmm_resources(cols, out);
     case INTENT_HIP_OP_GEMM_I8: return gemm_i8_resources(rows, cols, out);
+    case INTENT_HIP_OP_QUANTIZED_GEMM: return quantized_gemm_resources(out);
   }
   return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "unknown operator code %d", op);
 }

@@ -95,6 +95,58 @@ __device__ __forceinline__ uint4 select(bool keep, uint4 v) {
   return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
 }
 
+// Epilogues: quad(i, n, a, b, c, d) receives the f32 accumulators of output row i, columns n .. n+3
+// (n a multiple of 4); one(i, n, a) a single element (the general-shape kernel).
+// gemm / bf16_gemm: act(acc) rounded to E.
+template <typename E, int kAct>
+struct CastStore {
+  uint16_t *C;
+  int64_t ldc;
+  __device__ __forceinline__ void quad(int i, int n, float a, float b, float c, float d) const {
+    *reinterpret_cast<typename Elem<E>::x4 *>(C + static_cast<int64_t>(i) * ldc + n) = pack4<E, kAct>(a, b, c, d);
+  }
+  __device__ __forceinline__ void one(int i, int n, float a) const {
+    C[static_cast<int64_t>(i) * ldc + n] = f32_to_element<E>(activate<kAct>(a));
+  }
+};
+
+// quantized_gemm (contraction/gemm.py:95-121), each step an f32 operation as written there:
+// v = maximum(acc + bias[n], 0) (NaN propagates), v = v + residual[i][n], v = v / scale[n] (IEEE
+// division), v = minimum(maximum(v, -128), 127), then the cast to i8, which truncates toward
+// zero. NaN is an illegal cast input; it gives 0 here.
+struct QuantizeStore {
+  const float *bias;
+  const uint16_t *residual;   // f16 [M, N]
+  int64_t ldr;
+  const float *scale;
+  int8_t *out;
+  int64_t ldo;
+  __device__ __forceinline__ static int32_t quantize(float acc, float bias, float residual, float scale) {
+    float v = acc + bias;
+    v = v != v ? v : (v > 0.0f ? v : 0.0f);
+    v = v + residual;
+    v = __fdiv_rn(v, scale);
+    v = v != v ? v : (v < -128.0f ? -128.0f : (v > 127.0f ? 127.0f : v));
+    return v != v ? 0 : static_cast<int32_t>(v);
+  }
+  __device__ __forceinline__ float residual_at(int i, int n) const {
+    return element_to_f32<_Float16>(residual[static_cast<int64_t>(i) * ldr + n]);
+  }
+  __device__ __forceinline__ void quad(int i, int n, float a, float b, float c, float d) const {
+    const uint2 r = *reinterpret_cast<const uint2 *>(residual + static_cast<int64_t>(i) * ldr + n);
+    const float r0 = element_to_f32<_Float16>(static_cast<uint16_t>(r.x)), r1 = element_to_f32<_Float16>(static_cast<uint16_t>(r.x >> 16));
+    const float r2 = element_to_f32<_Float16>(static_cast<uint16_t>(r.y)), r3 = element_to_f32<_Float16>(static_cast<uint16_t>(r.y >> 16));
+    const uint32_t q = (static_cast<uint32_t>(quantize(a, bias[n], r0, scale[n])) & 0xffu) |
+                       ((static_cast<uint32_t>(quantize(b, bias[n + 1], r1, scale[n + 1])) & 0xffu) << 8) |
+                       ((static_cast<uint32_t>(quantize(c, bias[n + 2], r2, scale[n + 2])) & 0xffu) << 16) |
+                       (static_cast<uint32_t>(quantize(d, bias[n + 3], r3, scale[n + 3])) << 24);
+    *reinterpret_cast<uint32_t *>(out + static_cast<int64_t>(i) * ldo + n) = q;
+  }
+  __device__ __forceinline__ void one(int i, int n, float a) const {
+    out[static_cast<int64_t>(i) * ldo + n] = static_cast<int8_t>(quantize(a, bias[n], residual_at(i, n), scale[n]));
+  }
+};
+
 // Tile order: groups of kGroupM tile rows walked column by column, in dispatch order (the 8 XCDs
 // take consecutive workgroups round-robin). At 8192^3 the 256 resident tiles then span 8 tile
 // rows and all columns: each XCD holds 4 rows x 8 columns of them, and every A and B panel is
@@ -112,10 +164,10 @@ __device__ __forceinline__ void tile_of_block(int block, int tiles_m, int tiles_
   tn = in_group / rows_in_group;
 }
 
-template <typename E, int kAct, bool kEdge>
+template <typename E, typename Epi, bool kEdge>
 __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-                                          uint16_t *__restrict__ C, int M, int N, int K, int64_t lda,
-                                          int64_t ldb, int64_t ldc, int m0, int n0, uint4 *lds) {
+                                          const Epi &ep, int M, int N, int K, int64_t lda, int64_t ldb, int m0,
+                                          int n0, uint4 *lds) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -240,7 +292,6 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
   for (int mt = 0; mt < 4; ++mt) {
     const int i = m0 + wm * 128 + mt * 32 + frag_row;
     if (kEdge && i >= M) continue;
-    uint16_t *crow = C + static_cast<int64_t>(i) * ldc;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
@@ -248,8 +299,7 @@ __device__ __forceinline__ void gemm_tile(const uint16_t *__restrict__ A, const 
         const int n = n0 + wn * 64 + nt * 32 + 8 * g + 4 * frag_half;
         if (kEdge && n >= N) continue;
         const f32x16_t &v = acc[mt][nt];
-        *reinterpret_cast<typename Elem<E>::x4 *>(crow + n) =
-            pack4<E, kAct>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+        ep.quad(i, n, v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
       }
     }
   }
@@ -290,10 +340,10 @@ __device__ __forceinline__ void dma_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <typename E, int kAct>
+template <typename E, typename Epi>
 __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-                                              uint16_t *__restrict__ C, int K, int64_t lda, int64_t ldb,
-                                              int64_t ldc, int m0, int n0, uint4 *lds) {
+                                              const Epi &ep, int K, int64_t lda, int64_t ldb, int m0, int n0,
+                                              uint4 *lds) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -406,36 +456,33 @@ __device__ __forceinline__ void gemm_tile_dma(const uint16_t *__restrict__ A, co
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const int i = m0 + wm * 128 + mt * 32 + frag_row;
-    uint16_t *crow = C + static_cast<int64_t>(i) * ldc;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int n = n0 + wn * 64 + nt * 32 + 8 * g + 4 * half;
         const f32x16_t &v = acc[mt][nt];
-        *reinterpret_cast<typename Elem<E>::x4 *>(crow + n) =
-            pack4<E, kAct>(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+        ep.quad(i, n, v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
       }
   }
 }
 
-template <typename E, int kAct>
+template <typename E, typename Epi>
 __global__ __launch_bounds__(kThreads, 1) void gemm_mfma(const uint16_t *__restrict__ A,
-                                                              const uint16_t *__restrict__ B,
-                                                              uint16_t *__restrict__ C, int M, int N, int K,
-                                                              int64_t lda, int64_t ldb, int64_t ldc,
-                                                              int tiles_m, int tiles_n) {
+                                                              const uint16_t *__restrict__ B, Epi ep, int M,
+                                                              int N, int K, int64_t lda, int64_t ldb, int tiles_m,
+                                                              int tiles_n) {
   __shared__ uint4 lds[2 * kStageChunks > kDmaStages * kDmaStageChunks ? 2 * kStageChunks : kDmaStages * kDmaStageChunks];
   int tm, tn;
   tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const bool interior = m0 + kBM <= M && n0 + kBN <= N;
   if (interior && (K % kDmaBK) == 0)
-    gemm_tile_dma<E, kAct>(A, B, C, K, lda, ldb, ldc, m0, n0, lds);
+    gemm_tile_dma<E, Epi>(A, B, ep, K, lda, ldb, m0, n0, lds);
   else if (interior && (K % kBK) == 0)
-    gemm_tile<E, kAct, false>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
+    gemm_tile<E, Epi, false>(A, B, ep, M, N, K, lda, ldb, m0, n0, lds);
   else
-    gemm_tile<E, kAct, true>(A, B, C, M, N, K, lda, ldb, ldc, m0, n0, lds);
+    gemm_tile<E, Epi, true>(A, B, ep, M, N, K, lda, ldb, m0, n0, lds);
 }
 
 // ---------------------------------------------------------------- general-shape fallback
@@ -443,10 +490,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma(const uint16_t *__restr
 // f32 fused multiply-add in increasing k.
 constexpr int kFT = 64, kFK = 16;
 
-template <typename E, int kAct>
+template <typename E, typename Epi>
 __global__ __launch_bounds__(256) void gemm_simple(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-                                                        uint16_t *__restrict__ C, int M, int N, int K, int64_t lda,
-                                                        int64_t ldb, int64_t ldc) {
+                                                        Epi ep, int M, int N, int K, int64_t lda, int64_t ldb) {
   __shared__ float sa[kFK][kFT + 1];
   __shared__ float sb[kFK][kFT + 1];
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
@@ -475,7 +521,7 @@ __global__ __launch_bounds__(256) void gemm_simple(const uint16_t *__restrict__ 
     if (gm >= M) continue;
     for (int j = 0; j < 4; ++j) {
       const int gn = n0 + tx * 4 + j;
-      if (gn < N) C[static_cast<int64_t>(gm) * ldc + gn] = f32_to_element<E>(activate<kAct>(acc[i][j]));
+      if (gn < N) ep.one(gm, gn, acc[i][j]);
     }
   }
 }
@@ -488,15 +534,40 @@ bool fast_path(const void *a, const void *b, const void *c, int64_t n, int64_t k
 
 }  // namespace
 
+int quantized_gemm_resources(IntentHipKernelResources *out) {
+  return describe_kernel(reinterpret_cast<const void *>(&gemm_mfma<_Float16, QuantizeStore>), "gemm_mfma<f16,quantize>",
+                         kThreads, out);
+}
+
 int gemm_resources(int dtype, int64_t m, int64_t n, IntentHipKernelResources *out) {
   (void)m;
   (void)n;
   if (dtype == INTENT_HIP_F16)
-    return describe_kernel(reinterpret_cast<const void *>(&gemm_mfma<_Float16, 0>), "gemm_mfma<f16>", kThreads, out);
-  return describe_kernel(reinterpret_cast<const void *>(&gemm_mfma<__bf16, 0>), "gemm_mfma<bf16>", kThreads, out);
+    return describe_kernel(reinterpret_cast<const void *>(&gemm_mfma<_Float16, CastStore<_Float16, 0>>), "gemm_mfma<f16>",
+                           kThreads, out);
+  return describe_kernel(reinterpret_cast<const void *>(&gemm_mfma<__bf16, CastStore<__bf16, 0>>), "gemm_mfma<bf16>",
+                         kThreads, out);
 }
 
 namespace {
+
+// The MFMA kernel when `fast` (the operand shape and layout it takes), else the general one.
+template <typename E, typename Epi>
+int launch_epilogue(const uint16_t *A, const uint16_t *B, const Epi &ep, int64_t m, int64_t n, int64_t k, int64_t lda,
+                    int64_t ldb, bool fast, hipStream_t s) {
+  if (k > 0 && fast) {
+    const int tiles_m = static_cast<int>((m + kBM - 1) / kBM), tiles_n = static_cast<int>((n + kBN - 1) / kBN);
+    gemm_mfma<E, Epi><<<dim3(tiles_m * tiles_n), dim3(kThreads), 0, s>>>(
+        A, B, ep, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), lda, ldb, tiles_m, tiles_n);
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_mfma");
+    return INTENT_HIP_OK;
+  }
+  const dim3 grid(static_cast<unsigned>((n + kFT - 1) / kFT), static_cast<unsigned>((m + kFT - 1) / kFT));
+  gemm_simple<E, Epi><<<grid, dim3(256), 0, s>>>(A, B, ep, static_cast<int>(m), static_cast<int>(n),
+                                                 static_cast<int>(k), lda, ldb);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_simple");
+  return INTENT_HIP_OK;
+}
 
 template <typename E, int kAct>
 int launch_gemm(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
@@ -513,19 +584,8 @@ int launch_gemm(const void *a, const void *b, void *c, int64_t m, int64_t n, int
   const hipStream_t s = as_stream(stream);
   const auto *A = static_cast<const uint16_t *>(a);
   const auto *B = static_cast<const uint16_t *>(b);
-  auto *C = static_cast<uint16_t *>(c);
-  if (k > 0 && fast_path(a, b, c, n, k, lda, ldb, ldc)) {
-    const int tiles_m = static_cast<int>((m + kBM - 1) / kBM), tiles_n = static_cast<int>((n + kBN - 1) / kBN);
-    gemm_mfma<E, kAct><<<dim3(tiles_m * tiles_n), dim3(kThreads), 0, s>>>(
-        A, B, C, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k), lda, ldb, ldc, tiles_m, tiles_n);
-    if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_mfma");
-    return INTENT_HIP_OK;
-  }
-  const dim3 grid(static_cast<unsigned>((n + kFT - 1) / kFT), static_cast<unsigned>((m + kFT - 1) / kFT));
-  gemm_simple<E, kAct><<<grid, dim3(256), 0, s>>>(A, B, C, static_cast<int>(m), static_cast<int>(n),
-                                                  static_cast<int>(k), lda, ldb, ldc);
-  if (hipPeekAtLastError() != hipSuccess) return launch_status("gemm_simple");
-  return INTENT_HIP_OK;
+  const CastStore<E, kAct> ep{static_cast<uint16_t *>(c), ldc};
+  return launch_epilogue<E>(A, B, ep, m, n, k, lda, ldb, fast_path(a, b, c, n, k, lda, ldb, ldc), s);
 }
 
 }  // namespace
@@ -549,4 +609,25 @@ extern "C" int intent_hip_gemm(int dtype, int activation, const void *a, const v
     return activation ? launch_gemm<__bf16, 1>(a, b, c, m, n, k, lda, ldb, ldc, stream)
                       : launch_gemm<__bf16, 0>(a, b, c, m, n, k, lda, ldb, ldc, stream);
   return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "16-bit GEMM dtype code %d (1 = f16, 2 = bf16)", dtype);
+}
+
+extern "C" int intent_hip_quantized_gemm(const void *a, const void *b, const float *bias, const void *residual,
+                                         const float *output_scale, void *out, int64_t m, int64_t n, int64_t k,
+                                         int64_t lda, int64_t ldb, int64_t ldr, int64_t ldo, void *stream) {
+  if (m < 0 || n < 0 || k < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (m > INT32_MAX / 2 || n > INT32_MAX / 2 || k > INT32_MAX / 2)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "GEMM extents must stay below 2^30");
+  if (m == 0 || n == 0) return INTENT_HIP_OK;
+  if (out == nullptr || bias == nullptr || residual == nullptr || output_scale == nullptr ||
+      (k > 0 && (a == nullptr || b == nullptr)))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  if (lda < (m > 1 ? k : 0) || ldb < (k > 1 ? n : 0) || ldr < (m > 1 ? n : 0) || ldo < (m > 1 ? n : 0))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "row stride smaller than the row length");
+  const QuantizeStore ep{bias, static_cast<const uint16_t *>(residual), ldr, output_scale, static_cast<int8_t *>(out),
+                         ldo};
+  // The MFMA kernel's epilogue reads 4 residuals as 8 bytes and stores 4 outputs as 4 bytes.
+  const bool fast = k % 8 == 0 && n % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned(a, 16) && aligned(b, 16) &&
+                    ldr % 4 == 0 && aligned(residual, 8) && ldo % 4 == 0 && aligned(out, 4);
+  return launch_epilogue<_Float16>(static_cast<const uint16_t *>(a), static_cast<const uint16_t *>(b), ep, m, n, k, lda,
+                                   ldb, fast, as_stream(stream));
 }

@@ -1,7 +1,7 @@
 """Dense GEMM definitions (interface of the reference's
-`python/intent/examples/kernels/contraction/gemm.py:10-92`): gemm_f32, linear_f32, gemm_i8 (int8
-operands, int32 accumulator and bias), the f16 `gemm` with its ACTIVATION constexpr, and
-bf16_gemm."""
+`python/intent/examples/kernels/contraction/gemm.py:10-121`): gemm_f32, linear_f32, gemm_i8 (int8
+operands, int32 accumulator and bias), the f16 `gemm` with its ACTIVATION constexpr, bf16_gemm,
+and quantized_gemm (f16 operands, int8 output through a bias, ReLU, residual and scale)."""
 import intent_amd as intent
 import intent_amd.language as I
 
@@ -78,3 +78,18 @@ def bf16_gemm(
     _, N = b.shape
     m, n, k = I.domain(0, M), I.domain(0, N), I.domain(0, K)
     c[m, n] = I.cast(I.matmul(a[m, k], b[k, n], acc_dtype=I.f32), I.bf16)
+
+
+@intent.kernel
+def quantized_gemm(
+    a: I.In[I.f16, ("M", "K")],
+    b: I.In[I.f16, ("K", "N")],
+    bias: I.In[I.f32, ("N",)],
+    residual: I.In[I.f16, ("M", "N")],
+    output_scale: I.In[I.f32, ("N",)],
+    output: I.Out[I.i8, ("M", "N")],
+):
+    m, n, k = I.domain(0, a.shape[0]), I.domain(0, b.shape[1]), I.domain(0, a.shape[1])
+    summed = I.matmul(a[m, k], b[k, n], acc_dtype=I.f32)
+    rectified = I.maximum(summed + bias[n], 0.0) + I.cast(residual[m, n], I.f32)
+    output[m, n] = I.cast(I.minimum(I.maximum(rectified / output_scale[n], -128.0), 127.0), I.i8)

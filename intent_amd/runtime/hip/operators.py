@@ -14,6 +14,7 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   linear_f32              contraction/gemm.py:30-38        intent_hip_gemm_f32 (transpose_b 1)
   gemm_i8                 contraction/gemm.py:41-51        intent_hip_gemm_i8
   gemm                    contraction/gemm.py:54-73        intent_hip_gemm (f16, ACTIVATION)
+  quantized_gemm          contraction/gemm.py:95-121       intent_hip_quantized_gemm
   bf16_gemm               contraction/gemm.py:76-92        intent_hip_gemm_bf16
   flash_attention_fwd     streaming/attention.py:428-466   intent_hip_attention_fwd_f16
   flash_gqa_attention_fwd streaming/attention.py:469-507   intent_hip_attention_fwd (f16, HEAD_GROUP)
@@ -45,7 +46,7 @@ from typing import Callable
 
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, STATIC_SCRATCH_BYTES, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
-                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8,
+                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8, OP_QUANTIZED_GEMM,
                       OP_CSR_SPMM_F32, OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
@@ -248,6 +249,21 @@ def _gemm_i8(lib, bound, constexprs, device):
             _row_stride(ck))
     return Launch("intent_hip_gemm_i8", lambda stream: fn(*args, stream), tuple(keep), tuple(before), tuple(after),
                   (("m", m), ("n", n), ("k", k)), lambda: lib.kernel_resources(OP_GEMM_I8, 0, m, n))
+
+
+def _quantized_gemm(lib, bound, constexprs, device):
+    a, b, bias, residual, scale, out = bound.arguments
+    keep, before, after = [a, b, bias, residual, scale, out], [], []
+    ak, bk = _readable(a, keep, before), _readable(b, keep, before)
+    biask, rk, sk = _readable(bias, keep, before), _readable(residual, keep, before), _readable(scale, keep, before)
+    ok = _writable(out, keep, after)
+    m, k = a.shape
+    n = b.shape[1]
+    fn = lib.fn["quantized_gemm"]
+    args = (ak.data_ptr(), bk.data_ptr(), biask.data_ptr(), rk.data_ptr(), sk.data_ptr(), ok.data_ptr(), m, n, k,
+            _row_stride(ak), _row_stride(bk), _row_stride(rk), _row_stride(ok))
+    return Launch("intent_hip_quantized_gemm", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("m", m), ("n", n), ("k", k)), lambda: lib.kernel_resources(OP_QUANTIZED_GEMM, 0, m, n))
 
 
 # ------------------------------------------------------------------------------ attention
@@ -584,6 +600,8 @@ _SPECS = (
                  _gemm_i8),
     OperatorSpec("gemm", (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(OUT, "f16", 2)), ("ACTIVATION",),
                  _gemm16(F16)),
+    OperatorSpec("quantized_gemm", (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(IN, "f32", 1), _view(IN, "f16", 2),
+                                    _view(IN, "f32", 1), _view(OUT, "i8", 2)), (), _quantized_gemm),
     OperatorSpec("bf16_gemm", (_view(IN, "bf16", 2), _view(IN, "bf16", 2), _view(OUT, "bf16", 2)), (),
                  _gemm_bf16),
     OperatorSpec("flash_attention_fwd", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),

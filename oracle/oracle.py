@@ -202,6 +202,26 @@ def gemm_i8(a: np.ndarray, b: np.ndarray, bias: np.ndarray) -> np.ndarray:
     return total.astype(np.uint64).astype(np.uint32).view(np.int32)
 
 
+def quantized_gemm(a: np.ndarray, b: np.ndarray, bias: np.ndarray, residual: np.ndarray,
+                   output_scale: np.ndarray, *, pre_cast: bool = False) -> np.ndarray:
+    """quantized_gemm (contraction/gemm.py:95-121): f16 a [m,k], b [k,n], residual [m,n]; f32 bias
+    and output_scale [n]; int8 output. The f32 accumulator is the exact sum rounded once to f32 (the
+    products of f16 values are exact in float64, and so are their sums at these sizes); the rest
+    runs in f32 steps as the definition writes them: maximum(acc + bias, 0) propagating NaN, plus
+    the residual, IEEE division by the scale, minimum(maximum(v, -128), 127), then truncation toward
+    zero. NaN, an illegal cast input, gives 0. With pre_cast, returns the f32 value before the cast."""
+    acc = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        v = acc + bias.astype(np.float32)[None, :]
+        v = np.where(np.isnan(v), v, np.maximum(v, np.float32(0)))
+        v = v + residual.astype(np.float32)
+        v = v / output_scale.astype(np.float32)[None, :]
+        v = np.minimum(np.maximum(v, np.float32(-128)), np.float32(127))
+        if pre_cast:
+            return v
+        return np.where(np.isnan(v), 0, np.trunc(v)).astype(np.int8)
+
+
 def attention_varlen_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens: np.ndarray, scale: float,
                          causal: bool, *, head_group: int = 1, workers: int | None = None) -> np.ndarray:
     """Packed sequences (flash_varlen_attention_fwd, streaming/attention.py:839-877; with heads,

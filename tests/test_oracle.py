@@ -585,3 +585,36 @@ def test_gemm_i8_oracle_pinned():
     wrapped = oracle.gemm_i8(ones, np.full((7, 3), 2, np.int8), top)
     assert (wrapped == np.int32(-2**31 + 4)).all()             # 2^31 - 10 + 14 wraps
     assert oracle.gemm_i8(np.zeros((2, 0), np.int8), np.zeros((0, 3), np.int8), bias).tolist() == [bias.tolist()] * 2
+
+
+def test_quantized_gemm_oracle_pinned():
+    """quantized_gemm: a scalar f32 chain on a small case; small integers (every step exact) against
+    integer arithmetic with an exact division; ReLU before the residual, saturation on both sides,
+    and truncation toward zero for negative halves."""
+    g = np.random.default_rng(23)
+    a = g.normal(size=(4, 6)).astype(np.float16)
+    b = g.normal(size=(6, 5)).astype(np.float16)
+    bias = g.normal(size=5).astype(np.float32)
+    residual = (g.normal(size=(4, 5)) * 3).astype(np.float16)
+    scale = g.uniform(0.05, 0.5, 5).astype(np.float32)
+    out = oracle.quantized_gemm(a, b, bias, residual, scale)
+    for i in range(4):
+        for j in range(5):
+            acc = np.float32(sum(float(a[i, t]) * float(b[t, j]) for t in range(6)))
+            v = np.float32(max(np.float32(acc + bias[j]), np.float32(0)) + np.float32(residual[i, j]))
+            v = min(max(np.float32(v / scale[j]), np.float32(-128)), np.float32(127))
+            assert out[i, j] == int(np.trunc(v))
+    ia = g.integers(-3, 4, (16, 8)).astype(np.float16)
+    ib = g.integers(-3, 4, (8, 12)).astype(np.float16)
+    ibias = g.integers(-20, 21, 12).astype(np.float32)
+    ires = g.integers(-9, 10, (16, 12)).astype(np.float16)
+    exact = np.maximum(ia.astype(np.int64) @ ib.astype(np.int64) + ibias.astype(np.int64), 0) + ires.astype(np.int64)
+    assert (oracle.quantized_gemm(ia, ib, ibias, ires, np.full(12, 0.25, np.float32)) ==
+            np.clip(exact * 4, -128, 127)).all()                       # division by 1/4 is exact
+    halves = oracle.quantized_gemm(np.ones((1, 1), np.float16), np.ones((1, 3), np.float16),
+                                   np.array([-10.0, 300.0, 0.0], np.float32), np.array([[-3.0, 0.0, -3.0]], np.float16),
+                                   np.array([2.0, 1.0, 2.0], np.float32))
+    assert halves.tolist() == [[-1, 127, -1]]   # ReLU(-9) + -3 = -3 -> -1.5 -> -1; 301 saturates; (1 - 3) / 2
+    low = oracle.quantized_gemm(np.zeros((1, 1), np.float16), np.zeros((1, 1), np.float16), np.zeros(1, np.float32),
+                                np.array([[-1000.0]], np.float16), np.ones(1, np.float32))
+    assert low.tolist() == [[-128]]
