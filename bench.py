@@ -51,7 +51,8 @@ def parse():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
-                                "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill,gemm_i8,quantized_gemm")
+                                "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill,gemm_i8,quantized_gemm,"
+                                "attention_bias")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -577,6 +578,36 @@ def op_varlen_prefill(device, flush, cpu):
     return out
 
 
+def op_attention_bias(device, flush, cpu):
+    """flash_attention_bias_fwd at config 4's extents (B4 H32 S4096 D128), every key admitted, with
+    a normal(0, 2) f32 bias per (batch, head, key). FLOPs: the two products over all S x S pairs."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.streaming.attention import flash_attention_bias_fwd
+
+    q, k, v, scale = inputs.attention_f16()
+    b, h, s, d = q.shape
+    bias = (2.0 * np.random.default_rng(11).standard_normal((b, h, s))).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    call = intent.jit(flash_attention_bias_fwd, backend="hip").prepare(t(q), t(k), t(v), t(bias), scale)
+    ms = operator_ms(call.launch, flush)
+    flops = 4 * b * h * s * s * d
+    out = {"config": "key-biased attention fwd f16 B4 H32 S4096 D128, no mask (flash_attention_bias_fwd)",
+           "median_ms": round(ms, 4), "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        seconds = cpu_median_seconds(lambda: oracle.attention_bias_fwd(
+            q[:1, :1, :512], k[:1, :1], v[:1, :1], bias[:1, :1], scale))
+        sample_flops = 4 * 512 * s * d
+        out["cpu"] = {"tflops": round(sample_flops / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": "1 (batch, head) pair, first 512 queries over all 4096 keys"}
+    return out
+
+
 def _op_attention_bwd(device, flush, cpu, large):
     """The three-kernel attention backward (programs/attention_backward.py) as one prepared
     sequence: the reference example's shape (backward/attention.py:7-13: B2, HQ8, HK2, S1024, D64)
@@ -717,7 +748,7 @@ OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_att
              "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
              "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode,
              "spmm": op_spmm, "varlen_prefill": op_varlen_prefill, "gemm_i8": op_gemm_i8,
-             "quantized_gemm": op_quantized_gemm}
+             "quantized_gemm": op_quantized_gemm, "attention_bias": op_attention_bias}
 
 
 def read_traffic(name):

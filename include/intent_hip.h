@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 11
+#define INTENT_HIP_ABI_VERSION 12
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -59,7 +59,8 @@ enum IntentHipOperator {
   INTENT_HIP_OP_CSR_SPMM_F32 = 13,        /* cols = features */
   INTENT_HIP_OP_ATTENTION_VARLEN = 14,    /* packed sequences; dtype F16 or BF16, cols = d | dv << 16 */
   INTENT_HIP_OP_GEMM_I8 = 15,
-  INTENT_HIP_OP_QUANTIZED_GEMM = 16
+  INTENT_HIP_OP_QUANTIZED_GEMM = 16,
+  INTENT_HIP_OP_ATTENTION_BIAS = 17       /* f16; cols = d | dv << 16 */
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -177,6 +178,18 @@ int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void
                              int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
                              int64_t sk, int64_t d, int64_t dv, const int64_t strides[16],
                              float scale, int causal, void *stream);
+
+/* Attention forward with an additive per-key bias: flash_attention_bias_fwd
+ * (streaming/attention.py:800-836, scores of summarize_biased_attention_chunk :328-366):
+ * o[b,h,i,:] = sum_j softmax_j((q_i . k_j) scale + bias[b,h,j]) v[b,h,j,:], every key valid, no
+ * causal mask. q, k, v, o f16 as in intent_hip_attention_fwd_f16 (strides[16]); bias f32 at
+ * bias + b bias_strides[0] + h bias_strides[1] + j bias_strides[2], bias_strides[2] = 1, 4-byte
+ * aligned. A bias of -inf removes its key (weight 0); a row whose keys are all removed is 0 (the
+ * reference returns NaN for a query whose fold chunk is entirely -inf). */
+int intent_hip_attention_bias_fwd(const void *q, const void *k, const void *v, const float *bias,
+                                  void *o, int64_t batch, int64_t heads, int64_t sq, int64_t sk,
+                                  int64_t d, int64_t dv, const int64_t strides[16],
+                                  const int64_t bias_strides[3], float scale, void *stream);
 
 /* Fused attention forward over packed sequences: rows cu_seqlens[s] .. cu_seqlens[s+1] of
  * q [total,hq,d], k [total,hk,d], v [total,hk,dv] and o [total,hq,dv] form sequence s; each

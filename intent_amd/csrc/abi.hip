@@ -98,12 +98,12 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     // cols = d, or d | dv << 16 when dv differs from d.
     case INTENT_HIP_OP_ATTENTION_FWD_F16:
       return attention_resources(INTENT_HIP_F16, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF),
-                                 false, out);
+                                 0, out);
     case INTENT_HIP_OP_ATTENTION_FWD:
-      return attention_resources(dtype, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), false,
+      return attention_resources(dtype, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), 0,
                                  out);
     case INTENT_HIP_OP_ATTENTION_VARLEN:
-      return attention_resources(dtype, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), true,
+      return attention_resources(dtype, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), 1,
                                  out);
     case INTENT_HIP_OP_CSR_SPMV_F32: return spmv_resources(rows, cols, out);
     case INTENT_HIP_OP_ATTENTION_BWD_DELTA: return attention_bwd_resources(0, rows, cols, out);
@@ -114,6 +114,9 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     case INTENT_HIP_OP_CSR_SPMM_F32: return spmm_resources(cols, out);
     case INTENT_HIP_OP_GEMM_I8: return gemm_i8_resources(rows, cols, out);
     case INTENT_HIP_OP_QUANTIZED_GEMM: return quantized_gemm_resources(out);
+    case INTENT_HIP_OP_ATTENTION_BIAS:
+      return attention_resources(INTENT_HIP_F16, rows, cols & 0xFFFF, (cols >> 16) ? (cols >> 16) : (cols & 0xFFFF), 2,
+                                 out);
   }
   return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "unknown operator code %d", op);
 }

@@ -34,6 +34,12 @@
 //     beyond its own last query, and only tiles crossing the diagonal are masked; the
 //     heaviest query blocks are dispatched first. All query blocks of one head share an
 //     XCD (blocks of a head are 128 apart, a multiple of the 8 XCDs) and so its L2.
+//
+// The same kernel serves three modes: batched [B,H,S,D] tensors; packed sequences
+// (flash_varlen_attention_fwd / flash_varlen_gqa_prefill, attention.py:839-924), where a
+// workgroup's item names a sequence of rows in [U,H,D] tensors; and a per-key additive bias
+// (flash_attention_bias_fwd, attention.py:800-836), whose 64 floats per tile are DMA'd beside K
+// and V and enter each score as s (scale log2 e) + bias log2 e.
 #include "common.hpp"
 
 namespace intent_hip {
@@ -101,6 +107,16 @@ struct Ragged {
   int total;              // rows of q, k, v and the output
 };
 
+// Per-key additive bias (flash_attention_bias_fwd): row (batch b, head h) at p + b bs + h hs, unit
+// key stride; each tile's 64 floats are DMA'd beside its K and V.
+struct KeyBias {
+  const float *p;
+  int64_t bs, hs;
+};
+
+// Kernel modes: batched [B,H,S,D] tensors, packed sequences, or batched with a key bias.
+constexpr int kBatched = 0, kPacked = 1, kBiased = 2;
+
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -112,21 +128,23 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // raised when a tile's maximum exceeds it by more than this, so weights stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename E, int D, int DV, bool kVarlen>
+template <typename E, int D, int DV, int kMode>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__restrict__ Q,
                                                                   const uint16_t *__restrict__ K,
                                                                   const uint16_t *__restrict__ V,
                                                                   uint16_t *__restrict__ O, int heads,
                                                                   int head_group, int sq_all, int sk_all,
                                                                   Geometry g, float scale, int causal,
-                                                                  int q_blocks, Ragged r) {
+                                                                  int q_blocks, Ragged r, KeyBias kb) {
+  constexpr bool kVarlen = kMode == kPacked, kBias = kMode == kBiased;
   typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
   constexpr int kD = D, kDV = DV;
   constexpr int kKRow = kD / 8;               // 16-byte chunks per K row
   constexpr int kVRow = kDV / 8;              // 16-byte chunks per V row
   constexpr int kKChunks = kBK * kKRow;       // 16-byte chunks of a K tile (row = key)
   constexpr int kVChunks = kBK * kVRow;       // 16-byte chunks of a V tile (row = key)
-  constexpr int kStageChunks = kKChunks + kVChunks;
+  constexpr int kBiasChunks = kBias ? kBK / 4 : 0;   // 16-byte chunks of the tile's key bias
+  constexpr int kStageChunks = kKChunks + kVChunks + kBiasChunks;
   static_assert(kKChunks % kThreads == 0 && kVChunks % kThreads == 0, "DMA split");
   __shared__ uint4 lds[2 * kStageChunks];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -157,6 +175,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const uint16_t *kbase = K + b * g.ks[0] + kh * g.ks[1] + row0 * g.ks[2];
   const uint16_t *vbase = V + b * g.vs[0] + kh * g.vs[1] + row0 * g.vs[2];
   uint16_t *obase = O + b * g.os[0] + h * g.os[1] + row0 * g.os[2];
+  const float *bias_row = kBias ? kb.p + b * kb.bs + h * kb.hs : nullptr;
 
   const int q0 = qb * kBQ;
   const int wq0 = q0 + wave * 32;             // this wave's first query row
@@ -201,6 +220,11 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
       __builtin_amdgcn_global_load_lds(vbase + static_cast<int64_t>(key) * g.vs[2] + (pc ^ swz_v(DV, row)) * 8,
                                        (lds_void_t *)(stage + kKChunks + (wave * (kVChunks / kThreads) + i) * 64), 16,
                                        0, 0);
+    }
+    if constexpr (kBias) {   // wave 0, one key per lane (past the row's end, its last key: masked below)
+      if (wave == 0)
+        __builtin_amdgcn_global_load_lds(bias_row + min(key0 + lane, sk - 1),
+                                         (lds_void_t *)(stage + kKChunks + kVChunks), 4, 0, 0);
     }
   };
 
@@ -262,8 +286,23 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
       }
       __builtin_amdgcn_s_setprio(0);
     }
+    // With a key bias the scores become (s scale + bias) log2 e here, as one FMA each; lane keys
+    // 8 j + 4 half + 0..3 of each 32-key tile are one 16-byte LDS read.
+    if constexpr (kBias) {
+      const float *sbias = reinterpret_cast<const float *>(sk_tile + kKChunks + kVChunks);
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4 b4 = *reinterpret_cast<const float4 *>(sbias + st * 32 + 8 * j + 4 * half);
+          s[st][4 * j] = fmaf(s[st][4 * j], factor, b4.x * kLog2e);
+          s[st][4 * j + 1] = fmaf(s[st][4 * j + 1], factor, b4.y * kLog2e);
+          s[st][4 * j + 2] = fmaf(s[st][4 * j + 2], factor, b4.z * kLog2e);
+          s[st][4 * j + 3] = fmaf(s[st][4 * j + 3], factor, b4.w * kLog2e);
+        }
+    }
     // Mask (only tiles that cross the diagonal or the end) and the tile maximum of raw scores
-    // (scale * log2 e > 0, so the maximum commutes with the scaling).
+    // (scale * log2 e > 0, so the maximum commutes with the scaling; biased scores are final).
     const bool edge = causal ? (key0 + kBK - 1 > wq0) : false;
     const bool tail = key0 + kBK > sk;
     if (edge || tail) {                                        // wave-uniform
@@ -281,7 +320,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) tile_max = fmaxf(tile_max, s[st][e]);
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * factor;
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * (kBias ? 1.0f : factor);
     // Raise the running maximum only when this tile exceeds it by more than the slack.
     if (__any(tile_max > row_max + kRescaleSlack)) {
       const float new_max = fmaxf(row_max, tile_max);
@@ -299,7 +338,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[st][e], factor, -shift));
+        const float p = __builtin_amdgcn_exp2f(kBias ? s[st][e] - shift : fmaf(s[st][e], factor, -shift));
         row_den += p;
         pf[st * 2 + (e >> 3)][e & 7] = static_cast<E>(p);
       }
@@ -397,26 +436,28 @@ __global__ __launch_bounds__(1024) void attention_varlen_items(const int32_t *__
 }  // namespace
 
 // The kernel of a (dtype, d, dv, packed) choice; d and dv are each 64 or 128 (checked by the callers).
-template <typename E, bool kVarlen>
+template <typename E, int kMode>
 const void *attention_kernel(int64_t d, int64_t dv) {
-  if (d == 64) return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 64, 64, kVarlen>)
-                               : reinterpret_cast<const void *>(&attention_fwd<E, 64, 128, kVarlen>);
-  return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 128, 64, kVarlen>)
-                  : reinterpret_cast<const void *>(&attention_fwd<E, 128, 128, kVarlen>);
+  if (d == 64) return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 64, 64, kMode>)
+                               : reinterpret_cast<const void *>(&attention_fwd<E, 64, 128, kMode>);
+  return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 128, 64, kMode>)
+                  : reinterpret_cast<const void *>(&attention_fwd<E, 128, 128, kMode>);
 }
 
-int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, bool varlen, IntentHipKernelResources *out) {
+int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, int mode, IntentHipKernelResources *out) {
   (void)sq;
   if ((d != 64 && d != 128) || (dv != 64 && dv != 128))
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernels take d, dv in {64, 128}");
   char name[64];
   snprintf(name, sizeof name, "attention_fwd<%s,%d,%d%s>", dtype == INTENT_HIP_BF16 ? "bf16" : "f16",
-           static_cast<int>(d), static_cast<int>(dv), varlen ? ",packed" : "");
+           static_cast<int>(d), static_cast<int>(dv), mode == kPacked ? ",packed" : mode == kBiased ? ",bias" : "");
   const void *kernel;
-  if (dtype == INTENT_HIP_BF16)
-    kernel = varlen ? attention_kernel<__bf16, true>(d, dv) : attention_kernel<__bf16, false>(d, dv);
+  if (mode == kBiased)
+    kernel = attention_kernel<_Float16, kBiased>(d, dv);
+  else if (dtype == INTENT_HIP_BF16)
+    kernel = mode == kPacked ? attention_kernel<__bf16, kPacked>(d, dv) : attention_kernel<__bf16, kBatched>(d, dv);
   else
-    kernel = varlen ? attention_kernel<_Float16, true>(d, dv) : attention_kernel<_Float16, false>(d, dv);
+    kernel = mode == kPacked ? attention_kernel<_Float16, kPacked>(d, dv) : attention_kernel<_Float16, kBatched>(d, dv);
   return describe_kernel(kernel, name, kThreads, out);
 }
 
@@ -426,39 +467,41 @@ using namespace intent_hip;
 
 namespace {
 
-template <typename E, int D, int DV, bool kVarlen>
+template <typename E, int D, int DV, int kMode>
 void launch_fwd(dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O,
                 int heads, int head_group, int sq, int sk, const Geometry &g, float scale, int causal, int q_blocks,
-                const Ragged &r) {
-  attention_fwd<E, D, DV, kVarlen><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, O, heads, head_group, sq, sk, g, scale,
-                                                                   causal, q_blocks, r);
+                const Ragged &r, const KeyBias &kb) {
+  attention_fwd<E, D, DV, kMode><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, O, heads, head_group, sq, sk, g, scale,
+                                                                 causal, q_blocks, r, kb);
 }
 
 // One launch of the (dtype, d, dv) instantiation.
-template <bool kVarlen>
+template <int kMode>
 void launch_variant(int dtype, int64_t d, int64_t dv, dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K,
                     const uint16_t *V, uint16_t *O, int heads, int head_group, int sq, int sk, const Geometry &g,
-                    float scale, int causal, int q_blocks, const Ragged &r) {
-  if (dtype == INTENT_HIP_BF16) {
+                    float scale, int causal, int q_blocks, const Ragged &r,
+                    const KeyBias &kb = KeyBias{}) {
+  if (kMode != kBiased && dtype == INTENT_HIP_BF16) {
     if (d == 64)
-      dv == 64 ? launch_fwd<__bf16, 64, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
-               : launch_fwd<__bf16, 64, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+      dv == 64 ? launch_fwd<__bf16, 64, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
+               : launch_fwd<__bf16, 64, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
     else
-      dv == 64 ? launch_fwd<__bf16, 128, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
-               : launch_fwd<__bf16, 128, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+      dv == 64 ? launch_fwd<__bf16, 128, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
+               : launch_fwd<__bf16, 128, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
   } else {
     if (d == 64)
-      dv == 64 ? launch_fwd<_Float16, 64, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
-               : launch_fwd<_Float16, 64, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+      dv == 64 ? launch_fwd<_Float16, 64, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
+               : launch_fwd<_Float16, 64, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
     else
-      dv == 64 ? launch_fwd<_Float16, 128, 64, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r)
-               : launch_fwd<_Float16, 128, 128, kVarlen>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r);
+      dv == 64 ? launch_fwd<_Float16, 128, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
+               : launch_fwd<_Float16, 128, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
   }
 }
 
+// Batched attention; with kb, the key-biased form (f16, non-causal).
 int launch_attention(int dtype, const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
                      int64_t head_group, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
-                     float scale, int causal, void *stream) {
+                     float scale, int causal, void *stream, const KeyBias *kb = nullptr) {
   if (batch < 0 || heads < 0 || sq < 0 || sk < 0 || d < 0 || dv < 0)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
   if (head_group < 1 || (heads > 0 && heads % head_group != 0))
@@ -499,7 +542,10 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   const hipStream_t s = as_stream(stream);
   const int h = static_cast<int>(heads), grp = static_cast<int>(head_group);
   const int iq = static_cast<int>(sq), ik = static_cast<int>(sk), c = causal ? 1 : 0;
-  launch_variant<false>(dtype, d, dv, grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks, Ragged{});
+  if (kb != nullptr)
+    launch_variant<kBiased>(dtype, d, dv, grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks, Ragged{}, *kb);
+  else
+    launch_variant<kBatched>(dtype, d, dv, grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks, Ragged{});
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd");
   return INTENT_HIP_OK;
 }
@@ -518,6 +564,23 @@ extern "C" int intent_hip_attention_fwd(int dtype, const void *q, const void *k,
                                         void *stream) {
   return launch_attention(dtype, q, k, v, o, batch, q_heads, head_group, sq, sk, d, dv, strides, scale, causal,
                           stream);
+}
+
+extern "C" int intent_hip_attention_bias_fwd(const void *q, const void *k, const void *v, const float *bias, void *o,
+                                             int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d,
+                                             int64_t dv, const int64_t *strides, const int64_t *bias_strides,
+                                             float scale, void *stream) {
+  if (bias_strides == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  if (batch > 0 && heads > 0 && sq > 0 && sk > 0) {
+    if (bias == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+    if (bias_strides[2] != 1) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "bias needs unit key stride");
+    if (bias_strides[0] < 0 || bias_strides[1] < 0)
+      return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative bias stride");
+    if (!aligned(bias, 4)) return fail(INTENT_HIP_ERR_UNSUPPORTED, "bias must be 4-byte aligned");
+  }
+  const KeyBias kb{bias, bias_strides[0], bias_strides[1]};
+  return launch_attention(INTENT_HIP_F16, q, k, v, o, batch, heads, 1, sq, sk, d, dv, strides, scale, 0, stream,
+                          &kb);
 }
 
 // ---------------------------------------------------------------- packed sequences
@@ -585,7 +648,7 @@ extern "C" int intent_hip_attention_varlen_fwd(int dtype, const void *q, const v
                                             static_cast<int>(capacity));
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_varlen_items");
   const dim3 grid(static_cast<unsigned>(capacity * q_heads));
-  launch_variant<true>(dtype, d, dv, grid, s, static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
+  launch_variant<kPacked>(dtype, d, dv, grid, s, static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
                        static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), static_cast<int>(q_heads),
                        static_cast<int>(head_group), 0, 0, g, scale, causal ? 1 : 0, 1, r);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd (packed)");

@@ -31,7 +31,7 @@ int gemm_resources(int dtype, int64_t m, int64_t n, IntentHipKernelResources *ou
 int gemm_f32_resources(int64_t m, int64_t n, IntentHipKernelResources *out);
 int gemm_i8_resources(int64_t m, int64_t n, IntentHipKernelResources *out);
 int quantized_gemm_resources(IntentHipKernelResources *out);
-int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, bool varlen, IntentHipKernelResources *out);
+int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, int mode, IntentHipKernelResources *out);
 int spmv_resources(int64_t rows, int64_t nnz, IntentHipKernelResources *out);
 int attention_bwd_resources(int64_t which, int64_t rows, int64_t d, IntentHipKernelResources *out);
 int decode_resources(int64_t which, int64_t d, int64_t group, IntentHipKernelResources *out);

@@ -1,6 +1,7 @@
 """Attention forward definitions: flash_attention_fwd, flash_gqa_attention_fwd (key/value heads
-shared by HEAD_GROUP query heads) and flash_attention_bf16_fwd. Names, signatures and extents are
-the reference's (`python/intent/examples/kernels/streaming/attention.py:428-553`).
+shared by HEAD_GROUP query heads), flash_attention_bf16_fwd, flash_attention_bias_fwd and the
+packed-sequence forms. Names, signatures and extents are the reference's
+(`python/intent/examples/kernels/streaming/attention.py:428-553, 800-924`).
 
 What each computes, per (batch, query head) and query row i:
 
@@ -112,6 +113,33 @@ def flash_attention_bf16_fwd(
             shared = h // HEAD_GROUP
             output[b, h, :, :] = attend_head(q[b, h, :, :], k[b, shared, :, :], v[b, shared, :, :], scale, CAUSAL,
                                              I.bf16)
+
+
+# ------------------------------------------------------------------------------ additive key bias
+# flash_attention_bias_fwd (streaming/attention.py:800-836): every key is admitted and its logit
+# gains bias[b, h, j] before the base-2 scaling, logit[i, j] = ((q_i . k_j) * scale + bias[j]) *
+# log2(e) (summarize_biased_attention_chunk, :328-366). The hip kernel forms it as one fused
+# multiply-add, (q_i . k_j) * (scale log2 e) + bias[j] log2 e.
+@intent.kernel
+def flash_attention_bias_fwd(
+    q: I.In[I.f16, ("B", "H", "Q", "D")],
+    k: I.In[I.f16, ("B", "H", "K", "D")],
+    v: I.In[I.f16, ("B", "H", "K", "DV")],
+    bias: I.In[I.f32, ("B", "H", "K")],
+    output: I.Out[I.f16, ("B", "H", "Q", "DV")],
+    scale: I.f32,
+):
+    B, H = q.shape[0], q.shape[1]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, H)):
+            q_rows, k_rows = q[b, h, :, :], k[b, h, :, :]
+            logits = (I.matmul(q_rows, k_rows, transpose_rhs=True, acc_dtype=I.f32) * scale
+                      + bias[b, h, :][None, :]) * I.LOG2E
+            admitted = causal_pairs(I.indices(I.domain(0, q_rows.shape[0])), I.indices(I.domain(0, k_rows.shape[0])),
+                                    False)
+            summary = admitted_attention(logits, admitted, v[b, h, :, :], I.f16)
+            share = I.fdiv(1.0, summary.total, approximate=True, flush_to_zero=True)
+            output[b, h, :, :] = I.cast(I.select(summary.live[:, None], summary.mixed * share[:, None], 0.0), I.f16)
 
 
 # ------------------------------------------------------------------------------ packed sequences

@@ -19,6 +19,7 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   flash_attention_fwd     streaming/attention.py:428-466   intent_hip_attention_fwd_f16
   flash_gqa_attention_fwd streaming/attention.py:469-507   intent_hip_attention_fwd (f16, HEAD_GROUP)
   flash_attention_bf16_fwd streaming/attention.py:510-553  intent_hip_attention_fwd (bf16, HEAD_GROUP)
+  flash_attention_bias_fwd streaming/attention.py:800-836  intent_hip_attention_bias_fwd
   flash_varlen_attention_fwd streaming/attention.py:839-877 intent_hip_attention_varlen_fwd (one head, CAUSAL)
   flash_varlen_gqa_prefill streaming/attention.py:880-924  intent_hip_attention_varlen_fwd (HEAD_GROUP, causal)
   csr_spmv                sparse/csr_spmv.py:11-29         intent_hip_csr_spmv_f32
@@ -46,7 +47,7 @@ from typing import Callable
 
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, STATIC_SCRATCH_BYTES, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
-                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8, OP_QUANTIZED_GEMM,
+                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_BIAS, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8, OP_QUANTIZED_GEMM,
                       OP_CSR_SPMM_F32, OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
@@ -317,6 +318,31 @@ def _attention_grouped(dtype_code):
                                      ("sk", sk), ("d", d), ("dv", dv), ("causal", causal)),
                       lambda: lib.kernel_resources(OP_ATTENTION_FWD, dtype_code, sq, d | (dv << 16)))
     return plan
+
+
+def _attention_bias(lib, bound, constexprs, device):
+    """flash_attention_bias_fwd: scores (q . k) scale + bias[b, h, key] over every key, no mask
+    (attention.py:800-836, :328-366)."""
+    import ctypes
+
+    q, k, v, bias, o, scale = bound.arguments
+    batch, heads, sq, d = q.shape
+    sk, dv = k.shape[2], v.shape[3]
+    if tuple(bias.shape) != (batch, heads, sk):
+        raise ValueError(f"bias must be [B, H, K] = {(batch, heads, sk)}, got {tuple(bias.shape)}")
+    keep, before, after = [q, k, v, bias, o], [], []
+    qk, kk, vk, ok = (_readable(q, keep, before, 8), _readable(k, keep, before, 8),
+                      _readable(v, keep, before, 8), _writable(o, keep, after, 8))
+    bk = _readable(bias, keep, before)
+    strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
+    bias_strides = (ctypes.c_int64 * 3)(*bk.stride())
+    keep += [strides, bias_strides]
+    fn = lib.fn["attention_bias_fwd"]
+    args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), bk.data_ptr(), ok.data_ptr(), batch, heads, sq, sk, d, dv,
+            strides, bias_strides, float(scale))
+    return Launch("intent_hip_attention_bias_fwd", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("sk", sk), ("d", d), ("dv", dv)),
+                  lambda: lib.kernel_resources(OP_ATTENTION_BIAS, F16, sq, d | (dv << 16)))
 
 
 def _head_group(constexprs) -> int:
@@ -612,6 +638,9 @@ _SPECS = (
     OperatorSpec("flash_attention_bf16_fwd", (_view(IN, "bf16", 4), _view(IN, "bf16", 4), _view(IN, "bf16", 4),
                                               _view(OUT, "bf16", 4), ("scalar", "f32")), ("HEAD_GROUP", "CAUSAL"),
                  _attention_grouped(BF16)),
+    OperatorSpec("flash_attention_bias_fwd", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
+                                              _view(IN, "f32", 3), _view(OUT, "f16", 4), ("scalar", "f32")), (),
+                 _attention_bias),
     OperatorSpec("flash_varlen_attention_fwd",
                  (_view(IN, "f16", 2), _view(IN, "f16", 2), _view(IN, "f16", 2), _view(IN, "i32", 1),
                   _view(IN, "i32", 1), _view(OUT, "f16", 2), ("scalar", "f32")), ("CAUSAL",),

@@ -400,6 +400,79 @@ int oracle_attention_fwd(int dtype, const uint16_t *q, const uint16_t *k, const 
   return 0;
 }
 
+/* flash_attention_bias_fwd (streaming/attention.py:800-836) with summarize_biased_attention_chunk
+ * (:327-365): f16 q, k, v, o; bias [B,H,K] f32 (bias_strides: batch, head, key). Every key is
+ * valid; a chunk's scores are (dot * scale + bias[j]) * log2(e) and its maximum is the NaN-ignoring
+ * maximum, so a chunk whose scores are all -inf gives NaN weights, as the reference's does. */
+int oracle_attention_bias_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *bias, uint16_t *o,
+                              int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv,
+                              const int64_t *strides, const int64_t *bias_strides, float scale, int64_t chunk,
+                              int workers) {
+  if (batch <= 0 || heads <= 0 || sq <= 0) return 0;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const int64_t count = batch * heads * sq;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *scores = (float *)malloc(sizeof(float) * (size_t)chunk);
+    float *qrow = (float *)malloc(sizeof(float) * (size_t)d);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)dv);
+    float *cacc = (float *)malloc(sizeof(float) * (size_t)dv);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t bi = item / (heads * sq), hi = (item / sq) % heads, qi = item % sq;
+      const uint16_t *qp = q + bi * strides[0] + hi * strides[1] + qi * strides[2];
+      const float *bp = bias + bi * bias_strides[0] + hi * bias_strides[1];
+      for (int64_t t = 0; t < d; ++t) qrow[t] = load_elem(qp, 1, t * strides[3]);
+      int valid = 0;
+      float maximum = 0.0f, denominator = 0.0f;
+      for (int64_t t = 0; t < dv; ++t) acc[t] = 0.0f;
+      for (int64_t k0 = 0; k0 < sk; k0 += chunk) {
+        const int64_t k1 = k0 + chunk < sk ? k0 + chunk : sk;
+        float cmax = -INFINITY;
+        for (int64_t j = k0; j < k1; ++j) {
+          const uint16_t *kp = k + bi * strides[4] + hi * strides[5] + j * strides[6];
+          float dot = 0.0f;
+          for (int64_t t = 0; t < d; ++t) dot = dot + qrow[t] * load_elem(kp, 1, t * strides[7]);
+          scores[j - k0] = (dot * scale + bp[j * bias_strides[2]]) * log2e;
+          cmax = fmaxf(cmax, scores[j - k0]);   /* maximum_num: a NaN score is ignored */
+        }
+        float cden = 0.0f;
+        for (int64_t t = 0; t < dv; ++t) cacc[t] = 0.0f;
+        for (int64_t j = k0; j < k1; ++j) {
+          const float weight = exp2_approx_ftz(scores[j - k0] - cmax);
+          cden += weight;
+          const float w16 = oracle_half_to_float(oracle_float_to_half(weight));
+          const uint16_t *vp = v + bi * strides[8] + hi * strides[9] + j * strides[10];
+          for (int64_t t = 0; t < dv; ++t) cacc[t] = cacc[t] + w16 * load_elem(vp, 1, t * strides[11]);
+        }
+        /* merge (running, chunk); every chunk is valid */
+        const float merged = valid ? fmaxf(maximum, cmax) : cmax;
+        const float left = valid ? exp2_approx_ftz(maximum - merged) : 0.0f;
+        const float right = exp2_approx_ftz(cmax - merged);
+        denominator = left * denominator + right * cden;
+        for (int64_t t = 0; t < dv; ++t) acc[t] = left * acc[t] + right * cacc[t];
+        maximum = merged;
+        valid = 1;
+      }
+      uint16_t *op = o + bi * strides[12] + hi * strides[13] + qi * strides[14];
+      const float reciprocal = rcp_approx_ftz(valid ? denominator : 1.0f);
+      for (int64_t t = 0; t < dv; ++t) store_elem(op, 1, t * strides[15], valid ? acc[t] * reciprocal : 0.0f);
+    }
+    free(scores);
+    free(qrow);
+    free(acc);
+    free(cacc);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
 int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o, int64_t batch,
                              int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
                              float scale, int causal, int64_t chunk, int workers) {

@@ -39,6 +39,8 @@ def lib():
                                                 ctypes.POINTER(i64), f, i, i64, i]
         handle.oracle_attention_fwd_f16.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                     ctypes.POINTER(i64), f, i, i64, i]
+        handle.oracle_attention_bias_fwd.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i64, i64,
+                                                     ctypes.POINTER(i64), ctypes.POINTER(i64), f, i64, i]
         handle.oracle_csr_spmv_f32.argtypes = [p, p, p, p, p, i64, i]
         handle.oracle_csr_spmm_f32.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i]
         handle.oracle_paged_decode_partials.argtypes = [p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
@@ -241,6 +243,21 @@ def attention_varlen_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens
         part = [np.ascontiguousarray(t[lo:hi].transpose(1, 0, 2))[None] for t in (q, k, v)]
         o[lo:hi] = attention_fwd(*part, scale, causal, head_group=head_group, workers=workers)[0].transpose(1, 0, 2)
     return o[:, 0, :] if squeeze else o
+
+
+def attention_bias_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, bias: np.ndarray, scale: float, *,
+                       chunk: int = 64, workers: int | None = None) -> np.ndarray:
+    """flash_attention_bias_fwd: q [B,H,Q,D], k [B,H,K,D], v [B,H,K,DV] float16, bias [B,H,K] float32;
+    returns o [B,H,Q,DV] float16."""
+    batch, heads, sq, d = q.shape
+    sk, dv = k.shape[2], v.shape[3]
+    o = np.empty((batch, heads, sq, dv), np.float16)
+    strides = (ctypes.c_int64 * 16)(*(s // 2 for t in (q, k, v, o) for s in t.strides))
+    bias_strides = (ctypes.c_int64 * 3)(*(s // 4 for s in bias.strides))
+    lib().oracle_attention_bias_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(bias), _ptr(o), batch, heads, sq, sk, d, dv,
+                                    strides, bias_strides, float(np.float32(scale)), chunk,
+                                    workers or default_workers())
+    return o
 
 
 def attention_fwd_f16(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, causal: bool, *,

@@ -52,3 +52,21 @@ def test_argument_validation_without_gpu():
     assert small.value <= 4096                      # no row can be medium or large
     assert lib.fn["csr_spmv_f32"](1, 1, 1, 1, 1, 10, 10, 10, None, 0, None) == 5
     assert lib.fn["csr_spmv_f32"](1, 1, 1, 1, 1, 2**31 - 5, 10, 10, 1, 1 << 30, None) == 2
+
+
+def test_attention_bias_validation_without_gpu():
+    """The key-bias entry refuses a non-unit key stride, a negative stride and a null bias before
+    any HIP call; empty work is a successful no-op."""
+    lib = hiplib.library()
+    fn = lib.fn["attention_bias_fwd"]
+    strides = (ctypes.c_int64 * 16)(*([1 << 20, 1 << 16, 128, 1] * 4))
+
+    def call(bias, bias_strides, sq=4, sk=4):
+        return fn(16, 16, 16, bias, 16, 1, 1, sq, sk, 128, 128, strides, (ctypes.c_int64 * 3)(*bias_strides),
+                  0.1, None)
+
+    assert call(16, (64, 64, 2)) == 1 and b"unit key stride" in lib.fn["last_error"]()
+    assert call(16, (-64, 64, 1)) == 1 and b"negative" in lib.fn["last_error"]()
+    assert call(None, (64, 64, 1)) == 1 and b"null" in lib.fn["last_error"]()
+    assert call(18, (64, 64, 1)) == 2 and b"aligned" in lib.fn["last_error"]()
+    assert call(None, (64, 64, 1), sq=0) == 0

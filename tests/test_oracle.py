@@ -566,6 +566,81 @@ def test_attention_varlen_equals_batched_and_isolates_sequences():
     assert not (o2[seq:2 * seq].view(np.uint16) == o[seq:2 * seq].view(np.uint16)).all()
 
 
+# ------------------------------------------------------------------------------ key bias
+def _bias64(q, k, v, bias, scale):
+    """float64 softmax attention with an additive per-key bias, written out directly."""
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    logits = q @ k.transpose(0, 1, 3, 2) * scale + bias.astype(np.float64)[:, :, None, :]
+    w = np.exp(logits - logits.max(axis=3, keepdims=True))
+    return (w / w.sum(axis=3, keepdims=True)) @ v
+
+
+@pytest.mark.parametrize("sq,sk,d,dv", [(70, 200, 64, 128), (33, 64, 128, 64), (5, 1, 64, 64)])
+def test_attention_bias_against_float64(sq, sk, d, dv):
+    """Random biases of spread 3 (they move the softmax well away from the unbiased one): the
+    oracle meets float64 attention on every row, and a bias row of zeros gives the unbiased
+    non-causal oracle (bit for bit where the scale is a power of two), so a dropped or misplaced
+    bias term breaks one of the two."""
+    g = np.random.default_rng(sq + sk + d)
+    q, k = inputs.normal(g, (2, 3, sq, d), "f16"), inputs.normal(g, (2, 3, sk, d), "f16")
+    v = inputs.normal(g, (2, 3, sk, dv), "f16")
+    bias = (3.0 * g.standard_normal((2, 3, sk))).astype(np.float32)
+    scale = float(np.float32(d ** -0.5))
+    o = oracle.attention_bias_fwd(q, k, v, bias, scale).astype(np.float64)
+    want = _bias64(q, k, v, bias, scale)
+    assert np.all(np.abs(o - want) <= 2e-2 * np.abs(want) + 1e-2)
+    unbiased = _bias64(q, k, v, np.zeros_like(bias), scale)
+    assert sk == 1 or np.abs(want - unbiased).max() > 0.1   # the bias matters at this spread
+    zero = oracle.attention_bias_fwd(q, k, v, np.zeros_like(bias), scale)
+    plain = oracle.attention_fwd(q, k, v, scale, False)
+    if d == 64:     # scale 1/8: (dot scale) log2 e rounds as dot (scale log2 e) does
+        assert (zero.view(np.uint16) == plain.view(np.uint16)).all()
+    else:
+        assert np.abs(zero.astype(np.float64) - plain.astype(np.float64)).max() <= 2e-3
+
+
+def test_attention_bias_row_selection_and_layout():
+    """The bias of (batch b, head h) reaches only that row: a dominant key j0 (bias +40) returns
+    v[j0] in that head and leaves every other head unchanged; a constant bias row leaves its head
+    at the unbiased result; a strided bias view equals its contiguous copy."""
+    g = np.random.default_rng(5)
+    q, k = inputs.normal(g, (2, 2, 40, 64), "f16"), inputs.normal(g, (2, 2, 150, 64), "f16")
+    v = inputs.normal(g, (2, 2, 150, 64), "f16")
+    base = np.zeros((2, 2, 150), np.float32)
+    plain = oracle.attention_bias_fwd(q, k, v, base, 0.125)
+    dominant = base.copy()
+    dominant[1, 0, 97] = 40.0
+    o = oracle.attention_bias_fwd(q, k, v, dominant, 0.125)
+    assert np.abs(o[1, 0].astype(np.float64) - v[1, 0, 97].astype(np.float64)[None, :]).max() <= 2e-3
+    others = [(0, 0), (0, 1), (1, 1)]
+    for b, h in others:
+        assert (o[b, h].view(np.uint16) == plain[b, h].view(np.uint16)).all()
+    shifted = base.copy()
+    shifted[0, 1] = 7.5
+    o = oracle.attention_bias_fwd(q, k, v, shifted, 0.125).astype(np.float64)
+    assert np.abs(o[0, 1] - plain[0, 1].astype(np.float64)).max() <= 2e-3
+    wide = (g.standard_normal((2, 2, 160))).astype(np.float32)
+    view = wide[:, :, 5:155]
+    assert (oracle.attention_bias_fwd(q, k, v, view, 0.125).view(np.uint16)
+            == oracle.attention_bias_fwd(q, k, v, np.ascontiguousarray(view), 0.125).view(np.uint16)).all()
+
+
+def test_attention_bias_minus_infinity():
+    """-inf removes a key (weight 0) while its chunk keeps a finite score; a chunk whose every
+    score is -inf makes the row NaN, as the reference's chunk summary does (max - max of -inf)."""
+    g = np.random.default_rng(8)
+    q, k = inputs.normal(g, (1, 1, 8, 64), "f16"), inputs.normal(g, (1, 1, 128, 64), "f16")
+    v = inputs.normal(g, (1, 1, 128, 64), "f16")
+    bias = np.zeros((1, 1, 128), np.float32)
+    bias[0, 0, ::3] = -np.inf
+    o = oracle.attention_bias_fwd(q, k, v, bias, 0.125).astype(np.float64)
+    keep = np.isfinite(bias[0, 0])
+    want = _bias64(q[:, :, :, :], k[:, :, keep], v[:, :, keep], bias[:, :, keep], 0.125)
+    assert np.all(np.abs(o - want) <= 2e-2 * np.abs(want) + 1e-2)
+    bias[0, 0, 64:] = -np.inf
+    assert np.isnan(oracle.attention_bias_fwd(q, k, v, bias, 0.125, chunk=64).astype(np.float32)).all()
+
+
 # ------------------------------------------------------------------------------ int8 GEMM
 def test_gemm_i8_oracle_pinned():
     """gemm_i8: against a scalar loop on a small case, an identity operand (c = b + bias exactly),
