@@ -52,7 +52,7 @@ def parse():
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
                                 "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill,gemm_i8,quantized_gemm,"
-                                "attention_bias")
+                                "attention_bias,continuous_decode,grouped_decode,varlen_decode")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -711,6 +711,111 @@ def op_paged_decode(device, flush, cpu):
     return out
 
 
+def op_continuous_decode(device, flush, cpu):
+    """continuous_gqa_decode at the reference's GQA decode constants (streaming/attention.py:28-34):
+    B32, HQ32 over HK8, K8192, D128, token-major f16 caches, every key admitted. HBM bytes: the K and
+    V caches, the mask, q and the output, plus the split states written and read back."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples.kernels.streaming.attention import continuous_gqa_decode
+
+    batch, hq, hk, keys, d = 32, 32, 8, 8192, 128
+    generator = torch.Generator(device=device).manual_seed(12)     # 1 GiB of cache: drawn on the device
+    draw = lambda shape: torch.randn(shape, generator=generator, device=device).to(torch.float16)  # noqa: E731
+    q, k, v = draw((batch, hq, d)), draw((batch, keys, hk, d)), draw((batch, keys, hk, d))
+    mask = torch.ones((batch, keys, hk), dtype=torch.uint8, device=device)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    call = intent.jit(continuous_gqa_decode, backend="hip", constexprs={"HEAD_GROUP": hq // hk}).prepare(
+        q, k, v, mask, scale)
+    ms = operator_ms(call.launch, flush)
+    splits = 8                                   # 2048 workgroups: 1024 keys per split at this shape
+    state = batch * hq * splits * (d + 2) * 4
+    nbytes = 2 * k.numel() * 2 + mask.numel() + q.numel() * 2 + batch * hq * d * 2 + 2 * state
+    out = {"config": f"continuous GQA decode f16 B{batch} HQ{hq} HK{hk} K{keys} D{d}, token-major caches, all keys "
+                     f"admitted (continuous_gqa_decode: partials + merge)",
+           "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    if cpu:
+        import oracle
+
+        host = [a[:4].cpu().numpy() for a in (q, k, v, mask)]
+        seconds = cpu_median_seconds(lambda: oracle.continuous_gqa_decode(*host, scale))
+        out["cpu"] = {"gbs": round(nbytes / 8 / seconds / 1e9, 3), "cores": oracle.default_workers(), "kind": "port",
+                      "sample": "the first 4 of the 32 batch rows"}
+    return out
+
+
+def op_grouped_decode(device, flush, cpu):
+    """grouped_flash_decode_partials at the same constants in bf16 (head-major caches [B,HK,K,D]),
+    P = 8 parts of SPLIT_SIZE 1024. HBM bytes: the K and V caches, q and the partials written."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples.kernels.streaming.attention import grouped_flash_decode_partials
+
+    batch, hq, hk, keys, d, parts = 32, 32, 8, 8192, 128, 8
+    generator = torch.Generator(device=device).manual_seed(13)
+    draw = lambda shape: torch.randn(shape, generator=generator, device=device).to(torch.bfloat16)  # noqa: E731
+    q, k, v = draw((batch, hq, 1, d)), draw((batch, hk, keys, d)), draw((batch, hk, keys, d))
+    scale = float(np.float32(1 / np.sqrt(d)))
+    call = intent.jit(grouped_flash_decode_partials, backend="hip",
+                      constexprs={"HEAD_GROUP": hq // hk, "P": parts, "SPLIT_SIZE": keys // parts}).prepare(
+        q, k, v, scale)
+    ms = operator_ms(call.launch, flush)
+    nbytes = 2 * k.numel() * 2 + q.numel() * 2 + batch * hq * parts * (d * 2 + 4)
+    out = {"config": f"grouped flash decode partials bf16 B{batch} HQ{hq} HK{hk} K{keys} D{d}, P{parts} x "
+                     f"{keys // parts} (grouped_flash_decode_partials)",
+           "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    if cpu:
+        import oracle
+
+        host = [a[:4].float().cpu().numpy() for a in (q, k, v)]
+        bf = [oracle.float_to_bf16_bits(a) for a in host]
+        seconds = cpu_median_seconds(lambda: oracle.grouped_decode_partials(*bf, scale, parts=parts,
+                                                                            split_size=keys // parts))
+        out["cpu"] = {"gbs": round(nbytes / 8 / seconds / 1e9, 3), "cores": oracle.default_workers(), "kind": "port",
+                      "sample": "the first 4 of the 32 batch rows"}
+    return out
+
+
+def op_varlen_decode(device, flush, cpu):
+    """varlen_gqa_decode_with_sink_logits at the reference's constants (streaming/attention.py:18-27):
+    8 packed sequences of 1..4096 keys (uniform, seed 14), HQ32 over HK8, D64, MAX_BLOCKS 64."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.streaming.attention import varlen_gqa_decode_with_sink_logits
+
+    rng = np.random.default_rng(14)
+    lengths = rng.integers(1, 4097, 8)
+    cu = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
+    batch, hq, hk, d, rows = 8, 32, 8, 64, int(cu[-1])
+    q = inputs.normal(rng, (batch, hq, d), "f16")
+    k, v = inputs.normal(rng, (rows, hk, d), "f16"), inputs.normal(rng, (rows, hk, d), "f16")
+    sink = rng.uniform(0.0, 2.0, hq).astype(np.float32)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    call = intent.jit(varlen_gqa_decode_with_sink_logits, backend="hip",
+                      constexprs={"HEAD_GROUP": hq // hk, "MAX_BLOCKS": 64}).prepare(
+        t(q), t(k), t(v), t(cu), t(sink), scale)
+    ms = operator_ms(call.launch, flush)
+    nbytes = 2 * k.nbytes + q.nbytes + batch * hq * d * 2 + batch * hq * 64 * 4 * 2
+    out = {"config": f"packed GQA decode with sink and block logits f16, {batch} sequences of 1..4096 keys ({rows} "
+                     f"rows), HQ{hq} HK{hk} D{d} (varlen_gqa_decode_with_sink_logits)",
+           "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    if cpu:
+        import oracle
+
+        seconds = cpu_median_seconds(lambda: oracle.varlen_decode_sink(q, k, v, cu, sink, scale, max_blocks=64))
+        out["cpu"] = {"gbs": round(nbytes / seconds / 1e9, 3), "cores": oracle.default_workers(), "kind": "port",
+                      "sample": "the whole workload"}
+    return out
+
+
 def op_spmm(device, flush, cpu):
     """csr_spmm at the sparse/csr_spmm.py:5-9 constants: 8192 x 8192, 32 nonzeros per row, 128 f32
     features. The dense operand (4 MB) is re-read per nonzero from L2/MALL; algorithmic HBM bytes
@@ -748,7 +853,9 @@ OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_att
              "gqa": op_gqa, "attention_bf16": op_attention_bf16, "attention_bwd": op_attention_bwd,
              "attention_bwd_large": op_attention_bwd_large, "paged_decode": op_paged_decode,
              "spmm": op_spmm, "varlen_prefill": op_varlen_prefill, "gemm_i8": op_gemm_i8,
-             "quantized_gemm": op_quantized_gemm, "attention_bias": op_attention_bias}
+             "quantized_gemm": op_quantized_gemm, "attention_bias": op_attention_bias,
+             "continuous_decode": op_continuous_decode, "grouped_decode": op_grouped_decode,
+             "varlen_decode": op_varlen_decode}
 
 
 def read_traffic(name):

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 12
+#define INTENT_HIP_ABI_VERSION 13
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -60,7 +60,11 @@ enum IntentHipOperator {
   INTENT_HIP_OP_ATTENTION_VARLEN = 14,    /* packed sequences; dtype F16 or BF16, cols = d | dv << 16 */
   INTENT_HIP_OP_GEMM_I8 = 15,
   INTENT_HIP_OP_QUANTIZED_GEMM = 16,
-  INTENT_HIP_OP_ATTENTION_BIAS = 17       /* f16; cols = d | dv << 16 */
+  INTENT_HIP_OP_ATTENTION_BIAS = 17,      /* f16; cols = d | dv << 16 */
+  INTENT_HIP_OP_GROUPED_DECODE_PARTIALS = 18, /* rows = HEAD_GROUP, cols = head dimension */
+  INTENT_HIP_OP_CONTINUOUS_DECODE = 19,   /* rows = HEAD_GROUP, cols = head dimension */
+  INTENT_HIP_OP_VARLEN_DECODE = 20,       /* rows = HEAD_GROUP, cols = head dimension */
+  INTENT_HIP_OP_DECODE_MERGE = 21         /* cols = head dimension */
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -305,6 +309,53 @@ int intent_hip_paged_decode_partials(const void *q, const void *key_cache, const
 int intent_hip_splitk_reduce_f32_to_f16(const float *partial, const float *lse, void *out, int64_t batch,
                                         int64_t heads, int64_t splits, int64_t d, const int64_t strides[10],
                                         void *stream);
+
+/* Grouped-query decode partials over dense bf16 caches: grouped_flash_decode_partials
+ * (streaming/attention.py:556-627) with summarize_attention_chunk_bf16 (:195-237). q
+ * [batch, q_heads, 1, d], k [batch, kv_heads, keys, d], v [batch, kv_heads, keys, dv] (bf16);
+ * part p of (b, key head) covers keys p * split_size .. + split_size below `keys`. Weights are
+ * rounded to bf16 before P @ V. partial_lse f32 [batch, q_heads, parts] (max + ln(den) log2 e,
+ * -inf for a part with no key), partial_output bf16 [batch, q_heads, parts, dv] (acc / den, 0 for
+ * a part with no key). q_heads = kv_heads * head_group, head_group 1..16, d = dv = 64 or 128.
+ * strides[19]: q[4], k[4], v[4], partial_lse[3], partial_output[4]. */
+int intent_hip_grouped_decode_partials(const void *q, const void *k, const void *v, float *partial_lse,
+                                       void *partial_output, int64_t batch, int64_t q_heads,
+                                       int64_t kv_heads, int64_t head_group, int64_t keys, int64_t d,
+                                       int64_t dv, int64_t parts, int64_t split_size,
+                                       const int64_t strides[19], float scale, void *stream);
+
+/* Decode over a dense f16 cache with a validity mask: continuous_gqa_decode
+ * (streaming/attention.py:629-670) with summarize_masked_attention_chunk (:250-285). q
+ * [batch, q_heads, d], k [batch, keys, kv_heads, d], v [batch, keys, kv_heads, dv], valid_mask u8
+ * [batch, keys, kv_heads] (key j of head kh admitted where nonzero), output f16
+ * [batch, q_heads, dv] (0 for a query with no admitted key). The keys are split over workgroups
+ * whose states merge in a second kernel; the workspace (256-byte aligned) holds
+ * intent_hip_dense_decode_workspace_bytes(batch, q_heads, kv_heads, keys, dv) bytes.
+ * strides[17]: q[3], k[4], v[4], valid_mask[3], output[3]. */
+int intent_hip_dense_decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t keys,
+                                            int64_t dv, size_t *bytes);
+int intent_hip_continuous_gqa_decode(const void *q, const void *k, const void *v, const uint8_t *valid_mask,
+                                     void *out, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                     int64_t head_group, int64_t keys, int64_t d, int64_t dv,
+                                     const int64_t strides[17], float scale, void *workspace,
+                                     size_t workspace_bytes, void *stream);
+
+/* Decode over packed f16 sequences with a per-head sink and block logits:
+ * varlen_gqa_decode_with_sink_logits (streaming/attention.py:672-754). q [sequences, q_heads, d],
+ * k [rows, kv_heads, d], v [rows, kv_heads, dv]; sequence b is rows cu_seqlens[b] .. [b + 1]
+ * (offsets clamped into [0, rows]), of which the first 64 * max_blocks keys are attended, in
+ * 64-key blocks. With M the largest block maximum (exp2 domain) and den the merged denominator,
+ * output = acc / (den + sink[h]) (f16; 0 for an empty sequence) and block_logits[b, h, j] =
+ * exp2(max_j - M) / (den + sink[h]) for j < ceil(length / 64), else 0 (f32). The workspace
+ * (256-byte aligned) holds intent_hip_varlen_decode_workspace_bytes(sequences, q_heads, kv_heads,
+ * max_blocks, dv) bytes. strides[15]: q[3], k[3], v[3], output[3], block_logits[3]. */
+int intent_hip_varlen_decode_workspace_bytes(int64_t sequences, int64_t q_heads, int64_t kv_heads,
+                                             int64_t max_blocks, int64_t dv, size_t *bytes);
+int intent_hip_varlen_decode_sink(const void *q, const void *k, const void *v, const int32_t *cu_seqlens,
+                                  const float *sink, void *out, float *block_logits, int64_t sequences,
+                                  int64_t rows, int64_t q_heads, int64_t kv_heads, int64_t head_group,
+                                  int64_t d, int64_t dv, int64_t max_blocks, const int64_t strides[15],
+                                  float scale, void *workspace, size_t workspace_bytes, void *stream);
 
 /* CSR SpMV y = A x, f32 values, i32 indices.
  * csr_spmv (python/intent/examples/kernels/sparse/csr_spmv.py:11-29), with dynamic extents. Row r

@@ -111,6 +111,10 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     case INTENT_HIP_OP_ATTENTION_BWD_DKDV: return attention_bwd_resources(2, rows, cols, out);
     case INTENT_HIP_OP_PAGED_DECODE_PARTIALS: return decode_resources(0, cols, rows, out);
     case INTENT_HIP_OP_SPLITK_REDUCE: return decode_resources(1, cols, rows, out);
+    case INTENT_HIP_OP_GROUPED_DECODE_PARTIALS: return decode_resources(2, cols, rows, out);
+    case INTENT_HIP_OP_CONTINUOUS_DECODE: return decode_resources(3, cols, rows, out);
+    case INTENT_HIP_OP_VARLEN_DECODE: return decode_resources(4, cols, rows, out);
+    case INTENT_HIP_OP_DECODE_MERGE: return decode_resources(5, cols, rows, out);
     case INTENT_HIP_OP_CSR_SPMM_F32: return spmm_resources(cols, out);
     case INTENT_HIP_OP_GEMM_I8: return gemm_i8_resources(rows, cols, out);
     case INTENT_HIP_OP_QUANTIZED_GEMM: return quantized_gemm_resources(out);

@@ -30,6 +30,11 @@ HEADS = 32
 SEQUENCE = 4096
 HEAD_DIMENSION = 128
 SCALE = 1.0 / math.sqrt(HEAD_DIMENSION)
+# Decode extents of the reference's examples (streaming/attention.py:18-34).
+GQA_DECODE_BATCH, GQA_DECODE_QUERY_HEADS, GQA_DECODE_KV_HEADS = 32, 32, 8
+GQA_DECODE_SEQUENCE, GQA_DECODE_HEAD_DIMENSION = 8192, 128
+VARLEN_GQA_DECODE_BATCH, VARLEN_GQA_DECODE_QUERY_HEADS, VARLEN_GQA_DECODE_KV_HEADS = 8, 32, 8
+VARLEN_GQA_DECODE_HEAD_DIMENSION, VARLEN_GQA_DECODE_BLOCK_SIZE, VARLEN_GQA_DECODE_MAX_BLOCKS = 64, 64, 64
 
 
 @intent.fn
@@ -180,3 +185,109 @@ def flash_varlen_gqa_prefill(
             shared = h // HEAD_GROUP
             output[rows, h, :] = attend_head(q[rows, h, :], k[rows, shared, :], v[rows, shared, :], scale, True,
                                              I.f16)
+
+
+# ------------------------------------------------------------------------------ decode
+# One query row per (batch, query head) against a key/value cache (streaming/attention.py:556-754).
+# Each definition folds its keys as the forward ones do (exp2-domain logits, weights rounded to the
+# storage type before they weigh the values); they differ in where the keys live and what is kept.
+@intent.fn
+def decode_summary(query_row, k_rows, v_rows, admitted, scale, element):
+    logits = I.matmul(query_row, k_rows, transpose_rhs=True, acc_dtype=I.f32) * (scale * I.LOG2E)
+    return admitted_attention(logits, admitted, v_rows, element)
+
+
+@intent.kernel
+def grouped_flash_decode_partials(
+    q: I.In[I.bf16, ("B", "HQ", 1, "D")],
+    k: I.In[I.bf16, ("B", "HK", "K", "D")],
+    v: I.In[I.bf16, ("B", "HK", "K", "DV")],
+    partial_lse: I.Out[I.f32, ("B", "HQ", "P")],
+    partial_output: I.Out[I.bf16, ("B", "HQ", "P", "DV")],
+    scale: I.f32,
+    HEAD_GROUP: I.Constexpr[int],
+    P: I.Constexpr[int],
+    SPLIT_SIZE: I.Constexpr[int],
+):
+    """Part p of every (batch, query head) covers key slots p * SPLIT_SIZE .. + SPLIT_SIZE of its
+    key head, those below K taking part. It keeps the part's base-2 log-sum (peak + log2 of the
+    weight total; -inf when no slot takes part) and its normalised mix in bf16 (0 when none)."""
+    B, HQ, K = q.shape[0], q.shape[1], k.shape[2]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, HQ)):
+            shared = h // HEAD_GROUP
+            for part in I.parallel(I.domain(0, P)):
+                keys = I.domain(I.minimum(part * SPLIT_SIZE, K), I.minimum((part + 1) * SPLIT_SIZE, K))
+                admitted = causal_pairs(I.indices(I.domain(0, 1)), I.indices(keys), False)
+                summary = decode_summary(q[b, h, :, :], k[b, shared, keys, :], v[b, shared, keys, :], admitted,
+                                         scale, I.bf16)
+                share = I.fdiv(1.0, summary.total, approximate=True, flush_to_zero=True)
+                partial_lse[b, h, part] = I.select(summary.live[0], summary.peak[0] + I.log(summary.total[0]) * I.LOG2E,
+                                                   -I.inf)
+                partial_output[b, h, part, :] = I.cast(I.select(summary.live[0], summary.mixed[0] * share[0], 0.0),
+                                                       I.bf16)
+
+
+@intent.kernel
+def continuous_gqa_decode(
+    q: I.In[I.f16, ("B", "HQ", "D")],
+    k: I.In[I.f16, ("B", "K", "HK", "D")],
+    v: I.In[I.f16, ("B", "K", "HK", "DV")],
+    valid_mask: I.In[I.u8, ("B", "K", "HK")],
+    output: I.Out[I.f16, ("B", "HQ", "DV")],
+    scale: I.f32,
+    HEAD_GROUP: I.Constexpr[int],
+):
+    """Token-major cache; key j of key head kh takes part where valid_mask[b, j, kh] is nonzero. A
+    query with no admitted key gives 0."""
+    B, HQ, D = q.shape
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, HQ)):
+            shared = h // HEAD_GROUP
+            admitted = (valid_mask[b, :, shared] != 0)[None, :]
+            summary = decode_summary(I.reshape(q[b, h, :], (1, D)), k[b, :, shared, :], v[b, :, shared, :], admitted,
+                                     scale, I.f16)
+            share = I.fdiv(1.0, summary.total, approximate=True, flush_to_zero=True)
+            output[b, h, :] = I.cast(I.select(summary.live[0], summary.mixed[0] * share[0], 0.0), I.f16)
+
+
+@intent.kernel
+def varlen_gqa_decode_with_sink_logits(
+    q: I.In[I.f16, ("B", "HQ", "D")],
+    k: I.In[I.f16, ("U", "HK", "D")],
+    v: I.In[I.f16, ("U", "HK", "DV")],
+    cu_seqlens: I.In[I.i32, ("B_PLUS_1",)],
+    sink: I.In[I.f32, ("HQ",)],
+    output: I.Out[I.f16, ("B", "HQ", "DV")],
+    block_logits: I.Out[I.f32, ("B", "HQ", VARLEN_GQA_DECODE_MAX_BLOCKS)],
+    scale: I.f32,
+    HEAD_GROUP: I.Constexpr[int],
+    MAX_BLOCKS: I.Constexpr[int],
+):
+    """Sequence s's keys are rows cu_seqlens[s] .. cu_seqlens[s + 1], folded in blocks of
+    VARLEN_GQA_DECODE_BLOCK_SIZE; only the first MAX_BLOCKS blocks are read. With `peak` the
+    largest block peak and `total` the weight total against it, the sink of the query head joins
+    the total: output = mix / (total + sink[h]); block j's logit is exp2(peak_j - peak) / (total +
+    sink[h]) for the sequence's blocks, 0 past them. An empty sequence gives 0 everywhere."""
+    B, HQ, D = q.shape
+    size = VARLEN_GQA_DECODE_BLOCK_SIZE
+    for s in I.parallel(I.domain(0, B)):
+        begin, end = cu_seqlens[s], cu_seqlens[s + 1]
+        blocks = (end - begin + size - 1) // size
+        for h in I.parallel(I.domain(0, HQ)):
+            shared = h // HEAD_GROUP
+            query = I.reshape(q[s, h, :], (1, D))
+            rows = I.domain(begin, I.minimum(end, begin + size * MAX_BLOCKS))
+            admitted = causal_pairs(I.indices(I.domain(0, 1)), I.indices(rows), False)
+            summary = decode_summary(query, k[rows, shared, :], v[rows, shared, :], admitted, scale, I.f16)
+            share = I.fdiv(1.0, I.select(summary.live[0], summary.total[0] + sink[h], 1.0), approximate=True,
+                           flush_to_zero=True)
+            output[s, h, :] = I.cast(I.select(summary.live[0], summary.mixed[0] * share, 0.0), I.f16)
+            for j in I.domain(0, MAX_BLOCKS):
+                block = I.domain(I.minimum(begin + j * size, end), I.minimum(begin + (j + 1) * size, end))
+                peak_j = decode_summary(query, k[block, shared, :], v[block, shared, :],
+                                        causal_pairs(I.indices(I.domain(0, 1)), I.indices(block), False), scale,
+                                        I.f16).peak[0]
+                block_logits[s, h, j] = I.select(j < blocks,
+                                                 I.exp2(peak_j - summary.peak[0], approximate=True,
+                                                        flush_to_zero=True) * share, 0.0)

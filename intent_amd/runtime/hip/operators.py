@@ -28,6 +28,9 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   attention_backward_dq   backward/attention.py:171-211    intent_hip_attention_bwd_dq
   paged_gqa_decode_partials streaming/paged_attention.py:77-165  intent_hip_paged_decode_partials
   splitk_attention_f32_to_f16_reduce streaming/splitk_reduce.py:129-155  intent_hip_splitk_reduce_f32_to_f16
+  grouped_flash_decode_partials streaming/attention.py:556-627  intent_hip_grouped_decode_partials
+  continuous_gqa_decode   streaming/attention.py:629-670   intent_hip_continuous_gqa_decode
+  varlen_gqa_decode_with_sink_logits streaming/attention.py:672-754  intent_hip_varlen_decode_sink
   csr_spmm                sparse/csr_spmm.py:11-33         intent_hip_csr_spmm_f32
 
 (paths relative to python/intent/examples/kernels/ in the reference).
@@ -48,7 +51,7 @@ from typing import Callable
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, STATIC_SCRATCH_BYTES, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
                       OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_BIAS, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8, OP_QUANTIZED_GEMM,
-                      OP_CSR_SPMM_F32, OP_PAGED_DECODE_PARTIALS, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
+                      OP_CSR_SPMM_F32, OP_CONTINUOUS_DECODE, OP_GROUPED_DECODE_PARTIALS, OP_PAGED_DECODE_PARTIALS, OP_VARLEN_DECODE, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
 @dataclass
@@ -534,6 +537,112 @@ def _paged_decode_partials(lib, bound, constexprs, device):
                   lambda: lib.kernel_resources(OP_PAGED_DECODE_PARTIALS, F16, group, d))
 
 
+def _grouped_decode_partials(lib, bound, constexprs, device):
+    """grouped_flash_decode_partials: one workgroup per (batch, part, key head) over the bf16 caches."""
+    q, k, v, partial_lse, partial_output, scale = bound.arguments
+    group = _positive_constexpr(constexprs, "HEAD_GROUP")
+    parts = _positive_constexpr(constexprs, "P")
+    split = _positive_constexpr(constexprs, "SPLIT_SIZE")
+    batch, q_heads, _, d = q.shape
+    kv_heads, keys, dv = k.shape[1], k.shape[2], v.shape[3]
+    if partial_lse.shape[2] != parts:
+        raise ValueError(f"partial_lse holds {partial_lse.shape[2]} parts, P is {parts}")
+    if kv_heads * group != q_heads:
+        raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({kv_heads}) * HEAD_GROUP ({group})")
+    keep, before, after = [q, k, v, partial_lse, partial_output], [], []
+    qk, kk, vk = _readable(q, keep, before), _readable(k, keep, before, 8), _readable(v, keep, before, 8)
+    lk, ok = _writable(partial_lse, keep, after), _writable(partial_output, keep, after)
+    strides = _strides(qk, kk, vk, lk, ok)
+    keep.append(strides)
+    fn = lib.fn["grouped_decode_partials"]
+    args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), lk.data_ptr(), ok.data_ptr(), batch, q_heads, kv_heads, group,
+            keys, d, dv, parts, split, strides, float(scale))
+    return Launch("intent_hip_grouped_decode_partials", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("batch", batch), ("q_heads", q_heads), ("kv_heads", kv_heads), ("keys", keys),
+                                 ("d", d), ("parts", parts), ("split_size", split)),
+                  lambda: lib.kernel_resources(OP_GROUPED_DECODE_PARTIALS, BF16, group, d))
+
+
+def _decode_workspace(name):
+    if _static_workspace():
+        raise CompilationStageError(
+            "provider_preparation", f"{name} merges split states through a workspace; backend_options "
+            "workspace='static' has none for it, use workspace='prepare'")
+
+
+def _continuous_decode(lib, bound, constexprs, device):
+    """continuous_gqa_decode: the keys split over (batch, split, key head) workgroups whose states
+    merge in a second kernel, through a workspace allocated here."""
+    import ctypes
+
+    import torch
+
+    q, k, v, mask, output, scale = bound.arguments
+    group = _positive_constexpr(constexprs, "HEAD_GROUP")
+    batch, q_heads, d = q.shape
+    keys, kv_heads, dv = k.shape[1], k.shape[2], v.shape[3]
+    if kv_heads * group != q_heads:
+        raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({kv_heads}) * HEAD_GROUP ({group})")
+    _decode_workspace("continuous_gqa_decode")
+    keep, before, after = [q, k, v, mask, output], [], []
+    qk, kk, vk = _readable(q, keep, before), _readable(k, keep, before, 8), _readable(v, keep, before, 8)
+    mk, ok = _readable(mask, keep, before), _writable(output, keep, after)
+    strides = _strides(qk, kk, vk, mk, ok)
+    size = ctypes.c_size_t(0)
+    lib.check(lib.fn["dense_decode_workspace_bytes"](batch, q_heads, kv_heads, keys, dv, ctypes.byref(size)),
+              "provider_preparation")
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+    keep += [strides, workspace]
+    fn = lib.fn["continuous_gqa_decode"]
+    args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), mk.data_ptr(), ok.data_ptr(), batch, q_heads, kv_heads, group,
+            keys, d, dv, strides, float(scale), workspace.data_ptr(), size.value)
+    return Launch("intent_hip_continuous_gqa_decode", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("batch", batch), ("q_heads", q_heads), ("kv_heads", kv_heads), ("keys", keys),
+                                 ("d", d), ("workspace_bytes", size.value)),
+                  lambda: lib.kernel_resources(OP_CONTINUOUS_DECODE, F16, group, d))
+
+
+def _varlen_decode(lib, bound, constexprs, device):
+    """varlen_gqa_decode_with_sink_logits: packed sequences split over (sequence, split, key head)
+    workgroups; the merge adds the sink and turns the block maxima (kept in block_logits) into
+    block logits. The offsets stay on the device."""
+    import ctypes
+
+    import torch
+
+    q, k, v, cu, sink, output, block_logits, scale = bound.arguments
+    group = _positive_constexpr(constexprs, "HEAD_GROUP")
+    max_blocks = _positive_constexpr(constexprs, "MAX_BLOCKS")
+    sequences, q_heads, d = q.shape
+    rows, kv_heads, dv = k.shape[0], k.shape[1], v.shape[2]
+    if kv_heads * group != q_heads:
+        raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({kv_heads}) * HEAD_GROUP ({group})")
+    if cu.shape[0] != sequences + 1:
+        raise ValueError(f"cu_seqlens needs q.shape[0] + 1 = {sequences + 1} entries, got {cu.shape[0]}")
+    if max_blocks > block_logits.shape[2]:
+        raise ValueError(f"MAX_BLOCKS ({max_blocks}) exceeds the {block_logits.shape[2]} block_logits columns")
+    _decode_workspace("varlen_gqa_decode_with_sink_logits")
+    keep, before, after = [q, k, v, cu, sink, output, block_logits], [], []
+    qk, kk, vk = _readable(q, keep, before), _readable(k, keep, before, 8), _readable(v, keep, before, 8)
+    cuk, sk = _readable(cu, keep, before), _readable(sink, keep, before)
+    ok, bk = _writable(output, keep, after), _writable(block_logits, keep, after)
+    strides = _strides(qk, kk, vk, ok, bk)
+    size = ctypes.c_size_t(0)
+    lib.check(lib.fn["varlen_decode_workspace_bytes"](sequences, q_heads, kv_heads, max_blocks, dv,
+                                                      ctypes.byref(size)), "provider_preparation")
+    workspace = torch.empty(max(size.value, 1), dtype=torch.uint8, device=device)
+    keep += [strides, workspace]
+    fn = lib.fn["varlen_decode_sink"]
+    args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), cuk.data_ptr(), sk.data_ptr(), ok.data_ptr(), bk.data_ptr(),
+            sequences, rows, q_heads, kv_heads, group, d, dv, max_blocks, strides, float(scale),
+            workspace.data_ptr(), size.value)
+    return Launch("intent_hip_varlen_decode_sink", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("sequences", sequences), ("rows", rows), ("q_heads", q_heads),
+                                 ("kv_heads", kv_heads), ("d", d), ("max_blocks", max_blocks),
+                                 ("workspace_bytes", size.value)),
+                  lambda: lib.kernel_resources(OP_VARLEN_DECODE, F16, group, d))
+
+
 def _splitk_reduce(lib, bound, constexprs, device):
     partial, lse, output = bound.arguments
     keep, before, after = [partial, lse, output], [], []
@@ -664,6 +773,17 @@ _SPECS = (
                   _view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "i32", 1), _view(OUT, "f32", 3),
                   _view(OUT, "f32", 4), ("scalar", "f32")), ("PAGE_SIZE", "HEAD_GROUP", "SPLITS"),
                  _paged_decode_partials),
+    OperatorSpec("grouped_flash_decode_partials",
+                 (_view(IN, "bf16", 4), _view(IN, "bf16", 4), _view(IN, "bf16", 4), _view(OUT, "f32", 3),
+                  _view(OUT, "bf16", 4), ("scalar", "f32")), ("HEAD_GROUP", "P", "SPLIT_SIZE"),
+                 _grouped_decode_partials),
+    OperatorSpec("continuous_gqa_decode",
+                 (_view(IN, "f16", 3), _view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "u8", 3),
+                  _view(OUT, "f16", 3), ("scalar", "f32")), ("HEAD_GROUP",), _continuous_decode),
+    OperatorSpec("varlen_gqa_decode_with_sink_logits",
+                 (_view(IN, "f16", 3), _view(IN, "f16", 3), _view(IN, "f16", 3), _view(IN, "i32", 1),
+                  _view(IN, "f32", 1), _view(OUT, "f16", 3), _view(OUT, "f32", 3), ("scalar", "f32")),
+                 ("HEAD_GROUP", "MAX_BLOCKS"), _varlen_decode),
     OperatorSpec("splitk_attention_f32_to_f16_reduce", (_view(IN, "f32", 4), _view(IN, "f32", 3),
                                                         _view(OUT, "f16", 3)), (), _splitk_reduce),
     OperatorSpec("csr_spmm", (_view(IN, "i32", 1), _view(IN, "i32", 1), _view(IN, "f32", 1), _view(IN, "f32", 2),

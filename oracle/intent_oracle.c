@@ -739,6 +739,225 @@ int oracle_paged_decode_partials(const uint16_t *q, const uint16_t *kc, const ui
   return 0;
 }
 
+/* ------------------------------------------------------------------ decode variants
+ * The fold of one query over a list of keys, chunk by chunk, as the attention definitions write it
+ * (summarize_attention_chunk_f16 / _bf16 and summarize_masked_attention_chunk,
+ * streaming/attention.py:152-285, merged by merge_attention_summaries :82-114): scores
+ * dot * scale * log2e over active keys, the chunk maximum by maximum_num (0 for a chunk with no
+ * active key), weights exp2(s - chunk max) rounded to the storage type before P @ V, chunks merged
+ * with exp2 factors. krows[j] / vrows[j] are key j's rows (unit inner stride); active may be null
+ * (every key active). chunk_max, when not null, receives each chunk's maximum. */
+typedef struct {
+  int valid;
+  float maximum, denominator;
+} fold_state;
+
+static fold_state fold_keys(int dtype, const float *qrow, int64_t d, int64_t dv, const uint16_t *const *krows,
+                            const uint16_t *const *vrows, const unsigned char *active, int64_t n, float factor,
+                            int64_t chunk, float *scores, float *cacc, float *acc, float *chunk_max) {
+  fold_state st = {0, 0.0f, 0.0f};
+  for (int64_t t = 0; t < dv; ++t) acc[t] = 0.0f;
+  for (int64_t k0 = 0; k0 < n; k0 += chunk) {
+    const int64_t k1 = k0 + chunk < n ? k0 + chunk : n;
+    int cvalid = 0;
+    float cmax = -INFINITY;
+    for (int64_t j = k0; j < k1; ++j) {
+      const int on = active == NULL || active[j];
+      float dot = 0.0f;
+      if (on)
+        for (int64_t t = 0; t < d; ++t) dot = dot + qrow[t] * load_elem(krows[j], dtype, t);
+      scores[j - k0] = on ? dot * factor : -INFINITY;
+      if (on) {
+        cvalid = 1;
+        cmax = fmaxf(cmax, scores[j - k0]);
+      }
+    }
+    if (!cvalid) cmax = 0.0f;
+    if (chunk_max != NULL) chunk_max[k0 / chunk] = cmax;
+    float cden = 0.0f;
+    for (int64_t t = 0; t < dv; ++t) cacc[t] = 0.0f;
+    for (int64_t j = k0; j < k1; ++j) {
+      if (active != NULL && !active[j]) continue;
+      const float weight = exp2_approx_ftz(scores[j - k0] - cmax);
+      cden += weight;
+      const float rounded = dtype == ORACLE_BF16 ? oracle_bf16_to_float(oracle_float_to_bf16(weight))
+                                                 : oracle_half_to_float(oracle_float_to_half(weight));
+      for (int64_t t = 0; t < dv; ++t) cacc[t] = cacc[t] + rounded * load_elem(vrows[j], dtype, t);
+    }
+    float merged = st.valid ? st.maximum : cmax;
+    if (cvalid) merged = fmaxf(merged, cmax);
+    const float left = st.valid ? exp2_approx_ftz(st.maximum - merged) : 0.0f;
+    const float right = cvalid ? exp2_approx_ftz(cmax - merged) : 0.0f;
+    st.denominator = left * st.denominator + right * cden;
+    for (int64_t t = 0; t < dv; ++t) acc[t] = left * acc[t] + right * cacc[t];
+    st.maximum = merged;
+    st.valid = st.valid || cvalid;
+  }
+  return st;
+}
+
+/* grouped_flash_decode_partials (streaming/attention.py:556-627): bf16 q [B,HQ,1,D], k [B,HK,K,D],
+ * v [B,HK,K,DV] (contiguous); part p of (b, key head) covers key slots p * split .. + split, active
+ * below K. partial_lse [B,HQ,P] = max + logf(den) * log2e (-inf for an empty part),
+ * partial_output bf16 [B,HQ,P,DV] = acc * rcp(den) (0 for an empty part). */
+int oracle_grouped_decode_partials(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *partial_lse,
+                                   uint16_t *partial_out, int64_t batch, int64_t heads, int64_t kv_heads,
+                                   int64_t keys, int64_t d, int64_t dv, int64_t parts, int64_t split, float scale,
+                                   int64_t chunk, int workers) {
+  if (batch <= 0 || heads <= 0 || parts <= 0) return 0;
+  if (kv_heads < 1 || heads % kv_heads || split < 1) return 1;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const int64_t group = heads / kv_heads, count = batch * heads * parts;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    const uint16_t **krows = (const uint16_t **)malloc(sizeof(void *) * (size_t)split);
+    const uint16_t **vrows = (const uint16_t **)malloc(sizeof(void *) * (size_t)split);
+    float *qrow = (float *)malloc(sizeof(float) * (size_t)d), *scores = (float *)malloc(sizeof(float) * (size_t)chunk);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)dv), *cacc = (float *)malloc(sizeof(float) * (size_t)dv);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t b = item / (heads * parts), h = (item / parts) % heads, part = item % parts, kh = h / group;
+      for (int64_t t = 0; t < d; ++t) qrow[t] = oracle_bf16_to_float(q[(b * heads + h) * d + t]);
+      const int64_t first = part * split;
+      const int64_t n = first >= keys ? 0 : (keys - first < split ? keys - first : split);
+      for (int64_t j = 0; j < n; ++j) {
+        krows[j] = k + ((b * kv_heads + kh) * keys + first + j) * d;
+        vrows[j] = v + ((b * kv_heads + kh) * keys + first + j) * dv;
+      }
+      const fold_state st = fold_keys(ORACLE_BF16, qrow, d, dv, krows, vrows, NULL, n, scale * log2e, chunk, scores,
+                                      cacc, acc, NULL);
+      const float safe = st.valid ? st.denominator : 1.0f;
+      partial_lse[(b * heads + h) * parts + part] = st.valid ? st.maximum + logf(safe) * log2e : -INFINITY;
+      const float inverse = rcp_approx_ftz(safe);
+      uint16_t *op = partial_out + ((b * heads + h) * parts + part) * dv;
+      for (int64_t t = 0; t < dv; ++t) op[t] = oracle_float_to_bf16(st.valid ? acc[t] * inverse : 0.0f);
+    }
+    free(krows);
+    free(vrows);
+    free(qrow);
+    free(scores);
+    free(acc);
+    free(cacc);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+/* continuous_gqa_decode (streaming/attention.py:629-670): f16 q [B,HQ,D], k [B,K,HK,D],
+ * v [B,K,HK,DV], valid_mask u8 [B,K,HK] (contiguous); output f16 [B,HQ,DV] = acc * rcp(den), 0 for a
+ * query with no admitted key. */
+int oracle_continuous_gqa_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint8_t *mask,
+                                 uint16_t *out, int64_t batch, int64_t heads, int64_t kv_heads, int64_t keys,
+                                 int64_t d, int64_t dv, float scale, int64_t chunk, int workers) {
+  if (batch <= 0 || heads <= 0) return 0;
+  if (kv_heads < 1 || heads % kv_heads) return 1;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const int64_t group = heads / kv_heads, count = batch * heads;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    const size_t n = keys > 0 ? (size_t)keys : 1;
+    const uint16_t **krows = (const uint16_t **)malloc(sizeof(void *) * n);
+    const uint16_t **vrows = (const uint16_t **)malloc(sizeof(void *) * n);
+    unsigned char *active = (unsigned char *)malloc(n);
+    float *qrow = (float *)malloc(sizeof(float) * (size_t)d), *scores = (float *)malloc(sizeof(float) * (size_t)chunk);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)dv), *cacc = (float *)malloc(sizeof(float) * (size_t)dv);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t b = item / heads, h = item % heads, kh = h / group;
+      for (int64_t t = 0; t < d; ++t) qrow[t] = oracle_half_to_float(q[(b * heads + h) * d + t]);
+      for (int64_t j = 0; j < keys; ++j) {
+        krows[j] = k + ((b * keys + j) * kv_heads + kh) * d;
+        vrows[j] = v + ((b * keys + j) * kv_heads + kh) * dv;
+        active[j] = mask[(b * keys + j) * kv_heads + kh] != 0;
+      }
+      const fold_state st = fold_keys(ORACLE_F16, qrow, d, dv, krows, vrows, active, keys, scale * log2e, chunk,
+                                      scores, cacc, acc, NULL);
+      const float inverse = rcp_approx_ftz(st.valid ? st.denominator : 1.0f);
+      for (int64_t t = 0; t < dv; ++t)
+        out[(b * heads + h) * dv + t] = oracle_float_to_half(st.valid ? acc[t] * inverse : 0.0f);
+    }
+    free(krows);
+    free(vrows);
+    free(active);
+    free(qrow);
+    free(scores);
+    free(acc);
+    free(cacc);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
+/* varlen_gqa_decode_with_sink_logits (streaming/attention.py:672-754): f16 q [B,HQ,D], k [U,HK,D],
+ * v [U,HK,DV] (contiguous), cu [B+1], sink f32 [HQ]. Sequence b's keys are rows cu[b] .. cu[b+1]; the
+ * first 64 * max_blocks of them are folded in 64-key blocks. With M the merged maximum and
+ * inverse = rcp(den + sink[h]) (rcp(1) for an empty sequence): output = acc * inverse (0 when
+ * empty), block_logits [B,HQ,max_blocks] = exp2(block max - M) * inverse below ceil(length / 64),
+ * else 0. */
+int oracle_varlen_decode_sink(const uint16_t *q, const uint16_t *k, const uint16_t *v, const int32_t *cu,
+                              const float *sink, uint16_t *out, float *block_logits, int64_t sequences,
+                              int64_t heads, int64_t kv_heads, int64_t d, int64_t dv, int64_t max_blocks,
+                              float scale, int workers) {
+  if (sequences <= 0 || heads <= 0) return 0;
+  if (kv_heads < 1 || heads % kv_heads) return 1;
+  const uint32_t csr = enter_ieee();
+  const float log2e = 1.4426950408889634f;
+  const int64_t group = heads / kv_heads, count = sequences * heads, cap = 64 * max_blocks;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    const size_t n = cap > 0 ? (size_t)cap : 1;
+    const uint16_t **krows = (const uint16_t **)malloc(sizeof(void *) * n);
+    const uint16_t **vrows = (const uint16_t **)malloc(sizeof(void *) * n);
+    float *maxima = (float *)malloc(sizeof(float) * (max_blocks > 0 ? (size_t)max_blocks : 1));
+    float *qrow = (float *)malloc(sizeof(float) * (size_t)d), *scores = (float *)malloc(sizeof(float) * 64);
+    float *acc = (float *)malloc(sizeof(float) * (size_t)dv), *cacc = (float *)malloc(sizeof(float) * (size_t)dv);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t b = item / heads, h = item % heads, kh = h / group;
+      const int64_t length = (int64_t)cu[b + 1] - cu[b], blocks = (length + 63) / 64;
+      const int64_t taken = length < cap ? length : cap;
+      for (int64_t t = 0; t < d; ++t) qrow[t] = oracle_half_to_float(q[(b * heads + h) * d + t]);
+      for (int64_t j = 0; j < taken; ++j) {
+        krows[j] = k + ((cu[b] + j) * kv_heads + kh) * d;
+        vrows[j] = v + ((cu[b] + j) * kv_heads + kh) * dv;
+      }
+      const fold_state st = fold_keys(ORACLE_F16, qrow, d, dv, krows, vrows, NULL, taken, scale * log2e, 64, scores,
+                                      cacc, acc, maxima);
+      const float inverse = rcp_approx_ftz(st.valid ? st.denominator + sink[h] : 1.0f);
+      for (int64_t t = 0; t < dv; ++t)
+        out[(b * heads + h) * dv + t] = oracle_float_to_half(st.valid ? acc[t] * inverse : 0.0f);
+      for (int64_t j = 0; j < max_blocks; ++j)
+        block_logits[(b * heads + h) * max_blocks + j] =
+            j < blocks ? exp2_approx_ftz(maxima[j] - st.maximum) * inverse : 0.0f;
+    }
+    free(krows);
+    free(vrows);
+    free(maxima);
+    free(qrow);
+    free(scores);
+    free(acc);
+    free(cacc);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
 /* streaming/splitk_reduce.py:129-155 (splitk_attention_f32_to_f16_reduce): per (b, h),
  * m = maximum_num over splits of lse (identity -inf), w_s = expf(lse_s - m) (a natural exponential,
  * as the definition writes it), out = f16((sum_s w_s * partial_s) * rcp_approx(sum_s w_s)). All

@@ -46,6 +46,10 @@ def lib():
         handle.oracle_paged_decode_partials.argtypes = [p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                         i64, i64, i64, f, i64, i]
         handle.oracle_splitk_reduce_f32_to_f16.argtypes = [p, p, p, i64, i64, i64, i64, i]
+        handle.oracle_grouped_decode_partials.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i64, i64, i64, i64, f,
+                                                          i64, i]
+        handle.oracle_continuous_gqa_decode.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i64, i64, f, i64, i]
+        handle.oracle_varlen_decode_sink.argtypes = [p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64, f, i]
         handle.oracle_attention_bwd_delta.argtypes = [p, p, p, i64, i64, i64, i64, ctypes.POINTER(i64), i]
         handle.oracle_attention_bwd_dq.argtypes = [p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                    ctypes.POINTER(i64), f, i, i64, i]
@@ -336,6 +340,57 @@ def paged_decode_partials(q, key_cache, value_cache, page_offsets, page_indices,
     if status:
         raise ValueError(f"oracle_paged_decode_partials rejected the call ({status})")
     return lse, out
+
+
+def grouped_decode_partials(q_bits, k_bits, v_bits, scale: float, *, parts: int, split_size: int, chunk: int = 64,
+                            workers: int | None = None):
+    """grouped_flash_decode_partials: bf16 bit patterns q [B,HQ,1,D], k [B,HK,K,D], v [B,HK,K,DV];
+    returns (partial_lse [B,HQ,P] f32, partial_output [B,HQ,P,DV] bf16 bits)."""
+    q, k, v = (np.ascontiguousarray(a, np.uint16) for a in (q_bits, k_bits, v_bits))
+    batch, heads, _, d = q.shape
+    kv_heads, keys, dv = k.shape[1], k.shape[2], v.shape[3]
+    lse = np.empty((batch, heads, parts), np.float32)
+    out = np.empty((batch, heads, parts, dv), np.uint16)
+    status = lib().oracle_grouped_decode_partials(_ptr(q), _ptr(k), _ptr(v), _ptr(lse), _ptr(out), batch, heads,
+                                                  kv_heads, keys, d, dv, parts, split_size, float(np.float32(scale)),
+                                                  chunk, workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_grouped_decode_partials rejected the call ({status})")
+    return lse, out
+
+
+def continuous_gqa_decode(q, k, v, valid_mask, scale: float, *, chunk: int = 64, workers: int | None = None):
+    """continuous_gqa_decode: f16 q [B,HQ,D], k [B,K,HK,D], v [B,K,HK,DV], u8 valid_mask [B,K,HK];
+    returns output [B,HQ,DV] f16."""
+    q, k, v = (np.ascontiguousarray(a, np.float16) for a in (q, k, v))
+    mask = np.ascontiguousarray(valid_mask, np.uint8)
+    batch, heads, d = q.shape
+    keys, kv_heads, dv = k.shape[1], k.shape[2], v.shape[3]
+    out = np.empty((batch, heads, dv), np.float16)
+    status = lib().oracle_continuous_gqa_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(out), batch, heads,
+                                                kv_heads, keys, d, dv, float(np.float32(scale)), chunk,
+                                                workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_continuous_gqa_decode rejected the call ({status})")
+    return out
+
+
+def varlen_decode_sink(q, k, v, cu_seqlens, sink, scale: float, *, max_blocks: int, workers: int | None = None):
+    """varlen_gqa_decode_with_sink_logits: f16 q [B,HQ,D], k [U,HK,D], v [U,HK,DV], i32 cu [B+1],
+    f32 sink [HQ]; returns (output [B,HQ,DV] f16, block_logits [B,HQ,max_blocks] f32)."""
+    q, k, v = (np.ascontiguousarray(a, np.float16) for a in (q, k, v))
+    cu = np.ascontiguousarray(cu_seqlens, np.int32)
+    sink = np.ascontiguousarray(sink, np.float32)
+    sequences, heads, d = q.shape
+    kv_heads, dv = k.shape[1], v.shape[2]
+    out = np.empty((sequences, heads, dv), np.float16)
+    logits = np.empty((sequences, heads, max_blocks), np.float32)
+    status = lib().oracle_varlen_decode_sink(_ptr(q), _ptr(k), _ptr(v), _ptr(cu), _ptr(sink), _ptr(out), _ptr(logits),
+                                             sequences, heads, kv_heads, d, dv, max_blocks, float(np.float32(scale)),
+                                             workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_varlen_decode_sink rejected the call ({status})")
+    return out, logits
 
 
 def splitk_reduce_f32_to_f16(partial, partial_lse, *, workers: int | None = None) -> np.ndarray:

@@ -641,6 +641,125 @@ def test_attention_bias_minus_infinity():
     assert np.isnan(oracle.attention_bias_fwd(q, k, v, bias, 0.125, chunk=64).astype(np.float32)).all()
 
 
+# ------------------------------------------------------------------------------ decode variants
+def _dense_decode64(q, k, v, scale, active=None):
+    """float64 softmax of one query row per (batch, query head) over its key rows k [B,HQ,K,D]
+    (already gathered per query head); returns (output, log2 of the sum of exp2 of the base-2
+    logits)."""
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    logits = np.einsum("bhd,bhkd->bhk", q, k) * scale * np.log2(np.e)
+    if active is not None:
+        logits = np.where(active, logits, -np.inf)
+    peak = logits.max(axis=2, keepdims=True)
+    w = np.exp2(logits - np.where(np.isfinite(peak), peak, 0.0))
+    total = w.sum(axis=2, keepdims=True)
+    out = np.einsum("bhk,bhkd->bhd", w, v) / np.where(total > 0, total, 1.0)
+    return out, (peak + np.log2(np.where(total > 0, total, 1.0)))[..., 0]
+
+
+def test_grouped_decode_partials_oracle_pinned():
+    """One part over every key is the bf16 attention oracle bit for bit; parts merged by their
+    base-2 log-sums give float64 attention; a part past K is empty (-inf, 0); changing the keys of
+    one part leaves the other parts' bits unchanged."""
+    g = np.random.default_rng(21)
+    B, HQ, HK, K, D = 2, 8, 2, 300, 64
+    q = inputs._bf16_bits(g.standard_normal((B, HQ, 1, D)).astype(np.float32))
+    k = inputs._bf16_bits(g.standard_normal((B, HK, K, D)).astype(np.float32))
+    v = inputs._bf16_bits(g.standard_normal((B, HK, K, D)).astype(np.float32))
+    lse, out = oracle.grouped_decode_partials(q, k, v, 0.125, parts=1, split_size=512)
+    whole = oracle.attention_fwd(q, k, v, 0.125, False, head_group=4, storage="bf16")
+    assert (out[:, :, 0] == whole[:, :, 0]).all()
+    qf, kf, vf = (oracle.bf16_bits_to_float(a) for a in (q, k, v))
+    want, want_lse = _dense_decode64(qf[:, :, 0], np.repeat(kf, 4, axis=1), np.repeat(vf, 4, axis=1), 0.125)
+    assert np.abs(lse[:, :, 0] - want_lse).max() < 1e-3
+    lse, out = oracle.grouped_decode_partials(q, k, v, 0.125, parts=6, split_size=60)    # part 5: keys 300..359
+    assert np.isneginf(lse[:, :, 5]).all() and (out[:, :, 5] == 0).all()
+    weights = np.exp2(lse[:, :, :5] - lse[:, :, :5].max(axis=2, keepdims=True))
+    merged = (weights[..., None] * oracle.bf16_bits_to_float(out[:, :, :5])).sum(axis=2) / weights.sum(axis=2)[..., None]
+    assert np.all(np.abs(merged - want) <= 2e-2 * np.abs(want) + 1e-2)
+    k2 = k.copy()
+    k2[:, :, 60:120] = inputs._bf16_bits(g.standard_normal((B, HK, 60, D)).astype(np.float32))
+    lse2, out2 = oracle.grouped_decode_partials(q, k2, v, 0.125, parts=6, split_size=60)
+    keep = [0, 2, 3, 4, 5]
+    assert (out2[:, :, keep] == out[:, :, keep]).all() and (lse2[:, :, keep] == lse[:, :, keep]).all()
+    assert not (lse2[:, :, 1] == lse[:, :, 1]).all()
+
+
+def test_continuous_decode_oracle_pinned():
+    """With every key admitted the oracle is the attention oracle bit for bit (token-major caches
+    transposed); a random mask matches float64 attention over the admitted keys; a head whose
+    mask is all zero gives 0; a key head's mask reaches only its own query heads."""
+    g = np.random.default_rng(22)
+    B, HQ, HK, K, D = 2, 8, 2, 300, 64
+    q = inputs.normal(g, (B, HQ, D), "f16")
+    k, v = inputs.normal(g, (B, K, HK, D), "f16"), inputs.normal(g, (B, K, HK, D), "f16")
+    ones = np.ones((B, K, HK), np.uint8)
+    o = oracle.continuous_gqa_decode(q, k, v, ones, 0.125)
+    whole = oracle.attention_fwd(q[:, :, None].copy(), np.ascontiguousarray(k.transpose(0, 2, 1, 3)),
+                                 np.ascontiguousarray(v.transpose(0, 2, 1, 3)), 0.125, False, head_group=4)
+    assert (o.view(np.uint16) == whole[:, :, 0].view(np.uint16)).all()
+    mask = (g.random((B, K, HK)) < 0.4).astype(np.uint8)
+    mask[1, :, 1] = 0
+    o = oracle.continuous_gqa_decode(q, k, v, mask, 0.125).astype(np.float64)
+    kq = np.repeat(k.transpose(0, 2, 1, 3), 4, axis=1)
+    vq = np.repeat(v.transpose(0, 2, 1, 3), 4, axis=1)
+    active = np.repeat(mask.transpose(0, 2, 1), 4, axis=1) != 0
+    want, _ = _dense_decode64(q, kq, vq, 0.125, active)
+    assert np.all(np.abs(o - want) <= 2e-2 * np.abs(want) + 1e-2)
+    assert (o[1, 4:] == 0).all() and (np.abs(o[1, :4]) > 0).any()
+    mask2 = mask.copy()
+    mask2[:, :, 0] = 1 - mask2[:, :, 0]
+    o2 = oracle.continuous_gqa_decode(q, k, v, mask2, 0.125).astype(np.float64)
+    assert (o2[:, 4:] == o[:, 4:]).all() and not (o2[:, :4] == o[:, :4]).all()
+
+
+def test_varlen_decode_sink_oracle_pinned():
+    """Sequences of 0, 1, 64, 65, 200 and 300 keys with MAX_BLOCKS 4 (256 keys read at most).
+    With a zero sink the output is the attention oracle over the sequence's first 256 keys, bit for
+    bit; the block logits and a nonzero sink match float64; keys past the cap change nothing."""
+    g = np.random.default_rng(23)
+    lengths = np.array([0, 1, 64, 65, 200, 300])
+    cu = np.concatenate(([0], np.cumsum(lengths))).astype(np.int32)
+    B, HQ, HK, D, U, cap = len(lengths), 4, 2, 64, int(cu[-1]), 4
+    q = inputs.normal(g, (B, HQ, D), "f16")
+    k, v = inputs.normal(g, (U, HK, D), "f16"), inputs.normal(g, (U, HK, D), "f16")
+    zero = np.zeros(HQ, np.float32)
+    o, logits = oracle.varlen_decode_sink(q, k, v, cu, zero, 0.125, max_blocks=cap)
+    sink = np.array([0.0, 0.5, 3.0, 40.0], np.float32)
+    o_s, logits_s = oracle.varlen_decode_sink(q, k, v, cu, sink, 0.125, max_blocks=cap)
+    for b, n in enumerate(lengths):
+        if n == 0:
+            assert (o[b] == 0).all() and (logits[b] == 0).all() and (o_s[b] == 0).all()
+            continue
+        taken = min(n, 64 * cap)
+        rows = slice(cu[b], cu[b] + taken)
+        kb = np.ascontiguousarray(k[rows].transpose(1, 0, 2))[None]
+        vb = np.ascontiguousarray(v[rows].transpose(1, 0, 2))[None]
+        whole = oracle.attention_fwd(q[b][None, :, None].copy(), kb, vb, 0.125, False, head_group=2)[0, :, 0]
+        assert (o[b].view(np.uint16) == whole.view(np.uint16)).all()
+        scores = np.einsum("hd,hkd->hk", q[b].astype(np.float64),
+                           np.repeat(kb[0], 2, axis=0).astype(np.float64)) * 0.125 * np.log2(np.e)
+        peak = scores.max(axis=1)
+        den = np.exp2(scores - peak[:, None]).sum(axis=1)
+        blocks = -(-n // 64)
+        for j in range(cap):
+            if j < blocks:
+                block_peak = scores[:, 64 * j:64 * (j + 1)].max(axis=1)
+                for s_, lg in ((zero, logits), (sink, logits_s)):
+                    want = np.exp2(block_peak - peak) / (den + s_)
+                    assert np.allclose(lg[b, :, j], want, rtol=2e-3, atol=1e-6)
+            else:
+                assert (logits[b, :, j] == 0).all()
+        ratio = den / (den + sink)
+        assert np.all(np.abs(o_s[b].astype(np.float64) - o[b].astype(np.float64) * ratio[:, None])
+                      <= 2e-2 * np.abs(o[b].astype(np.float64)) + 1e-2)
+    k2, v2 = k.copy(), v.copy()
+    tail = slice(cu[-2] + 256, cu[-1])           # keys 256..299 of the last sequence
+    k2[tail], v2[tail] = 9.0, 9.0
+    o2, logits2 = oracle.varlen_decode_sink(q, k2, v2, cu, sink, 0.125, max_blocks=cap)
+    assert (o2.view(np.uint16) == o_s.view(np.uint16)).all() and (logits2 == logits_s).all()
+
+
 # ------------------------------------------------------------------------------ int8 GEMM
 def test_gemm_i8_oracle_pinned():
     """gemm_i8: against a scalar loop on a small case, an identity operand (c = b + bias exactly),

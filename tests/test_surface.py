@@ -243,6 +243,26 @@ def test_paged_decode_definitions_recognised_with_reference_signatures():
     assert PagedDecode.mutable_inputs == ()
 
 
+@pytest.mark.parametrize("name,options,parameters", [
+    ("flash_attention_bias_fwd", {}, ["q", "k", "v", "bias", "output", "scale"]),
+    ("grouped_flash_decode_partials", {"HEAD_GROUP": 4, "P": 8, "SPLIT_SIZE": 1024},
+     ["q", "k", "v", "partial_lse", "partial_output", "scale", "HEAD_GROUP", "P", "SPLIT_SIZE"]),
+    ("continuous_gqa_decode", {"HEAD_GROUP": 4},
+     ["q", "k", "v", "valid_mask", "output", "scale", "HEAD_GROUP"]),
+    ("varlen_gqa_decode_with_sink_logits", {"HEAD_GROUP": 4, "MAX_BLOCKS": 64},
+     ["q", "k", "v", "cu_seqlens", "sink", "output", "block_logits", "scale", "HEAD_GROUP", "MAX_BLOCKS"]),
+])
+def test_attention_variants_recognised_with_reference_signatures(name, options, parameters):
+    """streaming/attention.py:556-836: the bias and decode definitions keep the reference's
+    parameter names and order, and the provider recognises each by name and signature."""
+    import intent_amd.examples.kernels.streaming.attention as attention
+
+    definition = getattr(attention, name)
+    assert list(definition.signature.parameters) == parameters
+    iface = PublicInterface.from_definition(definition, options)
+    assert recognize(definition, iface, tuple(options)).name == name
+
+
 def test_csr_spmm_definition_recognised_with_reference_signature():
     from intent_amd.examples.kernels.sparse.csr_spmm import csr_spmm
 
