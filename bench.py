@@ -52,7 +52,7 @@ def parse():
     parser.add_argument("--operators",
                         default="softmax_f32,gemm,attention,spmv,gemm_f16_relu,gemm_f32,linear_f32,gqa,attention_bf16,"
                                 "attention_bwd,attention_bwd_large,paged_decode,spmm,varlen_prefill,gemm_i8,quantized_gemm,"
-                                "attention_bias,continuous_decode,grouped_decode,varlen_decode")
+                                "attention_bias,continuous_decode,grouped_decode,varlen_decode,mla_prefill,mla_prefill_large")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 20 device copies of 512 MiB (a known-traffic kernel for counter scaling)")
     parser.add_argument("--only", default=None,
@@ -578,6 +578,53 @@ def op_varlen_prefill(device, flush, cpu):
     return out
 
 
+def _op_mla_prefill(device, flush, cpu, large):
+    """mla_prefill at the reference's extents (streaming/attention.py:35-44): B1, 8 query heads over
+    2 key heads, S1024, content D128 and position P64, causal; `large`: config 4's B4 H32 (over 8
+    key heads) S4096. FLOPs: the causal half of the score product over D + P and of P @ V over D."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd.examples import inputs
+    from intent_amd.examples.kernels.streaming.attention import mla_prefill
+
+    rng = np.random.default_rng(15)
+    b, h, hk, s, d, p = (4, 32, 8, 4096, 128, 64) if large else (1, 8, 2, 1024, 128, 64)
+    arrays = (inputs.normal(rng, (b, h, s, d), "f16"), inputs.normal(rng, (b, h, s, p), "f16"),
+              inputs.normal(rng, (b, hk, s, d), "f16"), inputs.normal(rng, (b, 1, s, p), "f16"),
+              inputs.normal(rng, (b, hk, s, d), "f16"))
+    scale = float(np.float32(1 / np.sqrt(d + p)))
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    call = intent.jit(mla_prefill, backend="hip", constexprs={"HEAD_GROUP": h // hk}).prepare(
+        *(t(a) for a in arrays), scale)
+    ms = operator_ms(call.launch, flush)
+    flops = b * h * s * s * (2 * (d + p) + 2 * d) // 2
+    out = {"config": f"latent attention prefill f16 B{b} H{h} HK{hk} S{s} D{d} P{p}, causal (mla_prefill)",
+           "median_ms": round(ms, 4), "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if cpu:
+        import oracle
+
+        if large:
+            part = (arrays[0][:1, :4, :1024], arrays[1][:1, :4, :1024], arrays[2][:1, :1, :1024],
+                    arrays[3][:1, :, :1024], arrays[4][:1, :1, :1024])
+            sample_flops, sample = 4 * 1024 * 1024 * (2 * (d + p) + 2 * d) // 2, "4 query heads of one key head, first 1024 rows"
+        else:
+            part, sample_flops, sample = arrays, flops, "the whole workload"
+        seconds = cpu_median_seconds(lambda: oracle.mla_prefill(*part, scale))
+        out["cpu"] = {"tflops": round(sample_flops / seconds / 1e12, 5), "cores": oracle.default_workers(),
+                      "kind": "port", "sample": sample}
+    return out
+
+
+def op_mla_prefill(device, flush, cpu):
+    return _op_mla_prefill(device, flush, cpu, False)
+
+
+def op_mla_prefill_large(device, flush, cpu):
+    return _op_mla_prefill(device, flush, cpu, True)
+
+
 def op_attention_bias(device, flush, cpu):
     """flash_attention_bias_fwd at config 4's extents (B4 H32 S4096 D128), every key admitted, with
     a normal(0, 2) f32 bias per (batch, head, key). FLOPs: the two products over all S x S pairs."""
@@ -855,7 +902,8 @@ OPERATORS = {"softmax_f32": op_softmax_f32, "gemm": op_gemm, "attention": op_att
              "spmm": op_spmm, "varlen_prefill": op_varlen_prefill, "gemm_i8": op_gemm_i8,
              "quantized_gemm": op_quantized_gemm, "attention_bias": op_attention_bias,
              "continuous_decode": op_continuous_decode, "grouped_decode": op_grouped_decode,
-             "varlen_decode": op_varlen_decode}
+             "varlen_decode": op_varlen_decode, "mla_prefill": op_mla_prefill,
+             "mla_prefill_large": op_mla_prefill_large}
 
 
 def read_traffic(name):

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 13
+#define INTENT_HIP_ABI_VERSION 14
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -64,7 +64,8 @@ enum IntentHipOperator {
   INTENT_HIP_OP_GROUPED_DECODE_PARTIALS = 18, /* rows = HEAD_GROUP, cols = head dimension */
   INTENT_HIP_OP_CONTINUOUS_DECODE = 19,   /* rows = HEAD_GROUP, cols = head dimension */
   INTENT_HIP_OP_VARLEN_DECODE = 20,       /* rows = HEAD_GROUP, cols = head dimension */
-  INTENT_HIP_OP_DECODE_MERGE = 21         /* cols = head dimension */
+  INTENT_HIP_OP_DECODE_MERGE = 21,        /* cols = head dimension */
+  INTENT_HIP_OP_MLA_PREFILL = 22          /* cols = D | P << 16 */
 };
 
 /* Epilogue activations of intent_hip_gemm (the Activation enum of contraction/gemm.py:10-12). */
@@ -182,6 +183,17 @@ int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void
                              int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
                              int64_t sk, int64_t d, int64_t dv, const int64_t strides[16],
                              float scale, int causal, void *stream);
+
+/* Latent attention prefill: mla_prefill (streaming/attention.py:756-798, scores of
+ * summarize_mla_chunk :368-415): s = (q . k + qpe . kpe) scale log2 e with the causal rule
+ * key <= query, weights rounded to f16 before P @ V. q [b,h,sq,d], qpe [b,h,sq,p], k [b,hk,sk,d],
+ * kpe [b,1,sk,p] (one position row per key, shared by every head), v [b,hk,sk,d], o [b,h,sq,d],
+ * all f16; key head = h / head_group. d in {64, 128}, p = 64.
+ * strides[24]: q, qpe, k, kpe, v, o, each (batch, head, row, col), col stride 1. */
+int intent_hip_mla_prefill(const void *q, const void *qpe, const void *k, const void *kpe, const void *v,
+                           void *o, int64_t batch, int64_t heads, int64_t head_group, int64_t sq,
+                           int64_t sk, int64_t d, int64_t p, const int64_t strides[24], float scale,
+                           void *stream);
 
 /* Attention forward with an additive per-key bias: flash_attention_bias_fwd
  * (streaming/attention.py:800-836, scores of summarize_biased_attention_chunk :328-366):

@@ -115,6 +115,8 @@ extern "C" int intent_hip_kernel_resources(int op, int dtype, int64_t rows, int6
     case INTENT_HIP_OP_CONTINUOUS_DECODE: return decode_resources(3, cols, rows, out);
     case INTENT_HIP_OP_VARLEN_DECODE: return decode_resources(4, cols, rows, out);
     case INTENT_HIP_OP_DECODE_MERGE: return decode_resources(5, cols, rows, out);
+    case INTENT_HIP_OP_MLA_PREFILL:
+      return attention_resources(INTENT_HIP_F16, rows, cols & 0xFFFF, cols >> 16, 3, out);
     case INTENT_HIP_OP_CSR_SPMM_F32: return spmm_resources(cols, out);
     case INTENT_HIP_OP_GEMM_I8: return gemm_i8_resources(rows, cols, out);
     case INTENT_HIP_OP_QUANTIZED_GEMM: return quantized_gemm_resources(out);

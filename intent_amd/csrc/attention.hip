@@ -83,6 +83,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 // (ROCm 7.2) compiled the device code but silently emitted no host stubs for the kernel, so the
 // library failed to load with undefined kernel symbols.
 __host__ __device__ __forceinline__ int swz_k(int d, int row) {
+  if (d == 192) return (row >> 1) & 7;   // 24 chunks per row: the xor stays inside each group of 8
   return d == 128 ? (row & 15) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
 }
 __host__ __device__ __forceinline__ int swz_v(int d, int row) {
@@ -114,8 +115,17 @@ struct KeyBias {
   int64_t bs, hs;
 };
 
-// Kernel modes: batched [B,H,S,D] tensors, packed sequences, or batched with a key bias.
-constexpr int kBatched = 0, kPacked = 1, kBiased = 2;
+// The position parts of latent attention (mla_prefill): query rows qpe [B,H,Q,P] at strides qs
+// (batch, head, row) and key rows kpe [B,1,K,P], shared by every head, at strides ks (batch, row).
+struct RopeRows {
+  const uint16_t *qpe, *kpe;
+  int64_t qs[3], ks[2];
+};
+
+// Kernel modes: batched [B,H,S,D] tensors, packed sequences, batched with a key bias, or batched
+// latent attention, whose score dimensions are the DV content dimensions of q and k followed by
+// the position dimensions of qpe and kpe (D = DV + P).
+constexpr int kBatched = 0, kPacked = 1, kBiased = 2, kLatent = 3;
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
@@ -135,11 +145,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
                                                                   uint16_t *__restrict__ O, int heads,
                                                                   int head_group, int sq_all, int sk_all,
                                                                   Geometry g, float scale, int causal,
-                                                                  int q_blocks, Ragged r, KeyBias kb) {
-  constexpr bool kVarlen = kMode == kPacked, kBias = kMode == kBiased;
+                                                                  int q_blocks, Ragged r, KeyBias kb, RopeRows rr) {
+  constexpr bool kVarlen = kMode == kPacked, kBias = kMode == kBiased, kRope = kMode == kLatent;
   typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
   constexpr int kD = D, kDV = DV;
   constexpr int kKRow = kD / 8;               // 16-byte chunks per K row
+  constexpr int kContent = kRope ? kDV / 8 : kKRow;   // chunks of a K row read from k (the rest: kpe)
   constexpr int kVRow = kDV / 8;              // 16-byte chunks per V row
   constexpr int kKChunks = kBK * kKRow;       // 16-byte chunks of a K tile (row = key)
   constexpr int kVChunks = kBK * kVRow;       // 16-byte chunks of a V tile (row = key)
@@ -176,6 +187,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const uint16_t *vbase = V + b * g.vs[0] + kh * g.vs[1] + row0 * g.vs[2];
   uint16_t *obase = O + b * g.os[0] + h * g.os[1] + row0 * g.os[2];
   const float *bias_row = kBias ? kb.p + b * kb.bs + h * kb.hs : nullptr;
+  const uint16_t *qpe_base = kRope ? rr.qpe + b * rr.qs[0] + h * rr.qs[1] : nullptr;
+  const uint16_t *kpe_base = kRope ? rr.kpe + b * rr.ks[0] : nullptr;
 
   const int q0 = qb * kBQ;
   const int wq0 = q0 + wave * 32;             // this wave's first query row
@@ -187,9 +200,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   {
     const bool ok = lane_q < sq;
     const uint16_t *row = qbase + static_cast<int64_t>(ok ? lane_q : 0) * g.qs[2];
+    const uint16_t *pe_row = kRope ? qpe_base + static_cast<int64_t>(ok ? lane_q : 0) * rr.qs[2] : nullptr;
 #pragma unroll
-    for (int ks = 0; ks < kD / 16; ++ks)
-      qf[ks] = __builtin_bit_cast(f16x8_t, select(ok, *reinterpret_cast<const uint4 *>(row + ks * 16 + half * 8)));
+    for (int ks = 0; ks < kD / 16; ++ks) {
+      const uint16_t *src = ks * 2 < kContent ? row + ks * 16 + half * 8 : pe_row + (ks * 16 - kContent * 8) + half * 8;
+      qf[ks] = __builtin_bit_cast(f16x8_t, select(ok, *reinterpret_cast<const uint4 *>(src)));
+    }
   }
 
   const int q_last_block = min(q0 + kBQ, sq) - 1;
@@ -209,8 +225,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
       const int p = (wave * (kKChunks / kThreads) + i) * 64 + lane;
       const int row = p / kKRow, pc = p % kKRow;
       const int key = min(key0 + row, sk - 1);
-      __builtin_amdgcn_global_load_lds(kbase + static_cast<int64_t>(key) * g.ks[2] + (pc ^ swz_k(D, row)) * 8,
-                                       (lds_void_t *)(stage + (wave * (kKChunks / kThreads) + i) * 64), 16, 0, 0);
+      const int lc = pc ^ swz_k(D, row);   // the logical chunk this slot holds
+      const uint16_t *src = kbase + static_cast<int64_t>(key) * g.ks[2] + lc * 8;
+      if constexpr (kRope)
+        if (lc >= kContent) src = kpe_base + static_cast<int64_t>(key) * rr.ks[1] + (lc - kContent) * 8;
+      __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(stage + (wave * (kKChunks / kThreads) + i) * 64), 16, 0,
+                                       0);
     }
 #pragma unroll
     for (int i = 0; i < kVChunks / kThreads; ++i) {
@@ -446,6 +466,14 @@ const void *attention_kernel(int64_t d, int64_t dv) {
 
 int attention_resources(int dtype, int64_t sq, int64_t d, int64_t dv, int mode, IntentHipKernelResources *out) {
   (void)sq;
+  if (mode == kLatent) {   // d: content dimensions (= dv), dv: position dimensions
+    if ((d != 64 && d != 128) || dv != 64)
+      return fail(INTENT_HIP_ERR_UNSUPPORTED, "latent attention takes D in {64, 128} and P = 64");
+    return describe_kernel(d == 128 ? reinterpret_cast<const void *>(&attention_fwd<_Float16, 192, 128, kLatent>)
+                                    : reinterpret_cast<const void *>(&attention_fwd<_Float16, 128, 64, kLatent>),
+                           d == 128 ? "attention_fwd<f16,192,128,latent>" : "attention_fwd<f16,128,64,latent>",
+                           kThreads, out);
+  }
   if ((d != 64 && d != 128) || (dv != 64 && dv != 128))
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention kernels take d, dv in {64, 128}");
   char name[64];
@@ -470,9 +498,9 @@ namespace {
 template <typename E, int D, int DV, int kMode>
 void launch_fwd(dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O,
                 int heads, int head_group, int sq, int sk, const Geometry &g, float scale, int causal, int q_blocks,
-                const Ragged &r, const KeyBias &kb) {
+                const Ragged &r, const KeyBias &kb, const RopeRows &rr = RopeRows{}) {
   attention_fwd<E, D, DV, kMode><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, O, heads, head_group, sq, sk, g, scale,
-                                                                 causal, q_blocks, r, kb);
+                                                                 causal, q_blocks, r, kb, rr);
 }
 
 // One launch of the (dtype, d, dv) instantiation.
@@ -652,5 +680,64 @@ extern "C" int intent_hip_attention_varlen_fwd(int dtype, const void *q, const v
                        static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), static_cast<int>(q_heads),
                        static_cast<int>(head_group), 0, 0, g, scale, causal ? 1 : 0, 1, r);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd (packed)");
+  return INTENT_HIP_OK;
+}
+
+// ---------------------------------------------------------------- latent attention
+extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void *k, const void *kpe, const void *v,
+                                      void *o, int64_t batch, int64_t heads, int64_t head_group, int64_t sq,
+                                      int64_t sk, int64_t d, int64_t p, const int64_t *strides, float scale,
+                                      void *stream) {
+  if (batch < 0 || heads < 0 || sq < 0 || sk < 0 || d < 0 || p < 0)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  if (head_group < 1 || (heads > 0 && heads % head_group != 0))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "head_group %lld must be positive and divide the %lld query heads",
+                static_cast<long long>(head_group), static_cast<long long>(heads));
+  if (batch == 0 || heads == 0 || sq == 0 || d == 0) return INTENT_HIP_OK;
+  if ((d != 64 && d != 128) || p != 64)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "latent attention takes D in {64, 128} and P = 64 (got D=%lld, P=%lld)",
+                static_cast<long long>(d), static_cast<long long>(p));
+  if (strides == nullptr || q == nullptr || qpe == nullptr || o == nullptr ||
+      (sk > 0 && (k == nullptr || kpe == nullptr || v == nullptr)))
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null pointer");
+  if (sq > INT32_MAX / 2 || sk > INT32_MAX / 2 || batch * heads > INT32_MAX / 64)
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention extents too large for one launch");
+  // strides: q[4], qpe[4], k[4], kpe[4], v[4], o[4], each (batch, head, row, col)
+  Geometry g;
+  RopeRows rr{static_cast<const uint16_t *>(qpe), static_cast<const uint16_t *>(kpe), {strides[4], strides[5], strides[6]},
+              {strides[12], strides[14]}};
+  for (int i = 0; i < 4; ++i) {
+    g.qs[i] = strides[i];
+    g.ks[i] = strides[8 + i];
+    g.vs[i] = strides[16 + i];
+    g.os[i] = strides[20 + i];
+  }
+  for (int t = 0; t < 6; ++t)
+    if (strides[4 * t + 3] != 1) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "attention tensors need unit inner stride");
+  for (int t = 0; t < 6; ++t)
+    for (int i = 0; i < 3; ++i)
+      if (strides[4 * t + i] % (t == 5 ? 4 : 8))
+        return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention strides must be multiples of 8 elements");
+  if (!aligned(q, 16) || !aligned(qpe, 16) || (sk > 0 && (!aligned(k, 16) || !aligned(kpe, 16) || !aligned(v, 16))) ||
+      !aligned(o, 8))
+    return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention tensors must be 16-byte aligned");
+  const int q_blocks = static_cast<int>((sq + kBQ - 1) / kBQ);
+  const int64_t blocks = batch * heads * q_blocks;
+  if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many attention workgroups");
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const hipStream_t s = as_stream(stream);
+  const auto *Qp = static_cast<const uint16_t *>(q);
+  const auto *Kp = static_cast<const uint16_t *>(k);
+  const auto *Vp = static_cast<const uint16_t *>(v);
+  auto *Op = static_cast<uint16_t *>(o);
+  const int h = static_cast<int>(heads), grp = static_cast<int>(head_group);
+  const int iq = static_cast<int>(sq), ik = static_cast<int>(sk);
+  if (d == 128)
+    launch_fwd<_Float16, 192, 128, kLatent>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, 1, q_blocks, Ragged{},
+                                            KeyBias{}, rr);
+  else
+    launch_fwd<_Float16, 128, 64, kLatent>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, 1, q_blocks, Ragged{},
+                                           KeyBias{}, rr);
+  if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd (latent)");
   return INTENT_HIP_OK;
 }

@@ -120,6 +120,34 @@ def flash_attention_bf16_fwd(
                                              I.bf16)
 
 
+# ------------------------------------------------------------------------------ latent attention
+# mla_prefill (streaming/attention.py:756-798): each score adds a position product, qpe . kpe, to
+# the content product q . k before the base-2 scaling (summarize_mla_chunk, :368-415); kpe has one
+# row per key shared by every head; causal, with key heads shared by HEAD_GROUP query heads.
+@intent.kernel
+def mla_prefill(
+    q: I.In[I.f16, ("B", "H", "Q", "D")],
+    qpe: I.In[I.f16, ("B", "H", "Q", "P")],
+    k: I.In[I.f16, ("B", "HK", "K", "D")],
+    kpe: I.In[I.f16, ("B", 1, "K", "P")],
+    v: I.In[I.f16, ("B", "HK", "K", "D")],
+    output: I.Out[I.f16, ("B", "H", "Q", "D")],
+    scale: I.f32,
+    HEAD_GROUP: I.Constexpr[int],
+):
+    B, H = q.shape[0], q.shape[1]
+    for b in I.parallel(I.domain(0, B)):
+        for h in I.parallel(I.domain(0, H)):
+            shared = h // HEAD_GROUP
+            logits = (I.matmul(q[b, h, :, :], k[b, shared, :, :], transpose_rhs=True, acc_dtype=I.f32)
+                      + I.matmul(qpe[b, h, :, :], kpe[b, 0, :, :], transpose_rhs=True, acc_dtype=I.f32)) * (
+                          scale * I.LOG2E)
+            admitted = causal_pairs(I.indices(I.domain(0, q.shape[2])), I.indices(I.domain(0, k.shape[2])), True)
+            summary = admitted_attention(logits, admitted, v[b, shared, :, :], I.f16)
+            share = I.fdiv(1.0, summary.total, approximate=True, flush_to_zero=True)
+            output[b, h, :, :] = I.cast(I.select(summary.live[:, None], summary.mixed * share[:, None], 0.0), I.f16)
+
+
 # ------------------------------------------------------------------------------ additive key bias
 # flash_attention_bias_fwd (streaming/attention.py:800-836): every key is admitted and its logit
 # gains bias[b, h, j] before the base-2 scaling, logit[i, j] = ((q_i . k_j) * scale + bias[j]) *

@@ -11,7 +11,7 @@ from pathlib import Path
 
 from ...diagnostics import CompilationStageError
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 # INTENT_HIP_STATIC_SCRATCH_BYTES: the static scratch of intent_hip_csr_spmv_f32_static.
 STATIC_SCRATCH_BYTES = 32 << 20
 LIBRARY_NAME = "libintent_hip.so"
@@ -21,7 +21,8 @@ F32, F16, BF16 = 0, 1, 2
 (OP_SOFTMAX_FWD, OP_SOFTMAX_BWD, OP_GEMM_BF16, OP_ATTENTION_FWD_F16, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_F32,
  OP_ATTENTION_FWD, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DQ, OP_ATTENTION_BWD_DKDV, OP_PAGED_DECODE_PARTIALS,
  OP_SPLITK_REDUCE, OP_CSR_SPMM_F32, OP_ATTENTION_VARLEN, OP_GEMM_I8, OP_QUANTIZED_GEMM,
- OP_ATTENTION_BIAS, OP_GROUPED_DECODE_PARTIALS, OP_CONTINUOUS_DECODE, OP_VARLEN_DECODE, OP_DECODE_MERGE) = range(22)
+ OP_ATTENTION_BIAS, OP_GROUPED_DECODE_PARTIALS, OP_CONTINUOUS_DECODE, OP_VARLEN_DECODE, OP_DECODE_MERGE,
+ OP_MLA_PREFILL) = range(23)
 ACT_NONE, ACT_RELU = 0, 1
 
 _i64, _int, _p, _f32, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
@@ -60,6 +61,8 @@ SIGNATURES = {
                                             ctypes.POINTER(_i64), _f32, _int, _p)),
     "intent_hip_attention_fwd": (_int, (_int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                         ctypes.POINTER(_i64), _f32, _int, _p)),
+    "intent_hip_mla_prefill": (_int, (_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                      ctypes.POINTER(_i64), _f32, _p)),
     "intent_hip_attention_bias_fwd": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                              ctypes.POINTER(_i64), ctypes.POINTER(_i64), _f32, _p)),
     "intent_hip_attention_varlen_workspace_bytes": (_int, (_i64, _i64, ctypes.POINTER(_sz))),

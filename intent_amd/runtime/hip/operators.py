@@ -20,6 +20,7 @@ Recognised definitions (reference file:line of the semantics each kernel follows
   flash_gqa_attention_fwd streaming/attention.py:469-507   intent_hip_attention_fwd (f16, HEAD_GROUP)
   flash_attention_bf16_fwd streaming/attention.py:510-553  intent_hip_attention_fwd (bf16, HEAD_GROUP)
   flash_attention_bias_fwd streaming/attention.py:800-836  intent_hip_attention_bias_fwd
+  mla_prefill             streaming/attention.py:756-798   intent_hip_mla_prefill (HEAD_GROUP, causal)
   flash_varlen_attention_fwd streaming/attention.py:839-877 intent_hip_attention_varlen_fwd (one head, CAUSAL)
   flash_varlen_gqa_prefill streaming/attention.py:880-924  intent_hip_attention_varlen_fwd (HEAD_GROUP, causal)
   csr_spmv                sparse/csr_spmv.py:11-29         intent_hip_csr_spmv_f32
@@ -50,7 +51,7 @@ from typing import Callable
 
 from ...diagnostics import CompilationStageError
 from .library import (BF16, F16, F32, STATIC_SCRATCH_BYTES, OP_ATTENTION_BWD_DELTA, OP_ATTENTION_BWD_DKDV, OP_ATTENTION_BWD_DQ,
-                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_BIAS, OP_ATTENTION_VARLEN, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8, OP_QUANTIZED_GEMM,
+                      OP_ATTENTION_FWD, OP_ATTENTION_FWD_F16, OP_ATTENTION_BIAS, OP_ATTENTION_VARLEN, OP_MLA_PREFILL, OP_CSR_SPMV_F32, OP_GEMM, OP_GEMM_BF16, OP_GEMM_F32, OP_GEMM_I8, OP_QUANTIZED_GEMM,
                       OP_CSR_SPMM_F32, OP_CONTINUOUS_DECODE, OP_GROUPED_DECODE_PARTIALS, OP_PAGED_DECODE_PARTIALS, OP_VARLEN_DECODE, OP_SOFTMAX_BWD, OP_SOFTMAX_FWD, OP_SPLITK_REDUCE)
 
 
@@ -346,6 +347,26 @@ def _attention_bias(lib, bound, constexprs, device):
     return Launch("intent_hip_attention_bias_fwd", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
                   tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("sk", sk), ("d", d), ("dv", dv)),
                   lambda: lib.kernel_resources(OP_ATTENTION_BIAS, F16, sq, d | (dv << 16)))
+
+
+def _mla_prefill(lib, bound, constexprs, device):
+    """mla_prefill: causal latent attention, scores (q . k + qpe . kpe) scale (attention.py:756-798)."""
+    q, qpe, k, kpe, v, o, scale = bound.arguments
+    group = _head_group(constexprs)
+    batch, heads, sq, d = q.shape
+    sk, p = k.shape[2], qpe.shape[3]
+    if k.shape[1] * group != heads or v.shape[1] != k.shape[1]:
+        raise ValueError(f"query heads ({heads}) must equal key/value heads ({k.shape[1]}) * HEAD_GROUP ({group})")
+    keep, before, after = [q, qpe, k, kpe, v, o], [], []
+    views = [_readable(t, keep, before, 8) for t in (q, qpe, k, kpe, v)] + [_writable(o, keep, after, 8)]
+    strides = _strides(*views)
+    keep.append(strides)
+    fn = lib.fn["mla_prefill"]
+    args = (*(t.data_ptr() for t in views), batch, heads, group, sq, sk, d, p, strides, float(scale))
+    return Launch("intent_hip_mla_prefill", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                  tuple(after), (("batch", batch), ("heads", heads), ("head_group", group), ("sq", sq), ("sk", sk),
+                                 ("d", d), ("p", p)),
+                  lambda: lib.kernel_resources(OP_MLA_PREFILL, F16, sq, d | (p << 16)))
 
 
 def _head_group(constexprs) -> int:
@@ -747,6 +768,9 @@ _SPECS = (
     OperatorSpec("flash_attention_bf16_fwd", (_view(IN, "bf16", 4), _view(IN, "bf16", 4), _view(IN, "bf16", 4),
                                               _view(OUT, "bf16", 4), ("scalar", "f32")), ("HEAD_GROUP", "CAUSAL"),
                  _attention_grouped(BF16)),
+    OperatorSpec("mla_prefill", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
+                                 _view(IN, "f16", 4), _view(OUT, "f16", 4), ("scalar", "f32")), ("HEAD_GROUP",),
+                 _mla_prefill),
     OperatorSpec("flash_attention_bias_fwd", (_view(IN, "f16", 4), _view(IN, "f16", 4), _view(IN, "f16", 4),
                                               _view(IN, "f32", 3), _view(OUT, "f16", 4), ("scalar", "f32")), (),
                  _attention_bias),

@@ -473,6 +473,86 @@ int oracle_attention_bias_fwd(const uint16_t *q, const uint16_t *k, const uint16
   return 0;
 }
 
+/* mla_prefill (streaming/attention.py:756-798) with summarize_mla_chunk (:368-415): f16 q [B,H,Q,D],
+ * qpe [B,H,Q,P], k [B,HK,K,D], kpe [B,1,K,P], v [B,HK,K,D] (contiguous); output [B,H,Q,D]. Scores
+ * are (q . k + qpe . kpe) * scale * log2e, each product summed in f32 on its own and then added;
+ * key j is valid for query i iff i >= j; the chunk fold is the attention forward's. */
+int oracle_mla_prefill(const uint16_t *q, const uint16_t *qpe, const uint16_t *k, const uint16_t *kpe,
+                       const uint16_t *v, uint16_t *o, int64_t batch, int64_t heads, int64_t kv_heads, int64_t sq,
+                       int64_t sk, int64_t d, int64_t p, float scale, int64_t chunk, int workers) {
+  if (batch <= 0 || heads <= 0 || sq <= 0) return 0;
+  if (kv_heads < 1 || heads % kv_heads) return 1;
+  if (chunk <= 0) chunk = 64;
+  const uint32_t csr = enter_ieee();
+  const float factor = scale * 1.4426950408889634f;
+  const int64_t group = heads / kv_heads, count = batch * heads * sq;
+  const int size = team_size(workers, count);
+#pragma omp parallel num_threads(size)
+  {
+    const uint32_t inner = enter_ieee();
+    int64_t begin, end;
+    row_range(count, omp_get_thread_num(), size, &begin, &end);
+    float *scores = (float *)malloc(sizeof(float) * (size_t)chunk);
+    float *qrow = (float *)malloc(sizeof(float) * (size_t)(d + p));
+    float *acc = (float *)malloc(sizeof(float) * (size_t)d), *cacc = (float *)malloc(sizeof(float) * (size_t)d);
+    for (int64_t item = begin; item < end; ++item) {
+      const int64_t b = item / (heads * sq), h = (item / sq) % heads, qi = item % sq, kh = h / group;
+      for (int64_t t = 0; t < d; ++t) qrow[t] = oracle_half_to_float(q[((b * heads + h) * sq + qi) * d + t]);
+      for (int64_t t = 0; t < p; ++t) qrow[d + t] = oracle_half_to_float(qpe[((b * heads + h) * sq + qi) * p + t]);
+      int valid = 0;
+      float maximum = 0.0f, denominator = 0.0f;
+      for (int64_t t = 0; t < d; ++t) acc[t] = 0.0f;
+      for (int64_t k0 = 0; k0 < sk; k0 += chunk) {
+        const int64_t k1 = k0 + chunk < sk ? k0 + chunk : sk;
+        int cvalid = 0;
+        float cmax = -INFINITY;
+        for (int64_t j = k0; j < k1; ++j) {
+          const uint16_t *kp = k + ((b * kv_heads + kh) * sk + j) * d, *pp = kpe + (b * sk + j) * p;
+          float content = 0.0f, position = 0.0f;
+          for (int64_t t = 0; t < d; ++t) content = content + qrow[t] * oracle_half_to_float(kp[t]);
+          for (int64_t t = 0; t < p; ++t) position = position + qrow[d + t] * oracle_half_to_float(pp[t]);
+          const int ok = qi >= j;
+          scores[j - k0] = ok ? (content + position) * factor : -INFINITY;
+          if (ok) {
+            cvalid = 1;
+            cmax = fmaxf(cmax, scores[j - k0]);
+          }
+        }
+        if (!cvalid) cmax = 0.0f;
+        float cden = 0.0f;
+        for (int64_t t = 0; t < d; ++t) cacc[t] = 0.0f;
+        for (int64_t j = k0; j < k1; ++j) {
+          const float weight = qi >= j ? exp2_approx_ftz(scores[j - k0] - cmax) : 0.0f;
+          cden += weight;
+          const float w16 = oracle_half_to_float(oracle_float_to_half(weight));
+          const uint16_t *vp = v + ((b * kv_heads + kh) * sk + j) * d;
+          for (int64_t t = 0; t < d; ++t) cacc[t] = cacc[t] + w16 * oracle_half_to_float(vp[t]);
+        }
+        if (!cvalid)
+          for (int64_t t = 0; t < d; ++t) cacc[t] = 0.0f;
+        float merged = valid ? maximum : cmax;
+        if (cvalid) merged = fmaxf(merged, cmax);
+        const float left = valid ? exp2_approx_ftz(maximum - merged) : 0.0f;
+        const float right = cvalid ? exp2_approx_ftz(cmax - merged) : 0.0f;
+        denominator = left * denominator + right * cden;
+        for (int64_t t = 0; t < d; ++t) acc[t] = left * acc[t] + right * cacc[t];
+        maximum = merged;
+        valid = valid || cvalid;
+      }
+      uint16_t *op = o + ((b * heads + h) * sq + qi) * d;
+      const float reciprocal = rcp_approx_ftz(valid ? denominator : 1.0f);
+      for (int64_t t = 0; t < d; ++t) op[t] = oracle_float_to_half(valid ? acc[t] * reciprocal : 0.0f);
+    }
+    free(scores);
+    free(qrow);
+    free(acc);
+    free(cacc);
+    leave_ieee(inner);
+  }
+  leave_ieee(csr);
+  return 0;
+}
+
 int oracle_attention_fwd_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o, int64_t batch,
                              int64_t heads, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
                              float scale, int causal, int64_t chunk, int workers) {

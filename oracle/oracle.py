@@ -41,6 +41,7 @@ def lib():
                                                     ctypes.POINTER(i64), f, i, i64, i]
         handle.oracle_attention_bias_fwd.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i64, i64,
                                                      ctypes.POINTER(i64), ctypes.POINTER(i64), f, i64, i]
+        handle.oracle_mla_prefill.argtypes = [p, p, p, p, p, p, i64, i64, i64, i64, i64, i64, i64, f, i64, i]
         handle.oracle_csr_spmv_f32.argtypes = [p, p, p, p, p, i64, i]
         handle.oracle_csr_spmm_f32.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i]
         handle.oracle_paged_decode_partials.argtypes = [p, p, p, p, p, p, p, p, p, i64, i64, i64, i64, i64, i64,
@@ -261,6 +262,20 @@ def attention_bias_fwd(q: np.ndarray, k: np.ndarray, v: np.ndarray, bias: np.nda
     lib().oracle_attention_bias_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(bias), _ptr(o), batch, heads, sq, sk, d, dv,
                                     strides, bias_strides, float(np.float32(scale)), chunk,
                                     workers or default_workers())
+    return o
+
+
+def mla_prefill(q, qpe, k, kpe, v, scale: float, *, chunk: int = 64, workers: int | None = None) -> np.ndarray:
+    """mla_prefill: f16 q [B,H,Q,D], qpe [B,H,Q,P], k [B,HK,K,D], kpe [B,1,K,P], v [B,HK,K,D];
+    returns output [B,H,Q,D] f16 (causal, key head = head // (H / HK))."""
+    q, qpe, k, kpe, v = (np.ascontiguousarray(a, np.float16) for a in (q, qpe, k, kpe, v))
+    batch, heads, sq, d = q.shape
+    kv_heads, sk, pdim = k.shape[1], k.shape[2], qpe.shape[3]
+    o = np.empty((batch, heads, sq, d), np.float16)
+    status = lib().oracle_mla_prefill(_ptr(q), _ptr(qpe), _ptr(k), _ptr(kpe), _ptr(v), _ptr(o), batch, heads, kv_heads,
+                                      sq, sk, d, pdim, float(np.float32(scale)), chunk, workers or default_workers())
+    if status:
+        raise ValueError(f"oracle_mla_prefill rejected the call ({status})")
     return o
 
 

@@ -641,6 +641,35 @@ def test_attention_bias_minus_infinity():
     assert np.isnan(oracle.attention_bias_fwd(q, k, v, bias, 0.125, chunk=64).astype(np.float32)).all()
 
 
+# ------------------------------------------------------------------------------ latent attention
+def test_mla_prefill_oracle_pinned():
+    """Zero position parts give the causal grouped attention oracle bit for bit; in general the
+    oracle meets float64 causal attention over the concatenated [q | qpe] . [k | kpe] scores with
+    one kpe row shared by every head, and the pinned attention oracle over the concatenation."""
+    g = np.random.default_rng(31)
+    B, H, HK, S, D, P = 2, 8, 2, 150, 64, 64
+    q, qpe = inputs.normal(g, (B, H, S, D), "f16"), inputs.normal(g, (B, H, S, P), "f16")
+    k, kpe, v = (inputs.normal(g, (B, HK, S, D), "f16"), inputs.normal(g, (B, 1, S, P), "f16"),
+                 inputs.normal(g, (B, HK, S, D), "f16"))
+    scale = float(np.float32((D + P) ** -0.5))
+    zq, zk = np.zeros_like(qpe), np.zeros_like(kpe)
+    plain = oracle.attention_fwd(q, k, v, scale, True, head_group=4)
+    assert (oracle.mla_prefill(q, zq, k, zk, v, scale).view(np.uint16) == plain.view(np.uint16)).all()
+    o = oracle.mla_prefill(q, qpe, k, kpe, v, scale).astype(np.float64)
+    kq = np.repeat(k, 4, axis=1).astype(np.float64)
+    logits = (q.astype(np.float64) @ kq.transpose(0, 1, 3, 2)
+              + qpe.astype(np.float64) @ kpe.astype(np.float64).transpose(0, 1, 3, 2)) * scale
+    logits[..., np.triu_indices(S, 1)[0], np.triu_indices(S, 1)[1]] = -np.inf
+    w = np.exp(logits - logits.max(axis=3, keepdims=True))
+    want = (w / w.sum(axis=3, keepdims=True)) @ np.repeat(v, 4, axis=1).astype(np.float64)
+    assert np.all(np.abs(o - want) <= 2e-2 * np.abs(want) + 1e-2)
+    assert np.abs(o - plain.astype(np.float64)).max() > 0.05         # the position part matters
+    cat_q = np.concatenate([q, qpe], axis=3)
+    cat_k = np.concatenate([k, np.repeat(kpe, HK, axis=1)], axis=3)
+    cat = oracle.attention_fwd(cat_q, cat_k, v, scale, True, head_group=4)
+    assert np.abs(o - cat.astype(np.float64)).max() <= 4e-3
+
+
 # ------------------------------------------------------------------------------ decode variants
 def _dense_decode64(q, k, v, scale, active=None):
     """float64 softmax of one query row per (batch, query head) over its key rows k [B,HQ,K,D]

@@ -245,6 +245,7 @@ def test_paged_decode_definitions_recognised_with_reference_signatures():
 
 @pytest.mark.parametrize("name,options,parameters", [
     ("flash_attention_bias_fwd", {}, ["q", "k", "v", "bias", "output", "scale"]),
+    ("mla_prefill", {"HEAD_GROUP": 4}, ["q", "qpe", "k", "kpe", "v", "output", "scale", "HEAD_GROUP"]),
     ("grouped_flash_decode_partials", {"HEAD_GROUP": 4, "P": 8, "SPLIT_SIZE": 1024},
      ["q", "k", "v", "partial_lse", "partial_output", "scale", "HEAD_GROUP", "P", "SPLIT_SIZE"]),
     ("continuous_gqa_decode", {"HEAD_GROUP": 4},
