@@ -602,6 +602,8 @@ def _op_mla_prefill(device, flush, cpu, large):
     out = {"config": f"latent attention prefill f16 B{b} H{h} HK{hk} S{s} D{d} P{p}, causal (mla_prefill)",
            "median_ms": round(ms, 4), "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
            "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    if large:
+        out["traffic"] = read_traffic("mla_prefill_b4_h32_hk8_s4096")
     if cpu:
         import oracle
 
@@ -643,7 +645,8 @@ def op_attention_bias(device, flush, cpu):
     flops = 4 * b * h * s * s * d
     out = {"config": "key-biased attention fwd f16 B4 H32 S4096 D128, no mask (flash_attention_bias_fwd)",
            "median_ms": round(ms, 4), "achieved": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
-           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops}
+           "roofline_frac": round(flops / ms / 1e9 / MFMA_PEAK_TFLOPS, 4), "flops": flops,
+           "traffic": read_traffic("attention_bias_config4")}
     if cpu:
         import oracle
 
@@ -782,7 +785,8 @@ def op_continuous_decode(device, flush, cpu):
     out = {"config": f"continuous GQA decode f16 B{batch} HQ{hq} HK{hk} K{keys} D{d}, token-major caches, all keys "
                      f"admitted (continuous_gqa_decode: partials + merge)",
            "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
-           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+           "traffic": read_traffic("continuous_decode_partials_b32_hq32_hk8_k8192_d128")}
     if cpu:
         import oracle
 
@@ -814,7 +818,8 @@ def op_grouped_decode(device, flush, cpu):
     out = {"config": f"grouped flash decode partials bf16 B{batch} HQ{hq} HK{hk} K{keys} D{d}, P{parts} x "
                      f"{keys // parts} (grouped_flash_decode_partials)",
            "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
-           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+           "traffic": read_traffic("grouped_decode_partials_b32_hq32_hk8_k8192_d128")}
     if cpu:
         import oracle
 
@@ -853,7 +858,8 @@ def op_varlen_decode(device, flush, cpu):
     out = {"config": f"packed GQA decode with sink and block logits f16, {batch} sequences of 1..4096 keys ({rows} "
                      f"rows), HQ{hq} HK{hk} D{d} (varlen_gqa_decode_with_sink_logits)",
            "median_ms": round(ms, 4), "achieved": round(nbytes / ms / 1e6, 1), "unit": "GB/s",
-           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+           "roofline_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+           "traffic": read_traffic("varlen_decode_partials_8x1to4096_hq32_hk8_d64")}
     if cpu:
         import oracle
 

@@ -480,13 +480,16 @@ __global__ __launch_bounds__(64) void decode_merge(const float *__restrict__ sta
   float acc[kPer];
 #pragma unroll
   for (int e = 0; e < kPer; ++e) acc[e] = 0.0f;
-  for (int s = 0; s < splits; ++s) {
-    const float m = state_m[base + s];   // the same for every lane
-    if (m == -INFINITY) continue;
-    const float f = __builtin_amdgcn_exp2f(m - top);
-    const float *part = state_acc + (base + s) * D;
+  // Empty splits hold m = -inf and zero sums; no branch in the loop, so its loads issue together.
+  if (valid) {
+#pragma unroll 8
+    for (int s = 0; s < splits; ++s) {
+      const float m = state_m[base + s];   // the same for every lane
+      const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - top);
+      const float *part = state_acc + (base + s) * D;
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) acc[e] = fmaf(f, part[lane + 64 * e], acc[e]);
+      for (int e = 0; e < kPer; ++e) acc[e] = fmaf(f, part[lane + 64 * e], acc[e]);
+    }
   }
   uint16_t *orow = OUT + b * out_b + h * out_h;
 #pragma unroll
