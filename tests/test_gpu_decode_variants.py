@@ -116,3 +116,37 @@ def test_varlen_decode_sink_matches_oracle(device, max_blocks):
     err = np.abs(got[:, :, :max_blocks] - want_logits)
     assert (err <= 1e-3 * np.abs(want_logits) + 1e-6).all(), f"block logits max err {err.max()}"
     assert (got[:, :, max_blocks:] == 7.0).all()
+
+
+def test_decode_variants_refuse_bad_requests(device):
+    """Plans raise before any launch: MAX_BLOCKS past the block_logits columns, partials shaped for
+    another P, and workspace='static' for the two definitions that merge split states."""
+    from intent_amd.diagnostics import CompilationStageError
+
+    announce("decode variants: refusals")
+    g = np.random.default_rng(3)
+    q, k, v = (inputs.normal(g, shape, "f16") for shape in ((2, 8, 64), (100, 2, 64), (100, 2, 64)))
+    cu = np.array([0, 40, 100], np.int32)
+    sink = np.zeros(8, np.float32)
+    kernel = intent.jit(varlen_gqa_decode_with_sink_logits, backend="hip", constexprs={"HEAD_GROUP": 4, "MAX_BLOCKS": 65})
+    out = torch.empty((2, 8, 64), dtype=torch.float16, device=device)
+    logits = torch.empty((2, 8, 64), dtype=torch.float32, device=device)
+    with pytest.raises(ValueError, match="MAX_BLOCKS"):
+        kernel(t(q, device), t(k, device), t(v, device), t(cu, device), t(sink, device), out, logits, 0.125)
+    static = intent.jit(varlen_gqa_decode_with_sink_logits, backend="hip", backend_options={"workspace": "static"},
+                        constexprs={"HEAD_GROUP": 4, "MAX_BLOCKS": 8})
+    with pytest.raises(CompilationStageError):
+        static(t(q, device), t(k, device), t(v, device), t(cu, device), t(sink, device), out, logits, 0.125)
+    kc, vc = inputs.normal(g, (2, 100, 2, 64), "f16"), inputs.normal(g, (2, 100, 2, 64), "f16")
+    mask = np.ones((2, 100, 2), np.uint8)
+    static = intent.jit(continuous_gqa_decode, backend="hip", backend_options={"workspace": "static"},
+                        constexprs={"HEAD_GROUP": 4})
+    with pytest.raises(CompilationStageError):
+        static.run(t(q, device), t(kc, device), t(vc, device), t(mask, device), 0.125)
+    qb, kb = bits_tensor(bf16(g, (2, 8, 1, 64)), device), bits_tensor(bf16(g, (2, 2, 100, 64)), device)
+    grouped = intent.jit(grouped_flash_decode_partials, backend="hip",
+                         constexprs={"HEAD_GROUP": 4, "P": 4, "SPLIT_SIZE": 32})
+    lse = torch.empty((2, 8, 5), dtype=torch.float32, device=device)
+    part = torch.empty((2, 8, 5, 64), dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError, match="parts"):
+        grouped(qb, kb, kb, lse, part, 0.125)

@@ -70,3 +70,35 @@ def test_attention_bias_validation_without_gpu():
     assert call(None, (64, 64, 1)) == 1 and b"null" in lib.fn["last_error"]()
     assert call(18, (64, 64, 1)) == 2 and b"aligned" in lib.fn["last_error"]()
     assert call(None, (64, 64, 1), sq=0) == 0
+
+
+def test_decode_and_latent_validation_without_gpu():
+    """The decode variants and latent attention refuse bad requests on the host: head counts that
+    the group does not divide, unsupported head dimensions, a missing or short workspace, a null
+    mask; empty work is a successful no-op. Workspace sizes follow the split rule."""
+    lib = hiplib.library()
+    err = lambda: lib.fn["last_error"]()  # noqa: E731
+    s19, s17, s15, s24 = ((ctypes.c_int64 * n)(*([1 << 20] * (n - 1) + [1])) for n in (19, 17, 15, 24))
+    grouped = lib.fn["grouped_decode_partials"]
+    assert grouped(16, 16, 16, 16, 16, 1, 8, 2, 3, 64, 128, 128, 4, 16, s19, 0.1, None) == 1 and b"HEAD_GROUP" in err()
+    assert grouped(16, 16, 16, 16, 16, 1, 8, 2, 4, 64, 96, 96, 4, 16, s19, 0.1, None) == 2 and b"D = DV" in err()
+    assert grouped(16, 16, 16, 16, 16, 1, 8, 2, 4, 64, 128, 128, 4, 0, s19, 0.1, None) == 1
+    assert grouped(16, 16, 16, 16, 16, 0, 8, 2, 4, 64, 128, 128, 4, 16, s19, 0.1, None) == 0
+    size = ctypes.c_size_t(0)
+    assert lib.fn["dense_decode_workspace_bytes"](32, 32, 8, 8192, 128, ctypes.byref(size)) == 0
+    # 8 splits of 1024 keys: maxima and denominators, each from a 256-byte boundary, then 128 sums per split
+    n = 32 * 32 * 8
+    assert size.value == 2 * ((4 * n + 255) // 256 * 256) + 4 * n * 128
+    cont = lib.fn["continuous_gqa_decode"]
+    assert cont(16, 16, 16, 16, 16, 2, 8, 2, 4, 100, 128, 128, s17, 0.1, None, 0, None) == 5 and b"workspace" in err()
+    assert cont(16, 16, 16, None, 16, 2, 8, 2, 4, 100, 128, 128, s17, 0.1, 256, 1 << 20, None) == 1
+    assert lib.fn["varlen_decode_workspace_bytes"](8, 32, 8, 64, 64, ctypes.byref(size)) == 0
+    n = 8 * 32 * 16                                  # 16 splits of 256 keys over the 4096-key cap
+    assert size.value == 2 * ((4 * n + 255) // 256 * 256) + 4 * n * 64
+    varlen = lib.fn["varlen_decode_sink"]
+    assert varlen(16, 16, 16, 16, None, 16, 16, 8, 100, 32, 8, 4, 64, 64, 64, s15, 0.1, 256, 1 << 20, None) == 1
+    assert varlen(16, 16, 16, 16, 16, 16, 16, 8, 100, 32, 8, 4, 64, 64, 64, s15, 0.1, 256, 16, None) == 5
+    mla = lib.fn["mla_prefill"]
+    assert mla(16, 16, 16, 16, 16, 16, 1, 8, 4, 64, 64, 128, 32, s24, 0.1, None) == 2 and b"P = 64" in err()
+    assert mla(16, 16, 16, 16, 16, 16, 1, 8, 3, 64, 64, 128, 64, s24, 0.1, None) == 1
+    assert mla(16, 16, 16, 16, 16, 16, 0, 8, 4, 64, 64, 128, 64, s24, 0.1, None) == 0
