@@ -25,7 +25,7 @@ def test_every_reported_traffic_figure_has_its_profile():
 
     source = (ROOT / "bench.py").read_text()
     names = [part.split('")', 1)[0] for part in source.split('read_traffic("')[1:]]
-    assert len(names) == 7
+    assert len(names) == 12
     for name in names:
         traffic = bench.read_traffic(name)
         assert isinstance(traffic, int) and traffic > 0, name
