@@ -148,5 +148,5 @@ def test_decode_variants_refuse_bad_requests(device):
                          constexprs={"HEAD_GROUP": 4, "P": 4, "SPLIT_SIZE": 32})
     lse = torch.empty((2, 8, 5), dtype=torch.float32, device=device)
     part = torch.empty((2, 8, 5, 64), dtype=torch.bfloat16, device=device)
-    with pytest.raises(ValueError, match="parts"):
+    with pytest.raises(ValueError, match="partial_lse"):   # the interface binds P to the constexpr
         grouped(qb, kb, kb, lse, part, 0.125)
