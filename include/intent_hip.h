@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 14
+#define INTENT_HIP_ABI_VERSION 15
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -189,11 +189,17 @@ int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void
  * key <= query, weights rounded to f16 before P @ V. q [b,h,sq,d], qpe [b,h,sq,p], k [b,hk,sk,d],
  * kpe [b,1,sk,p] (one position row per key, shared by every head), v [b,hk,sk,d], o [b,h,sq,d],
  * all f16; key head = h / head_group. d in {64, 128}, p = 64.
- * strides[24]: q, qpe, k, kpe, v, o, each (batch, head, row, col), col stride 1. */
+ * strides[24]: q, qpe, k, kpe, v, o, each (batch, head, row, col), col stride 1.
+ * When batch * heads * ceil(sq / 256) leaves CUs idle, the keys of each query block are split
+ * over workgroups whose states a second kernel merges; that needs a workspace (256-byte aligned)
+ * of intent_hip_mla_prefill_workspace_bytes(...) bytes, 0 when no split applies. A null or
+ * smaller workspace gives the unsplit launch. */
+int intent_hip_mla_prefill_workspace_bytes(int64_t batch, int64_t heads, int64_t sq, int64_t sk,
+                                           int64_t d, size_t *bytes);
 int intent_hip_mla_prefill(const void *q, const void *qpe, const void *k, const void *kpe, const void *v,
                            void *o, int64_t batch, int64_t heads, int64_t head_group, int64_t sq,
                            int64_t sk, int64_t d, int64_t p, const int64_t strides[24], float scale,
-                           void *stream);
+                           void *workspace, size_t workspace_bytes, void *stream);
 
 /* Attention forward with an additive per-key bias: flash_attention_bias_fwd
  * (streaming/attention.py:800-836, scores of summarize_biased_attention_chunk :328-366):

@@ -122,6 +122,15 @@ struct RopeRows {
   int64_t qs[3], ks[2];
 };
 
+// Key split for small grids: with count > 1, workgroup (item, split) folds its query block against
+// the split-th share of the block's key tiles and writes each query row's unnormalised state
+// (maximum in the exp2 domain, denominator, DV sums) at slot (row * count + split) of m, den and
+// acc; attention_split_merge combines the splits. Batched modes only.
+struct KeySplit {
+  int count;
+  float *m, *den, *acc;
+};
+
 // Kernel modes: batched [B,H,S,D] tensors, packed sequences, batched with a key bias, or batched
 // latent attention, whose score dimensions are the DV content dimensions of q and k followed by
 // the position dimensions of qpe and kpe (D = DV + P).
@@ -145,7 +154,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
                                                                   uint16_t *__restrict__ O, int heads,
                                                                   int head_group, int sq_all, int sk_all,
                                                                   Geometry g, float scale, int causal,
-                                                                  int q_blocks, Ragged r, KeyBias kb, RopeRows rr) {
+                                                                  int q_blocks, Ragged r, KeyBias kb, RopeRows rr,
+                                                                  KeySplit split) {
   constexpr bool kVarlen = kMode == kPacked, kBias = kMode == kBiased, kRope = kMode == kLatent;
   typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
   constexpr int kD = D, kDV = DV;
@@ -173,9 +183,11 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     sq = sk = end - start;
     row0 = start;
   } else {
-    const int bh_count = gridDim.x / q_blocks;
-    qb = q_blocks - 1 - static_cast<int>(blockIdx.x) / bh_count;   // heaviest blocks first
-    const int bh = static_cast<int>(blockIdx.x) % bh_count;
+    // With a key split the splits of one item are neighbours; without, item = workgroup.
+    const int item = static_cast<int>(blockIdx.x) / split.count;
+    const int bh_count = gridDim.x / split.count / q_blocks;
+    qb = q_blocks - 1 - item / bh_count;   // heaviest blocks first
+    const int bh = item % bh_count;
     b = bh / heads;
     h = bh % heads;
     sq = sq_all;
@@ -210,7 +222,11 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
 
   const int q_last_block = min(q0 + kBQ, sq) - 1;
   const int k_end = causal ? min(sk, q_last_block + 1) : sk;
-  const int tiles = (k_end + kBK - 1) / kBK;
+  const int tiles_all = (k_end + kBK - 1) / kBK;
+  // This workgroup's key tiles [t_begin, tiles): all of them, or its split's share.
+  const int share = (tiles_all + split.count - 1) / split.count;
+  const int t_begin = kVarlen ? 0 : min(tiles_all, static_cast<int>(blockIdx.x % split.count) * share);
+  const int tiles = kVarlen ? tiles_all : min(tiles_all, t_begin + share);
   const int wave_q_last = min(wq0 + 31, sq - 1);
 
   // DMA roles: each wave moves D / 32 x 64 chunks of K and DV / 32 x 64 chunks of V per tile.
@@ -262,8 +278,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const int v_key = 4 * (g16 >> 1) + (i16 >> 2);      // + 16 sl + 8 r
   const int v_dv = 16 * (g16 & 1) + 4 * (i16 & 3);    // + 32 mt
 
-  if (tiles > 0) issue(0);
-  for (int kt = 0; kt < tiles; ++kt) {
+  if (t_begin < tiles) issue(t_begin);
+  for (int kt = t_begin; kt < tiles; ++kt) {
     INTENT_WAIT_VMCNT(0);
     __syncthreads();          // tile kt is in LDS; every wave is done with tile kt - 1
     if (kt + 1 < tiles) issue(kt + 1);
@@ -397,6 +413,21 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   // Normalise and store: acc[mt][4 gq + e] is dv = 32 mt + 8 gq + 4 half + e of query lane_q.
   if (lane_q >= sq) return;
   const float den = row_den + __shfl_xor(row_den, 32);
+  if (!kVarlen && split.count > 1) {   // this split's state, unnormalised
+    const int64_t slot = ((static_cast<int64_t>(b) * heads + h) * sq + lane_q) * split.count + blockIdx.x % split.count;
+    if (half == 0) {
+      split.m[slot] = row_max;
+      split.den[slot] = den;
+    }
+    float *arow = split.acc + slot * kDV;
+#pragma unroll
+    for (int mt = 0; mt < kDV / 32; ++mt)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        *reinterpret_cast<float4 *>(arow + mt * 32 + 8 * gq + 4 * half) =
+            make_float4(acc[mt][4 * gq], acc[mt][4 * gq + 1], acc[mt][4 * gq + 2], acc[mt][4 * gq + 3]);
+    return;
+  }
   const bool valid = row_max != -INFINITY;
   const float inv = valid ? __builtin_amdgcn_rcpf(den) : 0.0f;
   uint16_t *orow = obase + static_cast<int64_t>(lane_q) * g.os[2];
@@ -456,6 +487,42 @@ __global__ __launch_bounds__(1024) void attention_varlen_items(const int32_t *__
 }  // namespace
 
 // The kernel of a (dtype, d, dv, packed) choice; d and dv are each 64 or 128 (checked by the callers).
+// The key splits of one query row merged as merge_attention_summaries does (exp2 factors against
+// the largest maximum), normalised by an approximate reciprocal and stored in f16; a row with no
+// admitted key in any split is 0. One wave per row; lanes own DV / 64 columns each.
+template <int DV>
+__global__ __launch_bounds__(64) void attention_split_merge(const float *__restrict__ m, const float *__restrict__ den,
+                                                            const float *__restrict__ acc, int splits, int heads, int sq,
+                                                            uint16_t *__restrict__ O, int64_t os_b, int64_t os_h,
+                                                            int64_t os_q) {
+  constexpr int kPer = DV / 64;
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * splits;
+  float top = -INFINITY;
+  for (int s = 0; s < splits; ++s) top = fmaxf(top, m[base + s]);
+  const bool valid = top != -INFINITY;
+  float total = 0.0f, sum[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) sum[e] = 0.0f;
+  if (valid) {
+#pragma unroll 4
+    for (int s = 0; s < splits; ++s) {
+      const float ms = m[base + s];
+      const float f = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - top);
+      total = fmaf(f, den[base + s], total);
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) sum[e] = fmaf(f, acc[(base + s) * DV + lane + 64 * e], sum[e]);
+    }
+  }
+  const float inv = valid ? __builtin_amdgcn_rcpf(total) : 0.0f;
+  const int64_t q = row % sq, bh = row / sq;
+  uint16_t *orow = O + (bh / heads) * os_b + (bh % heads) * os_h + q * os_q;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e)
+    orow[lane + 64 * e] = __builtin_bit_cast(uint16_t, round_to<_Float16>(sum[e] * inv));
+}
+
 template <typename E, int kMode>
 const void *attention_kernel(int64_t d, int64_t dv) {
   if (d == 64) return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 64, 64, kMode>)
@@ -498,9 +565,10 @@ namespace {
 template <typename E, int D, int DV, int kMode>
 void launch_fwd(dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O,
                 int heads, int head_group, int sq, int sk, const Geometry &g, float scale, int causal, int q_blocks,
-                const Ragged &r, const KeyBias &kb, const RopeRows &rr = RopeRows{}) {
+                const Ragged &r, const KeyBias &kb, const RopeRows &rr = RopeRows{},
+                const KeySplit &split = KeySplit{1, nullptr, nullptr, nullptr}) {
   attention_fwd<E, D, DV, kMode><<<grid, dim3(kThreads), 0, s>>>(Q, K, V, O, heads, head_group, sq, sk, g, scale,
-                                                                 causal, q_blocks, r, kb, rr);
+                                                                 causal, q_blocks, r, kb, rr, split);
 }
 
 // One launch of the (dtype, d, dv) instantiation.
@@ -684,10 +752,47 @@ extern "C" int intent_hip_attention_varlen_fwd(int dtype, const void *q, const v
 }
 
 // ---------------------------------------------------------------- latent attention
+namespace {
+
+// Key splits for a grid of `blocks` workgroups: 1 when the grid fills the 256 CUs, else enough to
+// reach about 512 workgroups, at most 8 and at most half the key tiles (two tiles per split).
+int64_t key_splits(int64_t blocks, int64_t sk) {
+  const int64_t tiles = (sk + kBK - 1) / kBK;
+  if (blocks <= 0 || blocks >= 256 || tiles < 4) return 1;
+  int64_t s = (512 + blocks - 1) / blocks;
+  s = s > 8 ? 8 : s;
+  s = s > tiles / 2 ? tiles / 2 : s;
+  return s < 1 ? 1 : s;
+}
+
+// Split state: maxima and denominators (each from a 256-byte boundary), then the sums.
+struct SplitLayout {
+  int64_t splits;
+  size_t den, acc, bytes;
+};
+SplitLayout split_layout(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t dv) {
+  const int64_t q_blocks = (sq + kBQ - 1) / kBQ;
+  const int64_t splits = key_splits(batch * heads * q_blocks, sk);
+  if (splits == 1) return SplitLayout{1, 0, 0, 0};
+  const size_t n = static_cast<size_t>(batch * heads * sq * splits);
+  const size_t part = (4 * n + 255) / 256 * 256;
+  return SplitLayout{splits, part, 2 * part, 2 * part + 4 * n * static_cast<size_t>(dv)};
+}
+
+}  // namespace
+
+extern "C" int intent_hip_mla_prefill_workspace_bytes(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d,
+                                                      size_t *bytes) {
+  if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
+  if (batch < 0 || heads < 0 || sq < 0 || sk < 0 || d < 0) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  *bytes = split_layout(batch, heads, sq, sk, d).bytes;
+  return INTENT_HIP_OK;
+}
+
 extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void *k, const void *kpe, const void *v,
                                       void *o, int64_t batch, int64_t heads, int64_t head_group, int64_t sq,
                                       int64_t sk, int64_t d, int64_t p, const int64_t *strides, float scale,
-                                      void *stream) {
+                                      void *workspace, size_t workspace_bytes, void *stream) {
   if (batch < 0 || heads < 0 || sq < 0 || sk < 0 || d < 0 || p < 0)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
   if (head_group < 1 || (heads > 0 && heads % head_group != 0))
@@ -722,7 +827,18 @@ extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void
       !aligned(o, 8))
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention tensors must be 16-byte aligned");
   const int q_blocks = static_cast<int>((sq + kBQ - 1) / kBQ);
-  const int64_t blocks = batch * heads * q_blocks;
+  // A key split needs the workspace intent_hip_mla_prefill_workspace_bytes names; without it (or
+  // when the grid fills the chip) the launch is unsplit.
+  const SplitLayout layout = split_layout(batch, heads, sq, sk, d);
+  const bool use_split = layout.splits > 1 && workspace != nullptr && workspace_bytes >= layout.bytes &&
+                         aligned(workspace, 256);
+  KeySplit ks{1, nullptr, nullptr, nullptr};
+  if (use_split) {
+    char *ws = static_cast<char *>(workspace);
+    ks = KeySplit{static_cast<int>(layout.splits), reinterpret_cast<float *>(ws), reinterpret_cast<float *>(ws + layout.den),
+                  reinterpret_cast<float *>(ws + layout.acc)};
+  }
+  const int64_t blocks = batch * heads * q_blocks * ks.count;
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many attention workgroups");
   const dim3 grid(static_cast<unsigned>(blocks));
   const hipStream_t s = as_stream(stream);
@@ -734,10 +850,20 @@ extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void
   const int iq = static_cast<int>(sq), ik = static_cast<int>(sk);
   if (d == 128)
     launch_fwd<_Float16, 192, 128, kLatent>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, 1, q_blocks, Ragged{},
-                                            KeyBias{}, rr);
+                                            KeyBias{}, rr, ks);
   else
     launch_fwd<_Float16, 128, 64, kLatent>(grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, 1, q_blocks, Ragged{},
-                                           KeyBias{}, rr);
+                                           KeyBias{}, rr, ks);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd (latent)");
+  if (ks.count > 1) {
+    const dim3 rows(static_cast<unsigned>(batch * heads * sq));
+    if (d == 128)
+      attention_split_merge<128><<<rows, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, h, iq, Op, g.os[0], g.os[1],
+                                                            g.os[2]);
+    else
+      attention_split_merge<64><<<rows, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, h, iq, Op, g.os[0], g.os[1],
+                                                           g.os[2]);
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_split_merge");
+  }
   return INTENT_HIP_OK;
 }

@@ -351,6 +351,10 @@ def _attention_bias(lib, bound, constexprs, device):
 
 def _mla_prefill(lib, bound, constexprs, device):
     """mla_prefill: causal latent attention, scores (q . k + qpe . kpe) scale (attention.py:756-798)."""
+    import ctypes
+
+    import torch
+
     q, qpe, k, kpe, v, o, scale = bound.arguments
     group = _head_group(constexprs)
     batch, heads, sq, d = q.shape
@@ -361,8 +365,17 @@ def _mla_prefill(lib, bound, constexprs, device):
     views = [_readable(t, keep, before, 8) for t in (q, qpe, k, kpe, v)] + [_writable(o, keep, after, 8)]
     strides = _strides(*views)
     keep.append(strides)
+    # Small grids split the keys over workgroups through a workspace; with workspace='static' the
+    # launch stays unsplit.
+    size = ctypes.c_size_t(0)
+    lib.check(lib.fn["mla_prefill_workspace_bytes"](batch, heads, sq, sk, d, ctypes.byref(size)), "provider_preparation")
+    workspace = None
+    if size.value and not _static_workspace():
+        workspace = torch.empty(size.value, dtype=torch.uint8, device=device)
+        keep.append(workspace)
     fn = lib.fn["mla_prefill"]
-    args = (*(t.data_ptr() for t in views), batch, heads, group, sq, sk, d, p, strides, float(scale))
+    args = (*(t.data_ptr() for t in views), batch, heads, group, sq, sk, d, p, strides, float(scale),
+            workspace.data_ptr() if workspace is not None else None, size.value if workspace is not None else 0)
     return Launch("intent_hip_mla_prefill", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
                   tuple(after), (("batch", batch), ("heads", heads), ("head_group", group), ("sq", sq), ("sk", sk),
                                  ("d", d), ("p", p)),

@@ -99,6 +99,6 @@ def test_decode_and_latent_validation_without_gpu():
     assert varlen(16, 16, 16, 16, None, 16, 16, 8, 100, 32, 8, 4, 64, 64, 64, s15, 0.1, 256, 1 << 20, None) == 1
     assert varlen(16, 16, 16, 16, 16, 16, 16, 8, 100, 32, 8, 4, 64, 64, 64, s15, 0.1, 256, 16, None) == 5
     mla = lib.fn["mla_prefill"]
-    assert mla(16, 16, 16, 16, 16, 16, 1, 8, 4, 64, 64, 128, 32, s24, 0.1, None) == 2 and b"P = 64" in err()
-    assert mla(16, 16, 16, 16, 16, 16, 1, 8, 3, 64, 64, 128, 64, s24, 0.1, None) == 1
-    assert mla(16, 16, 16, 16, 16, 16, 0, 8, 4, 64, 64, 128, 64, s24, 0.1, None) == 0
+    assert mla(16, 16, 16, 16, 16, 16, 1, 8, 4, 64, 64, 128, 32, s24, 0.1, None, 0, None) == 2 and b"P = 64" in err()
+    assert mla(16, 16, 16, 16, 16, 16, 1, 8, 3, 64, 64, 128, 64, s24, 0.1, None, 0, None) == 1
+    assert mla(16, 16, 16, 16, 16, 16, 0, 8, 4, 64, 64, 128, 64, s24, 0.1, None, 0, None) == 0
