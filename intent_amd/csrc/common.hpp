@@ -20,6 +20,10 @@ inline bool aligned(const void *p, unsigned bytes) {
   return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
 }
 
+// Workgroups of `kernel` (with `block` threads) the current device holds at once: CUs x resident
+// workgroups per CU, queried once per device and kernel.
+int resident_blocks(const void *kernel, int block);
+
 // Fills `out` from hipFuncGetAttributes of `kernel`.
 int describe_kernel(const void *kernel, const char *name, int block_threads,
                     IntentHipKernelResources *out);

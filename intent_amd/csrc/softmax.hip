@@ -395,25 +395,6 @@ struct Variant {
   bool persistent = false;    // grid of resident waves walking the rows (rows per wave: any)
 };
 
-// Workgroups of `kernel` the current device holds at once (CUs x resident workgroups per CU),
-// queried once per device and kernel.
-int resident_blocks(const void *kernel, int block) {
-  static std::mutex lock;
-  static struct { const void *kernel; int device; int blocks; } cache[16];
-  static int used = 0;
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess) return 1024;
-  std::lock_guard<std::mutex> guard(lock);
-  for (int i = 0; i < used; ++i)
-    if (cache[i].kernel == kernel && cache[i].device == device) return cache[i].blocks;
-  int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess || per_cu <= 0) per_cu = 1;
-  const int blocks = cus * per_cu;
-  if (used < 16) cache[used++] = {kernel, device, blocks};
-  return blocks;
-}
-
 template <typename T>
 Variant pick_fwd_pipe(int chunks) {
   switch (chunks) {
