@@ -247,9 +247,33 @@ def box_reference(device, flush):
     b = (torch.rand((8192, 8192), generator=g) * 2 - 1).to(torch.bfloat16).to(device)
     c = torch.empty((8192, 8192), dtype=torch.bfloat16, device=device)
     gemm_ms = operator_ms(lambda: torch.matmul(a, b, out=c), flush)
+    del a, b, c
+    probes = box_probes(device, flush)
     return {"torch_copy_gbs": round(2 * (512 << 20) / copy_ms / 1e6, 1),
             "hipblaslt_bf16_gemm_8192_tflops": round(2 * 8192 ** 3 / gemm_ms / 1e9, 1),
-            "hipblaslt_bf16_gemm_8192_ms": round(gemm_ms, 4)}
+            "hipblaslt_bf16_gemm_8192_ms": round(gemm_ms, 4), **probes}
+
+
+def box_probes(device, flush):
+    """The library's MFMA probe, timed like the operators: the sustained rate of
+    v_mfma_f32_32x32x16_{bf16,f16} on register operands, two waves per SIMD (TFLOP/s)."""
+    import torch
+
+    from intent_amd.runtime.hip.library import BF16, F16, library
+
+    lib = library()
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    blocks = 2 * lib.device_info(torch.device(device).index or 0)["compute_units"]
+    iterations = 2048
+    out = torch.empty(blocks * 4, dtype=torch.float32, device=device)
+    flops = blocks * 4 * iterations * 8 * 2 * 32 * 32 * 16
+    rates = {}
+    for name, code in (("bf16", BF16), ("f16", F16)):
+        ms = operator_ms(lambda code=code: lib.check(lib.fn["mfma_probe"](code, blocks, iterations, out.data_ptr(),
+                                                                          stream())), flush)
+        rates[f"mfma_{name}_probe_tflops"] = round(flops / ms / 1e9, 1)
+    return {**rates,
+            "mfma_probe": f"{blocks} workgroups x 4 waves x {iterations} rounds of 8 independent 32x32x16 MFMAs"}
 
 
 # ------------------------------------------------------------------------------ operators
@@ -944,6 +968,12 @@ def main():
         print(json.dumps({"copy_calibration": {"bytes_read": src.numel(), "bytes_written": dst.numel(),
                                                "launches": 20}}), flush=True)
         return
+    if args.only == "box":
+        import intent_amd  # noqa: F401
+
+        device = torch.device("cuda", 0)
+        print(json.dumps(box_reference(device, Flush(device))), flush=True)
+        return
     if args.only in OPERATORS:
         import intent_amd  # noqa: F401
 
@@ -1047,6 +1077,15 @@ def main():
         log("box reference figures")
         reference = box_reference(device, Flush(device))
         torch.cuda.empty_cache()
+        # Matrix operators also read against the MFMA rate this box sustains (the probe), beside
+        # the published dense peak their roofline_frac uses.
+        sustained = {"bf16": reference.get("mfma_bf16_probe_tflops"), "f16": reference.get("mfma_f16_probe_tflops")}
+        for op in operators:
+            config = op.get("config", "")
+            if op.get("unit") == "TFLOP/s" and "achieved" in op and "f32" not in config.split(",")[0]:
+                peak = sustained["bf16"] if "bf16" in config else sustained["f16"]
+                if peak:
+                    op["frac_of_box_mfma"] = round(op["achieved"] / peak, 4)
 
     cpu_baseline = None
     if not args.no_cpu_baseline:

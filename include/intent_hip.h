@@ -410,6 +410,15 @@ int intent_hip_csr_spmm_f32(const int32_t *row_offsets, const int32_t *column_in
                             int64_t cols, int64_t nnz, int64_t features, int64_t ldd, int64_t ldo,
                             void *stream);
 
+/* Measurement probe (no counterpart in the reference): the box's own MFMA ceiling, reported by the
+ * benchmark beside the published peak, as the measurement protocol asks for an MFMA
+ * microbenchmark on the same box. `blocks` workgroups of 4 waves (two workgroups per CU give two
+ * waves per SIMD), each wave issuing `iterations` rounds of 8 independent
+ * v_mfma_f32_32x32x16_{f16,bf16} on register operands; dtype F16 or BF16.
+ * Work: blocks * 4 * iterations * 8 * 32768 FLOP. out: blocks * 4 floats (one sum per wave, so
+ * the work cannot be dropped). */
+int intent_hip_mfma_probe(int dtype, int64_t blocks, int64_t iterations, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -102,3 +102,11 @@ def test_decode_and_latent_validation_without_gpu():
     assert mla(16, 16, 16, 16, 16, 16, 1, 8, 4, 64, 64, 128, 32, s24, 0.1, None, 0, None) == 2 and b"P = 64" in err()
     assert mla(16, 16, 16, 16, 16, 16, 1, 8, 3, 64, 64, 128, 64, s24, 0.1, None, 0, None) == 1
     assert mla(16, 16, 16, 16, 16, 16, 0, 8, 4, 64, 64, 128, 64, s24, 0.1, None, 0, None) == 0
+
+
+def test_probe_validation_without_gpu():
+    """The measurement probe checks its arguments on the host before any HIP call."""
+    lib = hiplib.library()
+    assert lib.fn["mfma_probe"](hiplib.F32, 4, 1, 1, None) == 2                 # F16 or BF16 only
+    assert lib.fn["mfma_probe"](hiplib.BF16, 0, 1, 1, None) == 1                # at least one workgroup
+    assert lib.fn["mfma_probe"](hiplib.F16, 4, 1, None, None) == 1              # null output
