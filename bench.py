@@ -256,7 +256,9 @@ def box_reference(device, flush):
 
 def box_probes(device, flush):
     """The library's MFMA probe, timed like the operators: the sustained rate of
-    v_mfma_f32_32x32x16_{bf16,f16} on register operands, two waves per SIMD (TFLOP/s)."""
+    v_mfma_f32_32x32x16_{bf16,f16} on register operands, two waves per SIMD (TFLOP/s), with varied
+    operands (the switching activity of real data; the figure operators are read against) and
+    with one fixed operand pair."""
     import torch
 
     from intent_amd.runtime.hip.library import BF16, F16, library
@@ -269,9 +271,10 @@ def box_probes(device, flush):
     flops = blocks * 4 * iterations * 8 * 2 * 32 * 32 * 16
     rates = {}
     for name, code in (("bf16", BF16), ("f16", F16)):
-        ms = operator_ms(lambda code=code: lib.check(lib.fn["mfma_probe"](code, blocks, iterations, out.data_ptr(),
-                                                                          stream())), flush)
-        rates[f"mfma_{name}_probe_tflops"] = round(flops / ms / 1e9, 1)
+        for varied, label in ((1, ""), (0, "_fixed_operands")):
+            ms = operator_ms(lambda code=code, varied=varied: lib.check(lib.fn["mfma_probe"](
+                code, varied, blocks, iterations, out.data_ptr(), stream())), flush)
+            rates[f"mfma_{name}_probe_tflops{label}"] = round(flops / ms / 1e9, 1)
     return {**rates,
             "mfma_probe": f"{blocks} workgroups x 4 waves x {iterations} rounds of 8 independent 32x32x16 MFMAs"}
 

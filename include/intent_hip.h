@@ -414,10 +414,13 @@ int intent_hip_csr_spmm_f32(const int32_t *row_offsets, const int32_t *column_in
  * benchmark beside the published peak, as the measurement protocol asks for an MFMA
  * microbenchmark on the same box. `blocks` workgroups of 4 waves (two workgroups per CU give two
  * waves per SIMD), each wave issuing `iterations` rounds of 8 independent
- * v_mfma_f32_32x32x16_{f16,bf16} on register operands; dtype F16 or BF16.
+ * v_mfma_f32_32x32x16_{f16,bf16} on register operands; dtype F16 or BF16. varied = 0: every MFMA
+ * multiplies the same two operands; varied = 1: each chain has its own operands with pseudo-random
+ * mantissas, switching as many multiplier bits as real data. Operand values lie in [0.5, 1).
  * Work: blocks * 4 * iterations * 8 * 32768 FLOP. out: blocks * 4 floats (one sum per wave, so
  * the work cannot be dropped). */
-int intent_hip_mfma_probe(int dtype, int64_t blocks, int64_t iterations, float *out, void *stream);
+int intent_hip_mfma_probe(int dtype, int varied, int64_t blocks, int64_t iterations, float *out,
+                          void *stream);
 
 #ifdef __cplusplus
 }

@@ -98,7 +98,7 @@ SIGNATURES = {
     "intent_hip_csr_spmv_f32": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p)),
     "intent_hip_csr_spmv_f32_static": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _p)),
     "intent_hip_csr_spmm_f32": (_int, (_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p)),
-    "intent_hip_mfma_probe": (_int, (_int, _i64, _i64, _p, _p)),
+    "intent_hip_mfma_probe": (_int, (_int, _int, _i64, _i64, _p, _p)),
 }
 
 

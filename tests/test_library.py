@@ -107,6 +107,6 @@ def test_decode_and_latent_validation_without_gpu():
 def test_probe_validation_without_gpu():
     """The measurement probe checks its arguments on the host before any HIP call."""
     lib = hiplib.library()
-    assert lib.fn["mfma_probe"](hiplib.F32, 4, 1, 1, None) == 2                 # F16 or BF16 only
-    assert lib.fn["mfma_probe"](hiplib.BF16, 0, 1, 1, None) == 1                # at least one workgroup
-    assert lib.fn["mfma_probe"](hiplib.F16, 4, 1, None, None) == 1              # null output
+    assert lib.fn["mfma_probe"](hiplib.F32, 1, 4, 1, 1, None) == 2              # F16 or BF16 only
+    assert lib.fn["mfma_probe"](hiplib.BF16, 1, 0, 1, 1, None) == 1             # at least one workgroup
+    assert lib.fn["mfma_probe"](hiplib.F16, 0, 4, 1, None, None) == 1           # null output
