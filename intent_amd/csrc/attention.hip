@@ -233,9 +233,51 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   // LDS chunk slot p of a tile is row p / (row chunks) (a key), physical chunk p % (row chunks);
   // rows store logical chunk pc ^ swz(key). Keys beyond sk read row sk - 1 (finite data that the
   // mask zeroes out; V tail rows are cleared in LDS below).
+  // Element offsets of this thread's chunks inside a full tile (key0 + row for every row): only
+  // the tile's base, a wave-uniform scalar, changes from tile to tile. The last tile of a row that
+  // ends inside it, and the latent mode (K chunks from two sources), take the clamped path below.
+  // (The DMA builtin takes each source as a named pointer: given the sum `k_tile + k_off[i]`
+  // directly, hipcc's host pass rejected the kernel template as a substitution failure.)
+  int64_t k_off[kKChunks / kThreads], v_off[kVChunks / kThreads];
+#pragma unroll
+  for (int i = 0; i < kKChunks / kThreads; ++i) {
+    const int p = (wave * (kKChunks / kThreads) + i) * 64 + lane;
+    const int row = p / kKRow, pc = p % kKRow;
+    k_off[i] = static_cast<int64_t>(row) * g.ks[2] + (pc ^ swz_k(D, row)) * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < kVChunks / kThreads; ++i) {
+    const int p = (wave * (kVChunks / kThreads) + i) * 64 + lane;
+    const int row = p / kVRow, pc = p % kVRow;
+    v_off[i] = static_cast<int64_t>(row) * g.vs[2] + (pc ^ swz_v(DV, row)) * 8;
+  }
   auto issue = [&](int kt) {
     uint4 *stage = lds + (kt & 1) * kStageChunks;
     const int key0 = kt * kBK;
+    if (!kRope && key0 + kBK <= sk) {   // wave-uniform: a full tile
+      const uint16_t *k_tile = kbase + static_cast<int64_t>(key0) * g.ks[2];
+      const uint16_t *v_tile = vbase + static_cast<int64_t>(key0) * g.vs[2];
+#pragma unroll
+      for (int i = 0; i < kKChunks / kThreads; ++i)
+      {
+        const uint16_t *src = k_tile + k_off[i];
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(stage + (wave * (kKChunks / kThreads) + i) * 64), 16, 0,
+                                         0);
+      }
+#pragma unroll
+      for (int i = 0; i < kVChunks / kThreads; ++i)
+      {
+        const uint16_t *src = v_tile + v_off[i];
+        __builtin_amdgcn_global_load_lds(src, (lds_void_t *)(stage + kKChunks + (wave * (kVChunks / kThreads) + i) * 64),
+                                         16, 0, 0);
+      }
+      if constexpr (kBias) {   // wave 0, one key per lane
+        if (wave == 0)
+          __builtin_amdgcn_global_load_lds(bias_row + key0 + lane, (lds_void_t *)(stage + kKChunks + kVChunks), 4, 0,
+                                           0);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < kKChunks / kThreads; ++i) {
       const int p = (wave * (kKChunks / kThreads) + i) * 64 + lane;
@@ -351,14 +393,20 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
           s[st][e] = key <= limit ? s[st][e] : -INFINITY;
         }
     }
-    float tile_max = -INFINITY;
+    // This lane's half of the tile maximum (its 16 keys of each 32-key tile; lane l ^ 32 holds the
+    // other half), in four independent chains. The maximum is exact, so the order is free.
+    float part[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) tile_max = fmaxf(tile_max, s[st][e]);
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * (kBias ? 1.0f : factor);
-    // Raise the running maximum only when this tile exceeds it by more than the slack.
-    if (__any(tile_max > row_max + kRescaleSlack)) {
+      for (int e = 0; e < 16; ++e) part[e & 3] = fmaxf(part[e & 3], s[st][e]);
+    const float half_max = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])) * (kBias ? 1.0f : factor);
+    // Raise the running maximum only when this tile exceeds it by more than the slack. Some lane's
+    // half exceeds it exactly when some query's whole tile does, so the two halves are combined
+    // (a cross-lane exchange, ds_bpermute, through the LDS unit) only in this rare branch. Scaling
+    // by factor > 0 commutes with the maximum, rounding included.
+    if (__any(half_max > row_max + kRescaleSlack)) {
+      const float tile_max = fmaxf(half_max, __shfl_xor(half_max, 32));
       const float new_max = fmaxf(row_max, tile_max);
       const float alpha = row_max == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(row_max - new_max);
       row_max = new_max;
