@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 15
+#define INTENT_HIP_ABI_VERSION 16
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,

@@ -11,7 +11,7 @@ from pathlib import Path
 
 from ...diagnostics import CompilationStageError
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 # INTENT_HIP_STATIC_SCRATCH_BYTES: the static scratch of intent_hip_csr_spmv_f32_static.
 STATIC_SCRATCH_BYTES = 32 << 20
 LIBRARY_NAME = "libintent_hip.so"
