@@ -354,6 +354,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
         }
       };
       read_k(0, 0);
+      __builtin_amdgcn_iglp_opt(0);   // hipcc's DS/MFMA interleave for the loop below
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int ks = 0; ks < kD / 16; ++ks) {
@@ -446,6 +447,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
         }
       };
       read_v(0, 0);
+      __builtin_amdgcn_iglp_opt(0);
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int sl = 0; sl < 4; ++sl) {

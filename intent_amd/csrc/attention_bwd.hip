@@ -347,6 +347,7 @@ __device__ __forceinline__ void attention_bwd_dq_body(
       f32x16_t s, dp;
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.0f;
+      __builtin_amdgcn_iglp_opt(0);   // hipcc's DS/MFMA interleave for the loop below
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
@@ -362,6 +363,7 @@ __device__ __forceinline__ void attention_bwd_dq_body(
         dsf[e >> 3][e & 7] = round_to<_Float16>(valid ? p * (dp[e] - dlt) : 0.0f);
       }
       // This half's 32 keys are 16-key slices 2 st and 2 st + 1 of the tile.
+      __builtin_amdgcn_iglp_opt(0);   // hipcc's DS/MFMA interleave for the loop below
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
@@ -572,6 +574,7 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
       f32x16_t s, dp;
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[e] = dp[e] = 0.0f;
+      __builtin_amdgcn_iglp_opt(0);   // hipcc's DS/MFMA interleave for the loop below
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
@@ -596,6 +599,7 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
         }
       }
       // This half's 32 queries are 16-query slices 2 st and 2 st + 1 of the tile.
+      __builtin_amdgcn_iglp_opt(0);   // hipcc's DS/MFMA interleave for the loop below
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
