@@ -36,6 +36,7 @@ MFMA_PEAK_TFLOPS = 2500.0          # dense bf16 / fp16
 INT8_PEAK_TOPS = 5000.0            # dense int8
 MFMA_F32_PEAK_TFLOPS = 157.3       # dense fp32 MFMA
 FWD_BYTES_PER_ELEMENT, BWD_BYTES_PER_ELEMENT = 4, 6
+ATTENTION_FLOP = 4 * 4 * 32 * 4096 * 4096 * 128 // 2   # config 4, causal half of 4*B*H*S^2*D
 
 
 def log(*parts):
@@ -248,10 +249,30 @@ def box_reference(device, flush):
     c = torch.empty((8192, 8192), dtype=torch.bfloat16, device=device)
     gemm_ms = operator_ms(lambda: torch.matmul(a, b, out=c), flush)
     del a, b, c
+    sdpa = box_sdpa(device, flush)
     probes = box_probes(device, flush)
     return {"torch_copy_gbs": round(2 * (512 << 20) / copy_ms / 1e6, 1),
             "hipblaslt_bf16_gemm_8192_tflops": round(2 * 8192 ** 3 / gemm_ms / 1e9, 1),
-            "hipblaslt_bf16_gemm_8192_ms": round(gemm_ms, 4), **probes}
+            "hipblaslt_bf16_gemm_8192_ms": round(gemm_ms, 4), **sdpa, **probes}
+
+
+def box_sdpa(device, flush):
+    """torch's scaled_dot_product_attention at config 4 (causal f16, B4 H32 S4096 D128), timed like
+    the operators: the box's own fused-attention library kernel beside attention_fwd."""
+    import torch
+    import torch.nn.functional as F
+
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q, k, v = (torch.randn((4, 32, 4096, 128), generator=g).to(torch.float16).to(device) for _ in range(3))
+    out = {}
+    try:
+        ms = operator_ms(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=128 ** -0.5), flush)
+        out = {"torch_sdpa_causal_f16_config4_ms": round(ms, 4),
+               "torch_sdpa_causal_f16_config4_tflops": round(ATTENTION_FLOP / ms / 1e9, 1)}
+    except RuntimeError as error:                         # a backend that refuses capture is reported, not fatal
+        out = {"torch_sdpa_causal_f16_config4_error": str(error)[:200]}
+    del q, k, v
+    return out
 
 
 def box_probes(device, flush):
@@ -976,6 +997,10 @@ def main():
 
         device = torch.device("cuda", 0)
         print(json.dumps(box_reference(device, Flush(device))), flush=True)
+        return
+    if args.only == "sdpa":
+        device = torch.device("cuda", 0)
+        print(json.dumps(box_sdpa(device, Flush(device))), flush=True)
         return
     if args.only in OPERATORS:
         import intent_amd  # noqa: F401
