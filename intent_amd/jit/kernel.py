@@ -10,9 +10,13 @@ Design here: the hip provider binds runtime shapes and strides at every call, so
 depends only on the device (and on the provider's specialization key, which is empty for hip).
 A `JITKernel` therefore keeps one `_DeviceSlot` per execution key, holding the resolved target
 and the artifacts made for it. The split of a positional call into inputs and Out buffers is
-read from the signature once (`_CallRoles`), not on every call. Artifacts come from the
-provider's `materialize` hook; a provider without one cannot be jitted (CompilationStageError,
-stage "provider_materialization").
+read from the signature once (`_CallRoles`), not on every call.
+
+As in the reference (`jit/kernel.py:52-68`), the local target must satisfy `ResolvedTarget`
+(else NotImplementedError), and an artifact is a generated program materialized through that
+target. The program comes from the provider's `generate` hook (the hip provider has no compiler
+stage); a provider without one cannot be jitted (CompilationStageError, stage
+"provider_generation").
 """
 from __future__ import annotations
 
@@ -22,6 +26,7 @@ from threading import RLock
 from ..api import KernelDefinition
 from ..diagnostics import CompilationStageError
 from ..language.annotations import ViewKind
+from ..targets.base import ResolvedTarget
 from ..targets.local import resolve_local, select_device
 from ..targets.provider import provider
 
@@ -107,17 +112,22 @@ class JITKernel:
                 raise RuntimeError(f"JIT kernel {self.__name__} is closed")
             slot = self._slots.get(key)
             if slot is None:
-                slot = _DeviceSlot(resolve_local(self.backend, device, workers=self.workers,
-                                                 backend_options=self.backend_options))
+                resolved = resolve_local(self.backend, device, workers=self.workers,
+                                         backend_options=self.backend_options)
+                if not isinstance(resolved, ResolvedTarget):
+                    raise NotImplementedError(f"{self.backend} has no local executable target")
+                slot = _DeviceSlot(resolved)
                 self._slots[key] = slot
             target, specialization = local.specialize(slot.target, self.definition, arguments, outputs)
             artifact = slot.artifacts.get(specialization)
             if artifact is None:
-                if self._provider.materialize is None:
-                    raise CompilationStageError("provider_materialization",
-                                                f"the {self.backend} provider cannot build definitions directly")
-                artifact = self._provider.materialize(target, self.definition, constexprs=self.constexprs,
-                                                      tuning_config=self.tuning_config, options=self.options)
+                if self._provider.generate is None:
+                    raise CompilationStageError("provider_generation",
+                                                f"the {self.backend} provider cannot generate definitions directly")
+                program = self._provider.generate(self.definition, target=target, compiler=self.compiler,
+                                                  constexprs=self.constexprs, tuning_config=self.tuning_config,
+                                                  options=self.options)
+                artifact = program.materialize()
                 slot.artifacts[specialization] = artifact
             return artifact
 

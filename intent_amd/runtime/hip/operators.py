@@ -77,6 +77,11 @@ class OperatorSpec:
     inplace_safe: bool = False    # an Out may be exactly one of the inputs (same address and strides)
     derived: tuple = ()           # (symbol, source symbol, offset): extent(symbol) = extent(source) + offset
 
+    @property
+    def entry_point(self) -> str:
+        """The C-ABI function (include/intent_hip.h) a launch of this definition calls."""
+        return ENTRY_POINTS[self.name]
+
 
 IN, OUT = 0, 1
 
@@ -103,6 +108,25 @@ def workspace_policy(policy: str):
 
 def _static_workspace() -> bool:
     return _WORKSPACE.get() == "static"
+
+
+# The program's compile options numerics: "source" keeps every low-precision cast where the
+# definition puts it; "relaxed_normalization" lets a plan pick a kernel that applies the
+# normalized-summary rewrite.
+_NUMERICS = contextvars.ContextVar("intent_hip_numerics", default="source")
+
+
+@contextlib.contextmanager
+def numerics_policy(numerics: str):
+    token = _NUMERICS.set(numerics)
+    try:
+        yield
+    finally:
+        _NUMERICS.reset(token)
+
+
+def _relaxed_normalization() -> bool:
+    return _NUMERICS.get() == "relaxed_normalization"
 
 
 # ------------------------------------------------------------------------------ layout helpers
@@ -830,6 +854,28 @@ _SPECS = (
 )
 
 SPECS = {spec.name: spec for spec in _SPECS}
+
+ENTRY_POINTS = {
+    "stable_softmax": "intent_hip_softmax_fwd", "stable_softmax_f16": "intent_hip_softmax_fwd",
+    "chunked_softmax_bf16": "intent_hip_softmax_fwd", "softmax_backward": "intent_hip_softmax_bwd",
+    "softmax_backward_f16": "intent_hip_softmax_bwd", "gemm_f32": "intent_hip_gemm_f32",
+    "linear_f32": "intent_hip_gemm_f32", "gemm_i8": "intent_hip_gemm_i8", "gemm": "intent_hip_gemm",
+    "quantized_gemm": "intent_hip_quantized_gemm", "bf16_gemm": "intent_hip_gemm_bf16",
+    "flash_attention_fwd": "intent_hip_attention_fwd_f16", "flash_gqa_attention_fwd": "intent_hip_attention_fwd",
+    "flash_attention_bf16_fwd": "intent_hip_attention_fwd", "mla_prefill": "intent_hip_mla_prefill",
+    "flash_attention_bias_fwd": "intent_hip_attention_bias_fwd",
+    "flash_varlen_attention_fwd": "intent_hip_attention_varlen_fwd",
+    "flash_varlen_gqa_prefill": "intent_hip_attention_varlen_fwd",
+    "attention_backward_delta": "intent_hip_attention_bwd_delta",
+    "attention_backward_dkdv": "intent_hip_attention_bwd_dkdv", "attention_backward_dq": "intent_hip_attention_bwd_dq",
+    "paged_gqa_decode_partials": "intent_hip_paged_decode_partials",
+    "grouped_flash_decode_partials": "intent_hip_grouped_decode_partials",
+    "continuous_gqa_decode": "intent_hip_continuous_gqa_decode",
+    "varlen_gqa_decode_with_sink_logits": "intent_hip_varlen_decode_sink",
+    "splitk_attention_f32_to_f16_reduce": "intent_hip_splitk_reduce_f32_to_f16",
+    "csr_spmm": "intent_hip_csr_spmm_f32", "csr_spmv": "intent_hip_csr_spmv_f32",
+}
+assert set(ENTRY_POINTS) == set(SPECS)
 
 
 def signature_of(interface) -> tuple:

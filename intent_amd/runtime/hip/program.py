@@ -18,7 +18,7 @@ from ..interface import PublicInterface, ViewParameter
 from ..invocation import bind_arguments
 from ..torch_views import allocate_output, observe_view
 from .library import library
-from .operators import OperatorSpec, recognize, workspace_policy
+from .operators import OperatorSpec, numerics_policy, workspace_policy
 
 
 def _symbols(definition, constexprs) -> dict[str, int]:
@@ -106,10 +106,12 @@ class HipPreparedCall:
 
 
 class HipProgram:
-    def __init__(self, spec: OperatorSpec, interface: PublicInterface, symbols: dict, constexprs: dict, target):
+    def __init__(self, spec: OperatorSpec, interface: PublicInterface, symbols: dict, constexprs: dict, target,
+                 *, numerics: str = "source"):
         import torch
 
         self.spec, self.interface, self.constexprs, self.target = spec, interface, dict(constexprs), target
+        self.numerics = numerics
         self.workspace = getattr(target, "workspace", "prepare")
         self.device = torch.device("cuda", target.device)
         self.library = library()
@@ -156,7 +158,7 @@ class HipProgram:
             raise TypeError("outputs must be a tuple in declared Out order")
         bound = self._bind(arguments, outputs)
         self._check_writable_overlap(bound)
-        with workspace_policy(self.workspace):
+        with workspace_policy(self.workspace), numerics_policy(self.numerics):
             launch = self.spec.plan(self.library, bound, self.constexprs, self.device)
         return HipPreparedCall(self, bound, launch)
 
@@ -198,33 +200,3 @@ class HipProgram:
 
     def close(self) -> None:
         self._closed = True
-
-
-def materialize_hip_artifact(target, definition, *, constexprs: dict, tuning_config=None,
-                             options=None) -> CompiledArtifact:
-    """Map `definition` to its hand-written kernel and wrap it as a `CompiledArtifact`."""
-    if tuning_config is not None:
-        raise CompilationStageError("provider_configuration",
-                                    "the hip provider has fixed kernel configurations; tuning_config is not accepted")
-    numerics = getattr(options, "numerics", "source") if options is not None else "source"
-    if numerics != "source":
-        raise CompilationStageError("provider_configuration", f"the hip provider supports numerics='source' only")
-    declared = _constexpr_parameters(definition)
-    names = tuple(name for name, _ in declared)
-    unknown = set(constexprs) - set(names)
-    if unknown:
-        raise CompilationStageError("frontend", f"unknown constexpr argument {sorted(unknown)[0]!r}")
-    values = {}
-    import inspect
-
-    for name, default in declared:
-        if name in constexprs:
-            values[name] = constexprs[name]
-        elif default is not inspect.Parameter.empty:
-            values[name] = default
-        else:
-            raise CompilationStageError("frontend", f"constexpr parameter {name!r} requires a value")
-    interface = PublicInterface.from_definition(definition, values)
-    spec = recognize(definition, interface, names)
-    program = HipProgram(spec, interface, _symbols(definition, values), values, target)
-    return CompiledArtifact(f"hip:{spec.name}", "", target.device, program, None, device_type="cuda")

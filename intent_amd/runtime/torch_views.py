@@ -19,9 +19,6 @@ from ..integrations.torch import torch_dtype
 from .interface import ViewParameter
 from .invocation import ViewFacts
 
-_EMPTY_ALLOCATION = "empty allocation"
-
-
 def byte_span(pointer: int, shape: tuple, strides: tuple, itemsize: int) -> tuple[int, int]:
     """[begin, end) of the bytes a strided view's elements occupy (empty views: an empty range)."""
     if 0 in shape:
@@ -52,7 +49,10 @@ def observe_view(parameter: ViewParameter, value, *, device, abstract: bool = Fa
         return ViewFacts(shape, strides, None, None, None, None, value.dtype, None, None, None)
     storage = value.untyped_storage()
     base, size = storage.data_ptr(), storage.nbytes()
-    identity = (value.device, base) if size else _EMPTY_ALLOCATION
+    # A zero-byte storage has no meaningful address (several may report the same or a null
+    # pointer), so each is identified by its own storage object, never by the pointer: two
+    # distinct empty buffers are two allocations (reference runtime/torch_views.py:53).
+    identity = (value.device, base) if size else (value.device, "empty", storage._cdata)
     begin, end = byte_span(value.data_ptr(), shape, strides, value.element_size())
     return ViewFacts(shape, strides, value.data_ptr(), base, base + size, value.storage_offset(), value.dtype,
                      begin, end, identity)

@@ -1,9 +1,10 @@
 """Provider registry (reference: `python/intent/targets/provider.py:26-56`).
 
 A provider is a module named in `components.json` that exports `PROVIDER`.
-`Provider.materialize` is this package's direct-materialization hook: a
-provider that maps definitions straight to native kernels (the hip provider)
-builds its artifact without the reference's KIR/MLIR `generate()` stage."""
+`Provider.generate` is this package's direct-generation hook: a provider that
+maps definitions straight to native kernels (the hip provider) makes its
+`GeneratedProgram` without the reference's KIR/MLIR compiler stage; the JIT then
+materializes that program through the resolved target, as for any provider."""
 from __future__ import annotations
 
 from collections.abc import Callable
@@ -46,7 +47,7 @@ class Provider:
     execution_model: str
     read_target: Callable | None
     environment_scope: str | None = None
-    materialize: Callable | None = None
+    generate: Callable | None = None
 
 
 def provider(name: str) -> Provider:

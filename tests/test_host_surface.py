@@ -167,8 +167,10 @@ def test_observe_and_allocate():
     assert (facts.begin, facts.end) == (view.data_ptr(), view.data_ptr() + 4 * (2 * 10 + 4 + 1))
     assert facts.offset == 12 and facts.allocation_identity == (cpu, base.data_ptr())
     assert observe_view(x_param, view, device=cpu, abstract=True).pointer is None
-    empty = [observe_view(x_param, torch.zeros(0, 3), device=cpu) for _ in range(2)]
-    assert empty[0].allocation_identity == empty[1].allocation_identity
+    empties = [torch.zeros(0, 3), torch.zeros(0, 3)]
+    empty = [observe_view(x_param, e, device=cpu) for e in empties]
+    assert empty[0].allocation_identity != empty[1].allocation_identity      # distinct storages
+    assert observe_view(x_param, empties[0][:, 1:], device=cpu).allocation_identity == empty[0].allocation_identity
     out, out_facts = allocate_output(y_param, (2, 3), device=cpu)
     assert out.shape == (2, 3) and out.dtype == torch.float32 and out_facts.strides == (3, 1)
     with pytest.raises(TypeError):

@@ -272,41 +272,6 @@ def test_csr_spmm_definition_recognised_with_reference_signature():
     assert list(csr_spmm.signature.parameters) == ["row_offsets", "column_indices", "values", "dense", "output"]
 
 
-def test_generated_program_save_load_roundtrip(tmp_path):
-    """generate -> save (kernel.source, kernel.mlir, artifact.json) -> load -> materialize, without a GPU."""
-    import json
-    from types import SimpleNamespace
-
-    target = SimpleNamespace(device=0, architecture="gfx950")
-    program = intent.generate(gemm, target=target, constexprs={"ACTIVATION": Activation.RELU})
-    path = program.save(tmp_path / "gemm_relu")
-    assert sorted(p.name for p in path.iterdir()) == ["artifact.json", "kernel.mlir", "kernel.source"]
-    loaded = intent.GeneratedProgram.load(path)
-    assert loaded.entry_name == "gemm" and loaded.metadata == program.metadata
-    assert loaded.metadata["constexprs"]["ACTIVATION"] == {"enum": "Activation", "name": "RELU", "value": 1}
-    assert loaded.interface.to_json() == PublicInterface.from_definition(
-        gemm, {"ACTIVATION": Activation.RELU}).to_json()
-    with pytest.raises(intent.CompilationStageError):
-        loaded.materialize()                                   # a loaded program has no device
-    artifact = loaded.materialize(target=target)
-    assert artifact.interface.to_json() == loaded.interface.to_json()
-    assert artifact.runtime.constexprs == {"ACTIVATION": 1}
-    with pytest.raises(intent.CompilationStageError):
-        program.save(path)                                     # never overwrites
-    with pytest.raises(intent.CompilationStageError):
-        loaded.materialize(target=SimpleNamespace(device=0, architecture="gfx942"))
-    metadata = json.loads((path / "artifact.json").read_text())
-    metadata["signature"][0][2] = "bf16"                       # tampered contract
-    (path / "artifact.json").write_text(json.dumps(metadata))
-    with pytest.raises(intent.CompilationStageError) as error:
-        intent.GeneratedProgram.load(path).materialize(target=target)
-    assert error.value.stage == "provider_recognition"
-    (path / "kernel.source").write_text("")
-    with pytest.raises(intent.CompilationStageError) as error:
-        intent.GeneratedProgram.load(path)
-    assert error.value.stage == "generated_program_loading"
-
-
 def test_definition_modules_export_the_reference_extents():
     """The reference's examples import the extent constants of the definition modules
     (examples/programs/irregular.py:14-15 imports ROWS, COLUMNS, NONZEROS, NONZEROS_PER_ROW from
