@@ -187,10 +187,40 @@ def sequence_kernel_ms(first, second, steps):
 
 
 # ------------------------------------------------------------------------------ CPU baseline
+# seconds of the last cpu_median_seconds call with every allowed CPU as the oracle's worker count
+_LAST_CPU_ALL = {}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_median_seconds(run):
     """Reference CPU protocol (runtime/mojo/compilation.py:34,56-91; mojo/program.py:28-34):
     64 MiB eviction write outside the interval, repetitions = clamp(10 ms / first, 1, 50),
-    median of 7 samples."""
+    median of 7 samples. Timed with the oracle's default worker count (the reference's
+    min(8, allowed CPUs), targets/execution.py:20-26), the figure returned, and again with every
+    allowed CPU, kept in _LAST_CPU_ALL for the operator's record."""
+    import oracle
+
+    seconds = _cpu_median_seconds(run)
+    allowed = len(os.sched_getaffinity(0))
+    default = oracle.default_workers
+    oracle.default_workers = lambda: allowed
+    try:
+        _LAST_CPU_ALL.update(seconds=_cpu_median_seconds(run), cores=allowed, default_seconds=seconds)
+    finally:
+        oracle.default_workers = default
+    return seconds
+
+
+def _cpu_median_seconds(run):
     import numpy as np
 
     evict = np.empty(64 << 20, np.uint8)
@@ -208,6 +238,21 @@ def cpu_median_seconds(run):
     return statistics.median(samples)
 
 
+def attach_all_cores(op):
+    """The operator's CPU record gains the host CPU model and its rate with every allowed CPU
+    (the rate fields scaled by the default-workers time over the all-CPU time of the same sample)."""
+    record = op.get("cpu")
+    if not isinstance(record, dict) or "seconds" not in _LAST_CPU_ALL:
+        return
+    ratio = _LAST_CPU_ALL["default_seconds"] / _LAST_CPU_ALL["seconds"]
+    rates = {key: round(value * ratio, 6) for key, value in record.items()
+             if key in ("gbs", "tflops", "tops") and isinstance(value, (int, float))}
+    if isinstance(record.get("ms"), (int, float)):
+        rates["ms"] = round(record["ms"] / ratio, 3)
+    record["cpu_model"] = cpu_model()
+    record["all_cores"] = {"cores": _LAST_CPU_ALL["cores"], **rates}
+
+
 def headline_cpu_baseline(x, dy):
     """The oracle on a bounded sample, with the reference's default worker count (min(8, allowed
     CPUs), targets/execution.py:20-26) and again with every allowed CPU."""
@@ -222,11 +267,11 @@ def headline_cpu_baseline(x, dy):
             y = oracle.softmax_fwd(xs, workers=workers)
             oracle.softmax_bwd(y, gs, workers=workers)
 
-        return round(nbytes / cpu_median_seconds(run) / 1e9, 3)
+        return round(nbytes / _cpu_median_seconds(run) / 1e9, 3)
 
     workers = oracle.default_workers()
     allowed = len(os.sched_getaffinity(0))
-    return {"value": rate(workers), "unit": "GB/s", "cores": workers, "kind": "port",
+    return {"value": rate(workers), "unit": "GB/s", "cores": workers, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"oracle softmax fwd+bwd f16 on rows 0..{rows - 1} of the 16384x4096 input "
                       f"(1/{x.shape[0] // rows} of the workload), median of 7 samples, "
                       f"{workers} OpenMP workers (min(8, allowed CPUs)); host has {os.cpu_count()} CPUs",
@@ -1091,7 +1136,9 @@ def main():
         for name in [n for n in args.operators.split(",") if n]:
             log(f"operator {name}")
             try:
+                _LAST_CPU_ALL.clear()
                 operators.append(OPERATORS[name](device, flush, not args.no_cpu_baseline))
+                attach_all_cores(operators[-1])
                 operator_graph_ms = _LAST_GRAPH_MS.pop("graph_ms", None)
                 if operator_graph_ms is not None:
                     operators[-1]["graph_ms"] = round(operator_graph_ms, 5)

@@ -53,17 +53,14 @@ __device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
   return static_cast<int32_t>(static_cast<uint32_t>(a) + static_cast<uint32_t>(b));
 }
 
-// ds_read_b64_tr_b8 of the LDS byte at `p`, as inline assembly. Through the builtin, hipcc put an
-// s_waitcnt vmcnt(0) in front of the first transposing read of every K step (it could not tell
-// the read from the stages the DMA is still writing), which waited for every DMA in flight. The
-// kernel waits lgkmcnt(0) itself before the barrier that precedes the MFMAs using the result; the
-// compiler's own lgkmcnt waits only get stricter with more LDS operations in flight than it counts.
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
+
+// ds_read_b64_tr_b8 of the LDS byte at `p`, through the compiler builtin, so the compiler tracks
+// the read's completion itself. `p` must be derived from the kernel's __shared__ array by pointer
+// arithmetic (not through an integer): the compiler then knows which LDS object the read touches,
+// and adds no wait for the DMA writes in flight before it.
 __device__ __forceinline__ i32x2_t ds_read_tr8(const int8_t *p) {
-  i32x2_t r;
-  // The low 32 bits of a generic pointer into LDS are its LDS address.
-  const uint32_t address = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
-  asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(address));
-  return r;
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t *)(p));
 }
 
 // Physical chunk of B's logical chunk c in row k (16 chunks per row).
@@ -90,16 +87,14 @@ __device__ __forceinline__ void tile_of_block(int t, int tiles_m, int tiles_n, i
   tn = in_group / rows_in_group;
 }
 
-// Interior tiles (rows beyond M read row M - 1 and are not stored).
-__global__ __launch_bounds__(kThreads, 1) void gemm_i8_mfma(const int8_t *__restrict__ A,
-                                                            const int8_t *__restrict__ B,
-                                                            const int32_t *__restrict__ bias,
-                                                            int32_t *__restrict__ C, int M, int K, int64_t lda,
-                                                            int64_t ldb, int64_t ldc, int tiles_m, int tiles_n) {
-  __shared__ uint4 lds[kStages * kStageChunks];
-  int tm, tn;
-  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * kBM, n0 = tn * kBN;
+// One interior tile (rows beyond M read row M - 1 and are not stored). A separate function with
+// __restrict__ operands, inlined into the kernel: the compiler then carries alias scopes on the
+// DMA and on the LDS reads, and adds no wait for the DMA in flight before the transposing reads
+// (the kernel's own vmcnt waits and barriers order them).
+__device__ __forceinline__ void gemm_i8_tile(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
+                                             const int32_t *__restrict__ bias, int32_t *__restrict__ C, int M,
+                                             int K, int64_t lda, int64_t ldb, int64_t ldc, int m0, int n0,
+                                             uint4 *lds) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
@@ -217,6 +212,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_mfma(const int8_t *__rest
                     wrap_add(v[4 * g + 2], bias[n + 2]), wrap_add(v[4 * g + 3], bias[n + 3])};
       }
   }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void gemm_i8_mfma(const int8_t *__restrict__ A,
+                                                            const int8_t *__restrict__ B,
+                                                            const int32_t *__restrict__ bias,
+                                                            int32_t *__restrict__ C, int M, int K, int64_t lda,
+                                                            int64_t ldb, int64_t ldc, int tiles_m, int tiles_n) {
+  __shared__ uint4 lds[kStages * kStageChunks];
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  gemm_i8_tile(A, B, bias, C, M, K, lda, ldb, ldc, tm * kBM, tn * kBN, lds);
 }
 
 // ---------------------------------------------------------------- general shapes

@@ -171,3 +171,25 @@ def test_softmax_bwd_golden(device, golden):
         torch.from_numpy(g["softmax_bwd_f16_p"]).to(device), torch.from_numpy(g["softmax_bwd_f16_dy"]).to(device))
     w = g["softmax_bwd_f16_dx"]
     assert np.all(np.abs(dx.cpu().numpy() - w) <= 2e-2 * np.abs(w) + 1e-2 * np.abs(w).max())
+
+
+def test_softmax_config2_seed0_fwd_bwd(device):
+    """The exact pair the bench times: x, dy of config 2 drawn from seed 0, the forward's y fed to
+    the backward through prepared calls, as bench.py's step does."""
+    announce("softmax config 2 seed 0 fwd+bwd")
+    x, dy = inputs.softmax_f16_fwd_bwd(seed=0, rows=16384, cols=4096)
+    fwd = intent.jit(stable_softmax_f16, backend="hip").prepare(torch.from_numpy(x).to(device))
+    bwd = intent.jit(softmax_backward_f16, backend="hip").prepare(fwd.result(), torch.from_numpy(dy).to(device))
+    fwd.launch()
+    bwd.launch()
+    y = fwd.result().cpu().numpy()
+    want_y = oracle.softmax_fwd(x)
+    assert_16bit(y, want_y)
+    ulps = f16_ulp_distance(y, want_y)
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.98
+    dx = bwd.result().cpu().numpy()
+    want = oracle.softmax_bwd(y, dy)
+    assert_16bit(dx, want)
+    p64 = y.astype(np.float64)
+    spread = 1e-5 * np.abs(p64) * np.sum(np.abs(p64 * dy.astype(np.float64)), axis=1, keepdims=True)
+    assert np.all(np.abs(dx.astype(np.float64) - want) <= 2 ** -9 * np.abs(want.astype(np.float64)) + spread + 6e-8)

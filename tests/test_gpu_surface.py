@@ -41,7 +41,9 @@ def test_run_prepare_launch_result(device):
     assert kernel.interface.parameters[0].name == "x"
     assert len(call.inspect_configurations()) == 1
     assert kernel.artifacts[0].observation is not None
-    assert kernel.artifacts[0].source == "hip:stable_softmax"
+    artifact = kernel.artifacts[0]
+    assert "stable_softmax" in artifact.source and "intent_hip_softmax_fwd" in artifact.source
+    assert artifact.ir["intent"] and "no KIR stage" in artifact.mlir
     explicit = torch.empty_like(x)
     assert kernel(x, explicit) is None
     assert_f32_rel(explicit.cpu().numpy(), oracle.softmax_fwd(x.cpu().numpy()))
