@@ -6,8 +6,12 @@
 // validity q_idx >= k_idx on absolute indices, masked scores -inf, maximum_num maxima,
 // p = exp2(s - max) (approximate, flush-to-zero: v_exp_f32), P rounded to f16 before P @ V
 // (f32 accumulation), output acc * rcp(den) (approximate: v_rcp_f32), cast to f16 (RNE).
-// The key axis is folded in 64-key chunks; the running maximum replaces the chunk maximum
-// before P is rounded (online softmax), which the 16-bit tolerance covers.
+// The key axis is folded in 64-key chunks, each summarised as the definition's author summarizer
+// does: weights against the chunk's own maximum, rounded to the element type, P @ V of the chunk
+// from zero, then merged into the running state with exp2 factors on both sides. (The running-
+// maximum rewrite of online softmax, which moves where P is rounded, is the compiler's
+// relaxed_normalization rewrite; it never applies to author summarizers,
+// doc/dsl/types-numerics-and-effects.en.md:142-152.)
 //
 // Design (d and dv each 64 or 128, independently):
 //   * a workgroup owns 256 query rows of one (batch, head): 8 waves x 32 rows, two per SIMD;
@@ -27,9 +31,10 @@
 //   * each wave raises its priority (s_setprio 1) while it issues an MFMA loop, so of the two
 //     waves on a SIMD the one with matrix work issues first and the other's exp and LDS work
 //     fills the gaps (0.621 against 0.638 ms at config 4);
-//   * the softmax scale is folded into one FMA per score, and the running maximum is only
-//     raised when a tile exceeds it by more than 8 (exp2 domain), which skips most rescales
-//     of O while keeping every weight <= 2^8;
+//   * the softmax scale is folded into one FMA per score. A chunk's maximum spans the lane pair
+//     (l, l ^ 32), exchanged with v_permlane32_swap (a VALU op, no LDS round trip); the chunk's
+//     P @ V runs one 32-dv block at a time from a zero accumulator and joins O with one FMA per
+//     element (O is first scaled only when some query's maximum rises);
 //   * causal: a workgroup visits key tiles up to its last query only, a wave skips tiles
 //     beyond its own last query, and only tiles crossing the diagonal are masked; the
 //     heaviest query blocks are dispatched first. All query blocks of one head share an
@@ -143,9 +148,21 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // s_waitcnt with only the vector-memory counter constrained (vmcnt <= n).
 #define INTENT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt((((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8)))
 
-// Rescale threshold of the online softmax, in the exp2 domain: the running maximum is only
-// raised when a tile's maximum exceeds it by more than this, so weights stay <= 2^8.
-constexpr float kRescaleSlack = 8.0f;
+// How far a chunk maximum may exceed the reference maximum of the running O^T and denominator
+// before they are rescaled to it (exp2 domain): chunk factors stay <= 2^8.
+constexpr float kRefSlack = 8.0f;
+
+// The values of lanes l % 32 (lo) and l % 32 + 32 (hi) of v, on every lane l: one
+// v_permlane32_swap_b32 of two copies (it swaps the upper 32 lanes of its first operand with the
+// lower 32 of its second). Inline assembly: hipcc's builtin for it returns both results from one
+// register. The s_nop 1 on each side gives the two wait states the instruction needs after a VALU
+// write of its operands, and before its results are read.
+__device__ __forceinline__ void lane_halves(float v, float &lo, float &hi) {
+  float a = v, b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  lo = a;
+  hi = b;
+}
 
 template <typename E, int D, int DV, int kMode>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__restrict__ Q,
@@ -311,8 +328,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   for (int mt = 0; mt < kDV / 32; ++mt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[mt][e] = 0.0f;
-  float row_max = -INFINITY;   // running maximum of valid scaled scores (exp2 domain)
-  float row_den = 0.0f;        // this lane's share of the denominator
+  // Running summary of this lane's query (merge_attention_summaries' record): validity, and the
+  // denominator (the same on both lanes of the pair) and O^T against the reference maximum row_ref,
+  // which stays within kRefSlack below the running maximum of valid scaled scores (exp2 domain).
+  bool row_valid = false;
+  float row_ref = 0.0f;   // reference maximum of row_den and acc (see the merge below)
+  float row_den = 0.0f;
   const float factor = scale * kLog2e;
   const int frag_row = lane & 31;
   // V^T transposed-read roles: group g16 = lane / 16, source index i16 = lane % 16.
@@ -380,11 +401,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
           s[st][4 * j + 3] = fmaf(s[st][4 * j + 3], factor, b4.w * kLog2e);
         }
     }
-    // Mask (only tiles that cross the diagonal or the end) and the tile maximum of raw scores
-    // (scale * log2 e > 0, so the maximum commutes with the scaling; biased scores are final).
+    // Mask (only tiles that cross the diagonal or the end) and the chunk maximum of raw scores
+    // (scale * log2 e > 0, so the maximum commutes with the scaling, rounding included; biased
+    // scores are final).
     const bool edge = causal ? (key0 + kBK - 1 > wq0) : false;
-    const bool tail = key0 + kBK > sk;
-    if (edge || tail) {                                        // wave-uniform
+    const bool partial = edge || key0 + kBK > sk;               // wave-uniform
+    if (partial) {
       const int limit = causal ? min(sk - 1, lane_q) : sk - 1;  // last valid key of this lane's query
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -394,67 +416,93 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
           s[st][e] = key <= limit ? s[st][e] : -INFINITY;
         }
     }
-    // This lane's half of the tile maximum (its 16 keys of each 32-key tile; lane l ^ 32 holds the
-    // other half), in four independent chains. The maximum is exact, so the order is free.
+    // This lane's 32 keys in four independent chains (maximum_num: NaN-ignoring, exact, any order),
+    // then the other half's from lane l ^ 32.
     float part[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) part[e & 3] = fmaxf(part[e & 3], s[st][e]);
-    const float half_max = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])) * (kBias ? 1.0f : factor);
-    // Raise the running maximum only when this tile exceeds it by more than the slack. Some lane's
-    // half exceeds it exactly when some query's whole tile does, so the two halves are combined
-    // (a cross-lane exchange, ds_bpermute, through the LDS unit) only in this rare branch. Scaling
-    // by factor > 0 commutes with the maximum, rounding included.
-    if (__any(half_max > row_max + kRescaleSlack)) {
-      const float tile_max = fmaxf(half_max, __shfl_xor(half_max, 32));
-      const float new_max = fmaxf(row_max, tile_max);
-      const float alpha = row_max == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(row_max - new_max);
-      row_max = new_max;
-      row_den *= alpha;
-#pragma unroll
-      for (int mt = 0; mt < kDV / 32; ++mt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[mt][e] *= alpha;
-    }
-    const float shift = row_max == -INFINITY ? 0.0f : row_max;
+    float max_lo, max_hi;
+    lane_halves(fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])), max_lo, max_hi);
+    // The chunk summary (summarize_attention_chunk_*): weights against the chunk maximum, 0 at
+    // masked keys. Every chunk this wave visits holds a valid key for each of its queries (tiles
+    // start at multiples of 64 keys and waves at multiples of 32 queries, and a wave visits tile key0
+    // only when key0 <= its last query, hence key0 <= its first; without the causal mask, key0 < sk),
+    // so the summarizer's empty-chunk case (maximum 0, accumulator selected to 0) never arises here.
+    // A masked key's score is -inf, so its weight exp2(-inf - max) is 0 for a finite or +inf chunk
+    // maximum, without a select. With a -inf or NaN chunk maximum (only from infinite or NaN
+    // inputs) the chunk's valid weights are NaN as the summarizer's are, and so is the row's output
+    // whatever the masked keys' weights.
+    const float chunk_max = fmaxf(max_lo, max_hi) * (kBias ? 1.0f : factor);
     f16x8_t pf[4];   // P^T fragments: slice sl = 2 st + (e / 8), slot j = e % 8
+    float den_part = 0.0f;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float p = __builtin_amdgcn_exp2f(kBias ? s[st][e] - shift : fmaf(s[st][e], factor, -shift));
-        row_den += p;
+        const float p = __builtin_amdgcn_exp2f(kBias ? s[st][e] - chunk_max : fmaf(s[st][e], factor, -chunk_max));
+        den_part += p;
         pf[st * 2 + (e >> 3)][e & 7] = static_cast<E>(p);
       }
-    // O^T += V^T P^T. The A operand (V^T rows dv, keys in slot order) comes from V's natural
-    // [key][dv] layout through ds_read_b64_tr_b16: read r of slice sl gives the lane keys
-    // 16 sl + 8 r + 4 half + 0..3 of its dv.
+    float den_lo, den_hi;
+    lane_halves(den_part, den_lo, den_hi);
+    // Merge (running summary, chunk), merge_attention_summaries' algebra: O^T and the denominator are
+    // kept against a reference maximum `row_ref` instead of the running maximum itself, and the
+    // chunk joins with the factor exp2(chunk max - row_ref). The reference rises to the running
+    // maximum only when a chunk maximum exceeds it by more than kRefSlack, so the factors stay
+    // <= 2^kRefSlack and O^T is rescaled (exp2(old - new) on both, as the merge's left factor) only
+    // then. Normalisation divides out the common factor exp2(running maximum - row_ref). The weights
+    // P above are rounded against the chunk's own maximum either way: the reference only moves the
+    // f32 products of the merge, not where the 16-bit rounding happens.
+    // A chunk maximum above row_ref + kRefSlack is above the running maximum too (that never rose
+    // more than kRefSlack above row_ref without a rescale), so it is the new running maximum.
+    if (__any(!row_valid || chunk_max > row_ref + kRefSlack)) {   // wave-uniform, rare
+      const float ref = !row_valid || chunk_max > row_ref + kRefSlack ? chunk_max : row_ref;
+      const float left = row_valid ? __builtin_amdgcn_exp2f(row_ref - ref) : 0.0f;
+      row_ref = ref;
+      row_den *= left;
+#pragma unroll
+      for (int mt = 0; mt < kDV / 32; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[mt][e] *= left;
+    }
+    row_valid = true;
+    const float right = __builtin_amdgcn_exp2f(chunk_max - row_ref);
+    row_den = fmaf(right, den_lo + den_hi, row_den);
+    // The chunk's O^T = V^T P^T, one 32-dv tile at a time from zero, joined as acc + right * chunk.
+    // The A operand (V^T rows dv, keys in slot order) comes from V's natural [key][dv] layout through
+    // ds_read_b64_tr_b16: read r of slice sl gives the lane keys 16 sl + 8 r + 4 half + 0..3 of its
+    // dv. Steps q = 4 mt + sl run over the dv tiles and key slices; fragment q lives in vf[q % 4] and
+    // is read two steps before its MFMA.
     {
-      f16x8_t vf[2][kDV / 32];
-      auto read_v = [&](int sl, int buf) {
+      constexpr int kSteps = kDV / 32 * 4;
+      f16x8_t vf[4];
+      auto read_v = [&](int q) {
+        const int mt = q >> 2, sl = q & 3;
+        i16x4_t parts[2];
 #pragma unroll
-        for (int mt = 0; mt < kDV / 32; ++mt) {
-          i16x4_t parts[2];
-#pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            const int key = sl * 16 + 8 * r + v_key;
-            const int dv = mt * 32 + v_dv;
-            const int chunk = (dv >> 3) ^ swz_v(DV, key);
-            parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kDV + chunk * 8 + (dv & 7)));
-          }
-          vf[buf][mt] = __builtin_bit_cast(f16x8_t, parts);
+        for (int r = 0; r < 2; ++r) {
+          const int key = sl * 16 + 8 * r + v_key;
+          const int dv = mt * 32 + v_dv;
+          const int chunk = (dv >> 3) ^ swz_v(DV, key);
+          parts[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(sv_tile + key * kDV + chunk * 8 + (dv & 7)));
         }
+        vf[q & 3] = __builtin_bit_cast(f16x8_t, parts);
       };
-      read_v(0, 0);
+      read_v(0);
+      read_v(1);
       __builtin_amdgcn_iglp_opt(0);
       __builtin_amdgcn_s_setprio(1);
+      f32x16_t chunk_acc;
 #pragma unroll
-      for (int sl = 0; sl < 4; ++sl) {
-        if (sl + 1 < 4) read_v(sl + 1, (sl + 1) & 1);
+      for (int q = 0; q < kSteps; ++q) {
+        if (q + 2 < kSteps) read_v(q + 2);
+        const int mt = q >> 2, sl = q & 3;
+        chunk_acc = Elem<E>::mma(vf[q & 3], pf[sl], sl == 0 ? f32x16_t{} : chunk_acc);
+        if (sl == 3)
 #pragma unroll
-        for (int mt = 0; mt < kDV / 32; ++mt)
-          acc[mt] = Elem<E>::mma(vf[sl & 1][mt], pf[sl], acc[mt]);
+          for (int e = 0; e < 16; ++e) acc[mt][e] = fmaf(right, chunk_acc[e], acc[mt][e]);
       }
       __builtin_amdgcn_s_setprio(0);
     }
@@ -462,11 +510,14 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
 
   // Normalise and store: acc[mt][4 gq + e] is dv = 32 mt + 8 gq + 4 half + e of query lane_q.
   if (lane_q >= sq) return;
-  const float den = row_den + __shfl_xor(row_den, 32);
-  if (!kVarlen && split.count > 1) {   // this split's state, unnormalised
+  const float den = row_den;
+  if (!kVarlen && split.count > 1) {
+    // This split's state, unnormalised: the denominator and O^T with the maximum they are taken
+    // against (row_ref; -inf for a split with no key), which is what attention_split_merge's exp2
+    // factors need.
     const int64_t slot = ((static_cast<int64_t>(b) * heads + h) * sq + lane_q) * split.count + blockIdx.x % split.count;
     if (half == 0) {
-      split.m[slot] = row_max;
+      split.m[slot] = row_valid ? row_ref : -INFINITY;
       split.den[slot] = den;
     }
     float *arow = split.acc + slot * kDV;
@@ -478,7 +529,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
             make_float4(acc[mt][4 * gq], acc[mt][4 * gq + 1], acc[mt][4 * gq + 2], acc[mt][4 * gq + 3]);
     return;
   }
-  const bool valid = row_max != -INFINITY;
+  const bool valid = row_valid;
   const float inv = valid ? __builtin_amdgcn_rcpf(den) : 0.0f;
   uint16_t *orow = obase + static_cast<int64_t>(lane_q) * g.os[2];
 #pragma unroll

@@ -117,3 +117,45 @@ def test_attention_config4_full(device):
     want = oracle.attention_fwd_f16(np.ascontiguousarray(q[sub]), np.ascontiguousarray(k[sub]),
                                     np.ascontiguousarray(v[sub]), scale, True)
     assert_16bit(o[sub].cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype,causal", [("f16", True), ("f16", False), ("bf16", True)])
+def test_attention_chunk_rounding_matches_oracle(device, dtype, causal):
+    """P is rounded against each 64-key chunk's own maximum, as summarize_attention_chunk_f16/bf16
+    (streaming/attention.py:152-237) does, under the default numerics. Scores here jump by tens of
+    units (exp2 domain) inside each tile and between tiles, so weights rounded against a running
+    maximum instead would differ in the low bits of many rows. Against the oracle (the same 64-key
+    fold): over 99% of output elements bit-identical, and every element within eps (|o| + 1), eps
+    the element type's spacing at 1 (2^-10 for f16, 2^-7 for bf16):
+    a unit or two in the last place of the 16-bit result (the MFMA sums in another order than the
+    oracle's loop), measured against |v| ~ 1 near zero, where cancellation leaves outputs whose unit
+    in the last place says nothing."""
+    announce("attention chunk rounding", dtype, causal)
+    from intent_amd.examples.kernels.streaming.attention import flash_attention_bf16_fwd
+    from tests.gpu_util import bf16_tensor_bits, bf16_to_f32, to_bf16_tensor
+
+    rng = np.random.default_rng(31)
+    shape = (2, 2, 384, 128)
+    q, k, v = (rng.standard_normal(shape, dtype=np.float32) * np.float32(s) for s in (4.0, 4.0, 1.0))
+    k *= 1.0 + np.linspace(0.0, 3.0, shape[2], dtype=np.float32)[None, None, :, None]   # later keys score higher
+    store = (lambda a: a.astype(np.float16)) if dtype == "f16" else inputs._bf16_bits
+    q, k, v = store(q), store(k), store(v)
+    scale = float(np.float32(128 ** -0.5))
+    if dtype == "f16":
+        o = run(device, q, k, v, scale, causal)
+        want = oracle.attention_fwd_f16(q, k, v, scale, causal)
+        ulps = np.abs(o.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
+    else:
+        t = lambda a: to_bf16_tensor(a, device)  # noqa: E731
+        got = intent.jit(flash_attention_bf16_fwd, backend="hip", constexprs={"HEAD_GROUP": 1, "CAUSAL": causal}).run(
+            t(q), t(k), t(v), scale)
+        got_bits = bf16_tensor_bits(got)
+        want_bits = oracle.attention_fwd(q, k, v, scale, causal, storage="bf16")
+        o, want = bf16_to_f32(got_bits), bf16_to_f32(want_bits)
+        ulps = np.abs(got_bits.astype(np.int32) - want_bits.astype(np.int32))
+    assert_16bit(o, want)
+    err = np.abs(np.asarray(o, np.float64) - np.asarray(want, np.float64))
+    announce(f"chunk rounding {dtype} causal={causal}: {(ulps == 0).mean():.5f} identical, max |err| {err.max():.3g}")
+    assert (ulps == 0).mean() > 0.99
+    eps = 2.0 ** -10 if dtype == "f16" else 2.0 ** -7
+    assert (err <= eps * (np.abs(np.asarray(want, np.float64)) + 1.0)).all()

