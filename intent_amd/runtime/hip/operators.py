@@ -174,6 +174,59 @@ def _refuse_staging(tensor, vector: int) -> None:
                          f"kernel needs {need}, got strides {tuple(tensor.stride())}")
 
 
+# ------------------------------------------------------------------------------ attention head dimensions
+# The attention kernels are built for key and value head dimensions of 64 and 128. Any other width up
+# to 128 (the reference declares D and DV symbolic, streaming/attention.py:428-553) runs on the next of
+# the two through zero-padded copies refreshed at each launch: zero dimensions add exact zeros to
+# every score's sum and give output columns that are dropped, so results equal the unpadded ones.
+_KERNEL_WIDTHS = (64, 128)
+
+
+def _kernel_width(extent: int, name: str) -> int:
+    for width in _KERNEL_WIDTHS:
+        if extent <= width:
+            return width
+    raise CompilationStageError("provider_configuration",
+                                f"{name} = {extent}: the hip attention kernels take head dimensions up to "
+                                f"{_KERNEL_WIDTHS[-1]}")
+
+
+def _padded_in(tensor, width, keep, before):
+    """`tensor` with its last dimension extended to `width` by zeros; the copy runs at each launch."""
+    _refuse_staging(tensor, 8)
+    staged = tensor.new_zeros(tuple(tensor.shape[:-1]) + (width,))
+    head = staged[..., :tensor.shape[-1]]
+    keep.append(staged)
+    before.append(lambda: head.copy_(tensor))
+    return staged
+
+
+def _padded_out(tensor, width, keep, after):
+    """A buffer of last dimension `width` whose first columns are copied into `tensor` after a launch."""
+    _refuse_staging(tensor, 8)
+    staged = tensor.new_empty(tuple(tensor.shape[:-1]) + (width,))
+    head = staged[..., :tensor.shape[-1]]
+    keep.append(staged)
+    after.append(lambda: tensor.copy_(head))
+    return staged
+
+
+def _attention_views(q, k, v, o, keep, before, after):
+    """q, k, v and o as an attention kernel reads them, and the kernel's (d, dv): unit inner stride,
+    16-byte aligned rows, head dimensions padded to 64 or 128 where they are not."""
+    d, dv = q.shape[-1], v.shape[-1]
+    kd, kdv = _kernel_width(d, "d"), _kernel_width(dv, "dv")
+    if kd != d:
+        qk, kk = _padded_in(q, kd, keep, before), _padded_in(k, kd, keep, before)
+    else:
+        qk, kk = _readable(q, keep, before, 8), _readable(k, keep, before, 8)
+    if kdv != dv:
+        vk, ok = _padded_in(v, kdv, keep, before), _padded_out(o, kdv, keep, after)
+    else:
+        vk, ok = _readable(v, keep, before, 8), _writable(o, keep, after, 8)
+    return qk, kk, vk, ok, kd, kdv
+
+
 def _row_stride(tensor):
     rows, cols = tensor.shape
     return tensor.stride(0) if rows > 1 else cols
@@ -302,10 +355,9 @@ def _attention_f16(lib, bound, constexprs, device):
     q, k, v, o, scale = bound.arguments
     causal = bool(constexprs["CAUSAL"])
     keep, before, after = [q, k, v, o], [], []
-    qk, kk, vk, ok = (_readable(q, keep, before, 8), _readable(k, keep, before, 8),
-                      _readable(v, keep, before, 8), _writable(o, keep, after, 8))
-    batch, heads, sq, d = q.shape
-    sk, dv = k.shape[2], v.shape[3]
+    qk, kk, vk, ok, d, dv = _attention_views(q, k, v, o, keep, before, after)
+    batch, heads, sq = q.shape[:3]
+    sk = k.shape[2]
     strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
     keep.append(strides)
     fn = lib.fn["attention_fwd_f16"]
@@ -333,9 +385,8 @@ def _attention_grouped(dtype_code):
             raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({k.shape[1]}) * HEAD_GROUP "
                              f"({group})")
         keep, before, after = [q, k, v, o], [], []
-        qk, kk, vk, ok = (_readable(q, keep, before, 8), _readable(k, keep, before, 8),
-                          _readable(v, keep, before, 8), _writable(o, keep, after, 8))
-        sk, dv = k.shape[2], v.shape[3]
+        qk, kk, vk, ok, d, dv = _attention_views(q, k, v, o, keep, before, after)
+        sk = k.shape[2]
         strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
         keep.append(strides)
         fn = lib.fn["attention_fwd"]
@@ -354,13 +405,12 @@ def _attention_bias(lib, bound, constexprs, device):
     import ctypes
 
     q, k, v, bias, o, scale = bound.arguments
-    batch, heads, sq, d = q.shape
-    sk, dv = k.shape[2], v.shape[3]
+    batch, heads, sq = q.shape[:3]
+    sk = k.shape[2]
     if tuple(bias.shape) != (batch, heads, sk):
         raise ValueError(f"bias must be [B, H, K] = {(batch, heads, sk)}, got {tuple(bias.shape)}")
     keep, before, after = [q, k, v, bias, o], [], []
-    qk, kk, vk, ok = (_readable(q, keep, before, 8), _readable(k, keep, before, 8),
-                      _readable(v, keep, before, 8), _writable(o, keep, after, 8))
+    qk, kk, vk, ok, d, dv = _attention_views(q, k, v, o, keep, before, after)
     bk = _readable(bias, keep, before)
     strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
     bias_strides = (ctypes.c_int64 * 3)(*bk.stride())
@@ -445,8 +495,8 @@ def _attention_varlen(grouped: bool):
                 "provider_preparation", "packed-sequence attention lists its work items in a workspace; "
                 "backend_options workspace='static' has none for it, use workspace='prepare'")
         keep, before, after = [q, k, v, lengths, cu, o], [], []
-        qk, kk, vk = _readable(q, keep, before, 8), _readable(k, keep, before, 8), _readable(v, keep, before, 8)
-        ok, cuk = _writable(o, keep, after, 8), _readable(cu, keep, before)
+        qk, kk, vk, ok, d, dv = _attention_views(q, k, v, o, keep, before, after)
+        cuk = _readable(cu, keep, before)
 
         def row_head_inner(t):
             return (t.stride(0), t.stride(1), t.stride(2)) if t.dim() == 3 else (t.stride(0), 0, t.stride(1))

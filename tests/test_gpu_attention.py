@@ -93,9 +93,24 @@ def test_attention_head_dim_64_matches_oracle(device, shape, sk, causal):
         assert (o[:, :, 0, :] == v[:, :, 0, :]).all()        # one valid key: exactly v[0]
 
 
+@pytest.mark.parametrize("d,dv,causal", [(96, 96, True), (32, 80, False), (100, 128, True), (1, 7, True),
+                                         (128, 48, False)])
+def test_attention_other_head_dims_match_oracle(device, d, dv, causal):
+    """D and DV are symbolic in the reference (streaming/attention.py:428-466): widths other than 64
+    and 128 run zero-padded to the next kernel width, which leaves every score and output unchanged."""
+    announce("attention d/dv", d, dv, causal)
+    rng = np.random.default_rng(d * 1000 + dv)
+    q, k = inputs.normal(rng, (2, 3, 200, d), "f16"), inputs.normal(rng, (2, 3, 200, d), "f16")
+    v = inputs.normal(rng, (2, 3, 200, dv), "f16")
+    scale = float(np.float32(d ** -0.5))
+    o = run(device, q, k, v, scale, causal)
+    assert o.shape == (2, 3, 200, dv)
+    assert_16bit(o, oracle.attention_fwd_f16(q, k, v, scale, causal))
+
+
 def test_attention_unsupported_head_dim(device):
-    announce("attention d=96")
-    q, k, v, scale = inputs.attention_f16(seed=1, batch=1, heads=1, seq=64, dim=96)
+    announce("attention d=160")
+    q, k, v, scale = inputs.attention_f16(seed=1, batch=1, heads=1, seq=64, dim=160)
     with pytest.raises(intent.CompilationStageError):
         run(device, q, k, v, scale, True)
 

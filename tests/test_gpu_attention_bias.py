@@ -92,3 +92,11 @@ def test_bias_attention_minus_infinity_masks_keys(device):
     assert np.isnan(o[0, 1]).all() and np.isnan(o[0, 2]).all()
     assert_16bit(o[0, 0], want[0, 0])
     assert_16bit(o[0, 0], _float64_masked(q, k, v, bias, 0.125)[0, 0])
+
+
+def test_bias_attention_other_head_dims(device):
+    """Head widths other than 64 and 128 (zero-padded to the kernel width by the provider)."""
+    announce("attention bias d=72 dv=24")
+    q, k, v, bias = case(7, 1, 2, 130, 190, 72, 24)
+    scale = float(np.float32(72 ** -0.5))
+    assert_16bit(run(device, q, k, v, bias, scale), oracle.attention_bias_fwd(q, k, v, bias, scale))

@@ -280,3 +280,23 @@ def test_attention_value_width_differs_from_key_width(device, d, dv, kind, group
         for part in (slice(0, 64), slice(64, 128)):
             piece = run_attention(device, defn, q, k, np.ascontiguousarray(v[..., part]), scale, group, causal, bf16)
             assert (piece.view(np.uint16) == o[..., part].view(np.uint16)).all()
+
+
+@pytest.mark.parametrize("d,dv,bf16", [(96, 96, False), (40, 112, True)])
+def test_grouped_attention_other_head_dims(device, d, dv, bf16):
+    """flash_gqa_attention_fwd / flash_attention_bf16_fwd with head widths other than 64 and 128
+    (zero-padded to the kernel width by the provider)."""
+    announce("gqa d/dv", d, dv, bf16)
+    rng = np.random.default_rng(d + dv)
+    kind = "bf16" if bf16 else "f16"
+    q = inputs.normal(rng, (1, 4, 150, d), kind)
+    k = inputs.normal(rng, (1, 2, 170, d), kind)
+    v = inputs.normal(rng, (1, 2, 170, dv), kind)
+    scale = float(np.float32(d ** -0.5))
+    definition = flash_attention_bf16_fwd if bf16 else flash_gqa_attention_fwd
+    o = run_attention(device, definition, q, k, v, scale, 2, True, bf16)
+    want = oracle.attention_fwd(q, k, v, scale, True, head_group=2, storage="bf16" if bf16 else None)
+    if bf16:
+        assert_16bit(bf16_to_f32(o), bf16_to_f32(want))
+    else:
+        assert_16bit(o, want)

@@ -111,3 +111,16 @@ def test_varlen_static_workspace_is_refused(device):
     with pytest.raises(Exception, match="workspace"):
         kernel.run(q, q, q, torch.tensor([4], dtype=torch.int32, device=device),
                    torch.tensor([0, 4], dtype=torch.int32, device=device), 0.125)
+
+
+def test_varlen_other_head_dims(device):
+    """Packed sequences with head widths other than 64 and 128 (zero-padded by the provider)."""
+    announce("varlen d=48 dv=100")
+    rng = np.random.default_rng(48)
+    lengths = [70, 1, 300, 129]
+    total = sum(lengths)
+    q, k = inputs.normal(rng, (total, 4, 48), "f16"), inputs.normal(rng, (total, 2, 48), "f16")
+    v = inputs.normal(rng, (total, 2, 100), "f16")
+    scale = float(np.float32(48 ** -0.5))
+    o = run_gqa(device, q, k, v, lengths, scale, 2)
+    assert_16bit(o, oracle.attention_varlen_fwd(q, k, v, offsets(lengths), scale, True, head_group=2))
