@@ -18,7 +18,8 @@ contract (`python/intent/runtime/contract.py:98-121`). That reader requires:
 and hands the whole object to the provider's `read_facts`. A hip program writes all of these, so
 the reference's own `GeneratedProgram.load(...)` accepts it, plus a `hip` object with the
 provider's facts: the definition it maps to, its runtime signature, constexpr values, dimension
-symbols, the C-ABI entry point and the library ABI version.
+symbols, the C-ABI entry point, the library ABI version and the effective tuning table (the
+provider's configuration rows, tuning_config families in place of their defaults).
 
 The `native` section describes the C-ABI binding of every public parameter: a pointer, then an
 i64 extent and an i64 stride per view axis, and each scalar by value. Views are "strided" (a
@@ -72,6 +73,7 @@ class HipFacts:
     symbols: dict
     entry_point: str
     abi_version: int
+    tuning: dict
 
 
 def read_hip_facts(metadata: dict) -> HipFacts:
@@ -90,8 +92,10 @@ def read_hip_facts(metadata: dict) -> HipFacts:
         raise TypeError("hip constexprs and symbols are JSON objects")
     signature = tuple(tuple(entry) for entry in hip["signature"])
     recognize_saved(hip["definition"], signature, tuple(hip["constexprs"]))
+    from ..runtime.hip.tuning import table_from_metadata
+
     return HipFacts(hip["definition"], signature, dict(hip["constexprs"]), dict(hip["symbols"]),
-                    hip["entry_point"], hip["abi_version"])
+                    hip["entry_point"], hip["abi_version"], table_from_metadata(hip.get("tuning")))
 
 
 def _native_section(interface, inplace_safe: bool) -> dict:
@@ -326,7 +330,8 @@ def bind_program(program, target):
     spec = recognize_saved(facts.definition, facts.signature, tuple(facts.constexprs))
     constexprs = {name: _decode_constexpr(value) for name, value in facts.constexprs.items()}
     interface = PublicInterface.read(metadata["interface"])
-    runtime = HipProgram(spec, interface, dict(facts.symbols), constexprs, target, numerics=options.numerics)
+    runtime = HipProgram(spec, interface, dict(facts.symbols), constexprs, target, numerics=options.numerics,
+                         tuning=facts.tuning)
     return CompiledArtifact(program.source, program.ir, target.device, runtime, None, device_type="cuda",
                             cache_directory=program.cache_directory)
 
@@ -386,9 +391,9 @@ def generate(definition, *, target, compiler=None, constexprs: dict | None = Non
     if compiler is not None:
         raise CompilationStageError("provider_configuration",
                                     "the hip provider has no compiler stage; compiler must be None")
-    if tuning_config is not None:
-        raise CompilationStageError("provider_configuration",
-                                    "the hip provider has fixed kernel configurations; tuning_config is not accepted")
+    from ..runtime.hip.tuning import DEFAULT_FAMILIES, read_tuning_config, table_metadata
+
+    table = dict(DEFAULT_FAMILIES) if tuning_config is None else read_tuning_config(tuning_config)
     try:
         policy = read_options(options)
     except (TypeError, ValueError) as error:
@@ -414,7 +419,8 @@ def generate(definition, *, target, compiler=None, constexprs: dict | None = Non
         "hip": {"format": FORMAT, "definition": spec.name,
                 "signature": [list(item) for item in signature_of(interface)],
                 "constexprs": {name: _encode_constexpr(value) for name, value in values.items()},
-                "symbols": _symbols(definition, values), "entry_point": entry, "abi_version": ABI_VERSION},
+                "symbols": _symbols(definition, values), "entry_point": entry, "abi_version": ABI_VERSION,
+                "tuning": table_metadata(table)},
     }
     try:
         return GeneratedProgram(source, ir, metadata, None, spec.name, _binding=binding)

@@ -66,6 +66,7 @@ class Launch:
     after: tuple = ()             # callables run on the launch stream after the kernel
     configuration: tuple = ()
     resources: Callable[[], dict | None] = field(default=lambda: None)
+    candidates: tuple = ()        # (row, eligible, reasons) of the definition's tuning family, table order
 
 
 @dataclass(frozen=True)
@@ -127,6 +128,44 @@ def numerics_policy(numerics: str):
 
 def _relaxed_normalization() -> bool:
     return _NUMERICS.get() == "relaxed_normalization"
+
+
+# The program's rows of its tuning family (runtime/hip/tuning.py), in table order.
+_TUNING = contextvars.ContextVar("intent_hip_tuning", default=None)
+
+
+@contextlib.contextmanager
+def tuning_policy(rows):
+    token = _TUNING.set(rows)
+    try:
+        yield
+    finally:
+        _TUNING.reset(token)
+
+
+def _split_choice(family: str, split_bytes: int) -> tuple[int, tuple]:
+    """The first eligible row of `family` (columns: split) and every row's assessment. split = 1
+    needs a grid small enough to split (split_bytes > 0: the workspace it takes) and a workspace
+    policy that allows one; split = 0 is always eligible."""
+    from .tuning import DEFAULT_FAMILIES
+
+    rows = _TUNING.get() or DEFAULT_FAMILIES[family]
+    candidates, chosen = [], None
+    for row in rows:
+        reasons = []
+        if row[0] == 1:
+            if _static_workspace():
+                reasons.append("backend_options workspace='static' allows no workspace")
+            if split_bytes <= 0:
+                reasons.append("the grid fills the device: there is nothing to split")
+        candidates.append((row, not reasons, tuple(reasons)))
+        if not reasons and chosen is None:
+            chosen = row[0]
+    if chosen is None:
+        raise CompilationStageError("provider_configuration",
+                                    f"no row of tuning family {family} is eligible for this call: "
+                                    + "; ".join(f"{list(r)}: {', '.join(why)}" for r, _, why in candidates))
+    return chosen, tuple(candidates)
 
 
 # ------------------------------------------------------------------------------ layout helpers
@@ -439,12 +478,13 @@ def _mla_prefill(lib, bound, constexprs, device):
     views = [_readable(t, keep, before, 8) for t in (q, qpe, k, kpe, v)] + [_writable(o, keep, after, 8)]
     strides = _strides(*views)
     keep.append(strides)
-    # Small grids split the keys over workgroups through a workspace; with workspace='static' the
-    # launch stays unsplit.
+    # Small grids split the keys over workgroups through a workspace (tuning family
+    # hip.latent_prefill; with workspace='static' or the unsplit row the launch stays unsplit).
     size = ctypes.c_size_t(0)
     lib.check(lib.fn["mla_prefill_workspace_bytes"](batch, heads, sq, sk, d, ctypes.byref(size)), "provider_preparation")
+    split, candidates = _split_choice("hip.latent_prefill", size.value)
     workspace = None
-    if size.value and not _static_workspace():
+    if split:
         workspace = torch.empty(size.value, dtype=torch.uint8, device=device)
         keep.append(workspace)
     fn = lib.fn["mla_prefill"]
@@ -452,8 +492,8 @@ def _mla_prefill(lib, bound, constexprs, device):
             workspace.data_ptr() if workspace is not None else None, size.value if workspace is not None else 0)
     return Launch("intent_hip_mla_prefill", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
                   tuple(after), (("batch", batch), ("heads", heads), ("head_group", group), ("sq", sq), ("sk", sk),
-                                 ("d", d), ("p", p)),
-                  lambda: lib.kernel_resources(OP_MLA_PREFILL, F16, sq, d | (p << 16)))
+                                 ("d", d), ("p", p), ("split", split)),
+                  lambda: lib.kernel_resources(OP_MLA_PREFILL, F16, sq, d | (p << 16)), candidates)
 
 
 def _head_group(constexprs) -> int:
@@ -580,23 +620,25 @@ def _attention_bwd(kind):
 
         import torch
 
+        # (tuning family hip.attention_backward: split = 0 runs the unsplit kernels)
         size = ctypes.c_size_t(0)
-        if not _static_workspace():
-            lib.check(lib.fn[f"attention_bwd_{kind}_workspace_bytes"](batch, q_heads, group, sq, sk, d,
-                                                                     ctypes.byref(size)), "provider_preparation")
-        workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
+        lib.check(lib.fn[f"attention_bwd_{kind}_workspace_bytes"](batch, q_heads, group, sq, sk, d,
+                                                                 ctypes.byref(size)), "provider_preparation")
+        split, candidates = _split_choice("hip.attention_backward", size.value)
+        workspace = torch.empty(size.value, dtype=torch.uint8, device=device) if split else None
         if workspace is not None:
             keep.append(workspace)
         fn = lib.fn[f"attention_bwd_{kind}_ws"]
-        args = (*args, workspace.data_ptr() if workspace is not None else None, size.value)
-        configuration += (("workspace_bytes", size.value),)
+        args = (*args, workspace.data_ptr() if workspace is not None else None,
+                size.value if workspace is not None else 0)
+        configuration += (("split", split), ("workspace_bytes", size.value if workspace is not None else 0))
         op = OP_ATTENTION_BWD_DQ if kind == "dq" else OP_ATTENTION_BWD_DKDV
         # The kernel variant depends on the rows of the call: batch x query heads x queries for dQ,
         # batch x key heads x keys for dK/dV.
         rows = batch * q_heads * sq if kind == "dq" else batch * (q_heads // group) * sk
         return Launch(f"intent_hip_attention_bwd_{kind}", lambda stream: fn(*args, stream), tuple(keep),
                       tuple(before), tuple(after), configuration,
-                      lambda: lib.kernel_resources(op, F16, rows, d))
+                      lambda: lib.kernel_resources(op, F16, rows, d), candidates)
     return plan
 
 

@@ -18,7 +18,8 @@ from ..interface import PublicInterface, ViewParameter
 from ..invocation import bind_arguments
 from ..torch_views import allocate_output, observe_view
 from .library import library
-from .operators import OperatorSpec, numerics_policy, workspace_policy
+from .operators import OperatorSpec, numerics_policy, tuning_policy, workspace_policy
+from .tuning import FAMILY_OF, SPLIT, TuningConfiguration
 
 
 def _symbols(definition, constexprs) -> dict[str, int]:
@@ -102,16 +103,30 @@ class HipPreparedCall:
         return self._program.observe(self._launch) if self._launched else None
 
     def inspect_configurations(self) -> tuple:
-        return (ConfigurationAssessment(self._launch.configuration, True, ()),)
+        """Every row of the definition's tuning family (the chosen one first) with its eligibility
+        and the reasons of an ineligible one; one fixed configuration otherwise."""
+        candidates = self._launch.candidates
+        if not candidates:
+            return (ConfigurationAssessment(self._launch.configuration, True, ()),)
+        chosen = dict(self._launch.configuration).get("split")
+        ordered = sorted(candidates, key=lambda c: (c[0][0] != chosen or not c[1]))
+        return tuple(ConfigurationAssessment(self._launch.configuration if row[0] == chosen else (("split", row[0]),),
+                                             eligible, reasons)
+                     for row, eligible, reasons in ordered)
 
 
 class HipProgram:
     def __init__(self, spec: OperatorSpec, interface: PublicInterface, symbols: dict, constexprs: dict, target,
-                 *, numerics: str = "source"):
+                 *, numerics: str = "source", tuning: dict | None = None):
         import torch
+
+        from .tuning import DEFAULT_FAMILIES
 
         self.spec, self.interface, self.constexprs, self.target = spec, interface, dict(constexprs), target
         self.numerics = numerics
+        self.tuning_family = FAMILY_OF.get(spec.name)
+        table = DEFAULT_FAMILIES if tuning is None else tuning
+        self.tuning_rows = table.get(self.tuning_family) if self.tuning_family else None
         self.workspace = getattr(target, "workspace", "prepare")
         self.device = torch.device("cuda", target.device)
         self.library = library()
@@ -158,7 +173,7 @@ class HipProgram:
             raise TypeError("outputs must be a tuple in declared Out order")
         bound = self._bind(arguments, outputs)
         self._check_writable_overlap(bound)
-        with workspace_policy(self.workspace), numerics_policy(self.numerics):
+        with workspace_policy(self.workspace), numerics_policy(self.numerics), tuning_policy(self.tuning_rows):
             launch = self.spec.plan(self.library, bound, self.constexprs, self.device)
         return HipPreparedCall(self, bound, launch)
 
@@ -170,6 +185,16 @@ class HipProgram:
     def launch(self, *arguments) -> None:
         inputs, outputs = self.interface.split_arguments(tuple(arguments))
         self.prepare_call(inputs, outputs=outputs).launch()
+
+    def tuning_configurations(self, *arguments) -> tuple:
+        """The eligible rows of this definition's tuning family for `arguments` (every runtime
+        argument, explicit Out buffers included), in table order; () for a definition the hip
+        kernels run in one fixed configuration. Binding may allocate, nothing is launched."""
+        if self.tuning_family is None:
+            return ()
+        inputs, outputs = self.interface.split_arguments(tuple(arguments))
+        call = self.prepare_call(inputs, outputs=outputs)
+        return tuple(TuningConfiguration((SPLIT,), row) for row, eligible, _ in call._launch.candidates if eligible)
 
     def infer_outputs(self, arguments: tuple):
         """Out buffers for `arguments` without touching device pointers (fake/meta tensors)."""

@@ -391,7 +391,9 @@ def test_static_workspace_option_runs_the_unsplit_kernels(device, shape, causal)
     prepared = AttentionBackward.from_jit(jit, head_group=hq // hk, causal=causal).prepare(
         t(q), t(k), t(v), t(o), t(do), t(lse), scale)
     for call in prepared.calls[1:]:
-        assert dict(call.inspect_configurations()[0].configuration)["workspace_bytes"] == 0
+        chosen, *others = call.inspect_configurations()
+        assert dict(chosen.configuration)["workspace_bytes"] == 0 and dict(chosen.configuration)["split"] == 0
+        assert all(not a.eligible and a.reasons for a in others)
     prepared.launch()
     grad_q, grad_k, grad_v = prepared.result()
     delta = oracle.attention_bwd_delta(o, do)
@@ -399,3 +401,33 @@ def test_static_workspace_option_runs_the_unsplit_kernels(device, shape, causal)
     close(grad_q.cpu().numpy(), oracle.attention_bwd_dq(q, k, v, do, lse, delta, scale, causal, head_group=hq // hk))
     close(grad_k.cpu().numpy(), want_dk)
     close(grad_v.cpu().numpy(), want_dv)
+
+
+def test_tuning_config_pins_the_unsplit_kernels(device, tmp_path):
+    """tuning_config {"hip.attention_backward": [[0]]} at the reference's example shape (which splits by
+    default): the unsplit kernels run, tuning_configurations lists only that row, and both bindings
+    meet the oracle. The default table lists the split row first and takes it here."""
+    import json
+
+    batch, hq, hk, sq, sk, d = 2, 8, 2, 1024, 1024, 64
+    announce("attention backward tuning_config")
+    q, k, v, o, do, lse = case(77, batch, hq, hk, sq, sk, d)
+    scale = float(np.float32(1 / np.sqrt(d)))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    config = tmp_path / "tuning.json"
+    config.write_text(json.dumps({"columns": ["split"], "families": {"hip.attention_backward": [[0]]}}))
+    delta = oracle.attention_bwd_delta(o, do)
+    want_dq = oracle.attention_bwd_dq(q, k, v, do, lse, delta, scale, True, head_group=hq // hk)
+    from intent_amd.examples.kernels.backward.attention import attention_backward_dq
+
+    for tuning, rows in ((None, [(1,), (0,)]), (config, [(0,)])):
+        kernel = intent.jit(attention_backward_dq, backend="hip", tuning_config=tuning,
+                            constexprs={"HEAD_GROUP": hq // hk, "CAUSAL": True})
+        args = (t(q), t(k), t(v), t(do), t(lse), t(delta), scale)
+        call = kernel.prepare(*args)
+        call.launch()
+        assert dict(call.inspect_configurations()[0].configuration)["split"] == rows[0][0]
+        out = torch.empty_like(args[0])
+        listed = kernel.artifacts[0].tuning_configurations(*args[:6], out, scale)
+        assert [c.values for c in listed] == rows and all(c.parameters[0].name == "split" for c in listed)
+        close(call.result().cpu().numpy(), want_dq)

@@ -189,3 +189,40 @@ def test_generate_refuses_what_the_hip_path_cannot_honour():
     with pytest.raises(intent.CompilationStageError) as error:
         intent.generate(gemm, target=SimpleNamespace(device=0))
     assert error.value.stage == "target_resolution"
+
+
+def test_tuning_config_rows_are_read_and_saved(tmp_path):
+    """jit/generate(tuning_config=path): the reference's table form ({"columns", "families"}); a
+    supplied family replaces its default rows, others keep theirs; rows outside what the kernels
+    implement, unknown families and malformed files are CompilationStageError at generation; a
+    saved program keeps its rows."""
+    from intent_amd.examples.kernels.backward.attention import attention_backward_dq
+    from intent_amd.runtime.hip.tuning import DEFAULT_FAMILIES
+
+    config = tmp_path / "tuning.json"
+    config.write_text(json.dumps({"columns": ["split"], "families": {"hip.attention_backward": [[0]]}}))
+    program = intent.generate(attention_backward_dq, target=resolved(), tuning_config=config,
+                              constexprs={"HEAD_GROUP": 1, "CAUSAL": True})
+    tuning = program.metadata["hip"]["tuning"]
+    assert tuning["families"]["hip.attention_backward"] == [[0]]
+    assert tuning["families"]["hip.latent_prefill"] == [list(r) for r in DEFAULT_FAMILIES["hip.latent_prefill"]]
+    loaded = intent.GeneratedProgram.load(program.save(tmp_path / "p"))
+    artifact = loaded.materialize(target=resolved())
+    assert artifact.runtime.tuning_family == "hip.attention_backward" and artifact.runtime.tuning_rows == ((0,),)
+    default = intent.generate(attention_backward_dq, target=resolved(), constexprs={"HEAD_GROUP": 1, "CAUSAL": True})
+    assert default.materialize().runtime.tuning_rows == ((1,), (0,))
+    assert intent.generate(gemm, target=resolved(), tuning_config=config,
+                           constexprs={"ACTIVATION": Activation.NONE}).materialize().runtime.tuning_family is None
+    for bad in ({"columns": ["split"], "families": {"hip.attention_backward": [[2]]}},
+                {"columns": ["split"], "families": {"hip.nonexistent": [[0]]}},
+                {"columns": ["tile"], "families": {}},
+                {"columns": ["split"], "families": {"hip.latent_prefill": []}},
+                {"families": {}}):
+        config.write_text(json.dumps(bad))
+        with pytest.raises(intent.CompilationStageError) as error:
+            intent.generate(attention_backward_dq, target=resolved(), tuning_config=config,
+                            constexprs={"HEAD_GROUP": 1, "CAUSAL": True})
+        assert error.value.stage == "provider_configuration"
+    with pytest.raises(intent.CompilationStageError):
+        intent.generate(gemm, target=resolved(), tuning_config=tmp_path / "missing.json",
+                        constexprs={"ACTIVATION": Activation.NONE})
