@@ -159,13 +159,15 @@ int intent_hip_quantized_gemm(const void *a, const void *b, const float *bias, c
 int intent_hip_gemm_i8(const void *a, const void *b, const int32_t *bias, int32_t *c, int64_t m,
                        int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, void *stream);
 
-/* Fused attention forward, f16 in/out, f32 online softmax in the exp2 domain.
+/* Fused attention forward, f16 in/out, f32 softmax in the exp2 domain.
  * flash_attention_fwd (python/intent/examples/kernels/streaming/attention.py:428-466) with
  * summarize_attention_chunk_f16 (:152-191), merge_attention_summaries (:82-114) and
- * normalize_attention_summary (:417-425).
+ * normalize_attention_summary (:417-425): keys folded in 64-key chunks, each chunk's weights
+ * rounded to f16 against that chunk's own maximum before P @ V, chunks merged with exp2 factors.
  * q [b,h,sq,d], k [b,h,sk,d], v [b,h,sk,dv], o [b,h,sq,dv]; strides[16] holds the four
  * element strides of q, k, v, o in that order (the last of each must be 1).
- * causal: key j is valid for query i iff i >= j (absolute indices). d and dv are each 64 or 128. */
+ * causal: key j is valid for query i iff i >= j (absolute indices). d and dv are each 64 or 128
+ * (the Python provider serves other widths up to 128 by zero-padding to these). */
 int intent_hip_attention_fwd_f16(const void *q, const void *k, const void *v, void *o,
                                  int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d,
                                  int64_t dv, const int64_t strides[16], float scale, int causal,
