@@ -17,10 +17,10 @@
 //   * 5 to 127: 16 lanes per row (spmv_rows);
 //   * medium (128 to big - 1): the row is cut at the boundaries of 8 column windows of C / 8
 //     columns, the share of x one XCD's 4 MB L2 holds, and the piece in window w runs on XCD w
-//     (hardware workgroup h runs on XCD h % 8), so its gathers hit that L2 (spmv_slices<false>);
+//     (hardware workgroup h runs on XCD h % 8), so its gathers hit that L2 (spmv_windows);
 //   * large (big = max(128, 32 S) or more): the row is cut at the boundaries of S slices of 32768
 //     columns; a workgroup stages one slice of x (128 KB) in LDS and runs that slice's piece of
-//     many large rows, gathering from LDS (spmv_slices<true>).
+//     many large rows, gathering from LDS (spmv_slices).
 // Each piece runs on one wave: coalesced loads of its columns and values, one reduction per piece.
 // The medium and large row lists are built without atomics: spmv_count counts each 1024-row
 // block's rows of each class, spmv_scan (one workgroup) turns the counts into list offsets, and
@@ -418,38 +418,130 @@ __global__ __launch_bounds__(256) void spmv_bounds(const int32_t *__restrict__ o
   }
 }
 
-// Pieces of listed rows for one part: a slice of the large rows (kLds, workgroups part * K + k; the
-// slice's kSliceCols columns of x are staged in LDS) or a window of the medium rows (workgroup h
-// takes window h % 8 and runs on XCD h % 8, whose L2 holds that window of x). Wave w takes the
-// pieces of list rows i = k + K t for t = w, w + 16, ..., one piece at a time: lanes stride the
-// piece 64 nonzeros at a time, kUnroll strides loaded together (coalesced), and the piece's sum is
-// one wave reduction in a fixed order. While a piece is summed, the next piece's cuts and first
-// kUnroll strides are already in flight. An entry outside the staged slice (possible with an
-// inexact cut) reads x from global memory.
+// Pieces of listed rows. Wave w of a workgroup takes the pieces of list rows i = k + K t for
+// t = w, w + 16, ..., one piece at a time: lanes stride the piece 64 nonzeros at a time, a block of
+// strides loaded together (coalesced), and the piece's sum is one wave reduction in a fixed order.
 constexpr int kSliceThreads = 1024;
 constexpr int kSliceWaves = kSliceThreads / 64;
-constexpr int kUnroll = 4;    // 64-nonzero strides of a piece loaded together
-template <bool kLds>
+
+// Medium rows, one column window per part: workgroup h takes window h % 8 and runs on XCD h % 8,
+// whose L2 holds that window of x. While a piece is summed, the next piece's cuts (scalar loads)
+// and first block are in flight. The pieces are short (77 nonzeros on average at config 5), so
+// lanes past a piece's end load nothing: issuing their loads anyway, so that the wait counters
+// could overlap two pieces ahead, measured slower (101.6 / 98.7 against 94.9 us with blocks of 4 /
+// 2 strides); the window gathers are bound by the loads issued, not by their latency.
+constexpr int kWindowUnroll = 4;
+__global__ __launch_bounds__(kSliceThreads) void spmv_windows(const int32_t *__restrict__ col,
+                                                             const float *__restrict__ val,
+                                                             const float *__restrict__ x, int32_t cols,
+                                                             const int32_t *__restrict__ cuts, int cut_stride,
+                                                             float *__restrict__ parts, int part_stride,
+                                                             const int32_t *__restrict__ count, int capacity) {
+  constexpr int kU = kWindowUnroll;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // Wave-uniform in a scalar register, so the cuts below are scalar loads (counted by lgkmcnt).
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = static_cast<int>(gridDim.x) / part_stride;
+  const int part = static_cast<int>(blockIdx.x % part_stride);
+  const int k = static_cast<int>(blockIdx.x / part_stride);
+  const int n_rows = min(*count, capacity);
+  if (n_rows <= k) return;   // workgroup-uniform
+  const int n_tile = (n_rows - k + K - 1) / K;
+  auto cut_at = [&](int t, int side) {
+    return __builtin_amdgcn_readfirstlane(cuts[(k + static_cast<int64_t>(K) * t) * cut_stride + part + side]);
+  };
+  auto load_block = [&](int32_t p0, int32_t e, int32_t (&cu)[kU], float (&vu)[kU]) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int32_t p = p0 + 64 * u + lane;
+      cu[u] = p < e ? __builtin_nontemporal_load(col + p) : 0;
+      vu[u] = p < e ? __builtin_nontemporal_load(val + p) : 0.0f;
+    }
+  };
+  // Masked lanes leave the sum as it was (a select after the FMA): multiplying their stand-in x by
+  // zero would turn an inf or NaN elsewhere in x into a NaN here.
+  auto add_block = [&](int32_t p0, int32_t e, const int32_t (&cu)[kU], const float (&vu)[kU], float &acc) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const bool ok = p0 + 64 * u + lane < e;
+      const float sum = fmaf(vu[u], x[clamp_col(ok ? cu[u] : 0, cols)], acc);
+      acc = ok ? sum : acc;
+    }
+  };
+  // Two register sets alternate: while piece t is summed from one, the next piece's first block
+  // loads into the other, and the cuts of the piece after next load (scalar). Unrolled by two so
+  // that no set is copied into the other, which would wait for the loads in flight.
+  int t = wave;
+  if (t >= n_tile) return;
+  int32_t b0 = cut_at(t, 0), e0 = cut_at(t, 1);
+  int32_t b1 = 0, e1 = 0;
+  if (t + kSliceWaves < n_tile) {
+    b1 = cut_at(t + kSliceWaves, 0);
+    e1 = cut_at(t + kSliceWaves, 1);
+  }
+  int32_t cu0[kU], cu1[kU];
+  float vu0[kU], vu1[kU];
+  load_block(b0, e0, cu0, vu0);
+  auto piece = [&](int32_t b, int32_t e, const int32_t (&cu)[kU], const float (&vu)[kU], int32_t nb, int32_t ne,
+                   int32_t (&ncu)[kU], float (&nvu)[kU], int32_t &fb, int32_t &fe) {
+    const bool more = t + kSliceWaves < n_tile;   // wave-uniform
+    if (more) load_block(nb, ne, ncu, nvu);
+    if (t + 2 * kSliceWaves < n_tile) {
+      fb = cut_at(t + 2 * kSliceWaves, 0);
+      fe = cut_at(t + 2 * kSliceWaves, 1);
+    }
+    float acc = 0.0f;
+    add_block(b, e, cu, vu, acc);
+    for (int32_t p0 = b + 64 * kU; p0 < e; p0 += 64 * kU) {   // wave-uniform: rest of the piece
+      int32_t cr[kU];
+      float vr[kU];
+      load_block(p0, e, cr, vr);
+      add_block(p0, e, cr, vr, acc);
+    }
+    const float sum = wave_sum(acc);
+    if (lane == 0) parts[(k + static_cast<int64_t>(K) * t) * part_stride + part] = sum;
+    return more;
+  };
+  while (true) {   // wave-uniform
+    if (!piece(b0, e0, cu0, vu0, b1, e1, cu1, vu1, b0, e0)) break;
+    t += kSliceWaves;
+    if (!piece(b1, e1, cu1, vu1, b0, e0, cu0, vu0, b1, e1)) break;
+    t += kSliceWaves;
+  }
+}
+
+// Large rows, one slice of kSliceCols columns per part (workgroups part * K + k): the slice of x is
+// staged in LDS and the pieces gather from it. An entry outside the slice (possible with an inexact
+// cut) reads x from global memory.
+//
+// Three pieces are in flight per wave: while piece t is summed, the first blocks of pieces t + 16
+// and t + 32 are loading. Vector loads and stores complete out of order with each other, so a
+// store among the loads would make the compiler wait for all of them; the piece sums therefore
+// collect in a register (lane j: piece 64 g + j) and are stored 64 at a time. Every load of a block
+// is unconditional (lanes past a piece's end re-read its last entry, one address for all of them),
+// so the wait for a block counts exactly the loads issued after it. The cuts come 64 pieces at a
+// time, one vector load per side, read with readlane: no scalar loads in the loop, whose
+// out-of-order returns would make every wait for the LDS gathers a full lgkmcnt(0).
+// Against the two-deep loop with per-piece stores: 100.2 against 110.2 us at config 5, bit-identical.
+constexpr int kSliceUnroll = 4;   // strides per block
 __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__restrict__ col,
                                                             const float *__restrict__ val,
                                                             const float *__restrict__ x, int32_t cols,
                                                             const int32_t *__restrict__ cuts, int cut_stride,
                                                             float *__restrict__ parts, int part_stride,
                                                             const int32_t *__restrict__ count, int capacity) {
-  __shared__ float sx[kLds ? kSliceCols : 1];
+  constexpr int kU = kSliceUnroll;
+  __shared__ float sx[kSliceCols];
   const int tid = threadIdx.x, lane = tid & 63;
-  // Wave-uniform in a scalar register, so the cuts below are scalar loads (counted by lgkmcnt):
-  // a vector load of them, waited with vmcnt, also waits for the prefetched strides.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = static_cast<int>(gridDim.x) / part_stride;
-  // Slices: workgroups part * K + k. Windows: part = h % 8, so window w's pieces run on XCD w.
-  const int part = kLds ? static_cast<int>(blockIdx.x) / K : static_cast<int>(blockIdx.x % part_stride);
-  const int k = kLds ? static_cast<int>(blockIdx.x) % K : static_cast<int>(blockIdx.x / part_stride);
+  const int part = static_cast<int>(blockIdx.x) / K;
+  const int k = static_cast<int>(blockIdx.x) % K;
   const int n_rows = min(*count, capacity);
   if (n_rows <= k) return;   // workgroup-uniform
-  const int64_t c0 = kLds ? static_cast<int64_t>(part) * kSliceCols : 0;
-  const int width = kLds ? static_cast<int>(min(static_cast<int64_t>(kSliceCols), cols - c0)) : 0;
-  if constexpr (kLds) {
+  const int64_t c0 = static_cast<int64_t>(part) * kSliceCols;
+  const int width = static_cast<int>(min(static_cast<int64_t>(kSliceCols), cols - c0));
+  {
     constexpr int kPer = kSliceCols / kSliceThreads;
     float staged[kPer];
 #pragma unroll
@@ -460,103 +552,108 @@ __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__re
 #pragma unroll
     for (int q = 0; q < kPer; ++q) sx[tid + kSliceThreads * q] = staged[q];
   }
-  if constexpr (kLds) __syncthreads();
+  __syncthreads();
   const int n_tile = (n_rows - k + K - 1) / K;
-  auto cut_at = [&](int t, int side) {
-    return __builtin_amdgcn_readfirstlane(cuts[(k + static_cast<int64_t>(K) * t) * cut_stride + part + side]);
+  if (wave >= n_tile) return;   // wave-uniform
+
+  // This wave's pieces i = 0 .. n_pieces - 1 are t = wave + 16 i. Their cuts come 64 at a time
+  // (lane j holds those of piece 64 g + j); a piece past the wave's last is empty, at the last
+  // piece's end (a valid position, so its loads stay in bounds).
+  const int n_pieces = (n_tile - wave + kSliceWaves - 1) / kSliceWaves;
+  int32_t lane_b = 0, lane_e = 0, group = -1;
+  auto cuts_of = [&](int i, int32_t &b, int32_t &e) {
+    if ((i >> 6) != group) {   // wave-uniform; once per 64 pieces
+      group = i >> 6;
+      const int t = wave + kSliceWaves * (64 * group + lane);
+      const int64_t at = (k + static_cast<int64_t>(K) * min(t, n_tile - 1)) * cut_stride + part;
+      const int32_t lb = cuts[at], le = cuts[at + 1];
+      lane_b = t < n_tile ? lb : le;
+      lane_e = le;
+    }
+    b = __builtin_amdgcn_readlane(lane_b, i & 63);
+    e = __builtin_amdgcn_readlane(lane_e, i & 63);
   };
-  // kUnroll strides of a piece [p0, e). With kLds they load raw: every lane loads (lanes past the end
-  // re-read the piece's last entry, or entry 0 of an empty piece), and add_block masks them where it
-  // uses them. Masked here with a select, hipcc put each load behind a branch on the lane mask, or
-  // placed the masking right after the loads; either way the compiler waited for every load in
-  // flight (vmcnt 0), the next piece's prefetched strides included, before the first gather
-  // (large rows 117 against 104 us). The medium rows' short pieces keep the select, so lanes past
-  // the end load nothing (92 against 98 us).
-  auto load_block = [&](int32_t p0, int32_t e, int32_t (&cu)[kUnroll], float (&vu)[kUnroll]) {
+  float sums = 0.0f;
+  auto store_sums = [&](int g) {   // the pieces 64 g + lane that exist
+    const int t = wave + kSliceWaves * (64 * g + lane);
+    if (t < n_tile) parts[(k + static_cast<int64_t>(K) * t) * part_stride + part] = sums;
+  };
+  // The block of [p0, e): every lane loads; lanes past the end re-read entry e - 1 (entry 0 of an
+  // empty piece at 0). add_block masks them where it uses them.
+  auto load_block = [&](int32_t p0, int32_t e, int32_t (&cu)[kU], float (&vu)[kU]) {
     const int32_t last = e > 0 ? e - 1 : 0;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const int32_t p = p0 + 64 * u + lane;
-      if constexpr (kLds) {
-        const int32_t at = p < e ? p : last;
-        cu[u] = __builtin_nontemporal_load(col + at);
-        vu[u] = __builtin_nontemporal_load(val + at);
-      } else {   // short pieces: lanes past the end load nothing
-        cu[u] = p < e ? __builtin_nontemporal_load(col + p) : 0;
-        vu[u] = p < e ? __builtin_nontemporal_load(val + p) : 0.0f;
-      }
+      const int32_t at = p < e ? p : last;
+      cu[u] = __builtin_nontemporal_load(col + at);
+      vu[u] = __builtin_nontemporal_load(val + at);
     }
   };
-  // Products of the block loaded for [p0, e) into acc; with kLds, those of entries outside the slice
-  // (possible with an inexact cut) go to `stray`, read from global x. The LDS and global reads stay
-  // separate: written as one select of an LDS and a global load, hipcc merged them into a generic
-  // flat load, which sent every gather through the vector memory path (125 against 117 us).
-  auto add_block = [&](int32_t p0, int32_t e, const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], float &acc,
+  // Products of the block of [p0, e) into acc; those of entries outside the slice go to `stray`,
+  // read from global x. Masked lanes leave the sums as they were (a select after the FMA):
+  // multiplying their stand-in x by zero would turn an inf or NaN elsewhere in x into a NaN here.
+  // The LDS and global reads stay separate: written as one select of an LDS and a global load,
+  // hipcc merged them into a generic flat load, which sent every gather through the vector memory
+  // path.
+  auto add_block = [&](int32_t p0, int32_t e, const int32_t (&cu)[kU], const float (&vu)[kU], float &acc,
                        float &stray) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      // Masked lanes leave the sums as they were (a select after the FMA): multiplying their
-      // stand-in x by zero would turn an inf or NaN elsewhere in x into a NaN here.
+    for (int u = 0; u < kU; ++u) {
       const bool ok = p0 + 64 * u + lane < e;
-      if constexpr (kLds) {
-        const int32_t local = cu[u] - static_cast<int32_t>(c0);
-        const bool in = !ok || static_cast<uint32_t>(local) < static_cast<uint32_t>(width);
-        const float xl = sx[ok && in ? local : 0];
-        const float sum = fmaf(vu[u], xl, acc);
-        acc = ok && in ? sum : acc;   // an entry outside the slice adds into stray only
-        if (__builtin_expect(__any(!in), 0)) {   // wave-uniform
-          if (!in) stray = fmaf(vu[u], __builtin_nontemporal_load(x + clamp_col(cu[u], cols)), stray);
-        }
-      } else {
-        const float sum = fmaf(vu[u], x[clamp_col(ok ? cu[u] : 0, cols)], acc);
-        acc = ok ? sum : acc;
+      const int32_t local = cu[u] - static_cast<int32_t>(c0);
+      const bool in = !ok || static_cast<uint32_t>(local) < static_cast<uint32_t>(width);
+      const float xl = sx[ok && in ? local : 0];
+      const float sum = fmaf(vu[u], xl, acc);
+      acc = ok && in ? sum : acc;   // an entry outside the slice adds into stray only
+      if (__builtin_expect(__any(!in), 0)) {   // wave-uniform
+        if (!in) stray = fmaf(vu[u], __builtin_nontemporal_load(x + clamp_col(cu[u], cols)), stray);
       }
     }
   };
-  // This wave's pieces t = wave + 16 i. Two register sets alternate: while piece t is summed from
-  // one, the next piece's first strides load into the other, and the cuts of the piece after next
-  // load (scalar). The loop is unrolled by two so that no set is ever copied into the other, which
-  // would wait for the loads in flight.
-  int t = wave;
-  if (t >= n_tile) return;
-  int32_t b0 = cut_at(t, 0), e0 = cut_at(t, 1);
-  int32_t b1 = 0, e1 = 0;
-  if (t + kSliceWaves < n_tile) { b1 = cut_at(t + kSliceWaves, 0); e1 = cut_at(t + kSliceWaves, 1); }
-  int32_t cu0[kUnroll], cu1[kUnroll];
-  float vu0[kUnroll], vu1[kUnroll];
-  load_block(b0, e0, cu0, vu0);
-  // Piece t: [b, e) summed from (cu, vu). Before that, the next piece's block [nb, ne) starts loading
-  // into (ncu, nvu), and the cuts of piece t + 32 into (fb, fe). Returns whether a next piece exists.
-  auto piece = [&](int32_t b, int32_t e, const int32_t (&cu)[kUnroll], const float (&vu)[kUnroll], int32_t nb,
-                   int32_t ne, int32_t (&ncu)[kUnroll], float (&nvu)[kUnroll], int32_t &fb, int32_t &fe) {
-    const bool more = t + kSliceWaves < n_tile;   // wave-uniform
-    if (more) load_block(nb, ne, ncu, nvu);
-    if (t + 2 * kSliceWaves < n_tile) {
-      fb = cut_at(t + 2 * kSliceWaves, 0);
-      fe = cut_at(t + 2 * kSliceWaves, 1);
+  // Piece i from set (b, e, cu, vu); the block of piece i + 2 loads into set (fb, fe, fcu, fvu).
+  auto piece = [&](int i, int32_t b, int32_t e, const int32_t (&cu)[kU], const float (&vu)[kU], int32_t &fb,
+                   int32_t &fe, int32_t (&fcu)[kU], float (&fvu)[kU]) {
+    if ((i & 63) == 0 && i > 0) {   // wave-uniform; once per 64 pieces
+      store_sums((i >> 6) - 1);
+      sums = 0.0f;
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));   // vmcnt(0): the store out of the way
     }
+    cuts_of(i + 2, fb, fe);
+    load_block(fb, fe, fcu, fvu);
+    // Nothing that waits for this piece's data moves above the loads of piece i + 2.
+    __builtin_amdgcn_sched_barrier(0);
     float acc = 0.0f, stray = 0.0f;
     add_block(b, e, cu, vu, acc, stray);
-    for (int32_t p0 = b + 64 * kUnroll; p0 < e; p0 += 64 * kUnroll) {   // wave-uniform: rest of the piece
-      int32_t cr[kUnroll];
-      float vr[kUnroll];
+    for (int32_t p0 = b + 64 * kU; p0 < e; p0 += 64 * kU) {   // wave-uniform: rest of the piece
+      int32_t cr[kU];
+      float vr[kU];
       load_block(p0, e, cr, vr);
       add_block(p0, e, cr, vr, acc, stray);
     }
     const float sum = wave_sum(acc + stray);
-    if (lane == 0) parts[(k + static_cast<int64_t>(K) * t) * part_stride + part] = sum;
-    return more;
+    sums = lane == (i & 63) ? sum : sums;
   };
-  while (true) {   // wave-uniform
-    // Piece t in set 0 (cuts b0, e0), piece t + 16 loading into set 1 (cuts b1, e1); the cuts of
-    // piece t + 32 replace b0, e0.
-    if (!piece(b0, e0, cu0, vu0, b1, e1, cu1, vu1, b0, e0)) break;
-    t += kSliceWaves;
-    // Piece t in set 1 (b1, e1), piece t + 16 loading into set 0 (b0, e0); piece t + 32's cuts
-    // replace b1, e1.
-    if (!piece(b1, e1, cu1, vu1, b0, e0, cu0, vu0, b1, e1)) break;
-    t += kSliceWaves;
+  int32_t b0, e0, b1, e1, b2 = 0, e2 = 0;
+  int32_t cu0[kU], cu1[kU], cu2[kU];
+  float vu0[kU], vu1[kU], vu2[kU];
+  // Issued in this order (the scheduler may not interleave them), so that the loop's first wait
+  // for piece 0's block leaves piece 1's in flight, as every later wait does.
+  cuts_of(0, b0, e0);
+  load_block(b0, e0, cu0, vu0);
+  __builtin_amdgcn_sched_barrier(0);
+  cuts_of(1, b1, e1);
+  load_block(b1, e1, cu1, vu1);
+  __builtin_amdgcn_sched_barrier(0);
+  // Three pieces per iteration (the last ones empty past the wave's end), so that the sets rotate
+  // without being copied (a copy waits for its loads) and no exit sits between them.
+  int i = 0;
+  for (; i < n_pieces; i += 3) {   // wave-uniform
+    piece(i, b0, e0, cu0, vu0, b2, e2, cu2, vu2);
+    piece(i + 1, b1, e1, cu1, vu1, b0, e0, cu0, vu0);
+    piece(i + 2, b2, e2, cu2, vu2, b1, e1, cu1, vu1);
   }
+  store_sums((i - 1) >> 6);
 }
 
 // y of every medium row (thread per row: windows 0..7 in order) and large row (wave per row: lane
@@ -589,7 +686,7 @@ __global__ __launch_bounds__(256) void spmv_combine(float *__restrict__ y, Plan 
 int spmv_resources(int64_t rows, int64_t nnz, IntentHipKernelResources *out) {
   (void)rows;
   (void)nnz;
-  return describe_kernel(reinterpret_cast<const void *>(&spmv_slices<true>), "spmv_slices<true>", kSliceThreads, out);
+  return describe_kernel(reinterpret_cast<const void *>(&spmv_slices), "spmv_slices", kSliceThreads, out);
 }
 
 }  // namespace intent_hip
@@ -630,12 +727,12 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   spmv_bounds<<<dim3(static_cast<unsigned>(bounds_blocks)), dim3(256), 0, s>>>(row_offsets, column_indices, c32, nnz,
                                                                               plan);
   if (plan.cap_mid > 0)
-    spmv_slices<false><<<dim3(kWindows * kWindowTiles), dim3(kSliceThreads), 0, s>>>(
+    spmv_windows<<<dim3(kWindows * kWindowTiles), dim3(kSliceThreads), 0, s>>>(
         column_indices, values, x, c32, plan.mid_cuts, kWindows + 1, plan.mid_parts, kWindows, plan.counters + 0,
         plan.cap_mid);
   if (plan.cap_big > 0) {
     const int K = static_cast<int>((kSliceTiles + plan.slices - 1) / plan.slices);
-    spmv_slices<true><<<dim3(static_cast<unsigned>(plan.slices) * static_cast<unsigned>(K)), dim3(kSliceThreads), 0,
+    spmv_slices<<<dim3(static_cast<unsigned>(plan.slices) * static_cast<unsigned>(K)), dim3(kSliceThreads), 0,
                   s>>>(column_indices, values, x, c32, plan.big_cuts, plan.slices + 1, plan.big_parts,
                        plan.slices, plan.counters + 1, plan.cap_big);
   }
