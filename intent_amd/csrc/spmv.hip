@@ -25,10 +25,10 @@
 // The medium and large row lists are built without atomics: spmv_count counts each 1024-row
 // block's rows of each class, spmv_scan (one workgroup) turns the counts into list offsets, and
 // spmv_rows writes each block's rows at its offset in row order. (Wave-level atomics on two list
-// counters cost 115 us at config 5.) spmv_bounds estimates each cut by interpolation search and
-// makes the cuts of a row non-decreasing with a prefix maximum, so the pieces partition the row
-// for any estimate and any column order; an entry outside its window or slice only reads x from
-// another place. spmv_combine adds the pieces of each medium or large row in window or slice order.
+// counters cost 115 us at config 5.) The cut workgroups of spmv_rows estimate each cut by
+// interpolation search and make the cuts of a row non-decreasing with a prefix maximum, so the
+// pieces partition the row for any estimate and any column order; an entry outside its window or
+// slice only reads x from another place. spmv_combine adds the pieces of each medium or large row in window or slice order.
 #include <mutex>
 
 #include "common.hpp"
@@ -210,13 +210,13 @@ __global__ __launch_bounds__(1024) void spmv_scan(Plan plan) {
 // folded by their lane (the loads of the thread's four rows issued together); rows of 5..127 by a
 // 16-lane group (four rows per wave at a time); medium and large rows are written to their lists
 // at the block's scanned offset, in row order.
-__global__ __launch_bounds__(256) void spmv_rows(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
-                                                 const float *__restrict__ val, const float *__restrict__ x,
-                                                 float *__restrict__ y, int32_t rows, int32_t cols, int64_t nnz,
-                                                 Plan plan) {
+__device__ __forceinline__ void rows_block(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
+                                           const float *__restrict__ val, const float *__restrict__ x,
+                                           float *__restrict__ y, int32_t rows, int32_t cols, int64_t nnz, Plan plan,
+                                           int block) {
   __shared__ int s_wave[2][4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kBlockRows;
+  const int64_t base = static_cast<int64_t>(block) * kBlockRows;
   int32_t begin[kRowsPerThread], length[kRowsPerThread];
 #pragma unroll
   for (int k = 0; k < kRowsPerThread; ++k) {
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(256) void spmv_rows(const int32_t *__restrict__ off
     }
   }
   // Lists: rank of each medium / large row within the block, in row order (k, then thread).
-  int first[2] = {plan.block_first[2 * blockIdx.x], plan.block_first[2 * blockIdx.x + 1]};
+  int first[2] = {plan.block_first[2 * block], plan.block_first[2 * block + 1]};
 #pragma unroll
   for (int k = 0; k < kRowsPerThread; ++k) {
     const bool is_mid = length[k] >= kGroupRow && length[k] < plan.big;
@@ -332,24 +332,26 @@ __device__ __forceinline__ void cut_row(const int32_t *__restrict__ col, int32_t
                                         int32_t *__restrict__ out) {
   int32_t carry = begin;   // running maximum of the cuts of earlier rounds
   for (int u0 = 0; u0 < rounds; u0 += 4) {
-    int32_t lo[4], hi[4];
-    int64_t thr[4], vlo[4], vhi[4];
+    // Thresholds at or past `cols` give the row end, so they are kept clamped to cols (32 bits);
+    // the interpolation product needs 64.
+    int32_t lo[4], hi[4], thr[4], vlo[4], vhi[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int k = gl + G * (u0 + u);
-      thr[u] = static_cast<int64_t>(k) * spacing;
+      const int64_t t = static_cast<int64_t>(k) * spacing;
+      thr[u] = static_cast<int32_t>(t < cols ? t : cols);
       lo[u] = begin;
       hi[u] = end;
       vlo[u] = -1;
       vhi[u] = cols;
-      if (k == 0 || thr[u] >= cols) lo[u] = hi[u] = k == 0 ? begin : end;
+      if (k == 0 || t >= cols) lo[u] = hi[u] = k == 0 ? begin : end;
     }
     for (int step = 0; step < kSearchSteps; ++step) {
       int32_t at[4], cv[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t span = hi[u] - lo[u] + 1, rise = vhi[u] - vlo[u];
-        int64_t guess = lo[u] - 1 + ((thr[u] - vlo[u]) * span + rise / 2) / (rise > 0 ? rise : 1);
+        const int64_t span = hi[u] - lo[u] + 1, rise = static_cast<int64_t>(vhi[u]) - vlo[u];
+        int64_t guess = lo[u] - 1 + ((static_cast<int64_t>(thr[u]) - vlo[u]) * span + rise / 2) / (rise > 0 ? rise : 1);
         guess = guess < lo[u] ? lo[u] : (guess > hi[u] - 1 ? hi[u] - 1 : guess);
         at[u] = static_cast<int32_t>(guess);
         cv[u] = lo[u] < hi[u] ? col[at[u]] : 0;
@@ -358,7 +360,7 @@ __device__ __forceinline__ void cut_row(const int32_t *__restrict__ col, int32_t
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if (lo[u] < hi[u]) {
-          if (static_cast<int64_t>(cv[u]) < thr[u]) {
+          if (cv[u] < thr[u]) {
             lo[u] = at[u] + 1;
             vlo[u] = cv[u];
           } else {
@@ -386,36 +388,72 @@ __device__ __forceinline__ void cut_row(const int32_t *__restrict__ col, int32_t
   }
 }
 
-// Cuts of the listed rows. Jobs, one per wave: job j < n_big is large row j (one wave, slices + 1
-// cuts); job n_big + q is medium rows 8q..8q+7 (one 8-lane group per row, 9 cuts: the starts of
-// windows 0..8). The launch holds as many waves as the device keeps resident, so a wave takes a
-// second job only when the jobs outnumber them (at config 5 there are 2092 + 2375 jobs). With
-// every wave taking a large row and then medium rows in 16-lane groups, the chains of dependent
-// probes ran back to back in the first waves (whole SpMV 435.2 against 429.1 us, interleaved).
+// Cuts of the medium and large rows of one 1024-row block, by one wave: the block's rows are
+// classified again (as spmv_count did) and ranked in row order, which gives each its list position
+// from the scanned block offsets, the position spmv_rows writes the row id at. Medium rows go eight
+// at a time, one 8-lane group per row (9 cuts: the starts of windows 0..8); large rows one at a
+// time, the whole wave (slices + 1 cuts). `list` is the wave's LDS scratch for the block's rows.
 constexpr int kMidGroup = 8;
-__global__ __launch_bounds__(256) void spmv_bounds(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
-                                                   int32_t cols, int64_t nnz, Plan plan) {
-  const int lane = threadIdx.x & 63;
-  const int64_t n_mid = min(plan.counters[0], plan.cap_mid), n_big = min(plan.counters[1], plan.cap_big);
-  const int64_t n_jobs = n_big + (n_mid + kMidGroup - 1) / kMidGroup;
-  const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
-  const int big_cuts = plan.slices + 1;
+__device__ __forceinline__ void cut_block(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
+                                          int32_t rows, int32_t cols, int64_t nnz, const Plan &plan, int block,
+                                          int lane, int32_t *list) {
+  const int64_t base = static_cast<int64_t>(block) * kBlockRows;
+  // Medium rows at list[0 ..), large rows at list[kBlockRows - 1] downwards, in row order.
+  int n_mid = 0, n_big = 0;
+  for (int k = 0; k < kBlockRows / 64; ++k) {
+    const int64_t r = base + 64 * k + lane;
+    int32_t b = 0, e = 0;
+    if (r < rows) row_span(off, r, nnz, b, e);
+    const int32_t len = r < rows ? e - b : 0;
+    const bool is_mid = len >= kGroupRow && len < plan.big, is_big = len >= plan.big;
+    const uint64_t m_mid = __ballot(is_mid), m_big = __ballot(is_big);
+    const uint64_t below = (1ull << lane) - 1;
+    if (is_mid) list[n_mid + __builtin_popcountll(m_mid & below)] = 64 * k + lane;
+    if (is_big) list[kBlockRows - 1 - n_big - __builtin_popcountll(m_big & below)] = 64 * k + lane;
+    n_mid += __builtin_popcountll(m_mid);
+    n_big += __builtin_popcountll(m_big);
+  }
+  __builtin_amdgcn_wave_barrier();
+  const int first_mid = plan.block_first[2 * block], first_big = plan.block_first[2 * block + 1];
   const int64_t window = (static_cast<int64_t>(cols) + kWindows - 1) / kWindows;
   const int g = lane / kMidGroup;
-  for (int64_t j = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); j < n_jobs; j += waves) {
-    if (j < n_big) {   // wave-uniform
-      int32_t b, e;
-      row_span(off, plan.big_rows[j], nnz, b, e);
-      cut_row<64>(col, b, e, big_cuts, (big_cuts + 63) / 64, kSliceCols, cols, lane, 0, plan.big_cuts + j * big_cuts);
-    } else {
-      const int64_t i = (j - n_big) * kMidGroup + g;
-      const bool ok = i < n_mid;
-      int32_t b = 0, e = 0;
-      if (ok) row_span(off, plan.mid_rows[i], nnz, b, e);
-      cut_row<kMidGroup>(col, b, e, ok ? kWindows + 1 : 0, (kWindows + 1 + kMidGroup - 1) / kMidGroup, window, cols,
-                         lane % kMidGroup, g * kMidGroup, plan.mid_cuts + (ok ? i : 0) * (kWindows + 1));
-    }
+  for (int q = 0; q < n_mid; q += 64 / kMidGroup) {   // wave-uniform
+    const int i = q + g;
+    const int at = first_mid + i;
+    const bool ok = i < n_mid && at < plan.cap_mid;
+    int32_t b = 0, e = 0;
+    if (ok) row_span(off, base + list[i], nnz, b, e);
+    cut_row<kMidGroup>(col, b, e, ok ? kWindows + 1 : 0, (kWindows + 1 + kMidGroup - 1) / kMidGroup, window, cols,
+                       lane % kMidGroup, g * kMidGroup, plan.mid_cuts + static_cast<int64_t>(ok ? at : 0) * (kWindows + 1));
   }
+  const int big_cuts = plan.slices + 1;
+  for (int i = 0; i < n_big; ++i) {   // wave-uniform
+    const int at = first_big + i;
+    if (at >= plan.cap_big) break;
+    int32_t b, e;
+    row_span(off, base + list[kBlockRows - 1 - i], nnz, b, e);
+    cut_row<64>(col, b, e, big_cuts, (big_cuts + 63) / 64, kSliceCols, cols, lane, 0,
+                plan.big_cuts + static_cast<int64_t>(at) * big_cuts);
+  }
+}
+
+// Short rows, row lists and cuts in one launch. The first cut_groups workgroups compute the cuts
+// (one wave per 1024-row block), the rest fold the short rows and write the lists (one workgroup
+// per block). The cuts are chains of dependent probes, the short rows are bound by the fabric's
+// random line fetches; in one grid the cut chains run beside the short rows instead of after them
+// (config 5: 165 us for both, against 140 + 52 us as two launches).
+__global__ __launch_bounds__(256) void spmv_rows(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
+                                                    const float *__restrict__ val, const float *__restrict__ x,
+                                                    float *__restrict__ y, int32_t rows, int32_t cols, int64_t nnz,
+                                                    Plan plan, int cut_groups) {
+  __shared__ int32_t s_list[4][kBlockRows];
+  if (static_cast<int>(blockIdx.x) < cut_groups) {   // workgroup-uniform
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int block = static_cast<int>(blockIdx.x) * 4 + wave;
+    if (block < plan.blocks) cut_block(off, col, rows, cols, nnz, plan, block, lane, s_list[wave]);
+    return;
+  }
+  rows_block(off, col, val, x, y, rows, cols, nnz, plan, static_cast<int>(blockIdx.x) - cut_groups);
 }
 
 // Pieces of listed rows. Wave w of a workgroup takes the pieces of list rows i = k + K t for
@@ -720,12 +758,12 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   const dim3 row_grid(static_cast<unsigned>(plan.blocks));
   spmv_count<<<row_grid, dim3(256), 0, s>>>(row_offsets, r32, nnz, plan);
   spmv_scan<<<1, 1024, 0, s>>>(plan);
-  spmv_rows<<<row_grid, dim3(256), 0, s>>>(row_offsets, column_indices, values, x, y, r32, c32, nnz, plan);
+  // No row can be medium or large: no cut workgroups.
+  const int cut_groups = plan.cap_mid == 0 && plan.cap_big == 0 ? 0 : (plan.blocks + 3) / 4;
+  spmv_rows<<<dim3(static_cast<unsigned>(plan.blocks + cut_groups)), dim3(256), 0, s>>>(
+      row_offsets, column_indices, values, x, y, r32, c32, nnz, plan, cut_groups);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_rows");
   if (plan.cap_mid == 0 && plan.cap_big == 0) return INTENT_HIP_OK;   // no row can be medium or large
-  const int bounds_blocks = resident_blocks(reinterpret_cast<const void *>(&spmv_bounds), 256);
-  spmv_bounds<<<dim3(static_cast<unsigned>(bounds_blocks)), dim3(256), 0, s>>>(row_offsets, column_indices, c32, nnz,
-                                                                              plan);
   if (plan.cap_mid > 0)
     spmv_windows<<<dim3(kWindows * kWindowTiles), dim3(kSliceThreads), 0, s>>>(
         column_indices, values, x, c32, plan.mid_cuts, kWindows + 1, plan.mid_parts, kWindows, plan.counters + 0,
