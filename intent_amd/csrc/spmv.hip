@@ -398,20 +398,32 @@ __device__ __forceinline__ void cut_block(const int32_t *__restrict__ off, const
                                           int32_t rows, int32_t cols, int64_t nnz, const Plan &plan, int block,
                                           int lane, int32_t *list) {
   const int64_t base = static_cast<int64_t>(block) * kBlockRows;
-  // Medium rows at list[0 ..), large rows at list[kBlockRows - 1] downwards, in row order.
+  // Medium rows at list[0 ..), large rows at list[kBlockRows - 1] downwards, in row order. The
+  // offsets are read 256 rows (4 per lane) at a time, all loads of a batch issued together (rows
+  // past the end read the last row's).
+  constexpr int kBatch = 4;
   int n_mid = 0, n_big = 0;
-  for (int k = 0; k < kBlockRows / 64; ++k) {
-    const int64_t r = base + 64 * k + lane;
-    int32_t b = 0, e = 0;
-    if (r < rows) row_span(off, r, nnz, b, e);
-    const int32_t len = r < rows ? e - b : 0;
-    const bool is_mid = len >= kGroupRow && len < plan.big, is_big = len >= plan.big;
-    const uint64_t m_mid = __ballot(is_mid), m_big = __ballot(is_big);
-    const uint64_t below = (1ull << lane) - 1;
-    if (is_mid) list[n_mid + __builtin_popcountll(m_mid & below)] = 64 * k + lane;
-    if (is_big) list[kBlockRows - 1 - n_big - __builtin_popcountll(m_big & below)] = 64 * k + lane;
-    n_mid += __builtin_popcountll(m_mid);
-    n_big += __builtin_popcountll(m_big);
+  for (int k0 = 0; k0 < kBlockRows / 64; k0 += kBatch) {
+    int32_t ob[kBatch], oe[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t r = min(base + 64 * (k0 + k) + lane, static_cast<int64_t>(rows) - 1);
+      ob[k] = off[r];
+      oe[k] = off[r + 1];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t cb = ob[k] < 0 ? 0 : (ob[k] > nnz ? nnz : static_cast<int64_t>(ob[k]));   // row_span's clamps
+      const int64_t ce = oe[k] < cb ? cb : (oe[k] > nnz ? nnz : static_cast<int64_t>(oe[k]));
+      const int64_t len = base + 64 * (k0 + k) + lane < rows ? ce - cb : 0;
+      const bool is_mid = len >= kGroupRow && len < plan.big, is_big = len >= plan.big;
+      const uint64_t m_mid = __ballot(is_mid), m_big = __ballot(is_big);
+      const uint64_t below = (1ull << lane) - 1;
+      if (is_mid) list[n_mid + __builtin_popcountll(m_mid & below)] = 64 * (k0 + k) + lane;
+      if (is_big) list[kBlockRows - 1 - n_big - __builtin_popcountll(m_big & below)] = 64 * (k0 + k) + lane;
+      n_mid += __builtin_popcountll(m_mid);
+      n_big += __builtin_popcountll(m_big);
+    }
   }
   __builtin_amdgcn_wave_barrier();
   const int first_mid = plan.block_first[2 * block], first_big = plan.block_first[2 * block + 1];
