@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define INTENT_HIP_ABI_VERSION 16
+#define INTENT_HIP_ABI_VERSION 17
 
 enum IntentHipStatus {
   INTENT_HIP_OK = 0,
@@ -185,6 +185,22 @@ int intent_hip_attention_fwd(int dtype, const void *q, const void *k, const void
                              int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
                              int64_t sk, int64_t d, int64_t dv, const int64_t strides[16],
                              float scale, int causal, void *stream);
+
+/* intent_hip_attention_fwd with a key split for small grids, the same three definitions (no
+ * counterpart call in the reference: its Triton launch has no workspace; the split changes only the
+ * association of the f32 merge of chunk summaries, merge_attention_summaries :82-114). When the
+ * grid of 256-query blocks holds fewer than 256 workgroups, each block's key tiles are divided over
+ * up to 8 workgroups, each writing its unnormalised state (maximum, denominator, O) to `workspace`,
+ * and a second kernel merges the splits in order with exp2 factors. The workspace must hold
+ * intent_hip_attention_fwd_workspace_bytes (0: nothing to split) and be 256-byte aligned; with a
+ * null or smaller workspace the launch is unsplit, as intent_hip_attention_fwd. */
+int intent_hip_attention_fwd_workspace_bytes(int64_t batch, int64_t q_heads, int64_t sq, int64_t sk,
+                                             int64_t dv, size_t *bytes);
+int intent_hip_attention_fwd_ws(int dtype, const void *q, const void *k, const void *v, void *o,
+                                int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
+                                int64_t sk, int64_t d, int64_t dv, const int64_t strides[16],
+                                float scale, int causal, void *workspace, size_t workspace_bytes,
+                                void *stream);
 
 /* Latent attention prefill: mla_prefill (streaming/attention.py:756-798, scores of
  * summarize_mla_chunk :368-415): s = (q . k + qpe . kpe) scale log2 e with the causal rule

@@ -589,9 +589,9 @@ __global__ __launch_bounds__(1024) void attention_varlen_items(const int32_t *__
 
 // The kernel of a (dtype, d, dv, packed) choice; d and dv are each 64 or 128 (checked by the callers).
 // The key splits of one query row merged as merge_attention_summaries does (exp2 factors against
-// the largest maximum), normalised by an approximate reciprocal and stored in f16; a row with no
-// admitted key in any split is 0. One wave per row; lanes own DV / 64 columns each.
-template <int DV>
+// the largest maximum), normalised by an approximate reciprocal and stored in the element type E;
+// a row with no admitted key in any split is 0. One wave per row; lanes own DV / 64 columns each.
+template <typename E, int DV>
 __global__ __launch_bounds__(64) void attention_split_merge(const float *__restrict__ m, const float *__restrict__ den,
                                                             const float *__restrict__ acc, int splits, int heads, int sq,
                                                             uint16_t *__restrict__ O, int64_t os_b, int64_t os_h,
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(64) void attention_split_merge(const float *__restr
   uint16_t *orow = O + (bh / heads) * os_b + (bh % heads) * os_h + q * os_q;
 #pragma unroll
   for (int e = 0; e < kPer; ++e)
-    orow[lane + 64 * e] = __builtin_bit_cast(uint16_t, round_to<_Float16>(sum[e] * inv));
+    orow[lane + 64 * e] = __builtin_bit_cast(uint16_t, round_to<E>(sum[e] * inv));
 }
 
 template <typename E, int kMode>
@@ -677,28 +677,88 @@ template <int kMode>
 void launch_variant(int dtype, int64_t d, int64_t dv, dim3 grid, hipStream_t s, const uint16_t *Q, const uint16_t *K,
                     const uint16_t *V, uint16_t *O, int heads, int head_group, int sq, int sk, const Geometry &g,
                     float scale, int causal, int q_blocks, const Ragged &r,
-                    const KeyBias &kb = KeyBias{}) {
+                    const KeyBias &kb = KeyBias{}, const KeySplit &ks = KeySplit{1, nullptr, nullptr, nullptr}) {
   if (kMode != kBiased && dtype == INTENT_HIP_BF16) {
     if (d == 64)
-      dv == 64 ? launch_fwd<__bf16, 64, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
-               : launch_fwd<__bf16, 64, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
+      dv == 64 ? launch_fwd<__bf16, 64, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks)
+               : launch_fwd<__bf16, 64, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks);
     else
-      dv == 64 ? launch_fwd<__bf16, 128, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
-               : launch_fwd<__bf16, 128, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
+      dv == 64 ? launch_fwd<__bf16, 128, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks)
+               : launch_fwd<__bf16, 128, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks);
   } else {
     if (d == 64)
-      dv == 64 ? launch_fwd<_Float16, 64, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
-               : launch_fwd<_Float16, 64, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
+      dv == 64 ? launch_fwd<_Float16, 64, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks)
+               : launch_fwd<_Float16, 64, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks);
     else
-      dv == 64 ? launch_fwd<_Float16, 128, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb)
-               : launch_fwd<_Float16, 128, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb);
+      dv == 64 ? launch_fwd<_Float16, 128, 64, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks)
+               : launch_fwd<_Float16, 128, 128, kMode>(grid, s, Q, K, V, O, heads, head_group, sq, sk, g, scale, causal, q_blocks, r, kb, RopeRows{}, ks);
   }
 }
 
-// Batched attention; with kb, the key-biased form (f16, non-causal).
+// Key splits for a grid of `blocks` workgroups: 1 when the grid fills the 256 CUs or the keys are
+// fewer than 8 tiles, else enough to reach about 512 workgroups, at most 8 and at most half the key
+// tiles (two tiles per split). With fewer tiles the merge launch costs more than the split saves
+// (the reference streaming example, 4 tiles: 14.8 us split in two against 13.2 us unsplit).
+int64_t key_splits(int64_t blocks, int64_t sk) {
+  const int64_t tiles = (sk + kBK - 1) / kBK;
+  if (blocks <= 0 || blocks >= 256 || tiles < 8) return 1;
+  int64_t s = (512 + blocks - 1) / blocks;
+  s = s > 8 ? 8 : s;
+  s = s > tiles / 2 ? tiles / 2 : s;
+  return s < 1 ? 1 : s;
+}
+
+// Split state: maxima and denominators (each from a 256-byte boundary), then the sums.
+struct SplitLayout {
+  int64_t splits;
+  size_t den, acc, bytes;
+};
+SplitLayout split_layout(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t dv) {
+  const int64_t q_blocks = (sq + kBQ - 1) / kBQ;
+  const int64_t splits = key_splits(batch * heads * q_blocks, sk);
+  if (splits == 1) return SplitLayout{1, 0, 0, 0};
+  const size_t n = static_cast<size_t>(batch * heads * sq * splits);
+  const size_t part = (4 * n + 255) / 256 * 256;
+  return SplitLayout{splits, part, 2 * part, 2 * part + 4 * n * static_cast<size_t>(dv)};
+}
+
+// The split state of a launch, when the grid is small enough to split and the workspace holds it
+// (256-byte aligned); else a single split.
+KeySplit key_split(const SplitLayout &layout, void *workspace, size_t workspace_bytes) {
+  if (layout.splits <= 1 || workspace == nullptr || workspace_bytes < layout.bytes || !aligned(workspace, 256))
+    return KeySplit{1, nullptr, nullptr, nullptr};
+  char *ws = static_cast<char *>(workspace);
+  return KeySplit{static_cast<int>(layout.splits), reinterpret_cast<float *>(ws),
+                  reinterpret_cast<float *>(ws + layout.den), reinterpret_cast<float *>(ws + layout.acc)};
+}
+
+// attention_split_merge<E, dv> over every query row of a split launch.
+void launch_merge(int dtype, int64_t dv, const KeySplit &ks, int64_t rows, int heads, int sq, uint16_t *O,
+                  const Geometry &g, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(rows));
+  if (dtype == INTENT_HIP_BF16) {
+    if (dv == 128)
+      attention_split_merge<__bf16, 128><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
+                                                                   g.os[0], g.os[1], g.os[2]);
+    else
+      attention_split_merge<__bf16, 64><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
+                                                                  g.os[0], g.os[1], g.os[2]);
+  } else {
+    if (dv == 128)
+      attention_split_merge<_Float16, 128><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
+                                                                     g.os[0], g.os[1], g.os[2]);
+    else
+      attention_split_merge<_Float16, 64><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
+                                                                    g.os[0], g.os[1], g.os[2]);
+  }
+}
+
+// Batched attention; with kb, the key-biased form (f16, non-causal). A workspace of
+// split_layout(...).bytes lets a small batched grid split its keys (merged by a second launch).
 int launch_attention(int dtype, const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
                      int64_t head_group, int64_t sq, int64_t sk, int64_t d, int64_t dv, const int64_t *strides,
-                     float scale, int causal, void *stream, const KeyBias *kb = nullptr) {
+                     float scale, int causal, void *stream, const KeyBias *kb = nullptr, void *workspace = nullptr,
+                     size_t workspace_bytes = 0) {
   if (batch < 0 || heads < 0 || sq < 0 || sk < 0 || d < 0 || dv < 0)
     return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
   if (head_group < 1 || (heads > 0 && heads % head_group != 0))
@@ -729,7 +789,9 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   if (!aligned(q, 16) || (sk > 0 && (!aligned(k, 16) || !aligned(v, 16))) || !aligned(o, 8))
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention tensors must be 16-byte aligned");
   const int q_blocks = static_cast<int>((sq + kBQ - 1) / kBQ);
-  const int64_t blocks = batch * heads * q_blocks;
+  const KeySplit ks = kb == nullptr ? key_split(split_layout(batch, heads, sq, sk, dv), workspace, workspace_bytes)
+                                    : KeySplit{1, nullptr, nullptr, nullptr};
+  const int64_t blocks = batch * heads * q_blocks * ks.count;
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many attention workgroups");
   const auto *Qp = static_cast<const uint16_t *>(q);
   const auto *Kp = static_cast<const uint16_t *>(k);
@@ -742,8 +804,13 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   if (kb != nullptr)
     launch_variant<kBiased>(dtype, d, dv, grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks, Ragged{}, *kb);
   else
-    launch_variant<kBatched>(dtype, d, dv, grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks, Ragged{});
+    launch_variant<kBatched>(dtype, d, dv, grid, s, Qp, Kp, Vp, Op, h, grp, iq, ik, g, scale, c, q_blocks, Ragged{},
+                             KeyBias{}, ks);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd");
+  if (ks.count > 1) {
+    launch_merge(dtype, dv, ks, batch * heads * sq, h, iq, Op, g, s);
+    if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_split_merge");
+  }
   return INTENT_HIP_OK;
 }
 
@@ -761,6 +828,23 @@ extern "C" int intent_hip_attention_fwd(int dtype, const void *q, const void *k,
                                         void *stream) {
   return launch_attention(dtype, q, k, v, o, batch, q_heads, head_group, sq, sk, d, dv, strides, scale, causal,
                           stream);
+}
+
+extern "C" int intent_hip_attention_fwd_workspace_bytes(int64_t batch, int64_t q_heads, int64_t sq, int64_t sk,
+                                                        int64_t dv, size_t *bytes) {
+  if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
+  if (batch < 0 || q_heads < 0 || sq < 0 || sk < 0 || dv < 0)
+    return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "negative extent");
+  *bytes = split_layout(batch, q_heads, sq, sk, dv).bytes;
+  return INTENT_HIP_OK;
+}
+
+extern "C" int intent_hip_attention_fwd_ws(int dtype, const void *q, const void *k, const void *v, void *o,
+                                           int64_t batch, int64_t q_heads, int64_t head_group, int64_t sq,
+                                           int64_t sk, int64_t d, int64_t dv, const int64_t *strides, float scale,
+                                           int causal, void *workspace, size_t workspace_bytes, void *stream) {
+  return launch_attention(dtype, q, k, v, o, batch, q_heads, head_group, sq, sk, d, dv, strides, scale, causal,
+                          stream, nullptr, workspace, workspace_bytes);
 }
 
 extern "C" int intent_hip_attention_bias_fwd(const void *q, const void *k, const void *v, const float *bias, void *o,
@@ -853,35 +937,6 @@ extern "C" int intent_hip_attention_varlen_fwd(int dtype, const void *q, const v
 }
 
 // ---------------------------------------------------------------- latent attention
-namespace {
-
-// Key splits for a grid of `blocks` workgroups: 1 when the grid fills the 256 CUs, else enough to
-// reach about 512 workgroups, at most 8 and at most half the key tiles (two tiles per split).
-int64_t key_splits(int64_t blocks, int64_t sk) {
-  const int64_t tiles = (sk + kBK - 1) / kBK;
-  if (blocks <= 0 || blocks >= 256 || tiles < 4) return 1;
-  int64_t s = (512 + blocks - 1) / blocks;
-  s = s > 8 ? 8 : s;
-  s = s > tiles / 2 ? tiles / 2 : s;
-  return s < 1 ? 1 : s;
-}
-
-// Split state: maxima and denominators (each from a 256-byte boundary), then the sums.
-struct SplitLayout {
-  int64_t splits;
-  size_t den, acc, bytes;
-};
-SplitLayout split_layout(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t dv) {
-  const int64_t q_blocks = (sq + kBQ - 1) / kBQ;
-  const int64_t splits = key_splits(batch * heads * q_blocks, sk);
-  if (splits == 1) return SplitLayout{1, 0, 0, 0};
-  const size_t n = static_cast<size_t>(batch * heads * sq * splits);
-  const size_t part = (4 * n + 255) / 256 * 256;
-  return SplitLayout{splits, part, 2 * part, 2 * part + 4 * n * static_cast<size_t>(dv)};
-}
-
-}  // namespace
-
 extern "C" int intent_hip_mla_prefill_workspace_bytes(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t d,
                                                       size_t *bytes) {
   if (bytes == nullptr) return fail(INTENT_HIP_ERR_INVALID_ARGUMENT, "null output");
@@ -930,15 +985,7 @@ extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void
   const int q_blocks = static_cast<int>((sq + kBQ - 1) / kBQ);
   // A key split needs the workspace intent_hip_mla_prefill_workspace_bytes names; without it (or
   // when the grid fills the chip) the launch is unsplit.
-  const SplitLayout layout = split_layout(batch, heads, sq, sk, d);
-  const bool use_split = layout.splits > 1 && workspace != nullptr && workspace_bytes >= layout.bytes &&
-                         aligned(workspace, 256);
-  KeySplit ks{1, nullptr, nullptr, nullptr};
-  if (use_split) {
-    char *ws = static_cast<char *>(workspace);
-    ks = KeySplit{static_cast<int>(layout.splits), reinterpret_cast<float *>(ws), reinterpret_cast<float *>(ws + layout.den),
-                  reinterpret_cast<float *>(ws + layout.acc)};
-  }
+  const KeySplit ks = key_split(split_layout(batch, heads, sq, sk, d), workspace, workspace_bytes);
   const int64_t blocks = batch * heads * q_blocks * ks.count;
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many attention workgroups");
   const dim3 grid(static_cast<unsigned>(blocks));
@@ -957,13 +1004,7 @@ extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void
                                            KeyBias{}, rr, ks);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd (latent)");
   if (ks.count > 1) {
-    const dim3 rows(static_cast<unsigned>(batch * heads * sq));
-    if (d == 128)
-      attention_split_merge<128><<<rows, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, h, iq, Op, g.os[0], g.os[1],
-                                                            g.os[2]);
-    else
-      attention_split_merge<64><<<rows, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, h, iq, Op, g.os[0], g.os[1],
-                                                           g.os[2]);
+    launch_merge(INTENT_HIP_F16, d, ks, batch * heads * sq, h, iq, Op, g, s);
     if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_split_merge");
   }
   return INTENT_HIP_OK;

@@ -29,7 +29,8 @@ class NativeObservation:
 
 @dataclass(frozen=True, slots=True)
 class ConfigurationAssessment:
-    """One candidate of a prepared call; the hip provider has exactly one per binding."""
+    """One candidate configuration of a prepared call, with its eligibility and the reasons of an
+    ineligible one (the hip provider lists the rows of the definition's tuning family)."""
 
     configuration: tuple[tuple[str, object], ...]
     eligible: bool

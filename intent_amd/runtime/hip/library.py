@@ -11,7 +11,7 @@ from pathlib import Path
 
 from ...diagnostics import CompilationStageError
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 # INTENT_HIP_STATIC_SCRATCH_BYTES: the static scratch of intent_hip_csr_spmv_f32_static.
 STATIC_SCRATCH_BYTES = 32 << 20
 LIBRARY_NAME = "libintent_hip.so"
@@ -61,6 +61,9 @@ SIGNATURES = {
                                             ctypes.POINTER(_i64), _f32, _int, _p)),
     "intent_hip_attention_fwd": (_int, (_int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                         ctypes.POINTER(_i64), _f32, _int, _p)),
+    "intent_hip_attention_fwd_workspace_bytes": (_int, (_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz))),
+    "intent_hip_attention_fwd_ws": (_int, (_int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                           ctypes.POINTER(_i64), _f32, _int, _p, _sz, _p)),
     "intent_hip_mla_prefill_workspace_bytes": (_int, (_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_sz))),
     "intent_hip_mla_prefill": (_int, (_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                       ctypes.POINTER(_i64), _f32, _p, _sz, _p)),

@@ -157,7 +157,7 @@ def _split_choice(family: str, split_bytes: int) -> tuple[int, tuple]:
             if _static_workspace():
                 reasons.append("backend_options workspace='static' allows no workspace")
             if split_bytes <= 0:
-                reasons.append("the grid fills the device: there is nothing to split")
+                reasons.append("nothing to split: the grid fills the device or the walk is too short")
         candidates.append((row, not reasons, tuple(reasons)))
         if not reasons and chosen is None:
             chosen = row[0]
@@ -388,53 +388,67 @@ def _quantized_gemm(lib, bound, constexprs, device):
 
 
 # ------------------------------------------------------------------------------ attention
-def _attention_f16(lib, bound, constexprs, device):
+def _attention_launch(lib, dtype_code, q, k, v, o, scale, group, causal, entry, device):
+    """The batched attention forward (head_group query heads per key head). A grid too small to fill
+    the device splits each query block's keys over workgroups through a workspace (tuning family
+    hip.attention_forward; with workspace='static' or the unsplit row the launch stays unsplit)."""
     import ctypes
 
-    q, k, v, o, scale = bound.arguments
-    causal = bool(constexprs["CAUSAL"])
+    import torch
+
     keep, before, after = [q, k, v, o], [], []
     qk, kk, vk, ok, d, dv = _attention_views(q, k, v, o, keep, before, after)
-    batch, heads, sq = q.shape[:3]
+    batch, q_heads, sq = q.shape[:3]
     sk = k.shape[2]
     strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
     keep.append(strides)
-    fn = lib.fn["attention_fwd_f16"]
-    args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, heads, sq, sk, d, dv, strides,
-            float(scale), int(causal))
-    return Launch("intent_hip_attention_fwd_f16", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
-                  tuple(after), (("batch", batch), ("heads", heads), ("sq", sq), ("sk", sk), ("d", d), ("dv", dv),
-                                 ("causal", causal)),
-                  lambda: lib.kernel_resources(OP_ATTENTION_FWD_F16, F16, sq, d | (dv << 16)))
+    size = ctypes.c_size_t(0)
+    lib.check(lib.fn["attention_fwd_workspace_bytes"](batch, q_heads, sq, sk, dv, ctypes.byref(size)),
+              "provider_preparation")
+    split, candidates = _split_choice("hip.attention_forward", size.value)
+    config = (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq), ("sk", sk), ("d", d),
+              ("dv", dv), ("causal", causal), ("split", split))
+    resources = lambda: lib.kernel_resources(OP_ATTENTION_FWD, dtype_code, sq, d | (dv << 16))  # noqa: E731
+    if split:
+        workspace = torch.empty(size.value, dtype=torch.uint8, device=device)
+        keep.append(workspace)
+        fn = lib.fn["attention_fwd_ws"]
+        args = (dtype_code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, q_heads, group, sq,
+                sk, d, dv, strides, float(scale), int(causal), workspace.data_ptr(), size.value)
+        return Launch("intent_hip_attention_fwd_ws", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
+                      tuple(after), config, resources, candidates)
+    if entry == "intent_hip_attention_fwd_f16":
+        fn = lib.fn["attention_fwd_f16"]
+        args = (qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, q_heads, sq, sk, d, dv, strides,
+                float(scale), int(causal))
+    else:
+        fn = lib.fn["attention_fwd"]
+        args = (dtype_code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, q_heads, group, sq,
+                sk, d, dv, strides, float(scale), int(causal))
+    return Launch(entry, lambda stream: fn(*args, stream), tuple(keep), tuple(before), tuple(after), config,
+                  resources if entry != "intent_hip_attention_fwd_f16"
+                  else (lambda: lib.kernel_resources(OP_ATTENTION_FWD_F16, F16, sq, d | (dv << 16))), candidates)
+
+
+def _attention_f16(lib, bound, constexprs, device):
+    q, k, v, o, scale = bound.arguments
+    return _attention_launch(lib, F16, q, k, v, o, scale, 1, bool(constexprs["CAUSAL"]),
+                             "intent_hip_attention_fwd_f16", device)
 
 
 def _attention_grouped(dtype_code):
     """flash_gqa_attention_fwd (f16) / flash_attention_bf16_fwd (bf16): key head = query head //
     HEAD_GROUP (attention.py:485, 528)."""
     def plan(lib, bound, constexprs, device):
-        import ctypes
-
         q, k, v, o, scale = bound.arguments
-        causal = bool(constexprs["CAUSAL"])
         group = constexprs["HEAD_GROUP"]
         if isinstance(group, bool) or not isinstance(group, int) or group < 1:
             raise CompilationStageError("provider_configuration", f"HEAD_GROUP must be a positive int, got {group!r}")
-        batch, q_heads, sq, d = q.shape
-        if k.shape[1] * group != q_heads:
-            raise ValueError(f"query heads ({q_heads}) must equal key/value heads ({k.shape[1]}) * HEAD_GROUP "
+        if k.shape[1] * group != q.shape[1]:
+            raise ValueError(f"query heads ({q.shape[1]}) must equal key/value heads ({k.shape[1]}) * HEAD_GROUP "
                              f"({group})")
-        keep, before, after = [q, k, v, o], [], []
-        qk, kk, vk, ok, d, dv = _attention_views(q, k, v, o, keep, before, after)
-        sk = k.shape[2]
-        strides = (ctypes.c_int64 * 16)(*(s for t in (qk, kk, vk, ok) for s in t.stride()))
-        keep.append(strides)
-        fn = lib.fn["attention_fwd"]
-        args = (dtype_code, qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), batch, q_heads, group, sq,
-                sk, d, dv, strides, float(scale), int(causal))
-        return Launch("intent_hip_attention_fwd", lambda stream: fn(*args, stream), tuple(keep), tuple(before),
-                      tuple(after), (("batch", batch), ("q_heads", q_heads), ("head_group", group), ("sq", sq),
-                                     ("sk", sk), ("d", d), ("dv", dv), ("causal", causal)),
-                      lambda: lib.kernel_resources(OP_ATTENTION_FWD, dtype_code, sq, d | (dv << 16)))
+        return _attention_launch(lib, dtype_code, q, k, v, o, scale, group, bool(constexprs["CAUSAL"]),
+                                 "intent_hip_attention_fwd", device)
     return plan
 
 

@@ -19,6 +19,8 @@ Each family below lists exactly that; a row outside it is a `CompilationStageErr
                            unsplit kernels.
   hip.latent_prefill       mla_prefill. split = 1: a small grid splits each query block's keys over
                            workgroups and merges the split states; split = 0: unsplit.
+  hip.attention_forward    flash_attention_fwd, flash_gqa_attention_fwd, flash_attention_bf16_fwd:
+                           the same key split for the batched attention forward.
 
 A prepared call takes the first row, in table order, that is eligible for its arguments (split = 1
 is eligible when the grid is small enough to split and the workspace policy allows a workspace).
@@ -35,6 +37,7 @@ COLUMNS = ("split",)
 DEFAULT_FAMILIES = {
     "hip.attention_backward": ((1,), (0,)),
     "hip.latent_prefill": ((1,), (0,)),
+    "hip.attention_forward": ((1,), (0,)),
 }
 IMPLEMENTED = {family: frozenset(rows) for family, rows in DEFAULT_FAMILIES.items()}
 
@@ -43,6 +46,9 @@ FAMILY_OF = {
     "attention_backward_dq": "hip.attention_backward",
     "attention_backward_dkdv": "hip.attention_backward",
     "mla_prefill": "hip.latent_prefill",
+    "flash_attention_fwd": "hip.attention_forward",
+    "flash_gqa_attention_fwd": "hip.attention_forward",
+    "flash_attention_bf16_fwd": "hip.attention_forward",
 }
 
 

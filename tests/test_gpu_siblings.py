@@ -225,6 +225,74 @@ def test_reference_streaming_example_attention(device):
     assert (o[:, :, 0, :] == v[:, np.arange(8) // 4, 0, :]).all()
 
 
+@pytest.mark.parametrize("kind,shape,sk,group,causal", [
+    ("f16", (1, 4, 1024, 128), 1024, 1, True),      # 16 workgroups: 8 key splits
+    ("gqa", (1, 8, 640, 64), 640, 4, True),        # 24 workgroups: 5 splits
+    ("bf16", (1, 8, 768, 64), 768, 4, True),       # 24 workgroups: 6 splits
+    ("f16", (1, 2, 300, 128), 700, 1, False),      # non-causal, rectangular: 5 splits
+])
+def test_attention_key_split_matches_oracle(device, tmp_path, kind, shape, sk, group, causal):
+    """Grids too small to fill the device split each query block's keys over workgroups (tuning
+    family hip.attention_forward, chosen first when eligible) and merge the split states with exp2
+    factors, the algebra of merge_attention_summaries (streaming/attention.py:82-114). Checked against
+    the oracle, against the unsplit launch the tuning row [[0]] pins (the two differ only in the
+    association of that f32 merge), and with workspace='static', which allows no workspace and so
+    runs unsplit."""
+    import json
+
+    from intent_amd.examples.kernels.streaming.attention import flash_attention_fwd
+
+    b, hq, sq, d = shape
+    announce("attention key split", kind, shape, sk, group, causal)
+    rng = np.random.default_rng(sq + hq + d)
+    storage = "bf16" if kind == "bf16" else "f16"
+    q = inputs.normal(rng, (b, hq, sq, d), storage)
+    k = inputs.normal(rng, (b, hq // group, sk, d), storage)
+    v = inputs.normal(rng, (b, hq // group, sk, d), storage)
+    scale = float(np.float32(d ** -0.5))
+    defn = {"f16": flash_attention_fwd, "gqa": flash_gqa_attention_fwd, "bf16": flash_attention_bf16_fwd}[kind]
+    constexprs = {"CAUSAL": causal} if kind == "f16" else {"HEAD_GROUP": group, "CAUSAL": causal}
+    conv = (lambda a: to_bf16_tensor(a, device)) if kind == "bf16" else (lambda a: t(a, device))  # noqa: E731
+    args = (conv(q), conv(k), conv(v), scale)
+    config = tmp_path / "tuning.json"
+    config.write_text(json.dumps({"columns": ["split"], "families": {"hip.attention_forward": [[0]]}}))
+    outs = {}
+    for label, kwargs in (("split", {}), ("unsplit", {"tuning_config": config}),
+                          ("static", {"backend_options": {"workspace": "static"}})):
+        call = intent.jit(defn, backend="hip", constexprs=constexprs, **kwargs).prepare(*args)
+        call.launch()
+        assert dict(call.inspect_configurations()[0].configuration)["split"] == (label == "split"), label
+        got = call.result()
+        outs[label] = bf16_to_f32(bf16_tensor_bits(got)) if kind == "bf16" else got.cpu().numpy()
+    if kind == "bf16":
+        want = bf16_to_f32(oracle.attention_fwd(q, k, v, scale, causal, head_group=group, storage="bf16"))
+        tol = {"rel": 4e-2, "abs_": 2e-2}
+    else:
+        want = oracle.attention_fwd(q, k, v, scale, causal, head_group=group)
+        tol = {}
+    for label, got in outs.items():
+        assert not np.isnan(got).any(), label
+        assert_16bit(got, want, **tol)
+    assert np.array_equal(outs["unsplit"], outs["static"])
+    assert_16bit(outs["split"], outs["unsplit"], **tol)
+    if causal:
+        first = v[:, np.arange(hq) // group, 0, :]
+        assert np.array_equal(outs["split"][:, :, 0, :], bf16_to_f32(first) if kind == "bf16" else first)
+
+
+def test_attention_short_key_range_stays_unsplit(device):
+    """The reference streaming example (16 workgroups, 4 key tiles): too few tiles for a split to pay
+    for its merge launch, so the unsplit row is the first eligible one."""
+    rng = np.random.default_rng(22)
+    q = inputs.normal(rng, (2, 8, 256, 64), "bf16")
+    k, v = (inputs.normal(rng, (2, 2, 256, 64), "bf16") for _ in range(2))
+    call = intent.jit(flash_attention_bf16_fwd, backend="hip", constexprs={"HEAD_GROUP": 4, "CAUSAL": True}).prepare(
+        to_bf16_tensor(q, device), to_bf16_tensor(k, device), to_bf16_tensor(v, device), 0.125)
+    chosen, *others = call.inspect_configurations()
+    assert dict(chosen.configuration)["split"] == 0
+    assert [c.eligible for c in others] == [False] and "nothing to split" in others[0].reasons[0]
+
+
 def test_gqa_head_dim_64_matches_oracle(device):
     announce("gqa d=64")
     rng = np.random.default_rng(64)

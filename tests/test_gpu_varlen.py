@@ -72,15 +72,21 @@ def test_varlen_gqa_prefill_matches_oracle(device, group):
                                                 head_group=group))
 
 
-def test_varlen_equals_batched_kernel(device):
-    """Four sequences of 1024 rows: the packed kernel and the batched kernel give the same bits."""
+def test_varlen_equals_batched_kernel(device, tmp_path):
+    """Four sequences of 1024 rows: the packed kernel and the batched kernel give the same bits. The
+    batched grid is small enough to split its keys by default; the tuning row [[0]] runs it unsplit,
+    as the packed kernel always is."""
+    import json
+
     announce("varlen equals batched")
     g = np.random.default_rng(43)
     batch, seq, hq, group = 4, 1024, 8, 2
     q = inputs.normal(g, (batch, hq, seq, 128), "f16")
     k, v = (inputs.normal(g, (batch, hq // group, seq, 128), "f16") for _ in range(2))
-    batched = intent.jit(flash_gqa_attention_fwd, backend="hip", constexprs={"HEAD_GROUP": group, "CAUSAL": True}
-                         ).run(t(q, device), t(k, device), t(v, device), 0.125).cpu().numpy()
+    config = tmp_path / "tuning.json"
+    config.write_text(json.dumps({"columns": ["split"], "families": {"hip.attention_forward": [[0]]}}))
+    batched = intent.jit(flash_gqa_attention_fwd, backend="hip", constexprs={"HEAD_GROUP": group, "CAUSAL": True},
+                         tuning_config=config).run(t(q, device), t(k, device), t(v, device), 0.125).cpu().numpy()
     pack = lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3).reshape(batch * seq, a.shape[1], 128))  # noqa
     o = run_gqa(device, pack(q), pack(k), pack(v), [seq] * batch, 0.125, group)
     assert (o.view(np.uint16) == pack(batched).view(np.uint16)).all()

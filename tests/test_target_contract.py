@@ -213,6 +213,13 @@ def test_tuning_config_rows_are_read_and_saved(tmp_path):
     assert default.materialize().runtime.tuning_rows == ((1,), (0,))
     assert intent.generate(gemm, target=resolved(), tuning_config=config,
                            constexprs={"ACTIVATION": Activation.NONE}).materialize().runtime.tuning_family is None
+    from intent_amd.examples.kernels.streaming.attention import (flash_attention_bf16_fwd, flash_attention_fwd,
+                                                                  flash_gqa_attention_fwd)
+    for defn, constexprs in ((flash_attention_fwd, {"CAUSAL": True}),
+                             (flash_gqa_attention_fwd, {"HEAD_GROUP": 2, "CAUSAL": True}),
+                             (flash_attention_bf16_fwd, {"HEAD_GROUP": 2, "CAUSAL": False})):
+        runtime = intent.generate(defn, target=resolved(), constexprs=constexprs).materialize().runtime
+        assert runtime.tuning_family == "hip.attention_forward" and runtime.tuning_rows == ((1,), (0,))
     for bad in ({"columns": ["split"], "families": {"hip.attention_backward": [[2]]}},
                 {"columns": ["split"], "families": {"hip.nonexistent": [[0]]}},
                 {"columns": ["tile"], "families": {}},
