@@ -29,6 +29,7 @@
 // interpolation search and make the cuts of a row non-decreasing with a prefix maximum, so the
 // pieces partition the row for any estimate and any column order; an entry outside its window or
 // slice only reads x from another place. spmv_combine adds the pieces of each medium or large row in window or slice order.
+#include <algorithm>
 #include <mutex>
 
 #include "common.hpp"
@@ -707,10 +708,13 @@ __global__ __launch_bounds__(kSliceThreads) void spmv_slices(const int32_t *__re
 }
 
 // y of every medium row (thread per row: windows 0..7 in order) and large row (wave per row: lane
-// l sums slices l, l + 64, ... in order, then a fixed reduction tree).
-__global__ __launch_bounds__(256) void spmv_combine(float *__restrict__ y, Plan plan) {
+// l sums slices l, l + 64, ... in order, then a fixed reduction tree). The first mid_groups
+// workgroups take the medium rows, the rest the large rows, as many as the list capacity needs up
+// to 128 and 512 (beyond that they loop), so that a wave sums about one large row at config 5: with
+// 64 workgroups for the large rows each wave summed eight (9.8 us).
+__global__ __launch_bounds__(256) void spmv_combine(float *__restrict__ y, Plan plan, int mid_groups) {
   const int64_t n_mid = min(plan.counters[0], plan.cap_mid), n_big = min(plan.counters[1], plan.cap_big);
-  const int half = gridDim.x / 2;
+  const int half = mid_groups;
   if (static_cast<int>(blockIdx.x) < half) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n_mid;
          i += static_cast<int64_t>(half) * 256) {
@@ -722,8 +726,9 @@ __global__ __launch_bounds__(256) void spmv_combine(float *__restrict__ y, Plan 
   }
   const int lane = threadIdx.x & 63;
   const int S = plan.slices;
+  const int64_t big_groups = static_cast<int64_t>(gridDim.x) - half;
   for (int64_t i = static_cast<int64_t>(blockIdx.x - half) * 4 + (threadIdx.x >> 6); i < n_big;
-       i += static_cast<int64_t>(half) * 4) {   // uniform within a wave
+       i += big_groups * 4) {   // uniform within a wave
     float acc = 0.0f;
     for (int s = lane; s < S; s += 64) acc += plan.big_parts[i * S + s];
     const float sum = wave_sum(acc);
@@ -786,7 +791,9 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
                   s>>>(column_indices, values, x, c32, plan.big_cuts, plan.slices + 1, plan.big_parts,
                        plan.slices, plan.counters + 1, plan.cap_big);
   }
-  spmv_combine<<<dim3(128), dim3(256), 0, s>>>(y, plan);
+  const int mid_groups = static_cast<int>(std::min<int64_t>((plan.cap_mid + 255) / 256, 128)) + 1;
+  const int big_groups = static_cast<int>(std::min<int64_t>((plan.cap_big + 3) / 4, 512)) + 1;
+  spmv_combine<<<dim3(static_cast<unsigned>(mid_groups + big_groups)), dim3(256), 0, s>>>(y, plan, mid_groups);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("spmv_combine");
   return INTENT_HIP_OK;
 }
