@@ -28,7 +28,8 @@
 // counters cost 115 us at config 5.) The cut workgroups of spmv_rows estimate each cut by
 // interpolation search and make the cuts of a row non-decreasing with a prefix maximum, so the
 // pieces partition the row for any estimate and any column order; an entry outside its window or
-// slice only reads x from another place. spmv_combine adds the pieces of each medium or large row in window or slice order.
+// slice only reads x from another place. spmv_combine adds the pieces of each medium or large row
+// in window or slice order.
 #include <algorithm>
 #include <mutex>
 
