@@ -129,11 +129,14 @@ struct RopeRows {
 
 // Key split for small grids: with count > 1, workgroup (item, split) folds its query block against
 // the split-th share of the block's key tiles and writes each query row's unnormalised state
-// (maximum in the exp2 domain, denominator, DV sums) at slot (row * count + split) of m, den and
-// acc; attention_split_merge combines the splits. Batched modes only.
+// (maximum in the exp2 domain, denominator, DV sums) at slot (split * rows + row) of m, den and
+// acc, rows = batch * heads * sq; the sums are laid out [column / 8][slot][column % 8], so the 32
+// rows of a wave store 1 KB contiguously per instruction. attention_split_merge combines the
+// splits. Batched modes only.
 struct KeySplit {
   int count;
   float *m, *den, *acc;
+  int64_t rows;
 };
 
 // Kernel modes: batched [B,H,S,D] tensors, packed sequences, batched with a key bias, or batched
@@ -515,17 +518,19 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     // This split's state, unnormalised: the denominator and O^T with the maximum they are taken
     // against (row_ref; -inf for a split with no key), which is what attention_split_merge's exp2
     // factors need.
-    const int64_t slot = ((static_cast<int64_t>(b) * heads + h) * sq + lane_q) * split.count + blockIdx.x % split.count;
+    const int64_t slot = static_cast<int64_t>(blockIdx.x % split.count) * split.rows +
+                         (static_cast<int64_t>(b) * heads + h) * sq + lane_q;
     if (half == 0) {
       split.m[slot] = row_valid ? row_ref : -INFINITY;
       split.den[slot] = den;
     }
-    float *arow = split.acc + slot * kDV;
+    const int64_t slots = split.count * split.rows;
+    float *arow = split.acc + slot * 8 + 4 * half;
 #pragma unroll
     for (int mt = 0; mt < kDV / 32; ++mt)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq)
-        *reinterpret_cast<float4 *>(arow + mt * 32 + 8 * gq + 4 * half) =
+        *reinterpret_cast<float4 *>(arow + (mt * 4 + gq) * slots * 8) =
             make_float4(acc[mt][4 * gq], acc[mt][4 * gq + 1], acc[mt][4 * gq + 2], acc[mt][4 * gq + 3]);
     return;
   }
@@ -590,38 +595,42 @@ __global__ __launch_bounds__(1024) void attention_varlen_items(const int32_t *__
 // The kernel of a (dtype, d, dv, packed) choice; d and dv are each 64 or 128 (checked by the callers).
 // The key splits of one query row merged as merge_attention_summaries does (exp2 factors against
 // the largest maximum), normalised by an approximate reciprocal and stored in the element type E;
-// a row with no admitted key in any split is 0. One wave per row; lanes own DV / 64 columns each.
+// a row with no admitted key in any split is 0. Four columns of one row per thread, threads in
+// the order of the sums' layout ([column / 8][row][column % 8] within each split), so that every
+// split's sums are read contiguously.
 template <typename E, int DV>
-__global__ __launch_bounds__(64) void attention_split_merge(const float *__restrict__ m, const float *__restrict__ den,
-                                                            const float *__restrict__ acc, int splits, int heads, int sq,
-                                                            uint16_t *__restrict__ O, int64_t os_b, int64_t os_h,
-                                                            int64_t os_q) {
-  constexpr int kPer = DV / 64;
-  const int lane = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const int64_t base = row * splits;
+__global__ __launch_bounds__(256) void attention_split_merge(const float *__restrict__ m, const float *__restrict__ den,
+                                                             const float *__restrict__ acc, int splits, int64_t rows,
+                                                             int heads, int sq, uint16_t *__restrict__ O, int64_t os_b,
+                                                             int64_t os_h, int64_t os_q) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= rows * (DV / 4)) return;
+  const int64_t e = 4 * t, row = e % (rows * 8) / 8, block = e / (rows * 8);
+  const int col = static_cast<int>(block) * 8 + static_cast<int>(e % 8);
+  const float *a = acc + (block * splits * rows + row) * 8 + e % 8;   // split s at + s * rows * 8
   float top = -INFINITY;
-  for (int s = 0; s < splits; ++s) top = fmaxf(top, m[base + s]);
+  for (int s = 0; s < splits; ++s) top = fmaxf(top, m[s * rows + row]);
   const bool valid = top != -INFINITY;
-  float total = 0.0f, sum[kPer];
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) sum[e] = 0.0f;
+  float total = 0.0f;
+  float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (valid) {
 #pragma unroll 4
     for (int s = 0; s < splits; ++s) {
-      const float ms = m[base + s];
+      const float ms = m[s * rows + row];
       const float f = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - top);
-      total = fmaf(f, den[base + s], total);
-#pragma unroll
-      for (int e = 0; e < kPer; ++e) sum[e] = fmaf(f, acc[(base + s) * DV + lane + 64 * e], sum[e]);
+      total = fmaf(f, den[s * rows + row], total);
+      const float4 v = *reinterpret_cast<const float4 *>(a + s * rows * 8);
+      sum = make_float4(fmaf(f, v.x, sum.x), fmaf(f, v.y, sum.y), fmaf(f, v.z, sum.z), fmaf(f, v.w, sum.w));
     }
   }
   const float inv = valid ? __builtin_amdgcn_rcpf(total) : 0.0f;
   const int64_t q = row % sq, bh = row / sq;
-  uint16_t *orow = O + (bh / heads) * os_b + (bh % heads) * os_h + q * os_q;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e)
-    orow[lane + 64 * e] = __builtin_bit_cast(uint16_t, round_to<E>(sum[e] * inv));
+  uint16_t *orow = O + (bh / heads) * os_b + (bh % heads) * os_h + q * os_q + col;
+  const uint32_t lo = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.x * inv))) |
+                      (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.y * inv))) << 16);
+  const uint32_t hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.z * inv))) |
+                      (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.w * inv))) << 16);
+  *reinterpret_cast<uint2 *>(orow) = make_uint2(lo, hi);
 }
 
 template <typename E, int kMode>
@@ -710,16 +719,16 @@ int64_t key_splits(int64_t blocks, int64_t sk) {
 
 // Split state: maxima and denominators (each from a 256-byte boundary), then the sums.
 struct SplitLayout {
-  int64_t splits;
+  int64_t splits, rows;
   size_t den, acc, bytes;
 };
 SplitLayout split_layout(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t dv) {
   const int64_t q_blocks = (sq + kBQ - 1) / kBQ;
   const int64_t splits = key_splits(batch * heads * q_blocks, sk);
-  if (splits == 1) return SplitLayout{1, 0, 0, 0};
+  if (splits == 1) return SplitLayout{1, 0, 0, 0, 0};
   const size_t n = static_cast<size_t>(batch * heads * sq * splits);
   const size_t part = (4 * n + 255) / 256 * 256;
-  return SplitLayout{splits, part, 2 * part, 2 * part + 4 * n * static_cast<size_t>(dv)};
+  return SplitLayout{splits, batch * heads * sq, part, 2 * part, 2 * part + 4 * n * static_cast<size_t>(dv)};
 }
 
 // The split state of a launch, when the grid is small enough to split and the workspace holds it
@@ -729,27 +738,27 @@ KeySplit key_split(const SplitLayout &layout, void *workspace, size_t workspace_
     return KeySplit{1, nullptr, nullptr, nullptr};
   char *ws = static_cast<char *>(workspace);
   return KeySplit{static_cast<int>(layout.splits), reinterpret_cast<float *>(ws),
-                  reinterpret_cast<float *>(ws + layout.den), reinterpret_cast<float *>(ws + layout.acc)};
+                  reinterpret_cast<float *>(ws + layout.den), reinterpret_cast<float *>(ws + layout.acc), layout.rows};
 }
 
 // attention_split_merge<E, dv> over every query row of a split launch.
-void launch_merge(int dtype, int64_t dv, const KeySplit &ks, int64_t rows, int heads, int sq, uint16_t *O,
-                  const Geometry &g, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(rows));
+void launch_merge(int dtype, int64_t dv, const KeySplit &ks, int heads, int sq, uint16_t *O, const Geometry &g,
+                  hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((ks.rows * (dv / 4) + 255) / 256)), block(256);
   if (dtype == INTENT_HIP_BF16) {
     if (dv == 128)
-      attention_split_merge<__bf16, 128><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
-                                                                   g.os[0], g.os[1], g.os[2]);
+      attention_split_merge<__bf16, 128><<<grid, block, 0, s>>>(ks.m, ks.den, ks.acc, ks.count, ks.rows, heads, sq, O,
+                                                                g.os[0], g.os[1], g.os[2]);
     else
-      attention_split_merge<__bf16, 64><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
-                                                                  g.os[0], g.os[1], g.os[2]);
+      attention_split_merge<__bf16, 64><<<grid, block, 0, s>>>(ks.m, ks.den, ks.acc, ks.count, ks.rows, heads, sq, O,
+                                                               g.os[0], g.os[1], g.os[2]);
   } else {
     if (dv == 128)
-      attention_split_merge<_Float16, 128><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
-                                                                     g.os[0], g.os[1], g.os[2]);
+      attention_split_merge<_Float16, 128><<<grid, block, 0, s>>>(ks.m, ks.den, ks.acc, ks.count, ks.rows, heads, sq,
+                                                                  O, g.os[0], g.os[1], g.os[2]);
     else
-      attention_split_merge<_Float16, 64><<<grid, dim3(64), 0, s>>>(ks.m, ks.den, ks.acc, ks.count, heads, sq, O,
-                                                                    g.os[0], g.os[1], g.os[2]);
+      attention_split_merge<_Float16, 64><<<grid, block, 0, s>>>(ks.m, ks.den, ks.acc, ks.count, ks.rows, heads, sq,
+                                                                 O, g.os[0], g.os[1], g.os[2]);
   }
 }
 
@@ -808,7 +817,7 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
                              KeyBias{}, ks);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd");
   if (ks.count > 1) {
-    launch_merge(dtype, dv, ks, batch * heads * sq, h, iq, Op, g, s);
+    launch_merge(dtype, dv, ks, h, iq, Op, g, s);
     if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_split_merge");
   }
   return INTENT_HIP_OK;
@@ -1004,7 +1013,7 @@ extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void
                                            KeyBias{}, rr, ks);
   if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_fwd (latent)");
   if (ks.count > 1) {
-    launch_merge(INTENT_HIP_F16, d, ks, batch * heads * sq, h, iq, Op, g, s);
+    launch_merge(INTENT_HIP_F16, d, ks, h, iq, Op, g, s);
     if (hipPeekAtLastError() != hipSuccess) return launch_status("attention_split_merge");
   }
   return INTENT_HIP_OK;

@@ -246,8 +246,10 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_delta(const uint16_t *
 // ---------------------------------------------------------------- dQ
 // kW waves of 32 queries per workgroup (4 or 8). With splits > 1 the key tiles of each query
 // block are divided into `splits` consecutive ranges, one workgroup each, which write unscaled
-// f32 partial sums to `partial` ([split][batch * heads][sq][D]); attention_bwd_dq_reduce folds
-// them in split order. Used when too few workgroups would run.
+// f32 partial sums to `partial` (split after split, each [D / 8][batch * heads * sq][8]: column
+// c of row r at (c / 8, r, c % 8), so the 32 rows of a wave store 1 KB contiguously per
+// instruction); attention_bwd_dq_reduce folds them in split order. Used when too few workgroups
+// would run.
 template <int D, int kW>
 __device__ __forceinline__ void attention_bwd_dq_body(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
@@ -396,12 +398,13 @@ __device__ __forceinline__ void attention_bwd_dq_body(
 
   if (!q_ok) return;
   if (partial != nullptr) {
-    float *prow = partial + ((static_cast<int64_t>(split) * bh_count + bh) * sq + lane_q) * D;
+    const int64_t rows = static_cast<int64_t>(bh_count) * sq;
+    float *pslot = partial + split * rows * D + (static_cast<int64_t>(bh) * sq + lane_q) * 8 + 4 * half;
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq)
-        *reinterpret_cast<float4 *>(prow + mt * 32 + 8 * gq + 4 * half) =
+        *reinterpret_cast<float4 *>(pslot + (mt * 4 + gq) * rows * 8) =
             make_float4(acc[mt][4 * gq], acc[mt][4 * gq + 1], acc[mt][4 * gq + 2], acc[mt][4 * gq + 3]);
     return;
   }
@@ -435,13 +438,13 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_dq_reduce(const float 
                                                                     float scale) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (t >= rows * (D / 4)) return;
-  const int64_t row = t / (D / 4);
-  const int col = static_cast<int>(t % (D / 4)) * 4;
+  const int64_t e = 4 * t, row = e % (rows * 8) / 8;   // partial layout: [column / 8][row][column % 8]
+  const int col = static_cast<int>(e / (rows * 8)) * 8 + static_cast<int>(e % 8);
   const int64_t q = row % sq, bh = row / sq;
   const int64_t b = bh / heads, h = bh % heads;
   float4 s4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   for (int i = 0; i < splits; ++i) {
-    const float4 a = *reinterpret_cast<const float4 *>(partial + (i * rows + row) * D + col);
+    const float4 a = *reinterpret_cast<const float4 *>(partial + i * rows * D + e);
     s4 = make_float4(s4.x + a.x, s4.y + a.y, s4.z + a.z, s4.w + a.w);
   }
   uint16_t *qrow = DQ + b * g.out0[0] + h * g.out0[1] + q * g.out0[2];
@@ -452,8 +455,9 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_dq_reduce(const float 
 // ---------------------------------------------------------------- dK / dV
 // kSplit: the workgroup takes one query head of the group and one of `qsplits` consecutive
 // ranges of its query tiles (grid x head_group x qsplits) and writes its unscaled f32 dK and dV
-// sums to `partial` ([head_group * qsplits][batch][kv_heads][sk][D], dK then dV), which
-// attention_bwd_dkdv_reduce folds. Used when too few workgroups would run.
+// sums to `partial` (head_group * qsplits parts of dK, then as many of dV, each
+// [D / 8][batch * kv_heads * sk][8] as in dQ), which attention_bwd_dkdv_reduce folds. Used when too
+// few workgroups would run.
 // kPart: dK and dV together, or one of them (DkdvPart); kW: waves of 32 keys per workgroup.
 template <int D, bool kSplit, int kPart, int kW>
 __device__ __forceinline__ void attention_bwd_dkdv_body(
@@ -650,18 +654,18 @@ __device__ __forceinline__ void attention_bwd_dkdv_body(
     const int64_t rows = static_cast<int64_t>(gridDim.x / (k_blocks * head_group * qsplits)) * sk;   // batch * kv_heads * sk
     const int64_t row = (static_cast<int64_t>(b) * kv_heads + kh) * sk + lane_k;
     const int parts = head_group * qsplits, part = split * qsplits + qs;
-    float *pk = partial + (static_cast<int64_t>(part) * rows + row) * D;
-    float *pv = partial + (static_cast<int64_t>(parts + part) * rows + row) * D;
+    float *pk = partial + part * rows * D + row * 8 + 4 * half;
+    float *pv = partial + (parts + part) * rows * D + row * 8 + 4 * half;
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const int col = mt * 32 + 8 * gq + 4 * half;
+        const int64_t block = (mt * 4 + gq) * rows * 8;   // partial layout: [column / 8][row][column % 8]
         if constexpr (kDoK)
-          *reinterpret_cast<float4 *>(pk + col) =
+          *reinterpret_cast<float4 *>(pk + block) =
               make_float4(acc_k[mt][4 * gq], acc_k[mt][4 * gq + 1], acc_k[mt][4 * gq + 2], acc_k[mt][4 * gq + 3]);
         if constexpr (kDoV)
-          *reinterpret_cast<float4 *>(pv + col) =
+          *reinterpret_cast<float4 *>(pv + block) =
               make_float4(acc_v[mt][4 * gq], acc_v[mt][4 * gq + 1], acc_v[mt][4 * gq + 2], acc_v[mt][4 * gq + 3]);
       }
     return;
@@ -705,14 +709,14 @@ __global__ __launch_bounds__(kThreads) void attention_bwd_dkdv_reduce(const floa
                                                                       BwdGeometry g, float scale) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (t >= rows * (D / 4)) return;
-  const int64_t row = t / (D / 4);
-  const int col = static_cast<int>(t % (D / 4)) * 4;
+  const int64_t e = 4 * t, row = e % (rows * 8) / 8;   // partial layout: [column / 8][row][column % 8]
+  const int col = static_cast<int>(e / (rows * 8)) * 8 + static_cast<int>(e % 8);
   const int64_t k = row % sk, bh = row / sk;
   const int64_t b = bh / kv_heads, kh = bh % kv_heads;
   float4 sk4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), sv4 = sk4;
   for (int i = 0; i < parts; ++i) {
-    const float4 a = *reinterpret_cast<const float4 *>(partial + (i * rows + row) * D + col);
-    const float4 c = *reinterpret_cast<const float4 *>(partial + ((parts + i) * rows + row) * D + col);
+    const float4 a = *reinterpret_cast<const float4 *>(partial + i * rows * D + e);
+    const float4 c = *reinterpret_cast<const float4 *>(partial + (parts + i) * rows * D + e);
     sk4 = make_float4(sk4.x + a.x, sk4.y + a.y, sk4.z + a.z, sk4.w + a.w);
     sv4 = make_float4(sv4.x + c.x, sv4.y + c.y, sv4.z + c.z, sv4.w + c.w);
   }
