@@ -176,6 +176,10 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
                                                                   Geometry g, float scale, int causal,
                                                                   int q_blocks, Ragged r, KeyBias kb, RopeRows rr,
                                                                   KeySplit split) {
+  // Every rounding of the softmax and merge is the one written: no product is fused into a later
+  // sum by the compiler (which it may otherwise do differently in different instantiations or
+  // copies of the loop, e.g. a rescale acc *= left joined into the next fmaf).
+#pragma clang fp contract(off)
   constexpr bool kVarlen = kMode == kPacked, kBias = kMode == kBiased, kRope = kMode == kLatent;
   typedef typename Elem<E>::x8 f16x8_t;   // operand fragments of 8 elements of E
   constexpr int kD = D, kDV = DV;
