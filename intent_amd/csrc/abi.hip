@@ -60,6 +60,19 @@ int resident_blocks(const void *kernel, int block) {
   return blocks;
 }
 
+int device_cus() {
+  static std::mutex lock;
+  static int cus[64] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+  std::lock_guard<std::mutex> guard(lock);
+  if (cus[device] <= 0 &&
+      (hipDeviceGetAttribute(&cus[device], hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+       cus[device] <= 0))
+    cus[device] = 256;
+  return cus[device];
+}
+
 }  // namespace intent_hip
 
 using namespace intent_hip;

@@ -132,11 +132,13 @@ struct RopeRows {
 // (maximum in the exp2 domain, denominator, DV sums) at slot (split * rows + row) of m, den and
 // acc, rows = batch * heads * sq; the sums are laid out [column / 8][slot][column % 8], so the 32
 // rows of a wave store 1 KB contiguously per instruction. attention_split_merge combines the
-// splits. Batched modes only.
+// splits. Batched modes only. With `grouped`, workgroup x folds split x / items of item
+// x % items (items = grid / count), else split x % count of item x / count.
 struct KeySplit {
   int count;
   float *m, *den, *acc;
   int64_t rows;
+  int grouped;
 };
 
 // Kernel modes: batched [B,H,S,D] tensors, packed sequences, batched with a key bias, or batched
@@ -195,6 +197,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in a scalar register
   int qb, b = 0, h, sq, sk;   // query block, batch entry, query head, rows of q and of k/v
+  int part = 0;               // the key split this workgroup folds (batched modes)
   int64_t row0 = 0;           // first row of the sequence (packed sequences)
   if constexpr (kVarlen) {
     const int item = static_cast<int>(blockIdx.x) / heads;   // the heads of an item are neighbours
@@ -207,9 +210,15 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     sq = sk = end - start;
     row0 = start;
   } else {
-    // With a key split the splits of one item are neighbours; without, item = workgroup.
-    const int item = static_cast<int>(blockIdx.x) / split.count;
-    const int bh_count = gridDim.x / split.count / q_blocks;
+    // With a key split the splits of one item are neighbours, or (grouped) `items` workgroups
+    // apart: then, when items is a multiple of 8, on one XCD (dispatch goes round-robin over the 8
+    // XCDs), where they share the item's query rows in L2. The launch groups only grids the device
+    // holds at once, so the order changes no workgroup's start. Without a split, item = workgroup.
+    const int items = gridDim.x / split.count;
+    const int x = static_cast<int>(blockIdx.x);
+    const int item = split.grouped ? x % items : x / split.count;
+    part = split.grouped ? x / items : x % split.count;
+    const int bh_count = items / q_blocks;
     qb = q_blocks - 1 - item / bh_count;   // heaviest blocks first
     const int bh = item % bh_count;
     b = bh / heads;
@@ -249,7 +258,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const int tiles_all = (k_end + kBK - 1) / kBK;
   // This workgroup's key tiles [t_begin, tiles): all of them, or its split's share.
   const int share = (tiles_all + split.count - 1) / split.count;
-  const int t_begin = kVarlen ? 0 : min(tiles_all, static_cast<int>(blockIdx.x % split.count) * share);
+  const int t_begin = kVarlen ? 0 : min(tiles_all, part * share);
   const int tiles = kVarlen ? tiles_all : min(tiles_all, t_begin + share);
   const int wave_q_last = min(wq0 + 31, sq - 1);
 
@@ -522,7 +531,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     // This split's state, unnormalised: the denominator and O^T with the maximum they are taken
     // against (row_ref; -inf for a split with no key), which is what attention_split_merge's exp2
     // factors need.
-    const int64_t slot = static_cast<int64_t>(blockIdx.x % split.count) * split.rows +
+    const int64_t slot = static_cast<int64_t>(part) * split.rows +
                          (static_cast<int64_t>(b) * heads + h) * sq + lane_q;
     if (half == 0) {
       split.m[slot] = row_valid ? row_ref : -INFINITY;
@@ -802,10 +811,11 @@ int launch_attention(int dtype, const void *q, const void *k, const void *v, voi
   if (!aligned(q, 16) || (sk > 0 && (!aligned(k, 16) || !aligned(v, 16))) || !aligned(o, 8))
     return fail(INTENT_HIP_ERR_UNSUPPORTED, "attention tensors must be 16-byte aligned");
   const int q_blocks = static_cast<int>((sq + kBQ - 1) / kBQ);
-  const KeySplit ks = kb == nullptr ? key_split(split_layout(batch, heads, sq, sk, dv), workspace, workspace_bytes)
-                                    : KeySplit{1, nullptr, nullptr, nullptr};
+  KeySplit ks = kb == nullptr ? key_split(split_layout(batch, heads, sq, sk, dv), workspace, workspace_bytes)
+                              : KeySplit{1, nullptr, nullptr, nullptr};
   const int64_t blocks = batch * heads * q_blocks * ks.count;
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many attention workgroups");
+  ks.grouped = ks.count > 1 && blocks <= device_cus();
   const auto *Qp = static_cast<const uint16_t *>(q);
   const auto *Kp = static_cast<const uint16_t *>(k);
   const auto *Vp = static_cast<const uint16_t *>(v);
@@ -998,9 +1008,10 @@ extern "C" int intent_hip_mla_prefill(const void *q, const void *qpe, const void
   const int q_blocks = static_cast<int>((sq + kBQ - 1) / kBQ);
   // A key split needs the workspace intent_hip_mla_prefill_workspace_bytes names; without it (or
   // when the grid fills the chip) the launch is unsplit.
-  const KeySplit ks = key_split(split_layout(batch, heads, sq, sk, d), workspace, workspace_bytes);
+  KeySplit ks = key_split(split_layout(batch, heads, sq, sk, d), workspace, workspace_bytes);
   const int64_t blocks = batch * heads * q_blocks * ks.count;
   if (blocks > INT32_MAX) return fail(INTENT_HIP_ERR_UNSUPPORTED, "too many attention workgroups");
+  ks.grouped = ks.count > 1 && blocks <= device_cus();
   const dim3 grid(static_cast<unsigned>(blocks));
   const hipStream_t s = as_stream(stream);
   const auto *Qp = static_cast<const uint16_t *>(q);

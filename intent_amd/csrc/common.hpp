@@ -24,6 +24,9 @@ inline bool aligned(const void *p, unsigned bytes) {
 // workgroups per CU, queried once per device and kernel.
 int resident_blocks(const void *kernel, int block);
 
+// Compute units of the current device, queried once per device.
+int device_cus();
+
 // Fills `out` from hipFuncGetAttributes of `kernel`.
 int describe_kernel(const void *kernel, const char *name, int block_threads,
                     IntentHipKernelResources *out);
