@@ -606,44 +606,57 @@ __global__ __launch_bounds__(1024) void attention_varlen_items(const int32_t *__
 }  // namespace
 
 // The kernel of a (dtype, d, dv, packed) choice; d and dv are each 64 or 128 (checked by the callers).
+// Key splits per query block: at most kMaxKeySplits (key_splits below).
+constexpr int kMaxKeySplits = 8;
+
 // The key splits of one query row merged as merge_attention_summaries does (exp2 factors against
 // the largest maximum), normalised by an approximate reciprocal and stored in the element type E;
-// a row with no admitted key in any split is 0. Four columns of one row per thread, threads in
-// the order of the sums' layout ([column / 8][row][column % 8] within each split), so that every
-// split's sums are read contiguously.
+// a row with no admitted key in any split is 0. One thread per row and 8-column block, threads in
+// the order of the sums' layout ([column / 8][row][column % 8] within each split), so a wave reads
+// 2 KB of every split contiguously. The splits are unrolled (at most kMaxKeySplits), with every
+// load issued unconditionally (indices clamped) and the splits past `splits` masked.
 template <typename E, int DV>
 __global__ __launch_bounds__(256) void attention_split_merge(const float *__restrict__ m, const float *__restrict__ den,
                                                              const float *__restrict__ acc, int splits, int64_t rows,
                                                              int heads, int sq, uint16_t *__restrict__ O, int64_t os_b,
                                                              int64_t os_h, int64_t os_q) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= rows * (DV / 4)) return;
-  const int64_t e = 4 * t, row = e % (rows * 8) / 8, block = e / (rows * 8);
-  const int col = static_cast<int>(block) * 8 + static_cast<int>(e % 8);
-  const float *a = acc + (block * splits * rows + row) * 8 + e % 8;   // split s at + s * rows * 8
+  if (t >= rows * (DV / 8)) return;
+  const int64_t row = t % rows, block = t / rows;
+  const float *a = acc + (block * splits * rows + row) * 8;   // split s at + s * rows * 8
+  float ms[kMaxKeySplits];
   float top = -INFINITY;
-  for (int s = 0; s < splits; ++s) top = fmaxf(top, m[s * rows + row]);
+#pragma unroll
+  for (int s = 0; s < kMaxKeySplits; ++s) {
+    const float v = m[min(s, splits - 1) * rows + row];
+    ms[s] = s < splits ? v : -INFINITY;
+    top = fmaxf(top, ms[s]);
+  }
   const bool valid = top != -INFINITY;
   float total = 0.0f;
-  float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (valid) {
-#pragma unroll 4
-    for (int s = 0; s < splits; ++s) {
-      const float ms = m[s * rows + row];
-      const float f = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - top);
-      total = fmaf(f, den[s * rows + row], total);
-      const float4 v = *reinterpret_cast<const float4 *>(a + s * rows * 8);
-      sum = make_float4(fmaf(f, v.x, sum.x), fmaf(f, v.y, sum.y), fmaf(f, v.z, sum.z), fmaf(f, v.w, sum.w));
+  float4 lo = make_float4(0.0f, 0.0f, 0.0f, 0.0f), hi = lo;
+#pragma unroll
+  for (int s = 0; s < kMaxKeySplits; ++s) {
+    const int64_t at = min(s, splits - 1) * rows;
+    const float d = den[at + row];
+    const float4 v0 = *reinterpret_cast<const float4 *>(a + at * 8);
+    const float4 v1 = *reinterpret_cast<const float4 *>(a + at * 8 + 4);
+    if (valid && s < splits) {
+      const float f = ms[s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[s] - top);
+      total = fmaf(f, d, total);
+      lo = make_float4(fmaf(f, v0.x, lo.x), fmaf(f, v0.y, lo.y), fmaf(f, v0.z, lo.z), fmaf(f, v0.w, lo.w));
+      hi = make_float4(fmaf(f, v1.x, hi.x), fmaf(f, v1.y, hi.y), fmaf(f, v1.z, hi.z), fmaf(f, v1.w, hi.w));
     }
   }
   const float inv = valid ? __builtin_amdgcn_rcpf(total) : 0.0f;
   const int64_t q = row % sq, bh = row / sq;
-  uint16_t *orow = O + (bh / heads) * os_b + (bh % heads) * os_h + q * os_q + col;
-  const uint32_t lo = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.x * inv))) |
-                      (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.y * inv))) << 16);
-  const uint32_t hi = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.z * inv))) |
-                      (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(sum.w * inv))) << 16);
-  *reinterpret_cast<uint2 *>(orow) = make_uint2(lo, hi);
+  uint16_t *orow = O + (bh / heads) * os_b + (bh % heads) * os_h + q * os_q + block * 8;
+  auto pack = [&](float x, float y) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(x * inv))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, round_to<E>(y * inv))) << 16);
+  };
+  reinterpret_cast<uint2 *>(orow)[0] = make_uint2(pack(lo.x, lo.y), pack(lo.z, lo.w));
+  reinterpret_cast<uint2 *>(orow)[1] = make_uint2(pack(hi.x, hi.y), pack(hi.z, hi.w));
 }
 
 template <typename E, int kMode>
@@ -725,7 +738,7 @@ int64_t key_splits(int64_t blocks, int64_t sk) {
   const int64_t tiles = (sk + kBK - 1) / kBK;
   if (blocks <= 0 || blocks >= 256 || tiles < 8) return 1;
   int64_t s = (512 + blocks - 1) / blocks;
-  s = s > 8 ? 8 : s;
+  s = s > kMaxKeySplits ? kMaxKeySplits : s;
   s = s > tiles / 2 ? tiles / 2 : s;
   return s < 1 ? 1 : s;
 }
@@ -757,7 +770,7 @@ KeySplit key_split(const SplitLayout &layout, void *workspace, size_t workspace_
 // attention_split_merge<E, dv> over every query row of a split launch.
 void launch_merge(int dtype, int64_t dv, const KeySplit &ks, int heads, int sq, uint16_t *O, const Geometry &g,
                   hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((ks.rows * (dv / 4) + 255) / 256)), block(256);
+  const dim3 grid(static_cast<unsigned>((ks.rows * (dv / 8) + 255) / 256)), block(256);
   if (dtype == INTENT_HIP_BF16) {
     if (dv == 128)
       attention_split_merge<__bf16, 128><<<grid, block, 0, s>>>(ks.m, ks.den, ks.acc, ks.count, ks.rows, heads, sq, O,
