@@ -605,7 +605,6 @@ __global__ __launch_bounds__(1024) void attention_varlen_items(const int32_t *__
 
 }  // namespace
 
-// The kernel of a (dtype, d, dv, packed) choice; d and dv are each 64 or 128 (checked by the callers).
 // Key splits per query block: at most kMaxKeySplits (key_splits below).
 constexpr int kMaxKeySplits = 8;
 
@@ -659,6 +658,7 @@ __global__ __launch_bounds__(256) void attention_split_merge(const float *__rest
   reinterpret_cast<uint2 *>(orow)[1] = make_uint2(pack(hi.x, hi.y), pack(hi.z, hi.w));
 }
 
+// The kernel of a (dtype, d, dv, mode) choice; d and dv are each 64 or 128 (checked by the callers).
 template <typename E, int kMode>
 const void *attention_kernel(int64_t d, int64_t dv) {
   if (d == 64) return dv == 64 ? reinterpret_cast<const void *>(&attention_fwd<E, 64, 64, kMode>)
