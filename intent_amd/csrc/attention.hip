@@ -15,8 +15,9 @@
 //
 // Design (d and dv each 64 or 128, independently):
 //   * a workgroup owns 256 query rows of one (batch, head): 8 waves x 32 rows, two per SIMD;
-//     key tiles of 64 keys stream through LDS in two stages (K: 16 KB, V: 16 KB per stage),
-//     written by global_load_lds_dwordx4 while the previous tile is consumed. Each K/V tile
+//     key tiles of 64 keys stream through LDS in four stages (K: 16 KB, V: 16 KB per stage),
+//     written by global_load_lds_dwordx4, two tiles per barrier: the next two are fetched while
+//     the waves fold the current two, so the waves synchronise once per 128 keys. Each K/V tile
 //     serves 256 queries, which halves the L2 -> LDS traffic of 128-query workgroups (4.3 GB
 //     at config 4) and measured 0.609 against 0.631 ms;
 //   * scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16, the wave's Q
@@ -192,8 +193,15 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   constexpr int kVChunks = kBK * kVRow;       // 16-byte chunks of a V tile (row = key)
   constexpr int kBiasChunks = kBias ? kBK / 4 : 0;   // 16-byte chunks of the tile's key bias
   constexpr int kStageChunks = kKChunks + kVChunks + kBiasChunks;
+  // Key tiles per barrier: the waves synchronise once per kGroup tiles, with kGroup more in flight,
+  // so 2 kGroup LDS stages. Two against one (interleaved, bit-identical): config 4 0.697 -> 0.690
+  // ms, D = 64 at config 4's extents 0.427 -> 0.406 ms; four at D = 64 (eight 16 KB stages) lost
+  // that gain again (0.418 ms).
+  constexpr int kGroup = 2;
+  constexpr int kStages = 2 * kGroup;
+  static_assert(kStages * kStageChunks * 16 <= 160 * 1024, "LDS stages");
   static_assert(kKChunks % kThreads == 0 && kVChunks % kThreads == 0, "DMA split");
-  __shared__ uint4 lds[2 * kStageChunks];
+  __shared__ uint4 lds[kStages * kStageChunks];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, kept in a scalar register
   int qb, b = 0, h, sq, sk;   // query block, batch entry, query head, rows of q and of k/v
@@ -285,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     v_off[i] = static_cast<int64_t>(row) * g.vs[2] + (pc ^ swz_v(DV, row)) * 8;
   }
   auto issue = [&](int kt) {
-    uint4 *stage = lds + (kt & 1) * kStageChunks;
+    uint4 *stage = lds + (kt & (kStages - 1)) * kStageChunks;
     const int key0 = kt * kBK;
     if (!kRope && key0 + kBK <= sk) {   // wave-uniform: a full tile
       const uint16_t *k_tile = kbase + static_cast<int64_t>(key0) * g.ks[2];
@@ -357,13 +365,16 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
   const int v_key = 4 * (g16 >> 1) + (i16 >> 2);      // + 16 sl + 8 r
   const int v_dv = 16 * (g16 & 1) + 4 * (i16 & 3);    // + 32 mt
 
-  if (t_begin < tiles) issue(t_begin);
+  for (int i = 0; i < kGroup && t_begin + i < tiles; ++i) issue(t_begin + i);
   for (int kt = t_begin; kt < tiles; ++kt) {
-    INTENT_WAIT_VMCNT(0);
-    __syncthreads();          // tile kt is in LDS; every wave is done with tile kt - 1
-    if (kt + 1 < tiles) issue(kt + 1);
+    if ((kt - t_begin) % kGroup == 0) {   // workgroup-uniform
+      INTENT_WAIT_VMCNT(0);
+      __syncthreads();   // tiles kt .. kt + kGroup - 1 are in LDS; every wave is done with the group before
+      for (int i = 0; i < kGroup; ++i)
+        if (kt + kGroup + i < tiles) issue(kt + kGroup + i);   // into the stages of the group before
+    }
     const int key0 = kt * kBK;
-    const uint4 *sk_tile = lds + (kt & 1) * kStageChunks;
+    const uint4 *sk_tile = lds + (kt & (kStages - 1)) * kStageChunks;
     const uint16_t *sv_tile = reinterpret_cast<const uint16_t *>(sk_tile + kKChunks);
     if (key0 + kBK > sk) {
       // Tail tile: clear the V rows past the last key so masked weights meet zeros.
