@@ -32,6 +32,14 @@ def compile_flags() -> list[str]:
             f"-I{ROOT / 'include'}", f"-I{SOURCES}"]
 
 
+# Machine-scheduler strategy per source where it measured faster than the default (interleaved
+# A/B at the benchmark configurations, outputs bit-identical: the scheduler only reorders
+# independent instructions). max-ilp: gemm_f32 3.755 -> 3.669 ms, linear_f32 3.884 -> 3.737 ms,
+# bf16 GEMM 8192^3 0.924 -> 0.913 ms, paged decode 57.4 -> 55.9 us. It made the attention forward
+# slower (0.683 -> 0.700 ms) and left SpMV, SpMM and gemm_i8 unchanged, so those keep the default.
+SCHEDULER = {"gemm.hip": "max-ilp", "gemm_f32.hip": "max-ilp", "decode.hip": "max-ilp"}
+
+
 def build(verbose: bool = False) -> Path:
     compiler = hipcc()
     objects_dir = PACKAGE / "_build"
@@ -41,6 +49,8 @@ def build(verbose: bool = False) -> Path:
     def compile_one(source: Path) -> Path:
         target = objects_dir / (source.stem + ".o")
         command = [compiler, *compile_flags(), "-c", str(source), "-o", str(target)]
+        if source.name in SCHEDULER:
+            command[-4:-4] = ["-mllvm", f"-amdgpu-sched-strategy={SCHEDULER[source.name]}"]
         result = subprocess.run(command, capture_output=True, text=True)
         noise = "'-packed-fp32-ops' is not a recognized feature"
         diagnostics = "\n".join(line for line in (result.stdout + result.stderr).splitlines() if noise not in line)
