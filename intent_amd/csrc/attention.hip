@@ -435,13 +435,14 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
     const bool partial = edge || key0 + kBK > sk;               // wave-uniform
     if (partial) {
       const int limit = causal ? min(sk - 1, lane_q) : sk - 1;  // last valid key of this lane's query
+      // Key key0 + 4 half + o of element (st, e), o = 32 st + 8 (e / 4) + e % 4 an immediate: one
+      // compare against the lane's room per element.
+      const int room = limit - key0 - 4 * half;
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = key0 + st * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-          s[st][e] = key <= limit ? s[st][e] : -INFINITY;
-        }
+        for (int e = 0; e < 16; ++e)
+          s[st][e] = st * 32 + 8 * (e >> 2) + (e & 3) <= room ? s[st][e] : -INFINITY;
     }
     // This lane's 32 keys in four independent chains (maximum_num: NaN-ignoring, exact, any order),
     // then the other half's from lane l ^ 32.
