@@ -549,6 +549,9 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd(const uint16_t *__r
       split.m[slot] = row_valid ? row_ref : -INFINITY;
       split.den[slot] = den;
     }
+    // The sums of a row with no key in this split are never read (the merge skips a split whose
+    // maximum is -inf), so they are not written.
+    if (!row_valid) return;
     const int64_t slots = split.count * split.rows;
     float *arow = split.acc + slot * 8 + 4 * half;
 #pragma unroll
@@ -648,12 +651,13 @@ __global__ __launch_bounds__(256) void attention_split_merge(const float *__rest
   float4 lo = make_float4(0.0f, 0.0f, 0.0f, 0.0f), hi = lo;
 #pragma unroll
   for (int s = 0; s < kMaxKeySplits; ++s) {
-    const int64_t at = min(s, splits - 1) * rows;
-    const float d = den[at + row];
-    const float4 v0 = *reinterpret_cast<const float4 *>(a + at * 8);
-    const float4 v1 = *reinterpret_cast<const float4 *>(a + at * 8 + 4);
-    if (valid && s < splits) {
-      const float f = ms[s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[s] - top);
+    // A split with no key for this row (maximum -inf) adds nothing; its sums were not written.
+    if (s < splits && ms[s] != -INFINITY) {
+      const int64_t at = s * rows;
+      const float d = den[at + row];
+      const float4 v0 = *reinterpret_cast<const float4 *>(a + at * 8);
+      const float4 v1 = *reinterpret_cast<const float4 *>(a + at * 8 + 4);
+      const float f = __builtin_amdgcn_exp2f(ms[s] - top);
       total = fmaf(f, d, total);
       lo = make_float4(fmaf(f, v0.x, lo.x), fmaf(f, v0.y, lo.y), fmaf(f, v0.z, lo.z), fmaf(f, v0.w, lo.w));
       hi = make_float4(fmaf(f, v1.x, hi.x), fmaf(f, v1.y, hi.y), fmaf(f, v1.z, hi.z), fmaf(f, v1.w, hi.w));
