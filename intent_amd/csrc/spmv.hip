@@ -23,9 +23,10 @@
 //     many large rows, gathering from LDS (spmv_slices).
 // Each piece runs on one wave: coalesced loads of its columns and values, one reduction per piece.
 // The medium and large row lists are built without atomics: spmv_count counts each 1024-row
-// block's rows of each class, spmv_scan (one workgroup) turns the counts into list offsets, and
-// spmv_rows writes each block's rows at its offset in row order. (Wave-level atomics on two list
-// counters cost 115 us at config 5.) The cut workgroups of spmv_rows estimate each cut by
+// block's rows of each class, and the totals of each group of 16 blocks; spmv_rows sums the
+// totals and counts before a block into its list offset and writes the block's rows there in row
+// order. (Wave-level atomics on two list counters cost 115 us at config 5; a one-workgroup scan
+// launch between the two kernels cost 9 us.) The cut workgroups of spmv_rows estimate each cut by
 // interpolation search and make the cuts of a row non-decreasing with a prefix maximum, so the
 // pieces partition the row for any estimate and any column order; an entry outside its window or
 // slice only reads x from another place. spmv_combine adds the pieces of each medium or large row
@@ -41,8 +42,9 @@ namespace {
 constexpr int kLaneRow = 4;         // rows of up to 4 nonzeros: one lane, exact ordered fold
 constexpr int kGroupRow = 128;      // rows below 128 nonzeros: 16 lanes
 constexpr int kGroup = 16;
-constexpr int kRowsPerThread = 4;   // spmv_count / spmv_rows: 1024 rows per 256-thread workgroup
+constexpr int kRowsPerThread = 4;   // spmv_rows: 1024 rows per 256-thread workgroup
 constexpr int kBlockRows = 256 * kRowsPerThread;
+constexpr int kSuperBlocks = 16;    // spmv_count: one wave per block, 16 blocks per workgroup
 constexpr int kWindows = 8;         // one column window per XCD
 constexpr int kSliceCols = 32768;   // 128 KB of x in LDS per workgroup
 constexpr int kSliceTiles = 256;    // slice workgroups per launch: one per CU, all resident at once
@@ -55,14 +57,14 @@ inline size_t align256(size_t bytes) { return (bytes + 255) & ~static_cast<size_
 struct Plan {
   int32_t *counters;      // [64]: [0] medium rows, [1] large rows
   int32_t *block_counts;  // [blocks][2]: medium and large rows of each 1024-row block
-  int32_t *block_first;   // [blocks][2]: their first list index (exclusive scan)
+  int32_t *super_counts;  // [supers][2]: the same of each group of kSuperBlocks blocks
   int32_t *mid_rows;      // [cap_mid] row ids of medium rows, in row order
   int32_t *big_rows;      // [cap_big]
   int32_t *mid_cuts;      // [cap_mid][9]: piece w is [cut w, cut w + 1)
   float *mid_parts;       // [cap_mid][8]
   int32_t *big_cuts;      // [cap_big][slices + 1]
   float *big_parts;       // [cap_big][slices]
-  int32_t cap_mid, cap_big, slices, big, blocks;
+  int32_t cap_mid, cap_big, slices, big, blocks, supers;
 };
 
 int64_t slice_count(int64_t cols) { return cols > 0 ? (cols + kSliceCols - 1) / kSliceCols : 1; }
@@ -74,13 +76,15 @@ int64_t big_capacity(int64_t rows, int64_t nnz, int64_t slices) {
   return by_nnz < rows ? by_nnz : rows;
 }
 int64_t block_count(int64_t rows) { return (rows + kBlockRows - 1) / kBlockRows; }
+int64_t super_count(int64_t rows) { return (block_count(rows) + kSuperBlocks - 1) / kSuperBlocks; }
 // Entries (cuts plus parts plus row ids) of the large-row region: cap_big * (2 S + 2) <= 18 nnz / 128
 // for every slice count S, so the bound below holds whatever the column count.
 int64_t big_entries_bound(int64_t nnz) { return (18 * nnz + 127) / 128 + 64; }
 
 size_t workspace_bytes(int64_t rows, int64_t nnz) {
   const int64_t cap_mid = mid_capacity(rows, nnz);
-  return 256 + 2 * align256(8 * static_cast<size_t>(block_count(rows))) + align256(4 * static_cast<size_t>(cap_mid)) +
+  return 256 + align256(8 * static_cast<size_t>(block_count(rows))) + align256(8 * static_cast<size_t>(super_count(rows))) +
+         align256(4 * static_cast<size_t>(cap_mid)) +
          align256(36 * static_cast<size_t>(cap_mid)) + align256(32 * static_cast<size_t>(cap_mid)) +
          align256(4 * static_cast<size_t>(big_entries_bound(nnz))) + 1024;
 }
@@ -92,13 +96,14 @@ Plan carve(void *base, int64_t rows, int64_t cols, int64_t nnz) {
   p.cap_mid = static_cast<int32_t>(mid_capacity(rows, nnz));
   p.cap_big = static_cast<int32_t>(big_capacity(rows, nnz, p.slices));
   p.blocks = static_cast<int32_t>(block_count(rows));
+  p.supers = static_cast<int32_t>(super_count(rows));
   char *c = static_cast<char *>(base);
   p.counters = reinterpret_cast<int32_t *>(c);
   c += 256;
   p.block_counts = reinterpret_cast<int32_t *>(c);
   c += align256(8 * static_cast<size_t>(p.blocks));
-  p.block_first = reinterpret_cast<int32_t *>(c);
-  c += align256(8 * static_cast<size_t>(p.blocks));
+  p.super_counts = reinterpret_cast<int32_t *>(c);
+  c += align256(8 * static_cast<size_t>(p.supers));
   p.mid_rows = reinterpret_cast<int32_t *>(c);
   c += align256(4 * static_cast<size_t>(p.cap_mid));
   p.mid_cuts = reinterpret_cast<int32_t *>(c);
@@ -140,78 +145,72 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   return v;
 }
 
-// Medium and large rows of every 1024-row block (rows base + tid + 256 k).
-__global__ __launch_bounds__(256) void spmv_count(const int32_t *__restrict__ off, int32_t rows, int64_t nnz,
-                                                  Plan plan) {
-  __shared__ int s_part[2][4];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kBlockRows;
+// Medium and large rows of every 1024-row block, and of every group of kSuperBlocks blocks (a
+// superblock): wave w of workgroup g counts block kSuperBlocks g + w, rows base + lane + 64 k, all
+// of its lane's offset loads issued together.
+__global__ __launch_bounds__(64 * kSuperBlocks) void spmv_count(const int32_t *__restrict__ off, int32_t rows,
+                                                              int64_t nnz, Plan plan) {
+  __shared__ int s_part[2][kSuperBlocks];
+  constexpr int kPer = kBlockRows / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int block = static_cast<int>(blockIdx.x) * kSuperBlocks + wave;
+  const int64_t base = static_cast<int64_t>(block) * kBlockRows;
   int mid = 0, big = 0;
+  if (block < plan.blocks) {   // wave-uniform
+    int32_t b[kPer], e[kPer];
 #pragma unroll
-  for (int k = 0; k < kRowsPerThread; ++k) {
-    const int64_t r = base + threadIdx.x + 256 * k;
-    if (r < rows) {
-      int32_t b, e;
-      row_span(off, r, nnz, b, e);
-      mid += (e - b >= kGroupRow && e - b < plan.big) ? 1 : 0;
-      big += (e - b >= plan.big) ? 1 : 0;
+    for (int k = 0; k < kPer; ++k) {
+      const int64_t r = base + lane + 64 * k;
+      b[k] = e[k] = 0;
+      if (r < rows) row_span(off, r, nnz, b[k], e[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      mid += (e[k] - b[k] >= kGroupRow && e[k] - b[k] < plan.big) ? 1 : 0;
+      big += (e[k] - b[k] >= plan.big) ? 1 : 0;
     }
   }
   mid = wave_sum_int(mid);
   big = wave_sum_int(big);
-  if ((threadIdx.x & 63) == 0) {
-    s_part[0][threadIdx.x >> 6] = mid;
-    s_part[1][threadIdx.x >> 6] = big;
+  if (lane == 0) {
+    if (block < plan.blocks) {
+      plan.block_counts[2 * block] = mid;
+      plan.block_counts[2 * block + 1] = big;
+    }
+    s_part[0][wave] = mid;
+    s_part[1][wave] = big;
   }
   __syncthreads();
-  if (threadIdx.x < 2)
-    plan.block_counts[2 * blockIdx.x + threadIdx.x] =
-        s_part[threadIdx.x][0] + s_part[threadIdx.x][1] + s_part[threadIdx.x][2] + s_part[threadIdx.x][3];
+  if (threadIdx.x < 2) {
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < kSuperBlocks; ++w) total += s_part[threadIdx.x][w];
+    plan.super_counts[2 * blockIdx.x + threadIdx.x] = total;
+  }
 }
 
-// Exclusive prefix sums of the block counts (one workgroup of 1024 threads); totals to counters.
-__global__ __launch_bounds__(1024) void spmv_scan(Plan plan) {
-  __shared__ int s_wave[2][16];
-  __shared__ int s_carry[2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < 2) s_carry[tid] = 0;
-  __syncthreads();
-  for (int b0 = 0; b0 < plan.blocks; b0 += 1024) {
-    const int b = b0 + tid;
-    int v[2];
-    int incl[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      v[c] = b < plan.blocks ? plan.block_counts[2 * b + c] : 0;
-      incl[c] = v[c];
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int up = __shfl_up(incl[c], d);
-        incl[c] += lane >= d ? up : 0;
-      }
-      if (lane == 63) s_wave[c][wave] = incl[c];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      int before = s_carry[c];
-      for (int w = 0; w < wave; ++w) before += s_wave[c][w];
-      if (b < plan.blocks) plan.block_first[2 * b + c] = before + incl[c] - v[c];
-    }
-    __syncthreads();
-    if (tid < 2) {
-      int total = s_carry[tid];
-      for (int w = 0; w < 16; ++w) total += s_wave[tid][w];
-      s_carry[tid] = total;
-    }
-    __syncthreads();
+// Medium and large rows before `block` (its lists' first positions), summed by the lanes of one
+// wave: the totals of the superblocks before its superblock, then the counts of the blocks before
+// it in its own. Every lane gets both sums.
+__device__ __forceinline__ void block_prefix(const Plan &plan, int block, int lane, int &first_mid, int &first_big) {
+  const int super = block / kSuperBlocks;
+  int mid = 0, big = 0;
+  for (int s = lane; s < super; s += 64) {
+    mid += plan.super_counts[2 * s];
+    big += plan.super_counts[2 * s + 1];
   }
-  if (tid < 2) plan.counters[tid] = s_carry[tid];
+  if (lane < block - super * kSuperBlocks) {
+    mid += plan.block_counts[2 * (super * kSuperBlocks + lane)];
+    big += plan.block_counts[2 * (super * kSuperBlocks + lane) + 1];
+  }
+  first_mid = wave_sum_int(mid);
+  first_big = wave_sum_int(big);
 }
 
 // Short rows and the row lists. Rows base + tid + 256 k of the block: rows of up to 4 nonzeros are
 // folded by their lane (the loads of the thread's four rows issued together); rows of 5..127 by a
 // 16-lane group (four rows per wave at a time); medium and large rows are written to their lists
-// at the block's scanned offset, in row order.
+// at the block's list offset (block_prefix), in row order.
 __device__ __forceinline__ void rows_block(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
                                            const float *__restrict__ val, const float *__restrict__ x,
                                            float *__restrict__ y, int32_t rows, int32_t cols, int64_t nnz, Plan plan,
@@ -257,7 +256,11 @@ __device__ __forceinline__ void rows_block(const int32_t *__restrict__ off, cons
     }
   }
   // Lists: rank of each medium / large row within the block, in row order (k, then thread).
-  int first[2] = {plan.block_first[2 * block], plan.block_first[2 * block + 1]};
+  int first[2];
+  block_prefix(plan, block, lane, first[0], first[1]);
+  // The last block's workgroup writes the list lengths that the piece kernels read.
+  if (block == plan.blocks - 1 && threadIdx.x < 2)
+    plan.counters[threadIdx.x] = first[threadIdx.x] + plan.block_counts[2 * block + threadIdx.x];
 #pragma unroll
   for (int k = 0; k < kRowsPerThread; ++k) {
     const bool is_mid = length[k] >= kGroupRow && length[k] < plan.big;
@@ -392,9 +395,9 @@ __device__ __forceinline__ void cut_row(const int32_t *__restrict__ col, int32_t
 
 // Cuts of the medium and large rows of one 1024-row block, by one wave: the block's rows are
 // classified again (as spmv_count did) and ranked in row order, which gives each its list position
-// from the scanned block offsets, the position spmv_rows writes the row id at. Medium rows go eight
-// at a time, one 8-lane group per row (9 cuts: the starts of windows 0..8); large rows one at a
-// time, the whole wave (slices + 1 cuts). `list` is the wave's LDS scratch for the block's rows.
+// from the block's list offset (block_prefix), the position spmv_rows writes the row id at. Medium
+// rows go eight at a time, one 8-lane group per row (9 cuts: the starts of windows 0..8); large
+// rows one at a time, the whole wave (slices + 1 cuts). `list` is the wave's LDS scratch for the block's rows.
 constexpr int kMidGroup = 8;
 __device__ __forceinline__ void cut_block(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
                                           int32_t rows, int32_t cols, int64_t nnz, const Plan &plan, int block,
@@ -428,7 +431,8 @@ __device__ __forceinline__ void cut_block(const int32_t *__restrict__ off, const
     }
   }
   __builtin_amdgcn_wave_barrier();
-  const int first_mid = plan.block_first[2 * block], first_big = plan.block_first[2 * block + 1];
+  int first_mid, first_big;
+  block_prefix(plan, block, lane, first_mid, first_big);
   const int64_t window = (static_cast<int64_t>(cols) + kWindows - 1) / kWindows;
   const int g = lane / kMidGroup;
   for (int q = 0; q < n_mid; q += 64 / kMidGroup) {   // wave-uniform
@@ -773,9 +777,8 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   const Plan plan = carve(workspace, rows, cols, nnz);
   const hipStream_t s = as_stream(stream);
   const int32_t r32 = static_cast<int32_t>(rows), c32 = static_cast<int32_t>(cols > 0 ? cols : 1);
-  const dim3 row_grid(static_cast<unsigned>(plan.blocks));
-  spmv_count<<<row_grid, dim3(256), 0, s>>>(row_offsets, r32, nnz, plan);
-  spmv_scan<<<1, 1024, 0, s>>>(plan);
+  spmv_count<<<dim3(static_cast<unsigned>(plan.supers)), dim3(64 * kSuperBlocks), 0, s>>>(row_offsets, r32, nnz,
+                                                                                         plan);
   // No row can be medium or large: no cut workgroups.
   const int cut_groups = plan.cap_mid == 0 && plan.cap_big == 0 ? 0 : (plan.blocks + 3) / 4;
   spmv_rows<<<dim3(static_cast<unsigned>(plan.blocks + cut_groups)), dim3(256), 0, s>>>(
