@@ -23,7 +23,7 @@
 //     many large rows, gathering from LDS (spmv_slices).
 // Each piece runs on one wave: coalesced loads of its columns and values, one reduction per piece.
 // The medium and large row lists are built without atomics: spmv_count counts each 1024-row
-// block's rows of each class, and the totals of each group of 16 blocks; spmv_rows sums the
+// block's rows of each class, and the totals of each group of 4 blocks; spmv_rows sums the
 // totals and counts before a block into its list offset and writes the block's rows there in row
 // order. (Wave-level atomics on two list counters cost 115 us at config 5; a one-workgroup scan
 // launch between the two kernels cost 9 us.) The cut workgroups of spmv_rows estimate each cut by
@@ -44,7 +44,7 @@ constexpr int kGroupRow = 128;      // rows below 128 nonzeros: 16 lanes
 constexpr int kGroup = 16;
 constexpr int kRowsPerThread = 4;   // spmv_rows: 1024 rows per 256-thread workgroup
 constexpr int kBlockRows = 256 * kRowsPerThread;
-constexpr int kSuperBlocks = 16;    // spmv_count: one wave per block, 16 blocks per workgroup
+constexpr int kSuperBlocks = 4;     // spmv_count: four blocks per 1024-thread workgroup
 constexpr int kWindows = 8;         // one column window per XCD
 constexpr int kSliceCols = 32768;   // 128 KB of x in LDS per workgroup
 constexpr int kSliceTiles = 256;    // slice workgroups per launch: one per CU, all resident at once
@@ -146,65 +146,81 @@ __device__ __forceinline__ int wave_sum_int(int v) {
 }
 
 // Medium and large rows of every 1024-row block, and of every group of kSuperBlocks blocks (a
-// superblock): wave w of workgroup g counts block kSuperBlocks g + w, rows base + lane + 64 k, all
-// of its lane's offset loads issued together.
-__global__ __launch_bounds__(64 * kSuperBlocks) void spmv_count(const int32_t *__restrict__ off, int32_t rows,
-                                                              int64_t nnz, Plan plan) {
-  __shared__ int s_part[2][kSuperBlocks];
-  constexpr int kPer = kBlockRows / 64;
+// superblock): threads 256 p .. 256 p + 255 of workgroup g count block kSuperBlocks g + p, four rows
+// each (rows base + t + 256 k, their offset loads issued together).
+__global__ __launch_bounds__(256 * kSuperBlocks) void spmv_count(const int32_t *__restrict__ off, int32_t rows,
+                                                               int64_t nnz, Plan plan) {
+  __shared__ int s_part[2][4 * kSuperBlocks];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int block = static_cast<int>(blockIdx.x) * kSuperBlocks + wave;
+  const int part = threadIdx.x >> 8, t = threadIdx.x & 255;
+  const int block = static_cast<int>(blockIdx.x) * kSuperBlocks + part;
   const int64_t base = static_cast<int64_t>(block) * kBlockRows;
   int mid = 0, big = 0;
-  if (block < plan.blocks) {   // wave-uniform
-    int32_t b[kPer], e[kPer];
+  int32_t b[kRowsPerThread], e[kRowsPerThread];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int64_t r = base + lane + 64 * k;
-      b[k] = e[k] = 0;
-      if (r < rows) row_span(off, r, nnz, b[k], e[k]);
-    }
+  for (int k = 0; k < kRowsPerThread; ++k) {
+    const int64_t r = base + t + 256 * k;
+    b[k] = e[k] = 0;
+    if (block < plan.blocks && r < rows) row_span(off, r, nnz, b[k], e[k]);
+  }
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      mid += (e[k] - b[k] >= kGroupRow && e[k] - b[k] < plan.big) ? 1 : 0;
-      big += (e[k] - b[k] >= plan.big) ? 1 : 0;
-    }
+  for (int k = 0; k < kRowsPerThread; ++k) {
+    mid += (e[k] - b[k] >= kGroupRow && e[k] - b[k] < plan.big) ? 1 : 0;
+    big += (e[k] - b[k] >= plan.big) ? 1 : 0;
   }
   mid = wave_sum_int(mid);
   big = wave_sum_int(big);
   if (lane == 0) {
-    if (block < plan.blocks) {
-      plan.block_counts[2 * block] = mid;
-      plan.block_counts[2 * block + 1] = big;
-    }
     s_part[0][wave] = mid;
     s_part[1][wave] = big;
   }
   __syncthreads();
-  if (threadIdx.x < 2) {
+  if (threadIdx.x < 2 * kSuperBlocks) {   // block counts: thread 2 p + c
+    const int p = threadIdx.x >> 1, c = threadIdx.x & 1;
+    const int blk = static_cast<int>(blockIdx.x) * kSuperBlocks + p;
+    if (blk < plan.blocks)
+      plan.block_counts[2 * blk + c] = s_part[c][4 * p] + s_part[c][4 * p + 1] + s_part[c][4 * p + 2] + s_part[c][4 * p + 3];
+  } else if (threadIdx.x < 2 * kSuperBlocks + 2) {   // superblock totals
+    const int c = threadIdx.x - 2 * kSuperBlocks;
     int total = 0;
 #pragma unroll
-    for (int w = 0; w < kSuperBlocks; ++w) total += s_part[threadIdx.x][w];
-    plan.super_counts[2 * blockIdx.x + threadIdx.x] = total;
+    for (int w = 0; w < 4 * kSuperBlocks; ++w) total += s_part[c][w];
+    plan.super_counts[2 * blockIdx.x + c] = total;
   }
 }
 
-// Medium and large rows before `block` (its lists' first positions), summed by the lanes of one
-// wave: the totals of the superblocks before its superblock, then the counts of the blocks before
-// it in its own. Every lane gets both sums.
-__device__ __forceinline__ void block_prefix(const Plan &plan, int block, int lane, int &first_mid, int &first_big) {
-  const int super = block / kSuperBlocks;
+// Medium and large rows in the superblocks before `super`, summed by every thread of a 256-thread
+// workgroup (all of them call it); `s_pre` is the workgroup's LDS scratch. Every thread gets both.
+__device__ __forceinline__ void superblock_prefix(const Plan &plan, int super, int &mid_before, int &big_before,
+                                                  int (*s_pre)[4]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int mid = 0, big = 0;
-  for (int s = lane; s < super; s += 64) {
+  for (int s = threadIdx.x; s < super; s += 256) {
     mid += plan.super_counts[2 * s];
     big += plan.super_counts[2 * s + 1];
   }
-  if (lane < block - super * kSuperBlocks) {
-    mid += plan.block_counts[2 * (super * kSuperBlocks + lane)];
-    big += plan.block_counts[2 * (super * kSuperBlocks + lane) + 1];
+  mid = wave_sum_int(mid);
+  big = wave_sum_int(big);
+  if (lane == 0) {
+    s_pre[0][wave] = mid;
+    s_pre[1][wave] = big;
   }
-  first_mid = wave_sum_int(mid);
-  first_big = wave_sum_int(big);
+  __syncthreads();
+  mid_before = s_pre[0][0] + s_pre[0][1] + s_pre[0][2] + s_pre[0][3];
+  big_before = s_pre[1][0] + s_pre[1][1] + s_pre[1][2] + s_pre[1][3];
+  __syncthreads();   // s_pre may be written again
+}
+
+// The list offsets of `block`: the superblocks before its own, then its own superblock's blocks
+// before it (at most kSuperBlocks - 1 counts, read by every lane).
+__device__ __forceinline__ void block_prefix(const Plan &plan, int block, int mid_super, int big_super, int &first_mid,
+                                             int &first_big) {
+  first_mid = mid_super;
+  first_big = big_super;
+  for (int j = block / kSuperBlocks * kSuperBlocks; j < block; ++j) {
+    first_mid += plan.block_counts[2 * j];
+    first_big += plan.block_counts[2 * j + 1];
+  }
 }
 
 // Short rows and the row lists. Rows base + tid + 256 k of the block: rows of up to 4 nonzeros are
@@ -257,7 +273,12 @@ __device__ __forceinline__ void rows_block(const int32_t *__restrict__ off, cons
   }
   // Lists: rank of each medium / large row within the block, in row order (k, then thread).
   int first[2];
-  block_prefix(plan, block, lane, first[0], first[1]);
+  {
+    __shared__ int s_pre[2][4];
+    int mid_super, big_super;
+    superblock_prefix(plan, block / kSuperBlocks, mid_super, big_super, s_pre);
+    block_prefix(plan, block, mid_super, big_super, first[0], first[1]);
+  }
   // The last block's workgroup writes the list lengths that the piece kernels read.
   if (block == plan.blocks - 1 && threadIdx.x < 2)
     plan.counters[threadIdx.x] = first[threadIdx.x] + plan.block_counts[2 * block + threadIdx.x];
@@ -401,7 +422,7 @@ __device__ __forceinline__ void cut_row(const int32_t *__restrict__ col, int32_t
 constexpr int kMidGroup = 8;
 __device__ __forceinline__ void cut_block(const int32_t *__restrict__ off, const int32_t *__restrict__ col,
                                           int32_t rows, int32_t cols, int64_t nnz, const Plan &plan, int block,
-                                          int lane, int32_t *list) {
+                                          int lane, int32_t *list, int first_mid, int first_big) {
   const int64_t base = static_cast<int64_t>(block) * kBlockRows;
   // Medium rows at list[0 ..), large rows at list[kBlockRows - 1] downwards, in row order. The
   // offsets are read 256 rows (4 per lane) at a time, all loads of a batch issued together (rows
@@ -431,8 +452,7 @@ __device__ __forceinline__ void cut_block(const int32_t *__restrict__ off, const
     }
   }
   __builtin_amdgcn_wave_barrier();
-  int first_mid, first_big;
-  block_prefix(plan, block, lane, first_mid, first_big);
+
   const int64_t window = (static_cast<int64_t>(cols) + kWindows - 1) / kWindows;
   const int g = lane / kMidGroup;
   for (int q = 0; q < n_mid; q += 64 / kMidGroup) {   // wave-uniform
@@ -467,8 +487,13 @@ __global__ __launch_bounds__(256) void spmv_rows(const int32_t *__restrict__ off
   __shared__ int32_t s_list[4][kBlockRows];
   if (static_cast<int>(blockIdx.x) < cut_groups) {   // workgroup-uniform
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int block = static_cast<int>(blockIdx.x) * 4 + wave;
-    if (block < plan.blocks) cut_block(off, col, rows, cols, nnz, plan, block, lane, s_list[wave]);
+    const int block = static_cast<int>(blockIdx.x) * 4 + wave;   // the four blocks of one superblock
+    __shared__ int s_pre[2][4];
+    int mid_super, big_super, first_mid, first_big;
+    superblock_prefix(plan, static_cast<int>(blockIdx.x), mid_super, big_super, s_pre);
+    block_prefix(plan, block, mid_super, big_super, first_mid, first_big);
+    if (block < plan.blocks)
+      cut_block(off, col, rows, cols, nnz, plan, block, lane, s_list[wave], first_mid, first_big);
     return;
   }
   rows_block(off, col, val, x, y, rows, cols, nnz, plan, static_cast<int>(blockIdx.x) - cut_groups);
@@ -777,8 +802,8 @@ extern "C" int intent_hip_csr_spmv_f32(const int32_t *row_offsets, const int32_t
   const Plan plan = carve(workspace, rows, cols, nnz);
   const hipStream_t s = as_stream(stream);
   const int32_t r32 = static_cast<int32_t>(rows), c32 = static_cast<int32_t>(cols > 0 ? cols : 1);
-  spmv_count<<<dim3(static_cast<unsigned>(plan.supers)), dim3(64 * kSuperBlocks), 0, s>>>(row_offsets, r32, nnz,
-                                                                                         plan);
+  spmv_count<<<dim3(static_cast<unsigned>(plan.supers)), dim3(256 * kSuperBlocks), 0, s>>>(row_offsets, r32, nnz,
+                                                                                          plan);
   // No row can be medium or large: no cut workgroups.
   const int cut_groups = plan.cap_mid == 0 && plan.cap_big == 0 ? 0 : (plan.blocks + 3) / 4;
   spmv_rows<<<dim3(static_cast<unsigned>(plan.blocks + cut_groups)), dim3(256), 0, s>>>(
