@@ -491,9 +491,10 @@ __global__ __launch_bounds__(256) void spmv_rows(const int32_t *__restrict__ off
     __shared__ int s_pre[2][4];
     int mid_super, big_super, first_mid, first_big;
     superblock_prefix(plan, static_cast<int>(blockIdx.x), mid_super, big_super, s_pre);
-    block_prefix(plan, block, mid_super, big_super, first_mid, first_big);
-    if (block < plan.blocks)
+    if (block < plan.blocks) {   // wave-uniform; the last group may hold fewer than four blocks
+      block_prefix(plan, block, mid_super, big_super, first_mid, first_big);
       cut_block(off, col, rows, cols, nnz, plan, block, lane, s_list[wave], first_mid, first_big);
+    }
     return;
   }
   rows_block(off, col, val, x, y, rows, cols, nnz, plan, static_cast<int>(blockIdx.x) - cut_groups);
