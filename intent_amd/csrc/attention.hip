@@ -627,8 +627,9 @@ constexpr int kMaxKeySplits = 8;
 // the largest maximum), normalised by an approximate reciprocal and stored in the element type E;
 // a row with no admitted key in any split is 0. One thread per row and 8-column block, threads in
 // the order of the sums' layout ([column / 8][row][column % 8] within each split), so a wave reads
-// 2 KB of every split contiguously. The splits are unrolled (at most kMaxKeySplits), with every
-// load issued unconditionally (indices clamped) and the splits past `splits` masked.
+// 2 KB of every split contiguously. The splits are unrolled (at most kMaxKeySplits): the maxima
+// are loaded first (indices clamped, the splits past `splits` masked), then the denominator and
+// sums of each split that holds a key for the row.
 template <typename E, int DV>
 __global__ __launch_bounds__(256) void attention_split_merge(const float *__restrict__ m, const float *__restrict__ den,
                                                              const float *__restrict__ acc, int splits, int64_t rows,
